@@ -1,0 +1,495 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) — TEST INFRASTRUCTURE ONLY.
+
+The oracle is a C++ restatement of the FerrisInfer reference CPU path (Rust sources under
+crates/ferrisinfer-{kernel,runtime,model}); each C++ function cites the reference
+file:line it follows.  Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module, and only as the checker or the timed CPU
+baseline.  The product path (ferrisinfer_amd) never imports it.
+
+Parity pinning of every oracle function is listed in tests/test_oracle_golden.py (reference
+known-answer vectors) and tests/test_oracle_invariants.py (closed forms / brute force).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+ERROR_KINDS = ["Io", "Parse", "InvalidShape", "InvalidLayout", "InvalidType", "InvalidConfig",
+               "MissingWeight", "Unsupported", "Runtime"]
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.kind = ERROR_KINDS[status - 1] if 0 < status <= len(ERROR_KINDS) else f"status{status}"
+        super().__init__(f"{self.kind}: {message}")
+
+
+def build(force: bool = False) -> str:
+    """Compiles liboracle.so with the committed Makefile (g++, -ffp-contract=off)."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-B" if force else "-s"], cwd=_HERE, check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+F32P = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+U32P = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+I32P = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+I64P = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+U16P = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+I64 = C.c_int64
+VP = C.c_void_p
+
+_SIGS = {
+    "orc_embedding_gather_f32": [F32P, I64, I64, U32P, I64, F32P],
+    "orc_rms_norm_f32": [F32P, F32P, I64, I64, C.c_float, F32P],
+    "orc_matmul_f32": [F32P, F32P, I64, I64, I64, F32P],
+    "orc_linear_f32_with_bias": [F32P, F32P, VP, I64, I64, I64, F32P],
+    "orc_matmul_rhs_transposed_f32": [F32P, F32P, I64, I64, I64, F32P],
+    "orc_matmul_rhs_transposed_argmax_f32": [F32P, F32P, I64, I64, C.POINTER(C.c_uint32),
+                                             C.POINTER(C.c_float)],
+    "orc_argmax_last_token": [F32P, I64, I64, C.POINTER(C.c_uint32), C.POINTER(C.c_float)],
+    "orc_rope_f32": [F32P, F32P, I64, I64, I64, I64, I64, I64, C.c_float],
+    "orc_prefixed_causal_attention_f32": [F32P, F32P, F32P, I64, I64, I64, I64, I64, F32P],
+    "orc_cached_prefixed_causal_attention_f32": [F32P, F32P, F32P, I64, F32P, F32P, I64, I64,
+                                                 I64, I64, F32P],
+    "orc_decode_causal_attention_f32": [F32P, F32P, F32P, I64, F32P, F32P, I64, I64, I64, F32P],
+    "orc_silu_f32_in_place": [F32P, I64],
+    "orc_mul_f32_in_place": [F32P, F32P, I64],
+    "orc_add_f32_in_place": [F32P, F32P, I64],
+    "orc_paged_decode_gather_attention": [F32P, F32P, F32P, I32P, I64, I32P, I64, I64, I64, I64,
+                                          I64, F32P],
+    "orc_paged_kv_write_sequence": [VP, I64, I64, I64, F32P, F32P],
+    "orc_paged_kv_write_slot": [VP, I64, I64, F32P, F32P],
+    "orc_paged_kv_read_prefix": [VP, I64, I64, F32P, F32P],
+    "orc_paged_kv_block_table": [VP, I64, I64, I64P, I64, C.POINTER(I64)],
+    "orc_paged_kv_page_infos": [VP, I64, I64P, I64, C.POINTER(I64)],
+    "orc_paged_kv_import_prefix": [VP, VP, I64],
+    "orc_model_set_weight": [VP, C.c_char_p, F32P, I64],
+    "orc_model_forward_logits": [VP, U32P, I64, F32P],
+    "orc_session_prefill": [VP, U32P, I64],
+    "orc_session_step": [VP, C.POINTER(C.c_uint32), C.POINTER(C.c_float)],
+    "orc_session_last_sample": [VP, C.POINTER(C.c_uint32), C.POINTER(C.c_float)],
+    "orc_session_last_hidden": [VP, F32P],
+    "orc_session_copy_prefix": [VP, VP, I64],
+    "orc_session_read_prefix": [VP, I64, I64, F32P, F32P],
+    "orc_scheduler_submit": [VP, U32P, I64, I64, I64, C.POINTER(C.c_uint64)],
+    "orc_scheduler_execute_next_tick": [VP, C.POINTER(C.c_int32)],
+    "orc_scheduler_last_report": [VP, C.POINTER(C.c_int32), I64P, F32P, I64, C.POINTER(I64)],
+    "orc_scheduler_last_released": [VP, I64, I64P, I64, C.POINTER(I64)],
+    "orc_scheduler_generated": [VP, C.c_uint64, U32P, I64, C.POINTER(I64)],
+    "orc_scheduler_block_ref_count": [VP, C.c_uint64, I64, I64, C.POINTER(I64)],
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = C.c_int32
+        L.orc_last_error.restype = C.c_char_p
+        L.orc_runtime_last_error.restype = C.c_char_p
+        L.orc_set_threads.argtypes = [I64]
+        L.orc_set_threads.restype = None
+        L.orc_threads.restype = I64
+        L.orc_f32_to_bf16_rne.argtypes = [F32P, U16P, I64]
+        L.orc_f32_to_bf16_rne.restype = None
+        L.orc_bf16_to_f32.argtypes = [U16P, F32P, I64]
+        L.orc_bf16_to_f32.restype = None
+        L.orc_paged_kv_create.argtypes = [I64] * 5
+        L.orc_paged_kv_create.restype = VP
+        L.orc_paged_kv_destroy.argtypes = [VP]
+        L.orc_paged_kv_destroy.restype = None
+        L.orc_paged_kv_reset.argtypes = [VP]
+        L.orc_paged_kv_reset.restype = None
+        L.orc_paged_kv_allocated_pages.argtypes = [VP, I64]
+        L.orc_paged_kv_allocated_pages.restype = I64
+        L.orc_paged_kv_free_pages.argtypes = [VP, I64]
+        L.orc_paged_kv_free_pages.restype = I64
+        L.orc_model_create.argtypes = [I64] * 7 + [C.c_float, C.c_float, I64, C.c_int32]
+        L.orc_model_create.restype = VP
+        L.orc_model_destroy.argtypes = [VP]
+        L.orc_model_destroy.restype = None
+        L.orc_session_create.argtypes = [VP, I64, I64, I64]
+        L.orc_session_create.restype = VP
+        L.orc_session_destroy.argtypes = [VP]
+        L.orc_session_destroy.restype = None
+        L.orc_session_position.argtypes = [VP]
+        L.orc_session_position.restype = I64
+        L.orc_scheduler_create.argtypes = [VP] + [I64] * 8
+        L.orc_scheduler_create.restype = VP
+        L.orc_scheduler_destroy.argtypes = [VP]
+        L.orc_scheduler_destroy.restype = None
+        L.orc_scheduler_has_pending.argtypes = [VP]
+        L.orc_scheduler_has_pending.restype = C.c_int32
+        _lib = L
+    return _lib
+
+
+def _check(status: int, runtime: bool = False):
+    if status != 0:
+        L = lib()
+        msg = (L.orc_runtime_last_error() if runtime else L.orc_last_error()) or b""
+        raise OracleError(status, msg.decode())
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def threads() -> int:
+    return int(lib().orc_threads())
+
+
+# ----------------------------------------------------------------- kernels
+def embedding_gather(embedding, ids):
+    e = f32(embedding)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    out = np.zeros((ids.size, e.shape[1]), np.float32)
+    _check(lib().orc_embedding_gather_f32(e, e.shape[0], e.shape[1], ids, ids.size, out))
+    return out
+
+
+def rms_norm(x, w, eps):
+    x = f32(x)
+    w = f32(w)
+    out = np.zeros_like(x)
+    hidden = x.shape[-1]
+    _check(lib().orc_rms_norm_f32(x, w, x.size // hidden, hidden, eps, out))
+    return out
+
+
+def matmul(a, b):
+    a, b = f32(a), f32(b)
+    out = np.zeros((a.shape[0], b.shape[1]), np.float32)
+    _check(lib().orc_matmul_f32(a, b, a.shape[0], a.shape[1], b.shape[1], out))
+    return out
+
+
+def linear_with_bias(x, w, bias=None):
+    x, w = f32(x), f32(w)
+    out = np.zeros((x.shape[0], w.shape[1]), np.float32)
+    bias_arr = f32(bias) if bias is not None else None
+    ptr = bias_arr.ctypes.data_as(C.c_void_p) if bias_arr is not None else None
+    _check(lib().orc_linear_f32_with_bias(x, w, ptr, x.shape[0], x.shape[1], w.shape[1], out))
+    return out
+
+
+def matmul_rhs_transposed(a, b):
+    a, b = f32(a), f32(b)
+    out = np.zeros((a.shape[0], b.shape[0]), np.float32)
+    _check(lib().orc_matmul_rhs_transposed_f32(a, b, a.shape[0], a.shape[1], b.shape[0], out))
+    return out
+
+
+def matmul_rhs_transposed_argmax(h, w):
+    h, w = f32(h), f32(w)
+    idx = C.c_uint32()
+    prob = C.c_float()
+    _check(lib().orc_matmul_rhs_transposed_argmax_f32(h, w, w.shape[1], w.shape[0],
+                                                      C.byref(idx), C.byref(prob)))
+    return int(idx.value), float(prob.value)
+
+
+def argmax_last_token(logits):
+    logits = f32(logits)
+    if logits.ndim == 1:
+        logits = logits[None, :]
+    idx = C.c_uint32()
+    prob = C.c_float()
+    _check(lib().orc_argmax_last_token(logits, logits.shape[0], logits.shape[1], C.byref(idx),
+                                       C.byref(prob)))
+    return int(idx.value), float(prob.value)
+
+
+def rope(q, k, position_offset, rotary_dims, theta):
+    """q [T,Hq,D], k [T,Hkv,D]; returns rotated copies."""
+    q, k = f32(q).copy(), f32(k).copy()
+    _check(lib().orc_rope_f32(q, k, q.shape[0], q.shape[1], k.shape[1], q.shape[2],
+                              position_offset, rotary_dims, theta))
+    return q, k
+
+
+def prefixed_causal_attention(q, k, v, cache_len):
+    q, k, v = f32(q), f32(k), f32(v)
+    out = np.zeros_like(q)
+    _check(lib().orc_prefixed_causal_attention_f32(q, k, v, q.shape[0], cache_len, q.shape[1],
+                                                   k.shape[1], q.shape[2], out))
+    return out
+
+
+def causal_self_attention(q, k, v):
+    return prefixed_causal_attention(q, k, v, 0)
+
+
+def cached_prefixed_causal_attention(q, ck, cv, cache_len, ks, vs):
+    q, ck, cv, ks, vs = (f32(x) for x in (q, ck, cv, ks, vs))
+    out = np.zeros_like(q)
+    _check(lib().orc_cached_prefixed_causal_attention_f32(q, ck, cv, cache_len, ks, vs,
+                                                          q.shape[0], q.shape[1], ks.shape[1],
+                                                          q.shape[2], out))
+    return out
+
+
+def decode_causal_attention(q, ck, cv, cache_len, kslot, vslot):
+    q, ck, cv, kslot, vslot = (f32(x) for x in (q, ck, cv, kslot, vslot))
+    out = np.zeros_like(q)
+    _check(lib().orc_decode_causal_attention_f32(q, ck, cv, cache_len, kslot, vslot, q.shape[1],
+                                                 kslot.shape[0], q.shape[2], out))
+    return out
+
+
+def silu(x):
+    x = f32(x).copy()
+    _check(lib().orc_silu_f32_in_place(x, x.size))
+    return x
+
+
+def mul(a, b):
+    a = f32(a).copy()
+    _check(lib().orc_mul_f32_in_place(a, f32(b), a.size))
+    return a
+
+
+def add(a, b):
+    a = f32(a).copy()
+    _check(lib().orc_add_f32_in_place(a, f32(b), a.size))
+    return a
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = f32(x)
+    out = np.zeros(x.shape, np.uint16)
+    lib().orc_f32_to_bf16_rne(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def bf16_to_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out = np.zeros(x.shape, np.float32)
+    lib().orc_bf16_to_f32(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def paged_decode_gather_attention(q, k_pages, v_pages, block_tables, context_lens, page_size):
+    """Reference paged decode (gather + cached-prefixed attention) over pages laid out
+    [num_blocks, page_size, Hkv, D]; q [B, Hq, D]."""
+    q, kp, vp = f32(q), f32(k_pages), f32(v_pages)
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    cl = np.ascontiguousarray(context_lens, dtype=np.int32)
+    out = np.zeros_like(q)
+    _check(lib().orc_paged_decode_gather_attention(q, kp, vp, bt, bt.shape[1], cl, q.shape[0],
+                                                   q.shape[1], kp.shape[2], q.shape[2],
+                                                   page_size, out), runtime=True)
+    return out
+
+
+# ----------------------------------------------------------------- paged KV storage
+class PagedKvStorage:
+    """runtime/paged_kv.rs PagedKvCacheStorage restated (per-layer pages, LIFO free list)."""
+
+    def __init__(self, layers, kv_heads, head_dim, max_seq, page_size):
+        self.h = lib().orc_paged_kv_create(layers, kv_heads, head_dim, max_seq, page_size)
+        if not self.h:
+            raise OracleError(6, lib().orc_runtime_last_error().decode())
+        self.kv_heads, self.head_dim, self.page_size, self.max_seq = kv_heads, head_dim, page_size, max_seq
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_paged_kv_destroy(self.h)
+            self.h = None
+
+    def write_sequence(self, layer, start, k, v):
+        k, v = f32(k), f32(v)
+        _check(lib().orc_paged_kv_write_sequence(self.h, layer, start, k.shape[0], k, v), True)
+
+    def write_slot(self, layer, pos, k, v):
+        _check(lib().orc_paged_kv_write_slot(self.h, layer, pos, f32(k), f32(v)), True)
+
+    def read_prefix(self, layer, length):
+        k = np.zeros((length, self.kv_heads, self.head_dim), np.float32)
+        v = np.zeros_like(k)
+        _check(lib().orc_paged_kv_read_prefix(self.h, layer, length, k, v), True)
+        return k, v
+
+    def block_table(self, layer, tokens):
+        cap = tokens // self.page_size + 2
+        e = np.zeros((cap, 4), np.int64)
+        n = I64()
+        _check(lib().orc_paged_kv_block_table(self.h, layer, tokens, e, cap, C.byref(n)), True)
+        return [tuple(int(x) for x in row) for row in e[: n.value]]
+
+    def page_infos(self, layer):
+        cap = self.max_seq // self.page_size + 2
+        e = np.zeros((cap, 3), np.int64)
+        n = I64()
+        _check(lib().orc_paged_kv_page_infos(self.h, layer, e, cap, C.byref(n)), True)
+        return [tuple(int(x) for x in row) for row in e[: n.value]]
+
+    def allocated_pages(self, layer):
+        return int(lib().orc_paged_kv_allocated_pages(self.h, layer))
+
+    def free_pages(self, layer):
+        return int(lib().orc_paged_kv_free_pages(self.h, layer))
+
+    def reset(self):
+        lib().orc_paged_kv_reset(self.h)
+
+    def import_prefix_from(self, source: "PagedKvStorage", tokens: int):
+        _check(lib().orc_paged_kv_import_prefix(self.h, source.h, tokens), True)
+
+
+# ----------------------------------------------------------------- model / session / scheduler
+class Model:
+    """Decoder-only model (model/config.rs, model/decoder.rs); weights [in, out] like the
+    reference's internal layout."""
+
+    def __init__(self, hidden, intermediate, layers, heads, kv_heads, vocab, max_pos=4096,
+                 eps=1e-6, theta=10000.0, rotary_dims=None, tie=False):
+        head_dim = hidden // heads
+        rotary = head_dim if rotary_dims is None else rotary_dims
+        self.h = lib().orc_model_create(hidden, intermediate, layers, heads, kv_heads, vocab,
+                                        max_pos, eps, theta, rotary, 1 if tie else 0)
+        if not self.h:
+            raise OracleError(6, lib().orc_runtime_last_error().decode())
+        self.vocab, self.hidden = vocab, hidden
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_model_destroy(self.h)
+            self.h = None
+
+    def set_weight(self, name, array):
+        a = f32(array).reshape(-1)
+        _check(lib().orc_model_set_weight(self.h, name.encode(), a, a.size), True)
+
+    def set_weights(self, weights: dict):
+        for k, v in weights.items():
+            self.set_weight(k, v)
+
+    def forward_logits(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.zeros((ids.size, self.vocab), np.float32)
+        _check(lib().orc_model_forward_logits(self.h, ids, ids.size, out), True)
+        return out
+
+
+class Session:
+    def __init__(self, model: Model, max_seq=4096, max_gen=512, page_size=0):
+        self.model = model
+        self.h = lib().orc_session_create(model.h, max_seq, max_gen, page_size)
+        if not self.h:
+            raise OracleError(6, lib().orc_runtime_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_session_destroy(self.h)
+            self.h = None
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        _check(lib().orc_session_prefill(self.h, ids, ids.size), True)
+
+    def step(self):
+        t, p = C.c_uint32(), C.c_float()
+        _check(lib().orc_session_step(self.h, C.byref(t), C.byref(p)), True)
+        return int(t.value), float(p.value)
+
+    def last_sample(self):
+        t, p = C.c_uint32(), C.c_float()
+        _check(lib().orc_session_last_sample(self.h, C.byref(t), C.byref(p)), True)
+        return int(t.value), float(p.value)
+
+    def last_hidden(self):
+        out = np.zeros(self.model.hidden, np.float32)
+        _check(lib().orc_session_last_hidden(self.h, out), True)
+        return out
+
+    @property
+    def position(self):
+        return int(lib().orc_session_position(self.h))
+
+    def copy_prefix_from(self, source: "Session", tokens: int):
+        _check(lib().orc_session_copy_prefix(self.h, source.h, tokens), True)
+
+
+class Scheduler:
+    def __init__(self, model: Model, max_seq=4096, max_gen=512, page_size=16, max_batch=16,
+                 max_chunk=256, max_batch_tokens=1024, max_consecutive_prefill=2, min_share=64):
+        self.model = model
+        self.h = lib().orc_scheduler_create(model.h, max_seq, max_gen, page_size, max_batch,
+                                            max_chunk, max_batch_tokens, max_consecutive_prefill,
+                                            min_share)
+        if not self.h:
+            raise OracleError(6, lib().orc_runtime_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_scheduler_destroy(self.h)
+            self.h = None
+
+    def submit(self, ids, max_new_tokens=128, stop_token=None):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = C.c_uint64()
+        _check(lib().orc_scheduler_submit(self.h, ids, ids.size, max_new_tokens,
+                                          -1 if stop_token is None else stop_token,
+                                          C.byref(out)), True)
+        return int(out.value)
+
+    def execute_next_tick(self):
+        """Returns None or (kind, [update dicts])."""
+        ex = C.c_int32()
+        _check(lib().orc_scheduler_execute_next_tick(self.h, C.byref(ex)), True)
+        if not ex.value:
+            return None
+        cap = 4096
+        rows = np.zeros((cap, 9), np.int64)
+        probs = np.zeros(cap, np.float32)
+        kind = C.c_int32()
+        n = I64()
+        _check(lib().orc_scheduler_last_report(self.h, C.byref(kind), rows, probs, cap,
+                                               C.byref(n)), True)
+        updates = []
+        for i in range(n.value):
+            r = rows[i]
+            rel = np.zeros((max(int(r[8]), 1), 3), np.int64)
+            nr = I64()
+            _check(lib().orc_scheduler_last_released(self.h, i, rel, rel.shape[0], C.byref(nr)),
+                   True)
+            updates.append(dict(sequence_id=int(r[0]), batch_kind=int(r[1]), reused=int(r[2]),
+                                appended=int(r[3]), token=(int(r[5]) if r[4] else None),
+                                probability=float(probs[i]), phase=int(r[6]),
+                                finish_reason=int(r[7]),
+                                released=[tuple(int(x) for x in row) for row in rel[: nr.value]]))
+        return int(kind.value), updates
+
+    def has_pending(self):
+        return bool(lib().orc_scheduler_has_pending(self.h))
+
+    def generated(self, seq):
+        out = np.zeros(65536, np.uint32)
+        n = I64()
+        _check(lib().orc_scheduler_generated(self.h, seq, out, out.size, C.byref(n)), True)
+        return [int(x) for x in out[: n.value]]
+
+    def block_ref_count(self, owner, layer, block):
+        out = I64()
+        _check(lib().orc_scheduler_block_ref_count(self.h, owner, layer, block, C.byref(out)),
+               True)
+        return int(out.value)

@@ -1,0 +1,90 @@
+// CPU oracle for the ferrisinfer_amd parity tests — TEST INFRASTRUCTURE ONLY.
+//
+// A C++17 restatement of the FerrisInfer reference CPU path (Rust, crates under
+// /root/reference/crates).  Every function follows the reference's arithmetic
+// order: sequential f32 sums, no FMA contraction (built with -ffp-contract=off),
+// multiply-by-reciprocal normalisation, glibc expf/sinf/cosf/powf.  Only
+// tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load the
+// library built from these sources, and only as the checker or the timed CPU
+// baseline — never as a product code path.
+//
+// Status codes: 0 = ok, otherwise ErrorKind index + 1 in the order of
+// crates/ferrisinfer-core/src/error.rs:6-16.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace orc {
+
+enum class ErrorKind : int32_t {
+  Io = 0,
+  Parse,
+  InvalidShape,
+  InvalidLayout,
+  InvalidType,
+  InvalidConfig,
+  MissingWeight,
+  Unsupported,
+  Runtime,
+};
+
+struct Error {
+  ErrorKind kind;
+  std::string message;
+};
+
+// Thrown by oracle internals; converted to a status code at the C boundary.
+struct OracleError {
+  ErrorKind kind;
+  std::string message;
+};
+
+[[noreturn]] void fail(ErrorKind kind, const std::string& message);
+
+// std::thread::available_parallelism() stand-in; settable so the CPU baseline
+// can pin a thread count (0 = hardware concurrency).
+size_t available_parallelism();
+void set_available_parallelism(size_t threads);
+
+// ---- kernel/cpu restatements (crates/ferrisinfer-kernel/src/cpu/*.rs) ----
+void embedding_gather_f32(const float* embedding, size_t vocab, size_t hidden,
+                          const uint32_t* token_ids, size_t rows, float* out);
+void rms_norm_f32(const float* input, const float* weight, size_t rows, size_t hidden,
+                  float eps, float* out);
+void matmul_f32(const float* lhs, const float* rhs, size_t m, size_t k, size_t n, float* out);
+void matmul_rhs_transposed_f32(const float* lhs, const float* rhs, size_t m, size_t k,
+                               size_t n, float* out);
+void matmul_rhs_transposed_argmax_f32(const float* lhs, const float* rhs, size_t k, size_t n,
+                                      uint32_t* best_index, float* probability);
+void linear_f32_with_bias(const float* input, const float* weight, const float* bias,
+                          size_t m, size_t k, size_t n, float* out);
+void rope_f32(float* query, float* key, size_t seq_len, size_t query_heads, size_t key_heads,
+              size_t head_dim, size_t position_offset, size_t rotary_dims, float theta);
+void prefixed_causal_attention_f32(const float* query, const float* key, const float* value,
+                                   size_t query_len, size_t cache_len, size_t num_query_heads,
+                                   size_t num_kv_heads, size_t head_dim, float* out);
+void cached_prefixed_causal_attention_f32(const float* query, const float* cached_key,
+                                          const float* cached_value, size_t cache_len,
+                                          const float* key_suffix, const float* value_suffix,
+                                          size_t query_len, size_t num_query_heads,
+                                          size_t num_kv_heads, size_t head_dim, float* out);
+void decode_causal_attention_f32(const float* query, const float* cached_key,
+                                 const float* cached_value, size_t cache_len,
+                                 const float* key_slot, const float* value_slot,
+                                 size_t num_query_heads, size_t num_kv_heads, size_t head_dim,
+                                 float* out);
+void silu_f32_in_place(float* values, size_t count);
+void mul_f32_in_place(float* out, const float* rhs, size_t count);
+void add_f32_in_place(float* out, const float* rhs, size_t count);
+void argmax_last_token(const float* logits, size_t seq_len, size_t vocab, uint32_t* token_id,
+                       float* probability);
+
+// bf16 storage helpers: widening is exact (crates/ferrisinfer-io/src/safetensors.rs:540-542);
+// narrowing is round-to-nearest-even (the GPU KV-append rule; the reference has no bf16 KV).
+float bf16_to_f32(uint16_t bits);
+uint16_t f32_to_bf16_rne(float value);
+
+}  // namespace orc
