@@ -1,0 +1,71 @@
+// Internal definitions shared by the HIP translation units of libferrisinfer_kernel.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/ferrisinfer_kernel.h"
+
+// Device-side fault bits (kernels OR them into fi_context::d_faults).
+enum : uint32_t {
+  FI_FAULT_SLOT_RANGE = 1u << 0,   // kv append: slot beyond the pool
+  FI_FAULT_TOKEN_RANGE = 1u << 1,  // embedding: token id beyond the vocabulary
+  FI_FAULT_BLOCK_RANGE = 1u << 2,  // attention: block id beyond the pool
+};
+
+struct fi_context {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t* d_faults = nullptr;  // [4] fault words, zeroed at create and by check_faults
+  void* workspace = nullptr;     // grow-only scratch for split-KV partials
+  size_t workspace_bytes = 0;
+  int compute_units = 0;
+};
+
+namespace fi {
+
+// Records `message` as the thread's last error and returns `code`.
+int32_t set_error(int32_t code, const std::string& message);
+
+// Maps a HIP error to Runtime with "<call> returned HIP error N (name)", the shape of
+// cuda_check (kernel/gpu/nvidia.rs:887-904).
+int32_t hip_error(hipError_t err, const char* call);
+
+// Makes ctx's device current; returns a status.
+int32_t enter(fi_context* ctx);
+
+// Ensures ctx->workspace holds at least `bytes` (grow-only; never shrinks).
+int32_t ensure_workspace(fi_context* ctx, size_t bytes);
+
+// Split-KV decode partials for the given launch shape.
+int32_t decode_scratch(fi_context* ctx, int32_t num_seqs, int32_t hq, int32_t parts, int32_t head_dim,
+                       float** part_acc, float** part_ml);
+
+}  // namespace fi
+
+#define FI_TRY_HIP(call)                                 \
+  do {                                                   \
+    hipError_t fi_err_ = (call);                         \
+    if (fi_err_ != hipSuccess) return fi::hip_error(fi_err_, #call); \
+  } while (0)
+
+#define FI_TRY(expr)                \
+  do {                              \
+    int32_t fi_st_ = (expr);        \
+    if (fi_st_ != FI_OK) return fi_st_; \
+  } while (0)
+
+#define FI_REQUIRE(cond, code, msg) \
+  do {                              \
+    if (!(cond)) return fi::set_error((code), (msg)); \
+  } while (0)
+
+// Launch-error check after a kernel launch.
+#define FI_CHECK_LAUNCH(name)                                 \
+  do {                                                        \
+    hipError_t fi_err_ = hipGetLastError();                   \
+    if (fi_err_ != hipSuccess) return fi::hip_error(fi_err_, name); \
+  } while (0)

@@ -1,0 +1,191 @@
+// Context, errors and device memory of libferrisinfer_kernel.so (host code only).
+// Mirrors the lifecycle and error shape of the reference's NVIDIA driver layer
+// (crates/ferrisinfer-kernel/src/gpu/nvidia.rs) on the HIP runtime.
+#include <cstring>
+#include <string>
+
+#include "fi_common.h"
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+namespace fi {
+
+int32_t set_error(int32_t code, const std::string& message) {
+  g_last_error = message;
+  return code;
+}
+
+int32_t hip_error(hipError_t err, const char* call) {
+  return set_error(FI_ERR_RUNTIME, std::string(call) + " returned HIP error " +
+                                       std::to_string(static_cast<int>(err)) + " (" +
+                                       hipGetErrorName(err) + ")");
+}
+
+int32_t enter(fi_context* ctx) {
+  FI_REQUIRE(ctx != nullptr, FI_ERR_INVALID_CONFIG, "null fi_context");
+  FI_TRY_HIP(hipSetDevice(ctx->device));
+  return FI_OK;
+}
+
+int32_t ensure_workspace(fi_context* ctx, size_t bytes) {
+  if (bytes <= ctx->workspace_bytes) return FI_OK;
+  if (ctx->workspace != nullptr) {
+    // The old workspace may still be read by queued kernels.
+    FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+    FI_TRY_HIP(hipFree(ctx->workspace));
+    ctx->workspace = nullptr;
+    ctx->workspace_bytes = 0;
+  }
+  size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+  FI_TRY_HIP(hipMalloc(&ctx->workspace, rounded));
+  ctx->workspace_bytes = rounded;
+  return FI_OK;
+}
+
+}  // namespace fi
+
+extern "C" {
+
+const char* fi_last_error(void) { return g_last_error.c_str(); }
+
+int32_t fi_ctx_create(int32_t ordinal, fi_context** out) {
+  FI_REQUIRE(out != nullptr, FI_ERR_INVALID_CONFIG, "fi_ctx_create: null output pointer");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0) {
+    return fi::set_error(FI_ERR_UNSUPPORTED, "no HIP device is available");
+  }
+  FI_REQUIRE(ordinal >= 0 && ordinal < count, FI_ERR_INVALID_CONFIG,
+             "device ordinal " + std::to_string(ordinal) + " out of range (" +
+                 std::to_string(count) + " devices)");
+  FI_TRY_HIP(hipSetDevice(ordinal));
+  hipDeviceProp_t prop;
+  FI_TRY_HIP(hipGetDeviceProperties(&prop, ordinal));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    return fi::set_error(FI_ERR_UNSUPPORTED, std::string("libferrisinfer_kernel is built for gfx950, device is ") +
+                                                 prop.gcnArchName);
+  }
+  auto* ctx = new fi_context();
+  ctx->device = ordinal;
+  ctx->compute_units = prop.multiProcessorCount;
+  hipError_t err = hipStreamCreate(&ctx->own_stream);
+  if (err != hipSuccess) {
+    delete ctx;
+    return fi::hip_error(err, "hipStreamCreate");
+  }
+  ctx->stream = ctx->own_stream;
+  err = hipMalloc(&ctx->d_faults, 4 * sizeof(uint32_t));
+  if (err == hipSuccess) err = hipMemset(ctx->d_faults, 0, 4 * sizeof(uint32_t));
+  if (err != hipSuccess) {
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return fi::hip_error(err, "hipMalloc(fault flags)");
+  }
+  *out = ctx;
+  return FI_OK;
+}
+
+int32_t fi_ctx_destroy(fi_context* ctx) {
+  if (ctx == nullptr) return FI_OK;
+  FI_TRY(fi::enter(ctx));
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->workspace) (void)hipFree(ctx->workspace);
+  if (ctx->d_faults) (void)hipFree(ctx->d_faults);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  delete ctx;
+  return FI_OK;
+}
+
+int32_t fi_ctx_sync(fi_context* ctx) {
+  FI_TRY(fi::enter(ctx));
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_ctx_set_stream(fi_context* ctx, void* stream) {
+  FI_TRY(fi::enter(ctx));
+  ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+  return FI_OK;
+}
+
+void* fi_ctx_stream(fi_context* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+int32_t fi_device_info(fi_context* ctx, char* name, size_t name_len, char* arch, size_t arch_len,
+                       uint64_t* hbm_bytes, int32_t* compute_units) {
+  FI_TRY(fi::enter(ctx));
+  hipDeviceProp_t prop;
+  FI_TRY_HIP(hipGetDeviceProperties(&prop, ctx->device));
+  if (name && name_len) {
+    std::strncpy(name, prop.name, name_len - 1);
+    name[name_len - 1] = '\0';
+  }
+  if (arch && arch_len) {
+    std::strncpy(arch, prop.gcnArchName, arch_len - 1);
+    arch[arch_len - 1] = '\0';
+  }
+  if (hbm_bytes) *hbm_bytes = prop.totalGlobalMem;
+  if (compute_units) *compute_units = prop.multiProcessorCount;
+  return FI_OK;
+}
+
+int32_t fi_buf_alloc(fi_context* ctx, size_t bytes, void** d_out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_buf_alloc: null output pointer");
+  FI_REQUIRE(bytes > 0, FI_ERR_INVALID_SHAPE, "device buffers must be larger than zero bytes");
+  FI_TRY_HIP(hipMalloc(d_out, bytes));
+  return FI_OK;
+}
+
+int32_t fi_buf_free(fi_context* ctx, void* d_ptr) {
+  FI_TRY(fi::enter(ctx));
+  if (d_ptr == nullptr) return FI_OK;
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  FI_TRY_HIP(hipFree(d_ptr));
+  return FI_OK;
+}
+
+int32_t fi_buf_upload(fi_context* ctx, void* d_dst, size_t dst_bytes, const void* src,
+                      size_t src_bytes) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(dst_bytes == src_bytes, FI_ERR_INVALID_SHAPE,
+             "upload requires matching lengths; buffer has " + std::to_string(dst_bytes) +
+                 " bytes but host slice has " + std::to_string(src_bytes) + " bytes");
+  if (src_bytes == 0) return FI_OK;
+  FI_TRY_HIP(hipMemcpyAsync(d_dst, src, src_bytes, hipMemcpyHostToDevice, ctx->stream));
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_buf_download(fi_context* ctx, void* dst, size_t dst_bytes, const void* d_src,
+                        size_t src_bytes) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(dst_bytes == src_bytes, FI_ERR_INVALID_SHAPE,
+             "download requires matching lengths; host slice has " + std::to_string(dst_bytes) +
+                 " bytes but buffer has " + std::to_string(src_bytes) + " bytes");
+  if (src_bytes == 0) return FI_OK;
+  FI_TRY_HIP(hipMemcpyAsync(dst, d_src, src_bytes, hipMemcpyDeviceToHost, ctx->stream));
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_ctx_check_faults(fi_context* ctx) {
+  FI_TRY(fi::enter(ctx));
+  uint32_t words[4] = {0, 0, 0, 0};
+  FI_TRY_HIP(hipMemcpyAsync(words, ctx->d_faults, sizeof(words), hipMemcpyDeviceToHost, ctx->stream));
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  uint32_t bits = words[0] | words[1] | words[2] | words[3];
+  if (bits == 0) return FI_OK;
+  uint32_t zero[4] = {0, 0, 0, 0};
+  FI_TRY_HIP(hipMemcpyAsync(ctx->d_faults, zero, sizeof(zero), hipMemcpyHostToDevice, ctx->stream));
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  std::string msg = "device kernels reported:";
+  if (bits & FI_FAULT_SLOT_RANGE) msg += " KV slot beyond the block pool;";
+  if (bits & FI_FAULT_TOKEN_RANGE) msg += " token id out of vocabulary range;";
+  if (bits & FI_FAULT_BLOCK_RANGE) msg += " block id beyond the block pool;";
+  return fi::set_error(FI_ERR_RUNTIME, msg);
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+"""ctypes binding of libferrisinfer_kernel.so (the C ABI in include/ferrisinfer_kernel.h).
+
+The shared library is the product: every op here calls straight into the HIP backend and
+raises :class:`FerrisError` with the reference's error kinds (core/error.rs:5-16) when it
+fails.  There is no fallback path: if the library is missing, importing ops raises.
+
+torch is used only as plumbing for device memory and streams: tensors are passed by
+``data_ptr()`` and the context enqueues on torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libferrisinfer_kernel.so")
+
+ERROR_KINDS = ["Io", "Parse", "InvalidShape", "InvalidLayout", "InvalidType", "InvalidConfig",
+               "MissingWeight", "Unsupported", "Runtime"]
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+
+class FerrisError(RuntimeError):
+    """FerrisError{kind, message} (core/error.rs:18-48) raised from a non-zero status."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = ERROR_KINDS[status - 1] if 0 < status <= len(ERROR_KINDS) else f"status{status}"
+        self.message = message
+        super().__init__(f"{self.kind}: {message}")
+
+
+_P = C.c_void_p
+_I32 = C.c_int32
+_I64 = C.c_int64
+_F32 = C.c_float
+_SZ = C.c_size_t
+
+# name -> argtypes; every function returns int32 status unless listed in _RESTYPES.
+_SIGNATURES = {
+    "fi_ctx_create": [_I32, C.POINTER(_P)],
+    "fi_ctx_destroy": [_P],
+    "fi_ctx_sync": [_P],
+    "fi_ctx_set_stream": [_P, _P],
+    "fi_ctx_stream": [_P],
+    "fi_ctx_check_faults": [_P],
+    "fi_device_info": [_P, C.c_char_p, _SZ, C.c_char_p, _SZ, C.POINTER(C.c_uint64), C.POINTER(_I32)],
+    "fi_buf_alloc": [_P, _SZ, C.POINTER(_P)],
+    "fi_buf_free": [_P, _P],
+    "fi_buf_upload": [_P, _P, _SZ, _P, _SZ],
+    "fi_buf_download": [_P, _P, _SZ, _P, _SZ],
+    "fi_buf_zero": [_P, _P, _SZ],
+    "fi_kv_append": [_P, _P, _P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32],
+    "fi_kv_copy_blocks": [_P, _P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
+    "fi_attn_decode_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32,
+                             _I32, _F32, _P],
+    "fi_attn_prefill_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32,
+                              _I32, _I32, _I32, _F32, _P],
+    "fi_rms_norm": [_P, _P, _P, _I32, _I32, _F32, _P],
+    "fi_rope": [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32],
+    "fi_rope_table": [_P, _I32, _I32, _I32, _F32, _P, _P],
+    "fi_embedding": [_P, _P, _I32, _I32, _P, _I32, _P],
+    "fi_silu_mul": [_P, _P, _P, _I64],
+    "fi_add": [_P, _P, _P, _I64],
+    "fi_gemm": [_P, _P, _P, _P, _I32, _I32, _I32, _P],
+    "fi_lm_head_logits": [_P, _P, _P, _I32, _I32, _I32, _P],
+    "fi_lm_head_argmax": [_P, _P, _P, _I32, _I32, _I32, _P, _P],
+}
+_RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load() -> C.CDLL:
+    """Loads the HIP backend; raises if it has not been built (no fallback exists)."""
+    global _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise FerrisError(8, f"HIP backend {LIB_PATH} is not built; run "
+                                 "`python -m ferrisinfer_amd.build` (or __graft_entry__.build())")
+        lib = C.CDLL(LIB_PATH)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                continue
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, _I32)
+        lib.fi_last_error.restype = C.c_char_p
+        lib.fi_last_error.argtypes = []
+        _lib = lib
+        return lib
+
+
+def exported_symbols() -> list:
+    lib = load()
+    return [n for n in _SIGNATURES if getattr(lib, n, None) is not None]
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = load().fi_last_error() or b""
+        raise FerrisError(int(status), msg.decode(errors="replace"))
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a torch tensor / int / None."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+class Context:
+    """fi_context: one device, one stream (kernel/gpu/nvidia.rs:214-262 lifecycle)."""
+
+    def __init__(self, ordinal: int = 0, use_torch_stream: bool = True):
+        lib = load()
+        h = _P()
+        check(lib.fi_ctx_create(ordinal, C.byref(h)))
+        self.handle = h
+        self.lib = lib
+        self.ordinal = ordinal
+        if use_torch_stream:
+            self.follow_torch_stream()
+
+    def follow_torch_stream(self) -> None:
+        import torch
+
+        s = torch.cuda.current_stream(self.ordinal)
+        check(self.lib.fi_ctx_set_stream(self.handle, s.cuda_stream))
+
+    def set_stream(self, stream_ptr) -> None:
+        check(self.lib.fi_ctx_set_stream(self.handle, stream_ptr))
+
+    @property
+    def stream(self) -> int:
+        return int(self.lib.fi_ctx_stream(self.handle) or 0)
+
+    def sync(self) -> None:
+        check(self.lib.fi_ctx_sync(self.handle))
+
+    def check_faults(self) -> None:
+        check(self.lib.fi_ctx_check_faults(self.handle))
+
+    def device_info(self) -> dict:
+        name = C.create_string_buffer(256)
+        arch = C.create_string_buffer(64)
+        hbm = C.c_uint64()
+        cus = _I32()
+        check(self.lib.fi_device_info(self.handle, name, 256, arch, 64, C.byref(hbm), C.byref(cus)))
+        return {"name": name.value.decode(), "arch": arch.value.decode(), "hbm_bytes": hbm.value,
+                "compute_units": cus.value}
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            check(self.lib.fi_ctx_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------ ops
+    def kv_append(self, key, value, slot_mapping, k_cache, v_cache, kv_dtype, num_blocks,
+                  block_size, num_kv_heads, head_dim):
+        check(self.lib.fi_kv_append(self.handle, ptr(key), ptr(value), ptr(slot_mapping),
+                                    int(slot_mapping.numel()), ptr(k_cache), ptr(v_cache), kv_dtype,
+                                    num_blocks, block_size, num_kv_heads, head_dim))
+
+    def kv_copy_blocks(self, k_cache, v_cache, kv_dtype, src_blocks, dst_blocks, token_counts,
+                       num_blocks, block_size, num_kv_heads, head_dim):
+        check(self.lib.fi_kv_copy_blocks(self.handle, ptr(k_cache), ptr(v_cache), kv_dtype,
+                                         ptr(src_blocks), ptr(dst_blocks), ptr(token_counts),
+                                         int(src_blocks.numel()), num_blocks, block_size,
+                                         num_kv_heads, head_dim))
+
+    def attn_decode_paged(self, q, k_cache, v_cache, kv_dtype, block_tables, context_lens,
+                          max_context_len, num_kv_heads, block_size, num_blocks, scale, out):
+        num_seqs, num_q_heads, head_dim = q.shape
+        check(self.lib.fi_attn_decode_paged(self.handle, ptr(q), ptr(k_cache), ptr(v_cache),
+                                            kv_dtype, ptr(block_tables), int(block_tables.shape[1]),
+                                            ptr(context_lens), num_seqs, int(max_context_len),
+                                            num_q_heads, num_kv_heads, head_dim, block_size,
+                                            num_blocks, float(scale), ptr(out)))

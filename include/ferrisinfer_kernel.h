@@ -1,0 +1,153 @@
+/*
+ * ferrisinfer_kernel.h — C ABI of the MI355X (gfx950) HIP backend of FerrisInfer's
+ * ragged-batch attention hot path.
+ *
+ * The reference has no compute FFI: its hot path is Rust free functions in
+ * crates/ferrisinfer-kernel/src/cpu/*.rs called from crates/ferrisinfer-runtime/src/reference.rs,
+ * KV storage behind the KvCacheStorage trait (runtime/kv_cache.rs:36-64), and a device
+ * layer that binds a C driver by dlsym (kernel/gpu/nvidia.rs:678-727).  This header is the
+ * C surface a `ferrisinfer-kernel-sys` crate (or ctypes / cgo) binds in their place.  Each
+ * declaration cites the reference interface it replaces.
+ *
+ * Conventions (mirroring kernel/gpu/nvidia.rs:887-932 and core/error.rs:5-16):
+ *   - every function returns int32_t status: 0 = ok, otherwise ErrorKind index + 1
+ *     (Io=1 Parse=2 InvalidShape=3 InvalidLayout=4 InvalidType=5 InvalidConfig=6
+ *      MissingWeight=7 Unsupported=8 Runtime=9); fi_last_error() gives the message
+ *     (thread-local, valid until the next failing call on that thread);
+ *   - pointers named d_* are device pointers (HBM); everything else is host memory;
+ *   - ops enqueue on the context's stream and return without synchronising; only
+ *     fi_buf_download and fi_ctx_sync wait;
+ *   - callers own every buffer; ops never allocate their outputs.  Split-KV decode keeps
+ *     a grow-only workspace inside the context;
+ *   - one host thread drives a context at a time (the reference scheduler is &mut self).
+ *
+ * Layouts:
+ *   activations are row-major f32: q [T, Hq, D], k/v [T, Hkv, D], hidden [T, H];
+ *   weights are [in, out] row-major f32 (model/decoder.rs:76-104);
+ *   the KV pool holds, per layer, K and V arrays [num_blocks, Hkv, block_size, D] in
+ *   f32 or bf16; physical slot = block_id * block_size + offset
+ *   (runtime/paged_kv.rs:605-606);
+ *   block_tables is int32 [num_seqs, max_blocks_per_seq]; context_lens int32 [num_seqs];
+ *   cu_seqlens int32 [num_seqs + 1]; slot_mapping int64 [T] (negative = skip).
+ */
+#ifndef FERRISINFER_KERNEL_H
+#define FERRISINFER_KERNEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FI_OK = 0,
+  FI_ERR_IO = 1,
+  FI_ERR_PARSE = 2,
+  FI_ERR_INVALID_SHAPE = 3,
+  FI_ERR_INVALID_LAYOUT = 4,
+  FI_ERR_INVALID_TYPE = 5,
+  FI_ERR_INVALID_CONFIG = 6,
+  FI_ERR_MISSING_WEIGHT = 7,
+  FI_ERR_UNSUPPORTED = 8,
+  FI_ERR_RUNTIME = 9
+};
+
+/* KV storage dtypes (core/dtype.rs:1-42 F32 / BF16). */
+enum { FI_DTYPE_F32 = 0, FI_DTYPE_BF16 = 1 };
+
+typedef struct fi_context fi_context;
+
+/* ---------------------------------------------------------------- errors / context */
+
+/* Message of the last failing call on this thread
+ * (FerrisError::message, core/error.rs:36-38). */
+const char* fi_last_error(void);
+
+/* Opens device `ordinal` and creates a context with its own stream.
+ * Replaces NvidiaCudaBackend::new / primary-context retain (kernel/gpu/nvidia.rs:214-262). */
+int32_t fi_ctx_create(int32_t ordinal, fi_context** out);
+
+/* Releases the context (RAII Drop of the reference context, kernel/gpu/nvidia.rs:409-415). */
+int32_t fi_ctx_destroy(fi_context* ctx);
+
+/* Waits for all work enqueued on the context's stream (cuCtxSynchronize, nvidia.rs:387-389). */
+int32_t fi_ctx_sync(fi_context* ctx);
+
+/* Uses `stream` (a hipStream_t of the same device) for all later ops; NULL restores the
+ * context's own stream.  No reference counterpart (the reference launches nothing). */
+int32_t fi_ctx_set_stream(fi_context* ctx, void* stream);
+
+/* The hipStream_t the context currently enqueues on. */
+void* fi_ctx_stream(fi_context* ctx);
+
+/* Device name, gfx arch, HBM bytes and CU count
+ * (device probe, kernel/gpu/nvidia.rs:756-804). */
+int32_t fi_device_info(fi_context* ctx, char* name, size_t name_len, char* arch, size_t arch_len,
+                       uint64_t* hbm_bytes, int32_t* compute_units);
+
+/* ---------------------------------------------------------------- memory */
+
+/* Device allocation; rejects 0 bytes like validate_buffer_len (kernel/gpu/nvidia.rs:910-919). */
+int32_t fi_buf_alloc(fi_context* ctx, size_t bytes, void** d_out);
+int32_t fi_buf_free(fi_context* ctx, void* d_ptr);
+/* Host->device / device->host copies with the exact-length rule of validate_copy_len
+ * (kernel/gpu/nvidia.rs:921-932; cuMemcpyHtoD/DtoH at nvidia.rs:340-470). */
+int32_t fi_buf_upload(fi_context* ctx, void* d_dst, size_t dst_bytes, const void* src,
+                      size_t src_bytes);
+int32_t fi_buf_download(fi_context* ctx, void* dst, size_t dst_bytes, const void* d_src,
+                        size_t src_bytes);
+/* Backend::fill_zero (kernel/backend.rs:40); the reference's NVIDIA backend returns
+ * Unsupported (nvidia.rs:319-323). */
+int32_t fi_buf_zero(fi_context* ctx, void* d_ptr, size_t bytes);
+
+/* ---------------------------------------------------------------- KV pool ops */
+
+/* Scatters this step's K/V rows into the paged pool by slot_mapping, converting f32 to the
+ * pool dtype (bf16: round-to-nearest-even).  Replaces KvCacheStorage::write_uncommitted_f32
+ * and write_sequence_uncommitted_f32 (runtime/kv_cache.rs:48-62; paged write path
+ * runtime/paged_kv.rs:583-631, 679-767).  Rows whose slot is negative are skipped; a slot
+ * beyond num_blocks * block_size is skipped and reported as Runtime by the next
+ * fi_ctx_check_faults(). */
+int32_t fi_kv_append(fi_context* ctx, const float* d_key, const float* d_value,
+                     const int64_t* d_slot_mapping, int32_t num_tokens, void* d_k_cache,
+                     void* d_v_cache, int32_t kv_dtype, int32_t num_blocks, int32_t block_size,
+                     int32_t num_kv_heads, int32_t head_dim);
+
+/* Copies `num_tokens` leading token rows of block src_blocks[i] into dst_blocks[i] for
+ * every pair (copy-on-write of a partially shared prefix block).  Replaces the page copy of
+ * PagedKvCacheStorage::import_prefix_from (runtime/paged_kv.rs:329-389) for a block that
+ * cannot be shared by id. */
+int32_t fi_kv_copy_blocks(fi_context* ctx, void* d_k_cache, void* d_v_cache, int32_t kv_dtype,
+                          const int32_t* d_src_blocks, const int32_t* d_dst_blocks,
+                          const int32_t* d_token_counts, int32_t num_pairs, int32_t num_blocks,
+                          int32_t block_size, int32_t num_kv_heads, int32_t head_dim);
+
+/* Reads and clears the context's device fault flags (out-of-range slots / token ids seen by
+ * kernels since the last check); returns Runtime with a message when any was set.  Waits
+ * for the stream. */
+int32_t fi_ctx_check_faults(fi_context* ctx);
+
+/* ---------------------------------------------------------------- attention */
+
+/* Paged decode attention, one query token per sequence, all keys [0, context_len) read
+ * through the block table (the current token's K/V must already be appended).
+ * Split-KV over fixed 256-token partitions with a log-sum-exp merge, so the summation order
+ * depends only on context_len.  Replaces, per sequence, read_prefix_f32 +
+ * cached_prefixed_causal_attention_f32 (runtime/reference.rs:497-508,
+ * runtime/paged_kv.rs:769-791, kernel/cpu/attention.rs:332-518) and
+ * decode_causal_attention_f32 (kernel/cpu/attention.rs:520-686).
+ * q/out: f32 [num_seqs, Hq, D]; scale is 1/sqrt(D) in the reference (attention.rs:659).
+ * max_context_len must bound every context_lens entry (it sizes the grid). */
+int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                             const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
+                             int32_t max_blocks_per_seq, const int32_t* d_context_lens,
+                             int32_t num_seqs, int32_t max_context_len, int32_t num_q_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             int32_t num_blocks, float scale, float* d_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRISINFER_KERNEL_H */

@@ -33,7 +33,7 @@ class OracleError(RuntimeError):
 def build(force: bool = False) -> str:
     """Compiles liboracle.so with the committed Makefile (g++, -ffp-contract=off)."""
     if force or not os.path.exists(LIB_PATH):
-        subprocess.run(["make", "-s", "-B" if force else "-s"], cwd=_HERE, check=True)
+        subprocess.run(["make", "-s"] + (["-B"] if force else []), cwd=_HERE, check=True)
     return LIB_PATH
 
 

@@ -18,3 +18,27 @@ def orc():
 
     oracle.build()
     return oracle
+
+
+def normwise_error(got, ref):
+    """max|got - ref| / max|ref| over the whole tensor (elementwise relative error is
+    undefined near zero)."""
+    import numpy as np
+
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    denom = max(float(np.abs(ref).max()), 1e-30)
+    return float(np.abs(got - ref).max()) / denom
+
+
+@pytest.fixture(scope="session")
+def gpu_ctx():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    from ferrisinfer_amd import Context
+
+    ctx = Context(0)
+    yield ctx
+    ctx.close()

@@ -1,0 +1,45 @@
+"""The C-ABI library loads and exports every symbol include/ferrisinfer_kernel.h declares
+(no compute calls: this runs without a GPU)."""
+import ctypes
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ferrisinfer_kernel.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for required in ("fi_ctx_create", "fi_kv_append", "fi_attn_decode_paged", "fi_last_error"):
+        assert required in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from ferrisinfer_amd import kernel
+
+    lib = ctypes.CDLL(kernel.library_path())
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_ctx_create_without_gpu_reports_unsupported():
+    """With no device the backend reports 'unavailable' instead of failing obscurely
+    (the reference degrades the same way, kernel/gpu/nvidia.rs:577-656)."""
+    import torch
+
+    if torch.cuda.is_available():
+        return
+    from ferrisinfer_amd import Context, FerrisError
+
+    try:
+        Context(0, use_torch_stream=False)
+    except FerrisError as e:
+        assert e.kind in ("Unsupported", "Runtime")
+    else:
+        raise AssertionError("context creation must fail without a GPU")

@@ -1,0 +1,191 @@
+"""GPU parity of paged decode attention and KV append against the CPU oracle.
+
+The oracle runs the reference's paged decode exactly: gather the committed prefix by block
+table, then cached-prefixed attention with the current token last
+(runtime/reference.rs:497-508).  Tolerances: f32 outputs within 1e-4
+normwise relative error, bf16-storage within 2e-2.
+"""
+import numpy as np
+import pytest
+
+from conftest import normwise_error
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _dev(x, torch):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def run_decode(ctx, wl, kv_dtype, torch):
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+
+    if kv_dtype == "bf16":
+        import oracle
+
+        kp = torch.from_numpy(oracle.f32_to_bf16(wl.k_pool).view(np.int16)).cuda()
+        vp = torch.from_numpy(oracle.f32_to_bf16(wl.v_pool).view(np.int16)).cuda()
+        dt = DTYPE_BF16
+    else:
+        kp, vp, dt = _dev(wl.k_pool, torch), _dev(wl.v_pool, torch), DTYPE_F32
+    q = _dev(wl.q, torch)
+    bt = _dev(wl.block_tables, torch)
+    cl = _dev(wl.context_lens, torch)
+    out = torch.empty_like(q)
+    ctx.attn_decode_paged(q, kp, vp, dt, bt, cl, wl.max_context_len, wl.num_kv_heads,
+                          wl.block_size, wl.num_blocks, wl.scale, out)
+    torch.cuda.synchronize()
+    ctx.check_faults()
+    return out.cpu().numpy()
+
+
+def oracle_decode(orc, wl, kv_dtype):
+    k, v = wl.k_pool, wl.v_pool
+    if kv_dtype == "bf16":
+        k = orc.bf16_to_f32(orc.f32_to_bf16(k))
+        v = orc.bf16_to_f32(orc.f32_to_bf16(v))
+    return orc.paged_decode_gather_attention(wl.q, wl.pages_reference_layout(k),
+                                             wl.pages_reference_layout(v), wl.block_tables,
+                                             wl.context_lens, wl.block_size)
+
+
+SMALL_CASES = [
+    # (num_seqs, min_len, max_len, hq, hkv, d, block_size, num_blocks)
+    (3, 1, 40, 4, 4, 32, 16, 64),      # L=1 possible, MHA
+    (5, 200, 300, 8, 2, 32, 16, 128),  # crosses the 256-token partition
+    (4, 250, 770, 14, 2, 64, 16, 256),  # Qwen2-shaped GQA 7
+    (6, 1, 600, 8, 1, 64, 8, 512),      # group 8, block size 8
+    (4, 500, 1100, 32, 8, 128, 16, 512),
+    (2, 255, 258, 4, 2, 128, 32, 64),   # partition edges, block size 32
+]
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", SMALL_CASES)
+def test_decode_small_cases(orc, gpu_ctx, case, kv_dtype):
+    import torch
+
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    b, lo, hi, hq, hkv, d, bs, nb = case
+    print(f"decode case={case} dtype={kv_dtype}", flush=True)
+    wl = paged_decode_c2(seed=11, num_seqs=b, min_len=lo, max_len=hi, num_q_heads=hq,
+                         num_kv_heads=hkv, head_dim=d, block_size=bs, num_blocks=nb)
+    got = run_decode(gpu_ctx, wl, kv_dtype, torch)
+    ref = oracle_decode(orc, wl, kv_dtype)
+    err = normwise_error(got, ref)
+    assert err <= (F32_TOL if kv_dtype == "f32" else BF16_TOL), err
+    if kv_dtype == "bf16":
+        # the oracle attends the same widened bf16 values, so only summation order differs
+        assert err <= F32_TOL, err
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_decode_c2_full_size(orc, gpu_ctx, kv_dtype):
+    """BASELINE config C2 at its full size: 64 ragged sequences, L ~ U[128, 2048]."""
+    import torch
+
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    print(f"decode C2 full dtype={kv_dtype}", flush=True)
+    wl = paged_decode_c2(seed=0)
+    got = run_decode(gpu_ctx, wl, kv_dtype, torch)
+    ref = oracle_decode(orc, wl, kv_dtype)
+    err = normwise_error(got, ref)
+    assert err <= (F32_TOL if kv_dtype == "f32" else BF16_TOL), err
+
+
+def test_decode_batch_invariance(gpu_ctx):
+    """A sequence's output does not depend on the batch around it (bit-identical)."""
+    import torch
+
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    wl = paged_decode_c2(seed=3, num_seqs=16, num_blocks=4096)
+    full = run_decode(gpu_ctx, wl, "f32", torch)
+    for i in (0, 7, 15):
+        one = paged_decode_c2(seed=3, num_seqs=16, num_blocks=4096)
+        one.q = wl.q[i:i + 1].copy()
+        one.block_tables = wl.block_tables[i:i + 1].copy()
+        one.context_lens = wl.context_lens[i:i + 1].copy()
+        alone = run_decode(gpu_ctx, one, "f32", torch)
+        assert np.array_equal(alone[0], full[i])
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_kv_append_scatter_exact(orc, gpu_ctx, kv_dtype):
+    """fi_kv_append writes each token row to block_id*bs+offset, bit-exact (bf16: RNE)."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+
+    rng = np.random.default_rng(5)
+    nb, bs, hkv, d, t = 64, 16, 4, 64, 300
+    slots = rng.permutation(nb * bs)[:t].astype(np.int64)
+    slots[::37] = -1  # padding rows are skipped
+    key = rng.standard_normal((t, hkv, d), dtype=np.float32)
+    val = rng.standard_normal((t, hkv, d), dtype=np.float32)
+    torch_dt = torch.float32 if kv_dtype == "f32" else torch.int16
+    kc = torch.zeros((nb, hkv, bs, d), dtype=torch_dt, device="cuda")
+    vc = torch.zeros_like(kc)
+    gpu_ctx.kv_append(_dev(key, torch), _dev(val, torch), _dev(slots, torch), kc, vc,
+                      DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16, nb, bs, hkv, d)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    exp_k = np.zeros((nb, hkv, bs, d), np.float32)
+    exp_v = np.zeros_like(exp_k)
+    for i, s in enumerate(slots):
+        if s < 0:
+            continue
+        exp_k[s // bs, :, s % bs, :] = key[i]
+        exp_v[s // bs, :, s % bs, :] = val[i]
+    if kv_dtype == "f32":
+        assert np.array_equal(kc.cpu().numpy(), exp_k)
+        assert np.array_equal(vc.cpu().numpy(), exp_v)
+    else:
+        assert np.array_equal(kc.cpu().numpy().view(np.uint16), orc.f32_to_bf16(exp_k))
+        assert np.array_equal(vc.cpu().numpy().view(np.uint16), orc.f32_to_bf16(exp_v))
+
+
+def test_kv_append_out_of_range_slot_reported(gpu_ctx):
+    """A slot beyond the pool is skipped on device and reported as Runtime by the host."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32, FerrisError
+
+    nb, bs, hkv, d = 4, 16, 2, 32
+    kc = torch.zeros((nb, hkv, bs, d), device="cuda")
+    vc = torch.zeros_like(kc)
+    key = torch.ones((2, hkv, d), device="cuda")
+    slots = torch.tensor([3, nb * bs + 5], dtype=torch.int64, device="cuda")
+    gpu_ctx.kv_append(key, key, slots, kc, vc, DTYPE_F32, nb, bs, hkv, d)
+    with pytest.raises(FerrisError) as e:
+        gpu_ctx.check_faults()
+    assert e.value.kind == "Runtime"
+    assert float(kc[0, :, 3].sum()) == hkv * d
+    gpu_ctx.check_faults()  # flags were cleared
+
+
+def test_kv_copy_blocks(gpu_ctx):
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32
+
+    nb, bs, hkv, d = 8, 16, 2, 64
+    kc = torch.randn((nb, hkv, bs, d), device="cuda")
+    vc = torch.randn((nb, hkv, bs, d), device="cuda")
+    k0, v0 = kc.clone(), vc.clone()
+    src = torch.tensor([1, 4], dtype=torch.int32, device="cuda")
+    dst = torch.tensor([6, 2], dtype=torch.int32, device="cuda")
+    cnt = torch.tensor([5, 16], dtype=torch.int32, device="cuda")
+    gpu_ctx.kv_copy_blocks(kc, vc, DTYPE_F32, src, dst, cnt, nb, bs, hkv, d)
+    torch.cuda.synchronize()
+    exp_k, exp_v = k0.clone(), v0.clone()
+    exp_k[6, :, :5] = k0[1, :, :5]
+    exp_v[6, :, :5] = v0[1, :, :5]
+    exp_k[2] = k0[4]
+    exp_v[2] = v0[4]
+    assert torch.equal(kc, exp_k) and torch.equal(vc, exp_v)
