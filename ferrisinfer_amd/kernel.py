@@ -58,15 +58,15 @@ _SIGNATURES = {
     "fi_attn_decode_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                              _I32, _F32, _P],
     "fi_attn_prefill_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32,
-                              _I32, _I32, _I32, _F32, _P],
-    "fi_rms_norm": [_P, _P, _P, _I32, _I32, _F32, _P],
-    "fi_rope": [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32],
+                              _I32, _I32, _F32, _P],
+    "fi_rms_norm": [_P, _P, _P, _P, _I32, _I32, _F32],
+    "fi_add_rms_norm": [_P, _P, _P, _P, _P, _P, _I32, _I32, _F32],
+    "fi_rope": [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32],
     "fi_rope_table": [_P, _I32, _I32, _I32, _F32, _P, _P],
     "fi_embedding": [_P, _P, _I32, _I32, _P, _I32, _P],
     "fi_silu_mul": [_P, _P, _P, _I64],
     "fi_add": [_P, _P, _P, _I64],
-    "fi_gemm": [_P, _P, _P, _P, _I32, _I32, _I32, _P],
-    "fi_lm_head_logits": [_P, _P, _P, _I32, _I32, _I32, _P],
+    "fi_gemm": [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32],
     "fi_lm_head_argmax": [_P, _P, _P, _I32, _I32, _I32, _P, _P],
 }
 _RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
@@ -195,3 +195,58 @@ class Context:
                                             ptr(context_lens), num_seqs, int(max_context_len),
                                             num_q_heads, num_kv_heads, head_dim, block_size,
                                             num_blocks, float(scale), ptr(out)))
+
+    def embedding(self, table, ids, out):
+        check(self.lib.fi_embedding(self.handle, ptr(table), int(table.shape[0]),
+                                    int(table.shape[1]), ptr(ids), int(ids.numel()), ptr(out)))
+
+    def rms_norm(self, x, weight, out, eps):
+        hidden = int(x.shape[-1])
+        check(self.lib.fi_rms_norm(self.handle, ptr(x), ptr(weight), ptr(out),
+                                   int(x.numel() // hidden), hidden, float(eps)))
+
+    def add_rms_norm(self, a, residual, sum_out, weight, out, eps):
+        hidden = int(a.shape[-1])
+        check(self.lib.fi_add_rms_norm(self.handle, ptr(a), ptr(residual), ptr(sum_out),
+                                       ptr(weight), ptr(out), int(a.numel() // hidden), hidden,
+                                       float(eps)))
+
+    def rope_table(self, max_positions, head_dim, rotary_dims, theta, cos_out, sin_out):
+        check(self.lib.fi_rope_table(self.handle, int(max_positions), int(head_dim),
+                                     int(rotary_dims), float(theta), ptr(cos_out), ptr(sin_out)))
+
+    def rope(self, q, k, positions, cos_t, sin_t, rotary_dims, max_positions):
+        t, hq, d = q.shape
+        check(self.lib.fi_rope(self.handle, ptr(q), ptr(k), ptr(positions), ptr(cos_t),
+                               ptr(sin_t), int(t), int(hq), int(k.shape[1]), int(d),
+                               int(rotary_dims), int(max_positions)))
+
+    def silu_mul(self, up, gate, out):
+        check(self.lib.fi_silu_mul(self.handle, ptr(up), ptr(gate), ptr(out), int(up.numel())))
+
+    def add(self, a, b, out):
+        check(self.lib.fi_add(self.handle, ptr(a), ptr(b), ptr(out), int(a.numel())))
+
+    def gemm(self, a, b, out, bias=None, b_layout=0):
+        """out[M,N] = a[M,K] * b (+ bias); b is [K,N] (layout 0) or [N,K] (layout 1)."""
+        m, k = a.shape
+        n = b.shape[1] if b_layout == 0 else b.shape[0]
+        check(self.lib.fi_gemm(self.handle, ptr(a), ptr(b), ptr(bias), ptr(out), int(m), int(k),
+                               int(n), int(b_layout)))
+
+    def lm_head_argmax(self, hidden, weight, token_out, prob_out):
+        m, h = hidden.shape
+        check(self.lib.fi_lm_head_argmax(self.handle, ptr(hidden), ptr(weight), int(m), int(h),
+                                         int(weight.shape[0]), ptr(token_out), ptr(prob_out)))
+
+    def attn_prefill_paged(self, q, k_cache, v_cache, kv_dtype, block_tables, cu_seqlens,
+                           context_lens, max_query_len, num_kv_heads, block_size, num_blocks,
+                           scale, out):
+        t, num_q_heads, head_dim = q.shape
+        check(self.lib.fi_attn_prefill_paged(self.handle, ptr(q), ptr(k_cache), ptr(v_cache),
+                                             kv_dtype, ptr(block_tables),
+                                             int(block_tables.shape[1]), ptr(cu_seqlens),
+                                             ptr(context_lens), int(context_lens.numel()),
+                                             int(max_query_len), num_q_heads, num_kv_heads,
+                                             head_dim, block_size, num_blocks, float(scale),
+                                             ptr(out)))

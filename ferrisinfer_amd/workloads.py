@@ -76,3 +76,108 @@ def paged_decode_c2(seed: int = 0, num_seqs: int = 64, min_len: int = 128, max_l
     return PagedDecodeWorkload(num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                                num_blocks, lens, tables, q, k_pool, v_pool,
                                float(1.0 / np.sqrt(np.float32(head_dim))))
+
+
+@dataclass
+class PrefillWorkload:
+    """Config C3: ragged varlen causal prefill plus KV append with block-shared prefixes."""
+
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    num_blocks: int
+    prompt_lens: np.ndarray    # int32 [B] total tokens per sequence
+    shared_lens: np.ndarray    # int32 [B] prefix tokens shared by block id (0 = none)
+    source_of: np.ndarray      # int32 [B] index of the sequence whose blocks are shared (-1)
+    block_tables: np.ndarray   # int32 [B, max_blocks]
+    cu_seqlens: np.ndarray     # int32 [B+1] over the new (computed) tokens
+    context_lens: np.ndarray   # int32 [B] = prompt_lens
+    slot_mapping: np.ndarray   # int64 [T_new]
+    q: np.ndarray              # f32 [T_new, Hq, D]
+    k_new: np.ndarray          # f32 [T_new, Hkv, D]
+    v_new: np.ndarray
+    scale: float
+
+    @property
+    def query_lens(self) -> np.ndarray:
+        return np.diff(self.cu_seqlens)
+
+    def full_kv(self, b: int):
+        """K/V [L_b, Hkv, D] of sequence b's whole context (shared prefix + own rows)."""
+        own_k = self.k_new[self.cu_seqlens[b]:self.cu_seqlens[b + 1]]
+        own_v = self.v_new[self.cu_seqlens[b]:self.cu_seqlens[b + 1]]
+        s = int(self.shared_lens[b])
+        if s == 0:
+            return own_k, own_v
+        src = int(self.source_of[b])
+        sk, sv = self.full_kv(src)
+        return np.concatenate([sk[:s], own_k]), np.concatenate([sv[:s], own_v])
+
+    def attention_flops(self) -> int:
+        """4*Hq*D * sum over computed tokens of the keys each attends (causal, incl. self)."""
+        total = 0
+        for b, L in enumerate(self.context_lens):
+            start = int(L) - int(self.query_lens[b])
+            n = int(self.query_lens[b])
+            total += n * start + n * (n + 1) // 2
+        return 4 * self.num_q_heads * self.head_dim * total
+
+    def append_bytes(self, kv_bytes: int = 4) -> int:
+        t = int(self.cu_seqlens[-1])
+        return t * self.num_kv_heads * self.head_dim * 2 * (4 + kv_bytes) + 8 * t
+
+
+def prefill_c3(seed: int = 0, num_seqs: int = 16, min_len: int = 32, max_len: int = 1024,
+               groups: int = 4, group_size: int = 4, shared_prefix: int = 512,
+               num_q_heads: int = 32, num_kv_heads: int = 8, head_dim: int = 128,
+               block_size: int = 16, num_blocks: int = 4096) -> PrefillWorkload:
+    """C3: lengths ~ U[min_len, max_len]; groups of `group_size` consecutive sequences share
+    a prefix through the same block ids.  The group's source is its longest member, padded
+    to at least shared_prefix + 1 tokens; every other member shares
+    min(shared_prefix, floor((L - 1) / block_size) * block_size) tokens (block aligned and
+    never the whole prompt, as runtime/prefix_index.rs:98-109 keeps one token to compute)
+    and computes only its suffix.  The source computes all its tokens in the same batch;
+    KV append precedes attention, so members read the source's freshly written blocks."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(min_len, max_len + 1, size=num_seqs).astype(np.int32)
+    shared = np.zeros(num_seqs, np.int32)
+    source = np.full(num_seqs, -1, np.int32)
+    for g in range(min(groups, num_seqs // group_size)):
+        idx = np.arange(g * group_size, (g + 1) * group_size)
+        src = int(idx[np.argmax(lens[idx])])
+        lens[src] = max(int(lens[src]), shared_prefix + 1)
+        for b in idx:
+            if b == src:
+                continue
+            shared[b] = min(shared_prefix, (int(lens[b]) - 1) // block_size * block_size)
+            source[b] = src if shared[b] > 0 else -1
+    nblk = (lens + block_size - 1) // block_size
+    own_blocks = nblk - shared // block_size
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    if int(own_blocks.sum()) > num_blocks:
+        raise ValueError("pool too small")
+    tables = np.zeros((num_seqs, int(nblk.max())), np.int32)
+    cursor = 0
+    order = sorted(range(num_seqs), key=lambda b: shared[b] > 0)  # sources first
+    for b in order:
+        k = int(shared[b]) // block_size
+        if k:
+            tables[b, :k] = tables[int(source[b]), :k]
+        n = int(own_blocks[b])
+        tables[b, k:k + n] = perm[cursor:cursor + n]
+        cursor += n
+    qlens = (lens - shared).astype(np.int32)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    T = int(cu[-1])
+    slots = np.zeros(T, np.int64)
+    for b in range(num_seqs):
+        for i in range(int(qlens[b])):
+            pos = int(shared[b]) + i
+            slots[cu[b] + i] = int(tables[b, pos // block_size]) * block_size + pos % block_size
+    q = rng.standard_normal((T, num_q_heads, head_dim), dtype=np.float32)
+    k = rng.standard_normal((T, num_kv_heads, head_dim), dtype=np.float32)
+    v = rng.standard_normal((T, num_kv_heads, head_dim), dtype=np.float32)
+    return PrefillWorkload(num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, lens, shared,
+                           source, tables, cu, lens.copy(), slots, q, k, v,
+                           float(1.0 / np.sqrt(np.float32(head_dim))))

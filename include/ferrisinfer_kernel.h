@@ -3,7 +3,7 @@
  * ragged-batch attention hot path.
  *
  * The reference has no compute FFI: its hot path is Rust free functions in
- * crates/ferrisinfer-kernel/src/cpu/*.rs called from crates/ferrisinfer-runtime/src/reference.rs,
+ * crates/ferrisinfer-kernel/src/cpu/{attention,matmul,reduction,elementwise}.rs called from crates/ferrisinfer-runtime/src/reference.rs,
  * KV storage behind the KvCacheStorage trait (runtime/kv_cache.rs:36-64), and a device
  * layer that binds a C driver by dlsym (kernel/gpu/nvidia.rs:678-727).  This header is the
  * C surface a `ferrisinfer-kernel-sys` crate (or ctypes / cgo) binds in their place.  Each
@@ -132,7 +132,7 @@ int32_t fi_ctx_check_faults(fi_context* ctx);
 
 /* Paged decode attention, one query token per sequence, all keys [0, context_len) read
  * through the block table (the current token's K/V must already be appended).
- * Split-KV over fixed 256-token partitions with a log-sum-exp merge, so the summation order
+ * Split-KV over fixed 512-token partitions with a log-sum-exp merge, so the summation order
  * depends only on context_len.  Replaces, per sequence, read_prefix_f32 +
  * cached_prefixed_causal_attention_f32 (runtime/reference.rs:497-508,
  * runtime/paged_kv.rs:769-791, kernel/cpu/attention.rs:332-518) and
@@ -145,6 +145,86 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
                              int32_t num_seqs, int32_t max_context_len, int32_t num_q_heads,
                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                              int32_t num_blocks, float scale, float* d_out);
+
+/* Varlen causal prefill attention over the paged pool (MFMA).  Sequence b contributes
+ * qlen_b = cu_seqlens[b+1] - cu_seqlens[b] query rows of q/out [T, Hq, D] at positions
+ * [context_lens[b] - qlen_b, context_lens[b]); each attends keys [0, position] read through
+ * block_tables (the chunk's own K/V rows must already be appended).  Replaces
+ * causal_self_attention_f32 / cached_prefixed_causal_attention_f32 with the paged prefix
+ * gather (kernel/cpu/attention.rs:222-518, runtime/reference.rs:425-465,
+ * runtime/paged_kv.rs:769-791).  max_query_len must bound every qlen_b (it sizes the grid). */
+int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                              const void* d_v_cache, int32_t kv_dtype,
+                              const int32_t* d_block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* d_cu_seqlens, const int32_t* d_context_lens,
+                              int32_t num_seqs, int32_t max_query_len, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                              int32_t num_blocks, float scale, float* d_out);
+
+/* ---------------------------------------------------------------- decoder-block ops */
+
+/* out[r, :] = table[ids[r], :].  Replaces embedding_gather_f32
+ * (kernel/cpu/attention.rs:3-99).  An id >= vocab writes a zero row and is reported as
+ * Runtime by fi_ctx_check_faults (the reference returns InvalidShape, attention.rs:35-40;
+ * the host runtime validates ids before upload and raises that). */
+int32_t fi_embedding(fi_context* ctx, const float* d_table, int32_t vocab, int32_t hidden,
+                     const int32_t* d_ids, int32_t num_tokens, float* d_out);
+
+/* RMSNorm over rows: ms = sum(x^2)/H, out = (x / sqrt(ms + eps)) * w.
+ * Replaces rms_norm_f32 (kernel/cpu/reduction.rs:3-73). */
+int32_t fi_rms_norm(fi_context* ctx, const float* d_x, const float* d_weight, float* d_out,
+                    int32_t rows, int32_t hidden, float eps);
+
+/* sum = a + residual (stored), out = rms_norm(sum) * w: the residual add_f32_in_place
+ * followed by rms_norm_f32 of the decoder block (runtime/reference.rs:337-343, 827-833). */
+int32_t fi_add_rms_norm(fi_context* ctx, const float* d_a, const float* d_residual, float* d_sum,
+                        const float* d_weight, float* d_out, int32_t rows, int32_t hidden,
+                        float eps);
+
+/* Builds the RoPE cos/sin tables [max_positions, rotary_dims/2] on the host with the
+ * reference's loop (iterated f32 inverse frequency with exponent -2/head_dim, glibc sin/cos,
+ * kernel/cpu/attention.rs:1253-1277) and uploads them.  Validation as rope_f32
+ * (attention.rs:190-209). */
+int32_t fi_rope_table(fi_context* ctx, int32_t max_positions, int32_t head_dim,
+                      int32_t rotary_dims, float theta, float* d_cos, float* d_sin);
+
+/* Rotates q [T, Hq, D] and k [T, Hkv, D] in place at per-token positions (NeoX half
+ * split, products rounded before the add).  Replaces rope_f32 with position_offset
+ * (kernel/cpu/attention.rs:165-220) for a ragged batch; bit-identical to the reference. */
+int32_t fi_rope(fi_context* ctx, float* d_q, float* d_k, const int32_t* d_positions,
+                const float* d_cos, const float* d_sin, int32_t num_tokens, int32_t num_q_heads,
+                int32_t num_kv_heads, int32_t head_dim, int32_t rotary_dims,
+                int32_t max_positions);
+
+/* SwiGLU: out = up * (gate * (1 / (1 + exp(-gate)))).  Replaces silu_f32_in_place +
+ * mul_f32_in_place (kernel/cpu/elementwise.rs:118-207; use at runtime/reference.rs:346-360). */
+int32_t fi_silu_mul(fi_context* ctx, const float* d_up, const float* d_gate, float* d_out,
+                    int64_t n);
+
+/* out = a + b.  Replaces add_f32_in_place (kernel/cpu/elementwise.rs:48-76). */
+int32_t fi_add(fi_context* ctx, const float* d_a, const float* d_b, float* d_out, int64_t n);
+
+/* ---------------------------------------------------------------- projections */
+
+/* C[M,N] = A[M,K] * B (+ bias[N]) on MFMA (f32 in, f32 accumulate).  b_layout 0: B is
+ * [K, N] = the reference's [in, out] weight (matmul_f32 + bias add of linear_f32_with_bias,
+ * kernel/cpu/matmul.rs:46-118, runtime/reference.rs:1135-1191); b_layout 1: B is [N, K]
+ * (matmul_rhs_transposed_f32, kernel/cpu/matmul.rs:120-188: the lm_head logits against the
+ * [vocab, hidden] output or tied embedding weight).  Skinny shapes split K across
+ * workgroups and sum the splits in a fixed order (deterministic); the split partials use
+ * the context workspace. */
+int32_t fi_gemm(fi_context* ctx, const float* d_a, const float* d_b, const float* d_bias,
+                float* d_c, int32_t m, int32_t k, int32_t n, int32_t b_layout);
+
+/* Fused greedy head: for each of m rows, logits = hidden_row * W^T with W [vocab, hidden],
+ * returns the FIRST index of the maximum logit and 1 / sum(exp(logit - max)).  Replaces
+ * matmul_rhs_transposed_argmax_f32 (kernel/cpu/matmul.rs:190-274, 532-589): strict > within a
+ * tile, ties between tiles keep the left one.  Logits are never materialised.  The
+ * probability's rounding depends on the tiling, as the reference's depends on its thread
+ * chunks (matmul.rs:232-270). */
+int32_t fi_lm_head_argmax(fi_context* ctx, const float* d_hidden, const float* d_weight,
+                          int32_t m, int32_t hidden, int32_t vocab, int32_t* d_token,
+                          float* d_prob);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,107 @@
+"""GPU parity of KV append + varlen causal prefill attention over the paged pool against the
+CPU oracle's cached-prefixed attention (the reference's prefill with a cached prefix,
+runtime/reference.rs:425-465).  f32: 1e-4 normwise; bf16 KV: 2e-2 (here also 1e-4, since
+the oracle attends the same widened bf16 values)."""
+import numpy as np
+import pytest
+
+from conftest import normwise_error
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(ctx, wl, kv_dtype):
+    import torch
+
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+
+    dt = DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16
+    tdt = torch.float32 if kv_dtype == "f32" else torch.int16
+    shape = (wl.num_blocks, wl.num_kv_heads, wl.block_size, wl.head_dim)
+    kp = torch.zeros(shape, dtype=tdt, device="cuda")
+    vp = torch.zeros(shape, dtype=tdt, device="cuda")
+    d = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    ctx.kv_append(d(wl.k_new), d(wl.v_new), d(wl.slot_mapping), kp, vp, dt, wl.num_blocks,
+                  wl.block_size, wl.num_kv_heads, wl.head_dim)
+    q = d(wl.q)
+    out = torch.empty_like(q)
+    ctx.attn_prefill_paged(q, kp, vp, dt, d(wl.block_tables), d(wl.cu_seqlens),
+                           d(wl.context_lens), int(wl.query_lens.max()), wl.num_kv_heads,
+                           wl.block_size, wl.num_blocks, wl.scale, out)
+    torch.cuda.synchronize()
+    ctx.check_faults()
+    return out.cpu().numpy()
+
+
+def oracle_prefill(orc, wl, kv_dtype):
+    outs = []
+    for b in range(len(wl.context_lens)):
+        k, v = wl.full_kv(b)
+        if kv_dtype == "bf16":
+            k = orc.bf16_to_f32(orc.f32_to_bf16(k))
+            v = orc.bf16_to_f32(orc.f32_to_bf16(v))
+        start = int(wl.context_lens[b]) - int(wl.query_lens[b])
+        qb = wl.q[wl.cu_seqlens[b]:wl.cu_seqlens[b + 1]]
+        outs.append(orc.cached_prefixed_causal_attention(qb, k[:start], v[:start], start,
+                                                         k[start:], v[start:]))
+    return np.concatenate(outs)
+
+
+CASES = [
+    # (num_seqs, min_len, max_len, groups, group_size, shared, hq, hkv, d, bs)
+    (4, 1, 70, 0, 1, 0, 4, 4, 32, 16),        # no prefix, tiny, includes 1-token prompts
+    (8, 20, 200, 2, 4, 64, 8, 2, 32, 16),     # C1-shaped heads, block-shared prefixes
+    (6, 30, 300, 2, 3, 128, 14, 2, 64, 16),   # Qwen2-shaped GQA 7
+    (4, 100, 400, 1, 4, 96, 32, 8, 128, 8),   # block size 8
+]
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", CASES)
+def test_prefill_small(orc, gpu_ctx, case, kv_dtype):
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    b, lo, hi, g, gs, sh, hq, hkv, d, bs = case
+    print(f"prefill case={case} dtype={kv_dtype}", flush=True)
+    wl = prefill_c3(seed=5, num_seqs=b, min_len=lo, max_len=hi, groups=g, group_size=gs,
+                    shared_prefix=sh, num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                    block_size=bs, num_blocks=1024)
+    got = run_prefill(gpu_ctx, wl, kv_dtype)
+    err = normwise_error(got, oracle_prefill(orc, wl, kv_dtype))
+    assert err <= 1e-4, err
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_prefill_c3_full_size(orc, gpu_ctx, kv_dtype):
+    """16 seqs, L ~ U[32, 1024], 4 groups of 4 sharing 512-token
+    prefixes by block id, Hq 32 / Hkv 8, D 128."""
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    print(f"prefill C3 full dtype={kv_dtype}", flush=True)
+    wl = prefill_c3(seed=0)
+    assert (wl.shared_lens > 0).sum() >= 8  # the shared-prefix path is exercised
+    got = run_prefill(gpu_ctx, wl, kv_dtype)
+    err = normwise_error(got, oracle_prefill(orc, wl, kv_dtype))
+    assert err <= (1e-4 if kv_dtype == "f32" else 2e-2), err
+
+
+def test_prefill_one_token_matches_decode(gpu_ctx):
+    """A 1-token prefill chunk is a decode step: both kernels agree within f32 rounding."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    wl = paged_decode_c2(seed=4, num_seqs=8, min_len=1, max_len=900, num_blocks=512)
+    d = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    kp, vp, q = d(wl.k_pool), d(wl.v_pool), d(wl.q)
+    bt, cl = d(wl.block_tables), d(wl.context_lens)
+    out_d = torch.empty_like(q)
+    out_p = torch.empty_like(q)
+    gpu_ctx.attn_decode_paged(q, kp, vp, DTYPE_F32, bt, cl, wl.max_context_len, wl.num_kv_heads,
+                              wl.block_size, wl.num_blocks, wl.scale, out_d)
+    cu = d(np.arange(wl.num_seqs + 1, dtype=np.int32))
+    gpu_ctx.attn_prefill_paged(q, kp, vp, DTYPE_F32, bt, cu, cl, 1, wl.num_kv_heads,
+                               wl.block_size, wl.num_blocks, wl.scale, out_p)
+    torch.cuda.synchronize()
+    assert normwise_error(out_p.cpu().numpy(), out_d.cpu().numpy()) <= 1e-5
