@@ -45,6 +45,27 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP backend cannot be built")
 
 
+RUNTIME_LIB = "libferrisinfer_runtime.so"
+RUNTIME_PATH = os.path.join(PKG_DIR, RUNTIME_LIB)
+RUNTIME_SOURCES = ["runtime/fr_model.cpp", "runtime/fr_scheduler.cpp", "runtime/fr_capi.cpp"]
+
+
+def build_runtime(verbose: bool = False) -> str:
+    """Host runtime: plain C++17 (g++), linked against the kernel library's C ABI only."""
+    srcs = [os.path.join(CSRC, s) for s in RUNTIME_SOURCES]
+    tmp = RUNTIME_PATH + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-o", tmp, *srcs,
+           "-L" + PKG_DIR, "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, cwd=PKG_DIR, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"g++ failed building {RUNTIME_LIB} (exit {res.returncode})")
+    os.replace(tmp, RUNTIME_PATH)
+    return RUNTIME_PATH
+
+
 def build(verbose: bool = False) -> str:
     srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
     tmp = LIB_PATH + ".tmp"
@@ -56,6 +77,7 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed building {LIB_NAME} (exit {res.returncode})")
     os.replace(tmp, LIB_PATH)
+    build_runtime(verbose)
     return LIB_PATH
 
 

@@ -109,8 +109,8 @@ __global__ __launch_bounds__(kRowThreads) void rope_kernel(float* __restrict__ q
 }
 
 // SwiGLU (runtime/reference.rs:346-360): gate <- gate * (1 / (1 + exp(-gate))); out = up * gate.
-__global__ void silu_mul_kernel(const float* __restrict__ up, const float* __restrict__ gate,
-                                float* __restrict__ out, int64_t n) {
+// `out` may alias `up` or `gate` (each element is read before it is written).
+__global__ void silu_mul_kernel(const float* up, const float* gate, float* out, int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) {

@@ -1,0 +1,337 @@
+// Device-resident model, KV block pool and the batched decoder forward of the host runtime.
+// Every device operation goes through the C ABI of include/ferrisinfer_kernel.h.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "fr_runtime.h"
+
+namespace fr {
+
+void fail(ErrorKind kind, const std::string& message) { throw Error{kind, message}; }
+
+void check(int32_t status) {
+  if (status != FI_OK) {
+    const char* msg = fi_last_error();
+    throw Error{static_cast<ErrorKind>(status - 1), msg ? msg : "backend error"};
+  }
+}
+
+// ----------------------------------------------------------------------------- DeviceBuffer
+DeviceBuffer::DeviceBuffer(fi_context* ctx, size_t bytes) { reserve(ctx, bytes); }
+
+DeviceBuffer::~DeviceBuffer() {
+  if (ptr_ != nullptr) (void)fi_buf_free(ctx_, ptr_);
+}
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ctx_(o.ctx_), ptr_(o.ptr_), bytes_(o.bytes_) {
+  o.ptr_ = nullptr;
+  o.bytes_ = 0;
+}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
+  if (this != &o) {
+    if (ptr_ != nullptr) (void)fi_buf_free(ctx_, ptr_);
+    ctx_ = o.ctx_;
+    ptr_ = o.ptr_;
+    bytes_ = o.bytes_;
+    o.ptr_ = nullptr;
+    o.bytes_ = 0;
+  }
+  return *this;
+}
+
+void DeviceBuffer::reserve(fi_context* ctx, size_t bytes) {
+  if (bytes <= bytes_ && ptr_ != nullptr) return;
+  if (ptr_ != nullptr) {
+    check(fi_buf_free(ctx_, ptr_));
+    ptr_ = nullptr;
+    bytes_ = 0;
+  }
+  ctx_ = ctx;
+  check(fi_buf_alloc(ctx, bytes == 0 ? 4 : bytes, &ptr_));
+  bytes_ = bytes == 0 ? 4 : bytes;
+}
+
+// ----------------------------------------------------------------------------- model
+void ModelConfig::validate() const {
+  // model/config.rs:27-70
+  if (hidden_size <= 0 || intermediate_size <= 0 || num_layers <= 0 || num_attention_heads <= 0 ||
+      num_key_value_heads <= 0 || vocab_size <= 0 || max_position_embeddings <= 0) {
+    fail(ErrorKind::InvalidConfig, "model dimensions must be greater than zero");
+  }
+  if (hidden_size % num_attention_heads != 0) fail(ErrorKind::InvalidConfig, "hidden_size must be divisible by num_attention_heads");
+  if (num_attention_heads % num_key_value_heads != 0) {
+    fail(ErrorKind::InvalidConfig, "num_attention_heads must be divisible by num_key_value_heads");
+  }
+  if (rotary_dims > head_dim()) fail(ErrorKind::InvalidConfig, "rope.rotary_dims cannot exceed attention head dimension");
+}
+
+DeviceModel::DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions)
+    : ctx_(ctx), config_(config), layers_(config.num_layers), rope_positions_(rope_positions) {
+  config.validate();
+  const int pairs = config.rotary_dims / 2;
+  if (pairs > 0) {
+    rope_cos_.reserve(ctx, static_cast<size_t>(rope_positions) * pairs * sizeof(float));
+    rope_sin_.reserve(ctx, static_cast<size_t>(rope_positions) * pairs * sizeof(float));
+    check(fi_rope_table(ctx, rope_positions, config.head_dim(), config.rotary_dims, config.rope_theta,
+                        rope_cos_.f32(), rope_sin_.f32()));
+  }
+}
+
+void DeviceModel::set_weight(const std::string& name, const float* host, size_t count) {
+  const ModelConfig& c = config_;
+  const size_t h = c.hidden_size, f = c.intermediate_size, kvw = static_cast<size_t>(c.num_key_value_heads) * c.head_dim();
+  auto put = [&](DeviceBuffer* dst, size_t expected) {
+    if (count != expected) {
+      fail(ErrorKind::InvalidShape, "tensor " + name + " has " + std::to_string(count) + " elements, expected " +
+                                        std::to_string(expected));
+    }
+    dst->reserve(ctx_, count * sizeof(float));
+    check(fi_buf_upload(ctx_, dst->get(), count * sizeof(float), host, count * sizeof(float)));
+  };
+  if (name == "tok_embeddings.weight") return put(&tok_embeddings_, static_cast<size_t>(c.vocab_size) * h);
+  if (name == "norm.weight") return put(&norm_, h);
+  if (name == "output.weight") return put(&output_, static_cast<size_t>(c.vocab_size) * h);
+  const std::string prefix = "layers.";
+  if (name.compare(0, prefix.size(), prefix) == 0) {
+    const size_t dot = name.find('.', prefix.size());
+    const int layer = std::stoi(name.substr(prefix.size(), dot - prefix.size()));
+    if (layer < 0 || layer >= c.num_layers) fail(ErrorKind::InvalidShape, "layer index out of range in " + name);
+    const std::string rest = name.substr(dot + 1);
+    Layer& w = layers_[layer];
+    if (rest == "attention_norm.weight") return put(&w.attention_norm, h);
+    if (rest == "attention.wq.weight") return put(&w.wq, h * h);
+    if (rest == "attention.wq.bias") return put(&w.wq_bias, h);
+    if (rest == "attention.wk.weight") return put(&w.wk, h * kvw);
+    if (rest == "attention.wk.bias") return put(&w.wk_bias, kvw);
+    if (rest == "attention.wv.weight") return put(&w.wv, h * kvw);
+    if (rest == "attention.wv.bias") return put(&w.wv_bias, kvw);
+    if (rest == "attention.wo.weight") return put(&w.wo, h * h);
+    if (rest == "attention.wo.bias") return put(&w.wo_bias, h);
+    if (rest == "ffn_norm.weight") return put(&w.ffn_norm, h);
+    if (rest == "feed_forward.w1.weight") return put(&w.w1, h * f);
+    if (rest == "feed_forward.w1.bias") return put(&w.w1_bias, f);
+    if (rest == "feed_forward.w2.weight") return put(&w.w2, f * h);
+    if (rest == "feed_forward.w2.bias") return put(&w.w2_bias, h);
+    if (rest == "feed_forward.w3.weight") return put(&w.w3, h * f);
+    if (rest == "feed_forward.w3.bias") return put(&w.w3_bias, f);
+  }
+  fail(ErrorKind::MissingWeight, "unknown tensor name: " + name);
+}
+
+void DeviceModel::validate() const {
+  // model/decoder.rs:30-52 required_weight_keys
+  auto need = [](const DeviceBuffer& b, const std::string& name) {
+    if (b.get() == nullptr) fail(ErrorKind::MissingWeight, "missing required tensor: " + name);
+  };
+  need(tok_embeddings_, "tok_embeddings.weight");
+  for (int l = 0; l < config_.num_layers; ++l) {
+    const Layer& w = layers_[l];
+    const std::string p = "layers." + std::to_string(l) + ".";
+    need(w.attention_norm, p + "attention_norm.weight");
+    need(w.wq, p + "attention.wq.weight");
+    need(w.wk, p + "attention.wk.weight");
+    need(w.wv, p + "attention.wv.weight");
+    need(w.wo, p + "attention.wo.weight");
+    need(w.ffn_norm, p + "ffn_norm.weight");
+    need(w.w1, p + "feed_forward.w1.weight");
+    need(w.w2, p + "feed_forward.w2.weight");
+    need(w.w3, p + "feed_forward.w3.weight");
+  }
+  need(norm_, "norm.weight");
+  if (!config_.tie_word_embeddings) need(output_, "output.weight");
+}
+
+// ----------------------------------------------------------------------------- block pool
+BlockPool::BlockPool(fi_context* ctx, int32_t layers, int32_t num_blocks, int32_t block_size, int32_t kv_heads,
+                     int32_t head_dim, int32_t kv_dtype)
+    : num_blocks_(num_blocks), block_size_(block_size), kv_dtype_(kv_dtype) {
+  if (layers <= 0 || num_blocks <= 0 || block_size <= 0 || kv_heads <= 0 || head_dim <= 0) {
+    fail(ErrorKind::InvalidConfig, "KV cache dimensions must be greater than zero");
+  }
+  if (kv_dtype != FI_DTYPE_F32 && kv_dtype != FI_DTYPE_BF16) fail(ErrorKind::InvalidType, "KV dtype must be f32 or bf16");
+  free_.reserve(num_blocks);
+  for (int32_t b = num_blocks - 1; b >= 0; --b) free_.push_back(b);
+  refs_.assign(num_blocks, 0);
+  const size_t elem = kv_dtype == FI_DTYPE_F32 ? 4 : 2;
+  const size_t bytes = static_cast<size_t>(num_blocks) * kv_heads * block_size * head_dim * elem;
+  for (int32_t l = 0; l < layers; ++l) {
+    k_.emplace_back(ctx, bytes);
+    v_.emplace_back(ctx, bytes);
+  }
+}
+
+int32_t BlockPool::allocate() {
+  if (free_.empty()) fail(ErrorKind::Runtime, "KV block pool ran out of free blocks");
+  const int32_t b = free_.back();
+  free_.pop_back();
+  refs_[b] = 1;
+  return b;
+}
+
+void BlockPool::incref(int32_t block) { refs_.at(block) += 1; }
+
+void BlockPool::decref(int32_t block) {
+  int32_t& r = refs_.at(block);
+  if (r <= 0) fail(ErrorKind::Runtime, "KV block " + std::to_string(block) + " released twice");
+  if (--r == 0) free_.push_back(block);
+}
+
+// ----------------------------------------------------------------------------- forward
+ForwardExecutor::ForwardExecutor(const DeviceModel* model, BlockPool* pool)
+    : model_(model), pool_(pool), ctx_(model->ctx()) {}
+
+void ForwardExecutor::copy_only(const PackedBatch& b) {
+  // A tick whose sequences only shared a prefix still owes the copy-on-write of a partially
+  // filled shared block.
+  const int32_t n = static_cast<int32_t>(b.copy_src.size());
+  if (n == 0) return;
+  std::vector<int32_t> host(b.copy_src);
+  host.insert(host.end(), b.copy_dst.begin(), b.copy_dst.end());
+  host.insert(host.end(), b.copy_count.begin(), b.copy_count.end());
+  meta_.reserve(ctx_, host.size() * 4);
+  check(fi_buf_upload(ctx_, meta_.get(), host.size() * 4, host.data(), host.size() * 4));
+  const int32_t* d = static_cast<const int32_t*>(meta_.get());
+  const ModelConfig& c = model_->config();
+  for (int32_t l = 0; l < c.num_layers; ++l) {
+    check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(), d, d + n, d + 2 * n, n,
+                            pool_->num_blocks(), pool_->block_size(), c.num_key_value_heads, c.head_dim()));
+  }
+  check(fi_ctx_sync(ctx_));
+  check(fi_ctx_check_faults(ctx_));
+}
+
+void ForwardExecutor::reserve(size_t tokens, size_t seqs) {
+  if (tokens <= cap_tokens_ && seqs <= cap_seqs_) return;
+  cap_tokens_ = std::max(tokens, cap_tokens_);
+  cap_seqs_ = std::max(seqs, cap_seqs_);
+  const ModelConfig& c = model_->config();
+  const size_t t = cap_tokens_, h = c.hidden_size, f = c.intermediate_size;
+  const size_t kvw = static_cast<size_t>(c.num_key_value_heads) * c.head_dim();
+  hidden_.reserve(ctx_, t * h * 4);
+  normed_.reserve(ctx_, t * h * 4);
+  q_.reserve(ctx_, t * h * 4);
+  k_.reserve(ctx_, t * kvw * 4);
+  v_.reserve(ctx_, t * kvw * 4);
+  attn_.reserve(ctx_, t * h * 4);
+  tmp_.reserve(ctx_, t * h * 4);
+  h1_.reserve(ctx_, t * h * 4);
+  up_.reserve(ctx_, t * f * 4);
+  gate_.reserve(ctx_, t * f * 4);
+  last_.reserve(ctx_, cap_seqs_ * h * 4);
+  last_norm_.reserve(ctx_, cap_seqs_ * h * 4);
+  tok_.reserve(ctx_, cap_seqs_ * 4);
+  prob_.reserve(ctx_, cap_seqs_ * 4);
+}
+
+std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
+  const ModelConfig& c = model_->config();
+  const int32_t T = static_cast<int32_t>(b.token_ids.size());
+  const int32_t B = static_cast<int32_t>(b.context_lens.size());
+  if (T == 0 || B == 0) {
+    copy_only(b);
+    return {};
+  }
+  reserve(T, B);
+  const int32_t H = c.hidden_size, F = c.intermediate_size, hq = c.num_attention_heads;
+  const int32_t hkv = c.num_key_value_heads, D = c.head_dim(), kvw = hkv * D;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // attention.rs:659
+
+  // One upload of all integer metadata (8-byte aligned sections).
+  std::vector<uint8_t> host;
+  auto section = [&](const void* data, size_t bytes) {
+    size_t off = (host.size() + 7) & ~static_cast<size_t>(7);
+    host.resize(off + bytes);
+    if (bytes) std::memcpy(host.data() + off, data, bytes);
+    return off;
+  };
+  const size_t o_ids = section(b.token_ids.data(), b.token_ids.size() * 4);
+  const size_t o_pos = section(b.positions.data(), b.positions.size() * 4);
+  const size_t o_slot = section(b.slot_mapping.data(), b.slot_mapping.size() * 8);
+  const size_t o_cu = section(b.cu_seqlens.data(), b.cu_seqlens.size() * 4);
+  const size_t o_ctx = section(b.context_lens.data(), b.context_lens.size() * 4);
+  const size_t o_bt = section(b.block_tables.data(), b.block_tables.size() * 4);
+  const size_t o_last = section(b.last_rows.data(), b.last_rows.size() * 4);
+  const size_t o_cs = section(b.copy_src.data(), b.copy_src.size() * 4);
+  const size_t o_cd = section(b.copy_dst.data(), b.copy_dst.size() * 4);
+  const size_t o_cc = section(b.copy_count.data(), b.copy_count.size() * 4);
+  meta_.reserve(ctx_, host.size());
+  check(fi_buf_upload(ctx_, meta_.get(), host.size(), host.data(), host.size()));
+  auto at = [&](size_t off) { return static_cast<uint8_t*>(meta_.get()) + off; };
+  const int32_t* d_ids = reinterpret_cast<const int32_t*>(at(o_ids));
+  const int32_t* d_pos = reinterpret_cast<const int32_t*>(at(o_pos));
+  const int64_t* d_slot = reinterpret_cast<const int64_t*>(at(o_slot));
+  const int32_t* d_cu = reinterpret_cast<const int32_t*>(at(o_cu));
+  const int32_t* d_ctx = reinterpret_cast<const int32_t*>(at(o_ctx));
+  const int32_t* d_bt = reinterpret_cast<const int32_t*>(at(o_bt));
+  const int32_t* d_last = reinterpret_cast<const int32_t*>(at(o_last));
+  const int32_t n_copy = static_cast<int32_t>(b.copy_src.size());
+
+  float* hidden = hidden_.f32();
+  float* normed = normed_.f32();
+  float* q = q_.f32();
+  float* k = k_.f32();
+  float* v = v_.f32();
+  float* attn = attn_.f32();
+  float* tmp = tmp_.f32();
+  float* h1 = h1_.f32();
+  float* up = up_.f32();
+  float* gate = gate_.f32();
+
+  // runtime/reference.rs:372-423 / 664-710: embed, L blocks, final norm, greedy head
+  check(fi_embedding(ctx_, model_->tok_embeddings(), c.vocab_size, H, d_ids, T, hidden));
+  for (int32_t l = 0; l < c.num_layers; ++l) {
+    const DeviceModel::Layer& w = model_->layer(l);
+    // runtime/reference.rs:163-370: rmsnorm -> q,k,v (+bias) -> rope -> attention (KV
+    // appended first, so the chunk's own keys come from the pool) -> wo -> +x -> rmsnorm ->
+    // w1, w3 -> silu(w3) * w1 -> w2 -> +h1
+    check(fi_rms_norm(ctx_, hidden, w.attention_norm.f32(), normed, T, H, c.rms_norm_eps));
+    check(fi_gemm(ctx_, normed, w.wq.f32(), w.wq_bias.f32(), q, T, H, H, 0));
+    check(fi_gemm(ctx_, normed, w.wk.f32(), w.wk_bias.f32(), k, T, H, kvw, 0));
+    check(fi_gemm(ctx_, normed, w.wv.f32(), w.wv_bias.f32(), v, T, H, kvw, 0));
+    if (c.rotary_dims > 0) {
+      check(fi_rope(ctx_, q, k, d_pos, model_->rope_cos(), model_->rope_sin(), T, hq, hkv, D, c.rotary_dims,
+                    model_->rope_positions()));
+    }
+    check(fi_kv_append(ctx_, k, v, d_slot, T, pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(),
+                       pool_->block_size(), hkv, D));
+    if (n_copy > 0) {
+      check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(),
+                              reinterpret_cast<const int32_t*>(at(o_cs)), reinterpret_cast<const int32_t*>(at(o_cd)),
+                              reinterpret_cast<const int32_t*>(at(o_cc)), n_copy, pool_->num_blocks(),
+                              pool_->block_size(), hkv, D));
+    }
+    if (b.kind == BatchKind::Decode) {
+      check(fi_attn_decode_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), d_bt, b.max_blocks, d_ctx, B,
+                                 b.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
+                                 attn));
+    } else {
+      check(fi_attn_prefill_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), d_bt, b.max_blocks, d_cu,
+                                  d_ctx, B, b.max_query_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(),
+                                  scale, attn));
+    }
+    check(fi_gemm(ctx_, attn, w.wo.f32(), w.wo_bias.f32(), tmp, T, H, H, 0));
+    check(fi_add_rms_norm(ctx_, tmp, hidden, h1, w.ffn_norm.f32(), normed, T, H, c.rms_norm_eps));
+    check(fi_gemm(ctx_, normed, w.w1.f32(), w.w1_bias.f32(), up, T, H, F, 0));
+    check(fi_gemm(ctx_, normed, w.w3.f32(), w.w3_bias.f32(), gate, T, H, F, 0));
+    check(fi_silu_mul(ctx_, up, gate, up, static_cast<int64_t>(T) * F));  // in place over `up`
+    check(fi_gemm(ctx_, up, w.w2.f32(), w.w2_bias.f32(), tmp, T, F, H, 0));
+    check(fi_add(ctx_, tmp, h1, hidden, static_cast<int64_t>(T) * H));
+  }
+  // last row of every sequence -> final norm -> fused greedy head (matmul.rs:190-274)
+  check(fi_embedding(ctx_, hidden, T, H, d_last, B, last_.f32()));
+  check(fi_rms_norm(ctx_, last_.f32(), model_->norm(), last_norm_.f32(), B, H, c.rms_norm_eps));
+  check(fi_lm_head_argmax(ctx_, last_norm_.f32(), model_->output_weight(), B, H, c.vocab_size,
+                          static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  std::vector<int32_t> tok(B);
+  std::vector<float> prob(B);
+  check(fi_buf_download(ctx_, tok.data(), B * 4, tok_.get(), B * 4));
+  check(fi_buf_download(ctx_, prob.data(), B * 4, prob_.get(), B * 4));
+  check(fi_ctx_check_faults(ctx_));
+  std::vector<TokenSample> out(B);
+  for (int32_t i = 0; i < B; ++i) out[i] = TokenSample{static_cast<uint32_t>(tok[i]), prob[i]};
+  return out;
+}
+
+}  // namespace fr

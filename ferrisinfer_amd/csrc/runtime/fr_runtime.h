@@ -1,0 +1,345 @@
+// Host runtime of the MI355X path (C++17): the reference's ReferenceScheduler / Session /
+// KvCache API (crates/ferrisinfer-runtime/src/{scheduler,session,kv_cache,paged_kv,
+// block_manager,prefix_index,sequence}.rs) driving the HIP backend only through the C ABI of
+// include/ferrisinfer_kernel.h.
+//
+// The scheduler decides ticks exactly as the reference does, but executes each tick as ONE
+// ragged batch: every sequence of the tick is packed (cu_seqlens, positions, slot_mapping,
+// block tables, context lengths) and the decoder runs once over the batch.  KV lives in one
+// global block pool; a shared prefix is referenced by block id (refcounted) and only a
+// partially filled last block is copied.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "../../../include/ferrisinfer_kernel.h"
+
+namespace fr {
+
+// Mirrors core/error.rs:5-16; status codes are kind + 1 at the C boundary.
+enum class ErrorKind : int32_t {
+  Io = 0, Parse, InvalidShape, InvalidLayout, InvalidType, InvalidConfig, MissingWeight, Unsupported, Runtime,
+};
+
+struct Error {
+  ErrorKind kind;
+  std::string message;
+};
+
+[[noreturn]] void fail(ErrorKind kind, const std::string& message);
+// Throws the backend's error (status + fi_last_error) when status != 0.
+void check(int32_t status);
+
+// ---------------------------------------------------------------------------------------
+// Device memory owned by the runtime.
+class DeviceBuffer {
+ public:
+  DeviceBuffer() = default;
+  DeviceBuffer(fi_context* ctx, size_t bytes);
+  ~DeviceBuffer();
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  DeviceBuffer(DeviceBuffer&& o) noexcept;
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
+  void* get() const { return ptr_; }
+  float* f32() const { return static_cast<float*>(ptr_); }
+  size_t bytes() const { return bytes_; }
+  // Grows (reallocating, contents lost) to at least `bytes`.
+  void reserve(fi_context* ctx, size_t bytes);
+
+ private:
+  fi_context* ctx_ = nullptr;
+  void* ptr_ = nullptr;
+  size_t bytes_ = 0;
+};
+
+// ---------------------------------------------------------------------------------------
+// model/config.rs:5-72
+struct ModelConfig {
+  int32_t hidden_size = 0;
+  int32_t intermediate_size = 0;
+  int32_t num_layers = 0;
+  int32_t num_attention_heads = 0;
+  int32_t num_key_value_heads = 0;
+  int32_t vocab_size = 0;
+  int32_t max_position_embeddings = 0;
+  float rms_norm_eps = 1e-6f;
+  float rope_theta = 10000.0f;
+  int32_t rotary_dims = 0;
+  bool tie_word_embeddings = false;
+  int32_t head_dim() const { return hidden_size / num_attention_heads; }
+  void validate() const;
+};
+
+// Weights resident in HBM, named and shaped as model/decoder.rs:30-114 ([in, out] layout).
+class DeviceModel {
+ public:
+  struct Layer {
+    DeviceBuffer attention_norm, wq, wq_bias, wk, wk_bias, wv, wv_bias, wo, wo_bias;
+    DeviceBuffer ffn_norm, w1, w1_bias, w2, w2_bias, w3, w3_bias;
+  };
+  DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions);
+  void set_weight(const std::string& name, const float* host, size_t count);
+  void validate() const;  // every required tensor present (MissingWeight otherwise)
+  const ModelConfig& config() const { return config_; }
+  const Layer& layer(int i) const { return layers_.at(i); }
+  const float* tok_embeddings() const { return tok_embeddings_.f32(); }
+  const float* norm() const { return norm_.f32(); }
+  const float* output_weight() const {
+    return config_.tie_word_embeddings ? tok_embeddings_.f32() : output_.f32();
+  }
+  const float* rope_cos() const { return rope_cos_.f32(); }
+  const float* rope_sin() const { return rope_sin_.f32(); }
+  int32_t rope_positions() const { return rope_positions_; }
+  fi_context* ctx() const { return ctx_; }
+
+ private:
+  fi_context* ctx_;
+  ModelConfig config_;
+  std::vector<Layer> layers_;
+  DeviceBuffer tok_embeddings_, norm_, output_, rope_cos_, rope_sin_;
+  int32_t rope_positions_;
+};
+
+// ---------------------------------------------------------------------------------------
+// Global KV block pool: per layer K and V [num_blocks, Hkv, block_size, D].  The free list
+// generalises the reference's per-session LIFO page list (runtime/paged_kv.rs:469-527,
+// 794-796): it starts as [n-1, ..., 0] and pops from the back, so block 0 goes first; a block
+// returns to the back of the list when its refcount drops to zero.
+class BlockPool {
+ public:
+  BlockPool(fi_context* ctx, int32_t layers, int32_t num_blocks, int32_t block_size, int32_t kv_heads,
+            int32_t head_dim, int32_t kv_dtype);
+  int32_t allocate();
+  void incref(int32_t block);
+  void decref(int32_t block);
+  int32_t refcount(int32_t block) const { return refs_.at(block); }
+  size_t free_count() const { return free_.size(); }
+  int32_t num_blocks() const { return num_blocks_; }
+  int32_t block_size() const { return block_size_; }
+  int32_t kv_dtype() const { return kv_dtype_; }
+  void* k(int32_t layer) const { return k_.at(layer).get(); }
+  void* v(int32_t layer) const { return v_.at(layer).get(); }
+
+ private:
+  int32_t num_blocks_, block_size_, kv_dtype_;
+  std::vector<int32_t> free_;
+  std::vector<int32_t> refs_;
+  std::vector<DeviceBuffer> k_, v_;
+};
+
+// ---------------------------------------------------------------------------------------
+// runtime/sequence.rs:43-237
+enum class Phase : int32_t { Prefill = 0, Decode = 1, Finished = 2 };
+enum class FinishReason : int32_t {
+  None = -1, StopToken = 0, MaxNewTokens = 1, SessionLimit = 2, SequenceLength = 3, Cancelled = 4,
+};
+enum class BatchKind : int32_t { Prefill = 0, Decode = 1 };
+
+struct TokenSample {
+  uint32_t token_id = 0;
+  float probability = 0.0f;
+};
+
+// One request: the reference's SequenceState plus the state its Session keeps (position,
+// token history, last sample) and its KV block table in the global pool.
+struct Sequence {
+  uint64_t request_id = 0;
+  uint64_t sequence_id = 0;
+  std::vector<uint32_t> prompt;
+  std::vector<uint32_t> generated;
+  size_t cached_tokens = 0;
+  size_t requested_max_new_tokens = 0;
+  size_t max_new_tokens = 0;
+  std::optional<uint32_t> stop_token;
+  Phase phase = Phase::Prefill;
+  FinishReason finish_reason = FinishReason::None;
+  // session state (runtime/session.rs:92-102)
+  bool resident = true;
+  size_t position = 0;
+  std::vector<uint32_t> history;
+  std::optional<TokenSample> last_sample;
+  // KV: logical block i -> pool block blocks[i]
+  std::vector<int32_t> blocks;
+
+  size_t cached_prompt_tokens() const { return cached_tokens < prompt.size() ? cached_tokens : prompt.size(); }
+  size_t pending_prompt_tokens() const { return prompt.size() - cached_prompt_tokens(); }
+  size_t next_prefill_chunk_len(size_t max_chunk) const {
+    return pending_prompt_tokens() < max_chunk ? pending_prompt_tokens() : max_chunk;
+  }
+  bool generation_budget_reached() const { return generated.size() >= max_new_tokens; }
+  FinishReason generation_budget_finish_reason() const {
+    return requested_max_new_tokens > max_new_tokens ? FinishReason::SessionLimit : FinishReason::MaxNewTokens;
+  }
+  void record_prefill(size_t appended);
+  void record_generated_token(uint32_t token);
+  void finish(FinishReason reason) {
+    phase = Phase::Finished;
+    finish_reason = reason;
+  }
+};
+
+// runtime/block_manager.rs:5-56 (ManagedBlockId) — the reference's prefix metadata; layer
+// tables of one sequence are identical here since all layers share the block table.
+struct ManagedBlockId {
+  uint64_t owner_sequence_id;
+  int32_t layer_index;
+  int32_t block_id;
+  bool operator<(const ManagedBlockId& o) const {
+    if (owner_sequence_id != o.owner_sequence_id) return owner_sequence_id < o.owner_sequence_id;
+    if (layer_index != o.layer_index) return layer_index < o.layer_index;
+    return block_id < o.block_id;
+  }
+};
+
+struct PrefixHandle {
+  size_t token_count = 0;
+  int32_t layers = 0;
+  std::vector<int32_t> blocks;  // ceil(token_count / block_size) entries, same on every layer
+};
+
+class PrefixBlockManager {
+ public:
+  std::vector<ManagedBlockId> update_owned_prefix(uint64_t seq, std::optional<PrefixHandle> h);
+  std::vector<ManagedBlockId> update_shared_prefix(uint64_t seq, std::optional<std::pair<uint64_t, PrefixHandle>> a);
+  std::vector<ManagedBlockId> remove_sequence(uint64_t seq);
+  size_t ref_count(const ManagedBlockId& id) const;
+
+ private:
+  std::vector<ManagedBlockId> apply(uint64_t owner, const PrefixHandle& h, bool increment);
+  std::map<uint64_t, PrefixHandle> owned_;
+  std::map<uint64_t, std::pair<uint64_t, PrefixHandle>> shared_;
+  std::map<ManagedBlockId, size_t> refs_;
+};
+
+// runtime/prefix_index.rs:24-113
+class PrefixIndex {
+ public:
+  struct Entry {
+    uint64_t sequence_id;
+    const std::vector<uint32_t>* prompt;
+    size_t cached_prompt_tokens;
+    size_t session_position;
+  };
+  explicit PrefixIndex(size_t min_share) : min_share_(min_share) {}
+  void rebuild(const std::vector<Sequence>& seqs);
+  std::optional<std::pair<uint64_t, size_t>> best_match(uint64_t target, const std::vector<uint32_t>& prompt) const;
+
+ private:
+  size_t min_share_;
+  std::map<std::vector<uint32_t>, std::vector<Entry>> buckets_;
+};
+
+// runtime/scheduler.rs:16-35, session.rs:29-46
+struct SchedulerConfig {
+  size_t max_batch_size = 16;
+  size_t max_prefill_chunk_tokens = 256;
+  size_t max_prefill_batch_tokens = 1024;
+  size_t max_consecutive_prefill_ticks = 2;
+  size_t min_prefix_share_tokens = 64;
+};
+
+struct SessionConfig {
+  size_t max_sequence_length = 4096;
+  size_t max_generated_tokens = 512;
+};
+
+// runtime/scheduler.rs:54-71
+struct SequenceUpdate {
+  uint64_t request_id;
+  uint64_t sequence_id;
+  BatchKind batch_kind;
+  size_t reused_prompt_tokens;
+  size_t appended_prompt_tokens;
+  bool has_token;
+  TokenSample generated;
+  Phase phase;
+  FinishReason finish_reason;
+  std::vector<ManagedBlockId> released_prefix_blocks;
+};
+
+struct TickReport {
+  BatchKind kind;
+  std::vector<uint64_t> sequence_ids;
+  std::vector<SequenceUpdate> updates;
+};
+
+// Metadata of one packed ragged batch, as uploaded to the device (host copy for tests).
+struct PackedBatch {
+  BatchKind kind = BatchKind::Prefill;
+  std::vector<uint64_t> sequence_ids;      // sequences with tokens in the batch, in tick order
+  std::vector<int32_t> token_ids;          // [T]
+  std::vector<int32_t> positions;          // [T]
+  std::vector<int64_t> slot_mapping;       // [T]
+  std::vector<int32_t> cu_seqlens;         // [B+1]
+  std::vector<int32_t> context_lens;       // [B]
+  std::vector<int32_t> block_tables;       // [B, max_blocks]
+  int32_t max_blocks = 0;
+  std::vector<int32_t> last_rows;          // [B] index of each sequence's last token
+  std::vector<int32_t> copy_src, copy_dst, copy_count;  // copy-on-write of partial blocks
+  int32_t max_query_len = 0;
+  int32_t max_context_len = 0;
+};
+
+// Runs the decoder over packed batches (one launch sequence per tick).
+class ForwardExecutor {
+ public:
+  ForwardExecutor(const DeviceModel* model, BlockPool* pool);
+  // Returns one sample per batch sequence (the argmax of its last row).
+  std::vector<TokenSample> run(const PackedBatch& batch);
+
+ private:
+  void reserve(size_t tokens, size_t seqs);
+  void copy_only(const PackedBatch& batch);
+  const DeviceModel* model_;
+  BlockPool* pool_;
+  fi_context* ctx_;
+  DeviceBuffer meta_, hidden_, normed_, q_, k_, v_, attn_, tmp_, h1_, up_, gate_, last_, last_norm_, tok_, prob_;
+  size_t cap_tokens_ = 0, cap_seqs_ = 0;
+};
+
+// runtime/scheduler.rs:109-648 over the batched executor.
+class Scheduler {
+ public:
+  Scheduler(DeviceModel* model, BlockPool* pool, const SessionConfig& session, const SchedulerConfig& config);
+  uint64_t submit(const std::vector<uint32_t>& prompt, size_t max_new_tokens, std::optional<uint32_t> stop_token);
+  std::optional<std::pair<BatchKind, std::vector<uint64_t>>> plan_next_tick() const;
+  std::optional<TickReport> execute_next_tick();
+  bool has_pending() const;
+  const Sequence* sequence(uint64_t id) const;
+  const PackedBatch& last_batch() const { return last_batch_; }
+  const PrefixBlockManager& block_manager() const { return block_manager_; }
+  const BlockPool& pool() const { return *pool_; }
+
+ private:
+  size_t index_of(uint64_t id) const;
+  std::vector<uint64_t> collect_prefill_ids() const;
+  std::vector<uint64_t> collect_decode_ids() const;
+  bool should_schedule_decode(size_t prefill, size_t decode) const;
+  std::optional<PrefixHandle> prefix_handle(const Sequence& s, size_t tokens) const;
+  void refresh_prefix_metadata(uint64_t id);
+  size_t maybe_share_prefix(uint64_t id, PackedBatch* batch, uint64_t* source_id);
+  void share_blocks(Sequence& target, const Sequence& source, size_t tokens, PackedBatch* batch);
+  void append_to_batch(Sequence& s, const std::vector<uint32_t>& tokens, PackedBatch* batch);
+  std::vector<ManagedBlockId> release(uint64_t id);
+  void finalize_batch(PackedBatch* batch) const;
+
+  DeviceModel* model_;
+  BlockPool* pool_;
+  ForwardExecutor executor_;
+  SessionConfig session_;
+  SchedulerConfig config_;
+  uint64_t next_request_id_ = 0;
+  uint64_t next_sequence_id_ = 0;
+  size_t consecutive_prefill_ticks_ = 0;
+  PrefixIndex prefix_index_;
+  PrefixBlockManager block_manager_;
+  std::vector<Sequence> sequences_;
+  PackedBatch last_batch_;
+};
+
+}  // namespace fr

@@ -1,0 +1,187 @@
+"""ctypes binding of libferrisinfer_runtime.so (include/ferrisinfer_runtime.h): the host
+runtime that keeps the reference's ReferenceScheduler API and runs each tick as one packed
+ragged batch on the HIP backend."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from .kernel import DTYPE_BF16, DTYPE_F32, FerrisError, PKG_DIR, load as load_kernel
+
+LIB_PATH = os.path.join(PKG_DIR, "libferrisinfer_runtime.so")
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("hidden_size", C.c_int32), ("intermediate_size", C.c_int32),
+                ("num_layers", C.c_int32), ("num_attention_heads", C.c_int32),
+                ("num_key_value_heads", C.c_int32), ("vocab_size", C.c_int32),
+                ("max_position_embeddings", C.c_int32), ("rms_norm_eps", C.c_float),
+                ("rope_theta", C.c_float), ("rotary_dims", C.c_int32),
+                ("tie_word_embeddings", C.c_int32)]
+
+
+class RuntimeConfig(C.Structure):
+    _fields_ = [("max_sequence_length", C.c_int64), ("max_generated_tokens", C.c_int64),
+                ("max_batch_size", C.c_int64), ("max_prefill_chunk_tokens", C.c_int64),
+                ("max_prefill_batch_tokens", C.c_int64),
+                ("max_consecutive_prefill_ticks", C.c_int64),
+                ("min_prefix_share_tokens", C.c_int64), ("num_blocks", C.c_int32),
+                ("block_size", C.c_int32), ("kv_dtype", C.c_int32)]
+
+
+_P = C.c_void_p
+_I32 = C.c_int32
+_I64 = C.c_int64
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        load_kernel()  # raises when the HIP backend is missing
+        if not os.path.exists(LIB_PATH):
+            raise FerrisError(8, f"host runtime {LIB_PATH} is not built; run "
+                                 "`python -m ferrisinfer_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        sig = {
+            "fr_create": [_I32, C.POINTER(ModelConfig), C.POINTER(RuntimeConfig), C.POINTER(_P)],
+            "fr_destroy": [_P],
+            "fr_set_weight": [_P, C.c_char_p, _P, _I64],
+            "fr_submit": [_P, _P, _I64, _I64, _I64, C.POINTER(C.c_uint64)],
+            "fr_execute_next_tick": [_P, C.POINTER(_I32)],
+            "fr_has_pending": [_P],
+            "fr_last_report": [_P, C.POINTER(_I32), _P, _P, _I64, C.POINTER(_I64)],
+            "fr_last_released": [_P, _I64, _P, _I64, C.POINTER(_I64)],
+            "fr_generated": [_P, C.c_uint64, _P, _I64, C.POINTER(_I64)],
+            "fr_sequence_blocks": [_P, C.c_uint64, _P, _I64, C.POINTER(_I64)],
+            "fr_pool_free_count": [_P, C.POINTER(_I64)],
+            "fr_last_batch_sizes": [_P, _P],
+            "fr_last_batch": [_P] + [_P] * 10,
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _I32
+        L.fr_last_error.restype = C.c_char_p
+        _lib = L
+    return _lib
+
+
+def _check(status):
+    if status != 0:
+        raise FerrisError(int(status), (load().fr_last_error() or b"").decode(errors="replace"))
+
+
+def _addr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+class Runtime:
+    """A model, a KV block pool and a ReferenceScheduler-compatible scheduler on one GPU."""
+
+    def __init__(self, hidden, intermediate, layers, heads, kv_heads, vocab, max_pos=4096,
+                 eps=1e-6, theta=10000.0, rotary_dims=None, tie=False, max_seq=4096,
+                 max_gen=512, max_batch=16, max_chunk=256, max_batch_tokens=1024,
+                 max_consecutive_prefill=2, min_share=64, num_blocks=4096, block_size=16,
+                 kv_dtype="f32", ordinal=0):
+        L = load()
+        head_dim = hidden // heads
+        mc = ModelConfig(hidden, intermediate, layers, heads, kv_heads, vocab, max_pos, eps, theta,
+                         head_dim if rotary_dims is None else rotary_dims, 1 if tie else 0)
+        rc = RuntimeConfig(max_seq, max_gen, max_batch, max_chunk, max_batch_tokens,
+                           max_consecutive_prefill, min_share, num_blocks, block_size,
+                           DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16)
+        h = _P()
+        _check(L.fr_create(ordinal, C.byref(mc), C.byref(rc), C.byref(h)))
+        self.h = h
+        self.vocab = vocab
+
+    def close(self):
+        if getattr(self, "h", None):
+            _check(load().fr_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_weight(self, name, array):
+        a = np.ascontiguousarray(np.asarray(array, dtype=np.float32)).reshape(-1)
+        _check(load().fr_set_weight(self.h, name.encode(), _addr(a), a.size))
+
+    def set_weights(self, weights: dict):
+        for k, v in weights.items():
+            self.set_weight(k, v)
+
+    def submit(self, ids, max_new_tokens=128, stop_token=None):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = C.c_uint64()
+        _check(load().fr_submit(self.h, _addr(ids), ids.size, max_new_tokens,
+                                -1 if stop_token is None else stop_token, C.byref(out)))
+        return int(out.value)
+
+    def execute_next_tick(self):
+        """Returns None or (kind, [update dicts]) in the oracle Scheduler's format."""
+        L = load()
+        ex = C.c_int32()
+        _check(L.fr_execute_next_tick(self.h, C.byref(ex)))
+        if not ex.value:
+            return None
+        cap = 4096
+        rows = np.zeros((cap, 9), np.int64)
+        probs = np.zeros(cap, np.float32)
+        kind = C.c_int32()
+        n = _I64()
+        _check(L.fr_last_report(self.h, C.byref(kind), _addr(rows), _addr(probs), cap, C.byref(n)))
+        updates = []
+        for i in range(n.value):
+            r = rows[i]
+            rel = np.zeros((max(int(r[8]), 1), 3), np.int64)
+            nr = _I64()
+            _check(L.fr_last_released(self.h, i, _addr(rel), rel.shape[0], C.byref(nr)))
+            updates.append(dict(sequence_id=int(r[0]), batch_kind=int(r[1]), reused=int(r[2]),
+                                appended=int(r[3]), token=(int(r[5]) if r[4] else None),
+                                probability=float(probs[i]), phase=int(r[6]),
+                                finish_reason=int(r[7]),
+                                released=[tuple(int(x) for x in row) for row in rel[: nr.value]]))
+        return int(kind.value), updates
+
+    def has_pending(self):
+        return bool(load().fr_has_pending(self.h))
+
+    def generated(self, seq):
+        out = np.zeros(65536, np.uint32)
+        n = _I64()
+        _check(load().fr_generated(self.h, seq, _addr(out), out.size, C.byref(n)))
+        return [int(x) for x in out[: n.value]]
+
+    def sequence_blocks(self, seq):
+        out = np.zeros(65536, np.int32)
+        n = _I64()
+        _check(load().fr_sequence_blocks(self.h, seq, _addr(out), out.size, C.byref(n)))
+        return [int(x) for x in out[: n.value]]
+
+    def pool_free_count(self):
+        n = _I64()
+        _check(load().fr_pool_free_count(self.h, C.byref(n)))
+        return int(n.value)
+
+    def last_batch(self) -> dict:
+        L = load()
+        sizes = np.zeros(7, np.int64)
+        _check(L.fr_last_batch_sizes(self.h, _addr(sizes)))
+        T, B, mb, nc, kind, mq, mctx = (int(x) for x in sizes)
+        arr = dict(token_ids=np.zeros(T, np.int32), positions=np.zeros(T, np.int32),
+                   slot_mapping=np.zeros(T, np.int64), cu_seqlens=np.zeros(B + 1, np.int32),
+                   context_lens=np.zeros(B, np.int32), block_tables=np.zeros((B, mb), np.int32),
+                   copy_src=np.zeros(nc, np.int32), copy_dst=np.zeros(nc, np.int32),
+                   copy_count=np.zeros(nc, np.int32), sequence_ids=np.zeros(B, np.uint64))
+        order = ["token_ids", "positions", "slot_mapping", "cu_seqlens", "context_lens",
+                 "block_tables", "copy_src", "copy_dst", "copy_count", "sequence_ids"]
+        _check(L.fr_last_batch(self.h, *[_addr(arr[k]) for k in order]))
+        arr.update(kind=kind, max_query_len=mq, max_context_len=mctx)
+        return arr

@@ -181,3 +181,50 @@ def prefill_c3(seed: int = 0, num_seqs: int = 16, min_len: int = 32, max_len: in
     return PrefillWorkload(num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, lens, shared,
                            source, tables, cu, lens.copy(), slots, q, k, v,
                            float(1.0 / np.sqrt(np.float32(head_dim))))
+
+
+# ---------------------------------------------------------------------------------------
+# Decoder configurations (C4, C5) and seeded random weights.
+
+TINY_LLAMA_C1 = dict(hidden=256, intermediate=688, layers=4, heads=8, kv_heads=2, vocab=4096,
+                     max_pos=4096, eps=1e-6, theta=10000.0, tie=False)
+QWEN2_05B_C4 = dict(hidden=896, intermediate=4864, layers=24, heads=14, kv_heads=2, vocab=151936,
+                    max_pos=32768, eps=1e-6, theta=1000000.0, tie=True)
+
+
+def random_weights(cfg: dict, seed: int = 0, qkv_bias: bool = False, std: float = 0.02) -> dict:
+    """Weights named as model/decoder.rs:30-52 in the reference's [in, out] layout.  Matrices,
+    embeddings and (optional, Qwen2-style) q/k/v biases ~ N(0, std); RMSNorm weights = 1."""
+    rng = np.random.default_rng(seed)
+    h, f, v = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
+    kvw = cfg["kv_heads"] * (h // cfg["heads"])
+
+    def n(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+    w = {"tok_embeddings.weight": n(v, h)}
+    for layer in range(cfg["layers"]):
+        p = f"layers.{layer}."
+        w[p + "attention_norm.weight"] = np.ones(h, np.float32)
+        w[p + "attention.wq.weight"] = n(h, h)
+        w[p + "attention.wk.weight"] = n(h, kvw)
+        w[p + "attention.wv.weight"] = n(h, kvw)
+        if qkv_bias:
+            w[p + "attention.wq.bias"] = n(h)
+            w[p + "attention.wk.bias"] = n(kvw)
+            w[p + "attention.wv.bias"] = n(kvw)
+        w[p + "attention.wo.weight"] = n(h, h)
+        w[p + "ffn_norm.weight"] = np.ones(h, np.float32)
+        w[p + "feed_forward.w1.weight"] = n(h, f)
+        w[p + "feed_forward.w2.weight"] = n(f, h)
+        w[p + "feed_forward.w3.weight"] = n(h, f)
+    w["norm.weight"] = np.ones(h, np.float32)
+    if not cfg.get("tie", False):
+        w["output.weight"] = n(v, h)
+    return w
+
+
+def c1_requests(seed: int = 0, vocab: int = 4096):
+    """C1: 4 prompts of 16/24/32/48 ids ~ U[0, vocab), 32 greedy tokens each."""
+    rng = np.random.default_rng(seed + 1)
+    return [(rng.integers(0, vocab, size=n).astype(np.uint32), 32) for n in (16, 24, 32, 48)]

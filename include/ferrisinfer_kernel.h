@@ -196,7 +196,7 @@ int32_t fi_rope(fi_context* ctx, float* d_q, float* d_k, const int32_t* d_positi
                 int32_t num_kv_heads, int32_t head_dim, int32_t rotary_dims,
                 int32_t max_positions);
 
-/* SwiGLU: out = up * (gate * (1 / (1 + exp(-gate)))).  Replaces silu_f32_in_place +
+/* SwiGLU: out = up * (gate * (1 / (1 + exp(-gate)))); out may alias up or gate.  Replaces silu_f32_in_place +
  * mul_f32_in_place (kernel/cpu/elementwise.rs:118-207; use at runtime/reference.rs:346-360). */
 int32_t fi_silu_mul(fi_context* ctx, const float* d_up, const float* d_gate, float* d_out,
                     int64_t n);

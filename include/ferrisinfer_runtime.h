@@ -1,0 +1,90 @@
+/*
+ * ferrisinfer_runtime.h — C ABI of the host runtime above the HIP backend
+ * (libferrisinfer_runtime.so).  It keeps the reference's scheduler / session API
+ * (crates/ferrisinfer-runtime/src/scheduler.rs:109-648, session.rs:92-413): requests are
+ * submitted, ticks are planned exactly as ReferenceScheduler::plan_next_tick and executed as
+ * one packed ragged batch on the GPU, and each tick returns the reference's per-sequence
+ * execution report (scheduler.rs:54-71).  Status codes and fr_last_error() follow
+ * include/ferrisinfer_kernel.h.  A Rust host would keep its own scheduler and call the kernel
+ * ABI directly; this library is the C++ stand-in for that host.
+ */
+#ifndef FERRISINFER_RUNTIME_H
+#define FERRISINFER_RUNTIME_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ModelConfig (model/config.rs:5-20) with the Qwen2/Llama rope and norm parameters. */
+typedef struct fr_model_config {
+  int32_t hidden_size;
+  int32_t intermediate_size;
+  int32_t num_layers;
+  int32_t num_attention_heads;
+  int32_t num_key_value_heads;
+  int32_t vocab_size;
+  int32_t max_position_embeddings;
+  float rms_norm_eps;
+  float rope_theta;
+  int32_t rotary_dims;
+  int32_t tie_word_embeddings;
+} fr_model_config;
+
+/* SessionConfig (session.rs:29-46), SchedulerConfig (scheduler.rs:16-35) and the block pool. */
+typedef struct fr_runtime_config {
+  int64_t max_sequence_length;
+  int64_t max_generated_tokens;
+  int64_t max_batch_size;
+  int64_t max_prefill_chunk_tokens;
+  int64_t max_prefill_batch_tokens;
+  int64_t max_consecutive_prefill_ticks;
+  int64_t min_prefix_share_tokens;
+  int32_t num_blocks;
+  int32_t block_size;
+  int32_t kv_dtype; /* FI_DTYPE_F32 or FI_DTYPE_BF16 */
+} fr_runtime_config;
+
+const char* fr_last_error(void);
+
+/* Creates a runtime on device `ordinal`: device model (weights uploaded by fr_set_weight
+ * with the reference's names and [in, out] layout, model/decoder.rs:30-114), KV block pool
+ * and scheduler. */
+int32_t fr_create(int32_t ordinal, const fr_model_config* model, const fr_runtime_config* config,
+                  void** out);
+int32_t fr_destroy(void* runtime);
+int32_t fr_set_weight(void* runtime, const char* name, const float* data, int64_t count);
+
+/* ReferenceScheduler::submit (scheduler.rs:204-250); stop < 0 means no stop token. */
+int32_t fr_submit(void* runtime, const uint32_t* prompt, int64_t n, int64_t max_new_tokens,
+                  int64_t stop, uint64_t* sequence_id);
+/* ReferenceScheduler::execute_next_tick (scheduler.rs:393-415); *executed = 0 when idle. */
+int32_t fr_execute_next_tick(void* runtime, int32_t* executed);
+int32_t fr_has_pending(void* runtime);
+/* Report of the last tick: rows of 9 int64 (sequence_id, batch_kind, reused, appended,
+ * has_token, token_id, phase, finish_reason, released_block_count) + probabilities. */
+int32_t fr_last_report(void* runtime, int32_t* kind, int64_t* rows, float* probs, int64_t capacity,
+                       int64_t* n_out);
+/* Released prefix blocks of update `index`: (owner, layer, block) triples. */
+int32_t fr_last_released(void* runtime, int64_t index, int64_t* out, int64_t capacity,
+                         int64_t* n_out);
+int32_t fr_generated(void* runtime, uint64_t sequence_id, uint32_t* out, int64_t capacity,
+                     int64_t* n_out);
+int32_t fr_sequence_blocks(void* runtime, uint64_t sequence_id, int32_t* out, int64_t capacity,
+                           int64_t* n_out);
+int32_t fr_pool_free_count(void* runtime, int64_t* out);
+/* The last packed batch: sizes = [T, B, max_blocks, copies, kind, max_query_len,
+ * max_context_len]; then its arrays (token ids, positions, slot mapping, cu_seqlens, context
+ * lengths, block tables [B, max_blocks], copy-on-write src/dst/count, sequence ids). */
+int32_t fr_last_batch_sizes(void* runtime, int64_t* sizes);
+int32_t fr_last_batch(void* runtime, int32_t* token_ids, int32_t* positions, int64_t* slots,
+                      int32_t* cu_seqlens, int32_t* context_lens, int32_t* block_tables,
+                      int32_t* copy_src, int32_t* copy_dst, int32_t* copy_count,
+                      uint64_t* sequence_ids);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRISINFER_RUNTIME_H */

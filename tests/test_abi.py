@@ -43,3 +43,17 @@ def test_ctx_create_without_gpu_reports_unsupported():
         assert e.kind in ("Unsupported", "Runtime")
     else:
         raise AssertionError("context creation must fail without a GPU")
+
+
+RUNTIME_HEADER = os.path.join(ROOT, "include", "ferrisinfer_runtime.h")
+
+
+def test_runtime_library_exports_every_declared_symbol():
+    from ferrisinfer_amd import runtime
+
+    text = re.sub(r"/\*.*?\*/", "", open(RUNTIME_HEADER).read(), flags=re.S)
+    syms = sorted(set(re.findall(r"\b(fr_[a-z0-9_]+)\s*\(", text)))
+    assert "fr_execute_next_tick" in syms
+    lib = ctypes.CDLL(runtime.LIB_PATH)
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing

@@ -1,0 +1,134 @@
+"""End-to-end parity of the GPU runtime (batched ticks over the HIP backend) with the CPU
+oracle's restatement of the reference scheduler + sessions (sequential per-sequence
+forwards).  Tick compositions, reports and block accounting must be identical; greedy tokens
+must be identical except where the oracle's own top-2 logit gap is a near tie (< 1e-4
+relative), where summation order may legitimately pick the other token."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def build_pair(orc, cfg, weights, sched_kw, num_blocks=4096, kv_dtype="f32"):
+    from ferrisinfer_amd.runtime import Runtime
+
+    model = orc.Model(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
+                      cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
+                      tie=cfg["tie"])
+    model.set_weights(weights)
+    ref = orc.Scheduler(model, page_size=16, **sched_kw)
+    gpu = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
+                  cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
+                  tie=cfg["tie"], num_blocks=num_blocks, block_size=16, kv_dtype=kv_dtype,
+                  **sched_kw)
+    gpu.set_weights(weights)
+    return model, ref, gpu
+
+
+def drive(sched, requests):
+    ids = [sched.submit(p, max_new_tokens=n) for p, n in requests]
+    ticks = []
+    while True:
+        t = sched.execute_next_tick()
+        if t is None:
+            break
+        ticks.append(t)
+        assert len(ticks) < 10000
+    return ids, ticks
+
+
+def near_tie(model, history, vocab):
+    logits = model.forward_logits(np.asarray(history, np.uint32))[-1]
+    top = np.sort(logits)[-2:]
+    return float(top[1] - top[0]) <= 1e-4 * max(1.0, abs(float(top[1])))
+
+
+def compare(model, ref, gpu, requests):
+    rid, rticks = drive(ref, requests)
+    gid, gticks = drive(gpu, requests)
+    assert rid == gid
+    assert len(rticks) == len(gticks)
+    for (rk, ru), (gk, gu) in zip(rticks, gticks):
+        assert rk == gk
+        assert [u["sequence_id"] for u in ru] == [u["sequence_id"] for u in gu]
+        for a, b in zip(ru, gu):
+            for key in ("batch_kind", "reused", "appended", "phase", "finish_reason"):
+                assert a[key] == b[key], (key, a, b)
+            assert len(a["released"]) == len(b["released"])
+            assert (a["token"] is None) == (b["token"] is None)
+    ties = 0
+    for seq, (prompt, _) in zip(rid, requests):
+        r = ref.generated(seq)
+        g = gpu.generated(seq)
+        assert len(r) == len(g)
+        for i, (a, b) in enumerate(zip(r, g)):
+            if a != b:
+                hist = list(prompt) + r[:i]
+                assert near_tie(model, hist, None), f"seq {seq} token {i}: {a} vs {b}"
+                ties += 1
+                break
+    return rticks, ties
+
+
+def test_c1_tiny_llama_greedy_matches_reference(orc):
+    """tiny Llama (4 layers, H 256, 8/2 heads, D 32, F 688, V 4096),
+    4 requests (16/24/32/48-token prompts), 32 greedy tokens each, block 16, continuous
+    batching with the reference scheduler defaults."""
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1, c1_requests, random_weights
+
+    cfg = TINY_LLAMA_C1
+    weights = random_weights(cfg, seed=0)
+    model, ref, gpu = build_pair(orc, cfg, weights, {})
+    ticks, ties = compare(model, ref, gpu, c1_requests(0))
+    assert ties == 0
+    assert gpu.pool_free_count() == 4096  # every block returned once all requests finished
+
+
+def test_prefix_sharing_and_chunking_match_reference(orc):
+    """Shared prompt prefixes (min_share 16, block-aligned and not), chunked prefill (chunk 20,
+    batch budget 50), decode fairness with batch size 3: same ticks, reuse counts, released
+    blocks and tokens as the reference scheduler."""
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1, random_weights
+
+    cfg = dict(TINY_LLAMA_C1, layers=2)
+    weights = random_weights(cfg, seed=3)
+    rng = np.random.default_rng(7)
+    base = rng.integers(0, cfg["vocab"], size=40).astype(np.uint32)
+    reqs = [
+        (base.copy(), 6),                                                       # source
+        (np.concatenate([base[:37], rng.integers(0, 4096, 9)]).astype(np.uint32), 5),  # shares 37
+        (np.concatenate([base[:32], rng.integers(0, 4096, 3)]).astype(np.uint32), 4),  # shares 32
+        (base.copy(), 3),                                                       # whole prompt
+        (rng.integers(0, 4096, 23).astype(np.uint32), 7),                       # unrelated
+    ]
+    kw = dict(max_batch=3, max_chunk=20, max_batch_tokens=50, min_share=16)
+    model, ref, gpu = build_pair(orc, cfg, weights, kw)
+    ticks, ties = compare(model, ref, gpu, reqs)
+    assert any(u["reused"] > 0 for _, us in ticks for u in us)
+    assert gpu.pool_free_count() == 4096
+
+
+def test_runtime_errors(orc):
+    from ferrisinfer_amd import FerrisError
+    from ferrisinfer_amd.runtime import Runtime
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1, random_weights
+
+    cfg = dict(TINY_LLAMA_C1, layers=1)
+    rt = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
+                 cfg["vocab"], num_blocks=4, block_size=16, max_seq=256)
+    w = random_weights(cfg)
+    del w["norm.weight"]
+    rt.set_weights(w)
+    with pytest.raises(FerrisError) as e:
+        rt.submit([1, 2, 3])
+    assert e.value.kind == "MissingWeight"
+    rt2 = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
+                  cfg["vocab"], num_blocks=2, block_size=16, max_seq=256)
+    rt2.set_weights(random_weights(cfg))
+    with pytest.raises(FerrisError) as e:
+        rt2.submit([4096])
+    assert e.value.kind == "InvalidShape"  # token id out of vocabulary (attention.rs:35-40)
+    rt2.submit(list(range(40)), max_new_tokens=1)
+    with pytest.raises(FerrisError) as e:
+        rt2.execute_next_tick()  # 40 tokens need 3 blocks, the pool has 2
+    assert e.value.kind == "Runtime"
