@@ -86,6 +86,13 @@ _SIGS = {
     "orc_scheduler_last_released": [VP, I64, I64P, I64, C.POINTER(I64)],
     "orc_scheduler_generated": [VP, C.c_uint64, U32P, I64, C.POINTER(I64)],
     "orc_scheduler_block_ref_count": [VP, C.c_uint64, I64, I64, C.POINTER(I64)],
+    "orc_scheduler_attach_packer": [VP, I64, I64],
+    "orc_scheduler_packed_sizes": [VP, I64P],
+    "orc_scheduler_packed": [VP, I32P, I64P, I32P, I32P, I32P, I64, I32P, I32P, I32P,
+                             np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")],
+    "orc_scheduler_packer_free": [VP, C.POINTER(I64)],
+    "orc_scheduler_packer_pages": [VP, C.c_uint64, I32P, I64, C.POINTER(I64)],
+    "orc_scheduler_session_blocks": [VP, C.c_uint64, I64, I64, I64P, I64, C.POINTER(I64)],
 }
 
 
@@ -481,6 +488,47 @@ class Scheduler:
 
     def has_pending(self):
         return bool(lib().orc_scheduler_has_pending(self.h))
+
+    def attach_packer(self, num_pages, page_size):
+        """Packs every following tick over a global page pool (GlobalPagePacker)."""
+        _check(lib().orc_scheduler_attach_packer(self.h, num_pages, page_size), True)
+
+    def packed(self) -> dict:
+        sizes = np.zeros(5, np.int64)
+        _check(lib().orc_scheduler_packed_sizes(self.h, sizes), True)
+        T, B, mb, nc, kind = (int(x) for x in sizes)
+        out = dict(positions=np.zeros(T, np.int32), slot_mapping=np.zeros(T, np.int64),
+                   cu_seqlens=np.zeros(B + 1, np.int32), context_lens=np.zeros(B, np.int32),
+                   block_tables=np.zeros((B, mb), np.int32), copy_src=np.zeros(nc, np.int32),
+                   copy_dst=np.zeros(nc, np.int32), copy_count=np.zeros(nc, np.int32),
+                   sequence_ids=np.zeros(B, np.uint64))
+        _check(lib().orc_scheduler_packed(self.h, out["positions"], out["slot_mapping"],
+                                          out["cu_seqlens"], out["context_lens"],
+                                          out["block_tables"], mb, out["copy_src"],
+                                          out["copy_dst"], out["copy_count"],
+                                          out["sequence_ids"]), True)
+        out["kind"] = kind
+        return out
+
+    def session_blocks(self, seq, layer, tokens):
+        """Page ids of a live sequence's own paged storage (None once it was released)."""
+        out = np.zeros(tokens + 1, np.int64)
+        n = I64()
+        _check(lib().orc_scheduler_session_blocks(self.h, seq, layer, tokens, out, out.size,
+                                                  C.byref(n)), True)
+        return [int(x) for x in out[: n.value]] if n.value else None
+
+    def packer_pages(self, seq):
+        """Pages the packer holds for a sequence (empty once it finished)."""
+        out = np.zeros(1 << 16, np.int32)
+        n = I64()
+        _check(lib().orc_scheduler_packer_pages(self.h, seq, out, out.size, C.byref(n)), True)
+        return [int(x) for x in out[: n.value]]
+
+    def packer_free_pages(self):
+        n = I64()
+        _check(lib().orc_scheduler_packer_free(self.h, C.byref(n)), True)
+        return int(n.value)
 
     def generated(self, seq):
         out = np.zeros(65536, np.uint32)

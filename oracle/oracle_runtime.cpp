@@ -976,7 +976,7 @@ void ReferenceScheduler::refresh_sequence_prefix_metadata(uint64_t seq) {
   block_manager_.update_owned_prefix(seq, std::move(h));
 }
 
-size_t ReferenceScheduler::maybe_share_prefix(uint64_t seq) {
+size_t ReferenceScheduler::maybe_share_prefix(uint64_t seq, int64_t* source_out) {
   rebuild_prefix_index();
   if (config_.min_prefix_share_tokens == 0) return 0;
   size_t ti = index_of(seq);
@@ -987,6 +987,7 @@ size_t ReferenceScheduler::maybe_share_prefix(uint64_t seq) {
   size_t si = index_of(cand->first);
   size_t shared = cand->second;
   if (shared == 0) return 0;
+  *source_out = static_cast<int64_t>(cand->first);
   Entry& source = sequences_[si];
   if (!source.session) fail(ErrorKind::Runtime, "scheduler sequence no longer retains an active session");
   std::optional<SharedPrefixAssignment> assignment;
@@ -1009,7 +1010,8 @@ std::vector<ManagedBlockId> ReferenceScheduler::release_sequence_resources(uint6
 
 SequenceExecutionUpdate ReferenceScheduler::execute_prefill(uint64_t seq) {
   size_t max_chunk = config_.max_prefill_chunk_tokens;
-  size_t reused = maybe_share_prefix(seq);
+  int64_t source = -1;
+  size_t reused = maybe_share_prefix(seq, &source);
   Entry& e = sequences_[index_of(seq)];
   size_t appended = e.state.next_prefill_chunk_len(max_chunk);
   if (appended > 0) {
@@ -1031,6 +1033,7 @@ SequenceExecutionUpdate ReferenceScheduler::execute_prefill(uint64_t seq) {
   u.batch_kind = BatchKind::Prefill;
   u.reused_prompt_tokens = reused;
   u.appended_prompt_tokens = appended;
+  u.shared_from = reused > 0 ? source : -1;
   u.has_token = false;
   u.phase = e.state.phase;
   u.finish_reason = reason;
@@ -1044,6 +1047,7 @@ SequenceExecutionUpdate ReferenceScheduler::execute_decode(uint64_t seq) {
   u.request_id = e.state.request_id;
   u.sequence_id = seq;
   u.batch_kind = BatchKind::Decode;
+  u.shared_from = -1;
   FinishReason reason = FinishReason::None;
   if (e.session->position() >= e.session->config().max_sequence_length) {
     reason = FinishReason::SequenceLength;
@@ -1083,6 +1087,85 @@ std::optional<SchedulerReport> ReferenceScheduler::execute_next_tick() {
   }
   consecutive_prefill_ticks_ = tick->kind == BatchKind::Prefill ? consecutive_prefill_ticks_ + 1 : 0;
   return report;
+}
+
+// ===========================================================================
+// GlobalPagePacker
+// ===========================================================================
+GlobalPagePacker::GlobalPagePacker(size_t num_pages, size_t page_size) : page_size_(page_size) {
+  if (num_pages == 0 || page_size == 0) fail(ErrorKind::InvalidConfig, "page pool dimensions must be greater than zero");
+  for (size_t p = num_pages; p-- > 0;) free_.push_back(static_cast<int32_t>(p));
+  refs_.assign(num_pages, 0);
+}
+
+int32_t GlobalPagePacker::allocate() {
+  if (free_.empty()) fail(ErrorKind::Runtime, "page pool ran out of free pages");
+  int32_t p = free_.back();
+  free_.pop_back();
+  refs_[p] = 1;
+  return p;
+}
+
+void GlobalPagePacker::decref(int32_t page) {
+  if (--refs_.at(page) == 0) free_.push_back(page);
+}
+
+PackedTick GlobalPagePacker::pack(const SchedulerReport& report) {
+  PackedTick t;
+  t.kind = static_cast<int32_t>(report.tick.kind);
+  t.cu_seqlens.push_back(0);
+  std::vector<uint64_t> finished;
+  for (const auto& u : report.updates) {
+    Seq& s = seqs_[u.sequence_id];
+    size_t n = 0;
+    if (u.batch_kind == BatchKind::Prefill) {
+      if (u.reused_prompt_tokens > 0) {
+        // the target's pages become the source's: full pages by id, the partial one copied
+        Seq& src = seqs_.at(static_cast<uint64_t>(u.shared_from));
+        for (int32_t p : s.pages) decref(p);
+        s.pages.clear();
+        size_t full = u.reused_prompt_tokens / page_size_;
+        for (size_t i = 0; i < full; ++i) {
+          refs_.at(src.pages[i]) += 1;
+          s.pages.push_back(src.pages[i]);
+        }
+        size_t rem = u.reused_prompt_tokens % page_size_;
+        if (rem) {
+          int32_t p = allocate();
+          s.pages.push_back(p);
+          t.copy_src.push_back(src.pages[full]);
+          t.copy_dst.push_back(p);
+          t.copy_count.push_back(static_cast<int32_t>(rem));
+        }
+        s.position = u.reused_prompt_tokens;
+      }
+      n = u.appended_prompt_tokens;
+    } else {
+      n = u.has_token ? 1 : 0;
+    }
+    if (n > 0) {
+      size_t end = s.position + n;
+      while (s.pages.size() * page_size_ < end) s.pages.push_back(allocate());
+      for (size_t p = s.position; p < end; ++p) {
+        size_t logical = p / page_size_, offset = p % page_size_;
+        t.positions.push_back(static_cast<int32_t>(p));
+        t.slot_mapping.push_back(static_cast<int64_t>(s.pages[logical]) * static_cast<int64_t>(page_size_) +
+                                 static_cast<int64_t>(offset));
+      }
+      t.sequence_ids.push_back(u.sequence_id);
+      t.cu_seqlens.push_back(static_cast<int32_t>(t.positions.size()));
+      t.context_lens.push_back(static_cast<int32_t>(end));
+      t.block_tables.emplace_back(s.pages.begin(), s.pages.begin() + (end + page_size_ - 1) / page_size_);
+      s.position = end;
+    }
+    if (u.finish_reason != FinishReason::None) finished.push_back(u.sequence_id);
+  }
+  for (uint64_t id : finished) {
+    Seq& s = seqs_[id];
+    for (int32_t p : s.pages) decref(p);
+    s.pages.clear();
+  }
+  return t;
 }
 
 }  // namespace orc

@@ -343,6 +343,7 @@ struct SequenceExecutionUpdate {
   BatchKind batch_kind;
   size_t reused_prompt_tokens;
   size_t appended_prompt_tokens;
+  int64_t shared_from;  // sequence the prefix was copied from, -1 if none (test aid)
   bool has_token;
   TokenSample generated;
   SequencePhase phase;
@@ -381,7 +382,7 @@ class ReferenceScheduler {
   std::vector<uint64_t> collect_prefill_ids() const;
   std::vector<uint64_t> collect_decode_ids() const;
   bool should_schedule_decode(size_t prefill, size_t decode) const;
-  size_t maybe_share_prefix(uint64_t seq);
+  size_t maybe_share_prefix(uint64_t seq, int64_t* source);
   SequenceExecutionUpdate execute_prefill(uint64_t seq);
   SequenceExecutionUpdate execute_decode(uint64_t seq);
   void rebuild_prefix_index();
@@ -398,6 +399,44 @@ class ReferenceScheduler {
   PrefixIndex prefix_index_;
   PrefixBlockManager block_manager_;
   std::vector<Entry> sequences_;
+};
+
+// ---- Batch packer restated over a global page pool (test oracle for the GPU runtime's
+// packing).  It applies the reference's logical-block math (paged_kv.rs:605-606, 717-720:
+// position p -> logical block p / page_size, offset p % page_size, slot = block * page_size +
+// offset), first-touch allocation from a LIFO free list initialised [n-1 .. 0]
+// (paged_kv.rs:469-527, 794-796) shared by all sequences, prefix sharing by page id with a
+// copy of a partially filled last page, and release of a finished sequence's pages (in
+// block-table order, after its tick) when their reference count drops to zero.
+struct PackedTick {
+  int32_t kind = 0;
+  std::vector<uint64_t> sequence_ids;
+  std::vector<int32_t> positions;
+  std::vector<int64_t> slot_mapping;
+  std::vector<int32_t> cu_seqlens;
+  std::vector<int32_t> context_lens;
+  std::vector<std::vector<int32_t>> block_tables;  // per sequence, ceil(ctx / page) entries
+  std::vector<int32_t> copy_src, copy_dst, copy_count;
+};
+
+class GlobalPagePacker {
+ public:
+  GlobalPagePacker(size_t num_pages, size_t page_size);
+  PackedTick pack(const SchedulerReport& report);
+  size_t free_pages() const { return free_.size(); }
+  const std::vector<int32_t>& pages_of(uint64_t seq) { return seqs_[seq].pages; }
+
+ private:
+  struct Seq {
+    std::vector<int32_t> pages;
+    size_t position = 0;
+  };
+  int32_t allocate();
+  void decref(int32_t page);
+  size_t page_size_;
+  std::vector<int32_t> free_;
+  std::vector<int32_t> refs_;
+  std::map<uint64_t, Seq> seqs_;
 };
 
 }  // namespace orc

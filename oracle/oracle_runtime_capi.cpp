@@ -1,5 +1,6 @@
 // C entry points for the oracle's runtime restatement (paged KV, model forward, session,
 // scheduler) and the paged-decode CPU baseline — TEST INFRASTRUCTURE ONLY (see oracle.h).
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -203,6 +204,8 @@ int32_t orc_session_read_prefix(void* s, int64_t layer, int64_t len, float* k, f
 struct OrcScheduler {
   std::unique_ptr<ReferenceScheduler> sched;
   std::optional<SchedulerReport> last;
+  std::unique_ptr<GlobalPagePacker> packer;
+  PackedTick packed;
 };
 void* orc_scheduler_create(void* m, int64_t max_seq, int64_t max_gen, int64_t page_size,
                            int64_t max_batch, int64_t max_chunk, int64_t max_batch_tokens,
@@ -219,7 +222,9 @@ void* orc_scheduler_create(void* m, int64_t max_seq, int64_t max_gen, int64_t pa
     c.max_prefill_batch_tokens = max_batch_tokens;
     c.max_consecutive_prefill_ticks = max_consecutive_prefill;
     c.min_prefix_share_tokens = min_share;
-    s = new OrcScheduler{std::make_unique<ReferenceScheduler>(static_cast<OrcModel*>(m)->model, sc, c), {}};
+    auto o = std::make_unique<OrcScheduler>();
+    o->sched = std::make_unique<ReferenceScheduler>(static_cast<OrcModel*>(m)->model, sc, c);
+    s = o.release();
   });
   return s;
 }
@@ -238,8 +243,77 @@ int32_t orc_scheduler_execute_next_tick(void* s, int32_t* executed) {
     auto* o = static_cast<OrcScheduler*>(s);
     o->last = o->sched->execute_next_tick();
     *executed = o->last ? 1 : 0;
+    if (o->last && o->packer) o->packed = o->packer->pack(*o->last);
   });
 }
+// Attaches a global page packer (pool of num_pages pages of page_size) that packs every
+// following tick.
+int32_t orc_scheduler_attach_packer(void* s, int64_t num_pages, int64_t page_size) {
+  return guard([&] {
+    static_cast<OrcScheduler*>(s)->packer = std::make_unique<GlobalPagePacker>(num_pages, page_size);
+  });
+}
+// sizes: [T, B, max_blocks, copies, kind]
+int32_t orc_scheduler_packed_sizes(void* s, int64_t* sizes) {
+  return guard([&] {
+    const PackedTick& t = static_cast<OrcScheduler*>(s)->packed;
+    size_t mb = 1;
+    for (const auto& r : t.block_tables) mb = std::max(mb, r.size());
+    sizes[0] = static_cast<int64_t>(t.positions.size());
+    sizes[1] = static_cast<int64_t>(t.sequence_ids.size());
+    sizes[2] = static_cast<int64_t>(mb);
+    sizes[3] = static_cast<int64_t>(t.copy_src.size());
+    sizes[4] = t.kind;
+  });
+}
+// block_tables is [B, max_blocks], zero padded.
+int32_t orc_scheduler_packed(void* s, int32_t* positions, int64_t* slots, int32_t* cu, int32_t* ctx_lens,
+                             int32_t* block_tables, int64_t max_blocks, int32_t* copy_src, int32_t* copy_dst,
+                             int32_t* copy_count, uint64_t* seq_ids) {
+  return guard([&] {
+    const PackedTick& t = static_cast<OrcScheduler*>(s)->packed;
+    std::copy(t.positions.begin(), t.positions.end(), positions);
+    std::copy(t.slot_mapping.begin(), t.slot_mapping.end(), slots);
+    std::copy(t.cu_seqlens.begin(), t.cu_seqlens.end(), cu);
+    std::copy(t.context_lens.begin(), t.context_lens.end(), ctx_lens);
+    for (size_t b = 0; b < t.block_tables.size(); ++b) {
+      for (int64_t j = 0; j < max_blocks; ++j) {
+        block_tables[b * max_blocks + j] = j < static_cast<int64_t>(t.block_tables[b].size()) ? t.block_tables[b][j] : 0;
+      }
+    }
+    std::copy(t.copy_src.begin(), t.copy_src.end(), copy_src);
+    std::copy(t.copy_dst.begin(), t.copy_dst.end(), copy_dst);
+    std::copy(t.copy_count.begin(), t.copy_count.end(), copy_count);
+    std::copy(t.sequence_ids.begin(), t.sequence_ids.end(), seq_ids);
+  });
+}
+int32_t orc_scheduler_packer_pages(void* s, uint64_t seq, int32_t* out, int64_t capacity, int64_t* n_out) {
+  return guard([&] {
+    const auto& pages = static_cast<OrcScheduler*>(s)->packer->pages_of(seq);
+    if (static_cast<int64_t>(pages.size()) > capacity) fail(ErrorKind::InvalidShape, "page capacity too small");
+    std::copy(pages.begin(), pages.end(), out);
+    *n_out = static_cast<int64_t>(pages.size());
+  });
+}
+int32_t orc_scheduler_packer_free(void* s, int64_t* out) {
+  return guard([&] { *out = static_cast<int64_t>(static_cast<OrcScheduler*>(s)->packer->free_pages()); });
+}
+
+// Block ids of a live sequence's paged session storage for `tokens` tokens of `layer`
+// (PagedKvCacheStorage::block_table); n_out = 0 when the sequence holds no session.
+int32_t orc_scheduler_session_blocks(void* s, uint64_t seq, int64_t layer, int64_t tokens, int64_t* out,
+                                     int64_t capacity, int64_t* n_out) {
+  return guard([&] {
+    *n_out = 0;
+    const Session* sess = static_cast<OrcScheduler*>(s)->sched->session(seq);
+    if (!sess || !sess->kv_cache().paged_storage()) return;
+    auto t = sess->kv_cache().paged_storage()->block_table(layer, tokens);
+    if (static_cast<int64_t>(t.size()) > capacity) fail(ErrorKind::InvalidShape, "block capacity too small");
+    for (size_t i = 0; i < t.size(); ++i) out[i] = static_cast<int64_t>(t[i].block_id);
+    *n_out = static_cast<int64_t>(t.size());
+  });
+}
+
 int32_t orc_scheduler_has_pending(void* s) { return static_cast<OrcScheduler*>(s)->sched->has_pending() ? 1 : 0; }
 // Per-update rows: int64[9] = (sequence_id, batch_kind, reused, appended, has_token, token_id,
 // phase, finish_reason, released_block_count); probability in probs[i].

@@ -1,8 +1,10 @@
 """End-to-end parity of the GPU runtime (batched ticks over the HIP backend) with the CPU
 oracle's restatement of the reference scheduler + sessions (sequential per-sequence
-forwards).  Tick compositions, reports and block accounting must be identical; greedy tokens
-must be identical except where the oracle's own top-2 logit gap is a near tie (< 1e-4
-relative), where summation order may legitimately pick the other token."""
+forwards).  Tick compositions, reports and block accounting must be identical; each tick's
+packed metadata (positions, slot mapping, cu_seqlens, context lengths, block tables,
+copy-on-write list) must equal the oracle packer's bit for bit; greedy tokens must be
+identical except where the oracle's own top-2 logit gap is a near tie (< 1e-4 relative),
+where summation order may legitimately pick the other token."""
 import numpy as np
 import pytest
 
@@ -17,6 +19,7 @@ def build_pair(orc, cfg, weights, sched_kw, num_blocks=4096, kv_dtype="f32"):
                       tie=cfg["tie"])
     model.set_weights(weights)
     ref = orc.Scheduler(model, page_size=16, **sched_kw)
+    ref.attach_packer(num_blocks, 16)
     gpu = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
                   cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
                   tie=cfg["tie"], num_blocks=num_blocks, block_size=16, kv_dtype=kv_dtype,
@@ -25,7 +28,11 @@ def build_pair(orc, cfg, weights, sched_kw, num_blocks=4096, kv_dtype="f32"):
     return model, ref, gpu
 
 
-def drive(sched, requests):
+PACK_KEYS = ("positions", "slot_mapping", "cu_seqlens", "context_lens", "block_tables",
+             "copy_src", "copy_dst", "copy_count", "sequence_ids")
+
+
+def drive(sched, requests, packs=None):
     ids = [sched.submit(p, max_new_tokens=n) for p, n in requests]
     ticks = []
     while True:
@@ -33,6 +40,8 @@ def drive(sched, requests):
         if t is None:
             break
         ticks.append(t)
+        if packs is not None:
+            packs.append(sched.packed() if hasattr(sched, "packed") else sched.last_batch())
         assert len(ticks) < 10000
     return ids, ticks
 
@@ -44,10 +53,15 @@ def near_tie(model, history, vocab):
 
 
 def compare(model, ref, gpu, requests):
-    rid, rticks = drive(ref, requests)
-    gid, gticks = drive(gpu, requests)
+    rpacks, gpacks = [], []
+    rid, rticks = drive(ref, requests, rpacks)
+    gid, gticks = drive(gpu, requests, gpacks)
     assert rid == gid
     assert len(rticks) == len(gticks)
+    for i, (a, b) in enumerate(zip(rpacks, gpacks)):
+        assert a["kind"] == b["kind"], i
+        for key in PACK_KEYS:
+            assert np.array_equal(a[key], b[key]), (i, key, a[key], b[key])
     for (rk, ru), (gk, gu) in zip(rticks, gticks):
         assert rk == gk
         assert [u["sequence_id"] for u in ru] == [u["sequence_id"] for u in gu]
