@@ -7,6 +7,10 @@ from a seeded permutation of an 8192-block pool, f32 Q/K/V ~ N(0, 1).  One step 
 fi_attn_decode_paged launch over the whole batch (one layer's decode attention), inputs
 already resident in HBM.
 
+A second measurement, ``c4``, serves BASELINE config C4 (the Qwen2-0.5B-shaped model under
+continuous batching at max batch 64) through the GPU runtime and reports decode tokens/s by
+the reference's definition next to the CPU oracle on a declared subset.
+
 Prints ONE JSON line: value = decode tokens/s (64 query tokens per step); ``roofline`` is the
 decode kernel's achieved HBM bandwidth from hipEvents on the launch stream over the timed
 region (algorithmic bytes / average launch time); ``cpu_baseline`` is the CPU oracle (the
@@ -26,6 +30,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
+FP32_PEAK_TFS = 157.3  # MI355X dense fp32 (vector and MFMA), AMD public spec
 METRIC = "decode tokens/sec @ ragged batch 64; paged-attn achieved HBM GB/s (% peak)"
 
 
@@ -39,6 +44,11 @@ def parse_args():
                    help="CPU baseline repetitions of the full batch (0 = auto, ~10 s)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-c4", action="store_true",
+                   help="skip the C4 (Qwen2-0.5B-shaped) continuous-batching measurement")
+    p.add_argument("--c4-requests", type=int, default=128)
+    p.add_argument("--no-kernels", action="store_true",
+                   help="skip the C3 prefill/append and projection-GEMM kernel measurements")
     p.add_argument("--pmc-copy-reference", action="store_true",
                    help="only run a plain 512 MiB device copy (5 launches): the known-size "
                         "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -99,6 +109,171 @@ def cpu_baseline(wl, reps):
     }
 
 
+def timed(fn, reps, warmup=3):
+    """Average device time (ms) of fn over reps launches, hipEvents on torch's current
+    stream (the stream the library's context follows)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kernel_legs(ctx, seed):
+    """C3 varlen prefill attention (MFMA f32) and KV append (HBM) at full size, and the
+    projection GEMMs at the C4 shapes: a prefill chunk (M = 1024, MFMA-bound) and a decode
+    tick (M = 64, weight-streaming, HBM-bound)."""
+    import numpy as np
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    out = {}
+    wl = prefill_c3(seed=seed)
+    d = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    shape = (wl.num_blocks, wl.num_kv_heads, wl.block_size, wl.head_dim)
+    kp = torch.zeros(shape, device="cuda")
+    vp = torch.zeros(shape, device="cuda")
+    k_new, v_new, slots, q = d(wl.k_new), d(wl.v_new), d(wl.slot_mapping), d(wl.q)
+    bt, cu, cl = d(wl.block_tables), d(wl.cu_seqlens), d(wl.context_lens)
+    o = torch.empty_like(q)
+    T = int(wl.cu_seqlens[-1])
+
+    def append():
+        ctx.kv_append(k_new, v_new, slots, kp, vp, DTYPE_F32, wl.num_blocks, wl.block_size,
+                      wl.num_kv_heads, wl.head_dim)
+
+    def prefill():
+        ctx.attn_prefill_paged(q, kp, vp, DTYPE_F32, bt, cu, cl, int(wl.query_lens.max()),
+                               wl.num_kv_heads, wl.block_size, wl.num_blocks, wl.scale, o)
+
+    ms_a = timed(append, 50)
+    ms_p = timed(prefill, 20)
+    ctx.check_faults()
+    flops = wl.attention_flops()
+    ab = wl.append_bytes(4)
+    out["c3_prefill_attention"] = {
+        "kernel": "prefill_attention_kernel", "bound": "mfma (f32)",
+        "tokens": T, "flops_per_launch": flops, "avg_launch_us": round(ms_p * 1e3, 2),
+        "achieved_tflops": round(flops / (ms_p * 1e-3) / 1e12, 2), "peak_tflops": FP32_PEAK_TFS,
+        "frac": round(flops / (ms_p * 1e-3) / 1e12 / FP32_PEAK_TFS, 4)}
+    out["c3_kv_append"] = {
+        "kernel": "kv_append_kernel", "bound": "hbm", "tokens": T,
+        "bytes_per_launch": ab, "avg_launch_us": round(ms_a * 1e3, 2),
+        "achieved_gbs": round(ab / (ms_a * 1e-3) / 1e9, 1), "peak_gbs": HBM_PEAK_GBS,
+        "frac": round(ab / (ms_a * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kp, vp, k_new, v_new, slots, q, o
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for name, m, k, n in (("gemm_c4_prefill_w1", 1024, 896, 4864),
+                          ("gemm_c4_prefill_w2", 1024, 4864, 896),
+                          ("gemm_c4_decode_w1", 64, 896, 4864),
+                          ("gemm_c4_decode_w2", 64, 4864, 896)):
+        a = torch.randn(m, k, device="cuda", generator=g)
+        b = torch.randn(k, n, device="cuda", generator=g)
+        c = torch.empty(m, n, device="cuda")
+        ms = timed(lambda: ctx.gemm(a, b, c), 50)
+        fl = 2 * m * n * k
+        byt = 4 * (m * k + k * n + m * n)
+        out[name] = {"m": m, "k": k, "n": n, "avg_launch_us": round(ms * 1e3, 2),
+                     "achieved_tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                     "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / FP32_PEAK_TFS, 4),
+                     "achieved_gbs": round(byt / (ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ctx.check_faults()
+    return out
+
+
+def c4_continuous(seed, n_requests):
+    """C4: the Qwen2-0.5B-shaped model (f32, tied, q/k/v biases, random N(0, 0.02) weights)
+    served by the GPU runtime under continuous batching (max batch 64, block 16, the
+    reference scheduler's other defaults), Poisson arrivals at 8 req/s on 50 ms virtual
+    ticks.  Decode tok/s = generated tokens / summed decode-tick wall time, the reference's
+    continuous-batching definition (cli/main.rs:1502-1512, 1619-1622)."""
+    import numpy as np
+
+    from ferrisinfer_amd.runtime import Runtime
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, random_weights, run_continuous
+
+    cfg = QWEN2_05B_C4
+    weights = random_weights(cfg, seed=seed, qkv_bias=True)
+    rt = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
+                 cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"], tie=True, max_seq=4096,
+                 max_gen=512, max_batch=64, num_blocks=16384, block_size=16)
+    rt.set_weights(weights)
+    del weights
+    # warm-up: one short request through prefill and decode (module load, first launches)
+    run_continuous(rt, [dict(prompt=np.arange(300, dtype=np.uint32), max_new_tokens=3,
+                             arrival_tick=0)])
+    reqs = c4_requests(seed=seed, n=n_requests)
+    t0 = time.perf_counter()
+    rep = run_continuous(rt, reqs)
+    wall = time.perf_counter() - t0
+    full = [t for t in rep["ticks"] if t["kind"] == 1 and t["batch"] == 64]
+    full_s = sum(t["seconds"] for t in full)
+    dec = [t for t in rep["ticks"] if t["kind"] == 1]
+    split = {k: round(sum(t["profile"][k] for t in dec) / max(len(dec), 1) * 1e3, 3)
+             for k in ("schedule", "enqueue", "wait", "total")}
+    out = {
+        "workload": f"C4 Qwen2-0.5B shape, {n_requests} requests, Poisson 8/s on 50 ms virtual "
+                    "ticks, prompts lognormal(median 512, sigma 0.5) clipped [1,2048], outputs "
+                    "U[64,256], greedy, max batch 64, block 16, f32 weights+KV",
+        "decode_tok_s": round(rep["decode_tok_s"], 1),
+        "decode_tok_s_at_batch_64": round(64 * len(full) / full_s, 1) if full_s > 0 else None,
+        "ms_per_decode_tick_at_batch_64": round(full_s / len(full) * 1e3, 3) if full else None,
+        "prefill_tok_s": round(rep["prefill_tok_s"], 1),
+        "generated_tokens": rep["generated_tokens"],
+        "decode_ticks": rep["decode_ticks"],
+        "prefill_ticks": rep["prefill_ticks"],
+        "avg_decode_batch": round(rep["avg_decode_batch"], 2),
+        "decode_ticks_at_batch_64": len(full),
+        "decode_tick_host_ms": split,
+        "wall_s": round(wall, 3),
+    }
+    rt.close()
+    return out
+
+
+def c4_cpu_baseline(seed, threads):
+    """The oracle's restatement of the reference (per-sequence sessions, its thread fan-out)
+    on a declared C4 subset: the first 4 requests, prompts cut to 64 tokens, 8 new tokens."""
+    import oracle
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, random_weights, run_continuous
+
+    oracle.build()
+    oracle.set_threads(threads)
+    cfg = QWEN2_05B_C4
+    model = oracle.Model(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
+                         cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
+                         tie=True)
+    model.set_weights(random_weights(cfg, seed=seed, qkv_bias=True))
+    reqs = c4_requests(seed=seed)[:4]
+    for r in reqs:
+        r["prompt"] = r["prompt"][:64]
+        r["max_new_tokens"] = 8
+    rep = run_continuous(oracle.Scheduler(model, max_batch=64), reqs)
+    return {
+        "value": round(rep["decode_tok_s"], 3),
+        "unit": "decode tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": "C4 model, first 4 C4 requests with prompts cut to 64 tokens, 8 new tokens "
+                  f"each ({rep['generated_tokens']} decode tokens over {rep['decode_ticks']} "
+                  f"ticks); host {os.cpu_count()} cpus",
+        "prefill_tok_s": round(rep["prefill_tok_s"], 2),
+    }
+
+
 def main():
     args = parse_args()
     if args.pmc_copy_reference:
@@ -106,7 +281,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(no multi-GPU path exists; see DESIGN.md for how the path would shard)",
+              "(no multi-GPU path exists in this build)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -202,8 +377,18 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_reps)
-    print(json.dumps(result), flush=True)
+    del q, kp, vp, bt, cl, out
+    if not args.no_kernels:
+        print("bench: C3 prefill/append and GEMM kernels", file=sys.stderr, flush=True)
+        result["kernels"] = kernel_legs(ctx, args.seed)
     ctx.close()
+    if not args.no_c4:
+        print("bench: C4 continuous batching on the GPU runtime", file=sys.stderr, flush=True)
+        result["c4"] = c4_continuous(args.seed, args.c4_requests)
+        if not args.no_cpu_baseline:
+            print("bench: C4 CPU baseline (oracle, declared subset)", file=sys.stderr, flush=True)
+            result["c4"]["cpu_baseline"] = c4_cpu_baseline(args.seed, min(16, os.cpu_count() or 1))
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

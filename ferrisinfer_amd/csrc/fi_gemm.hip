@@ -10,6 +10,7 @@
 // next K tile is fetched into registers while the current one is multiplied.  Skinny
 // decode shapes split K across workgroups; partial tiles are summed by a second kernel in a
 // fixed order, so results are deterministic.
+#include <algorithm>
 #include <limits>
 
 #include "fi_common.h"
@@ -21,7 +22,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 64;
 constexpr int BN = 64;
-constexpr int BK = 16;
+constexpr int BK = 16;  // K depth per LDS stage (deeper stages measured slower at every shape)
 constexpr int kGemmThreads = 256;
 
 enum Epilogue : int { kStore = 0, kPartial = 1, kArgmax = 2 };
@@ -33,78 +34,92 @@ struct GemmArgs {
   float* c;           // [M, N] (kStore) or [splits, M, N] (kPartial)
   float* amax;        // kArgmax: per (row, n-tile) {max, index bits, sum}
   int m, k, n;
-  int k_chunk;        // K range per split (multiple of BK)
+  int k_chunk;        // K range per split (multiple of the stage depth)
   int n_tiles;
 };
 
-template <bool TRANS_B>
-__device__ __forceinline__ void load_tiles(const GemmArgs& g, int m0, int n0, int k0, int kend, float4& ra,
-                                           float4& rb) {
-  const int t = threadIdx.x;
-  // A: thread -> (row t/4, k quad t%4)
-  {
-    const int row = m0 + t / 4, kk = k0 + (t % 4) * 4;
-    if (row < g.m && kk + 3 < kend && ((g.k & 3) == 0)) {
-      ra = *reinterpret_cast<const float4*>(g.a + (size_t)row * g.k + kk);
+// Each thread moves QPT = BKT / 16 float4 quads of A and of B per K stage (64 x BKT each).
+// A [M, K]: quad q -> (row q / (BKT/4), k quad q % (BKT/4)), consecutive threads read
+// consecutive quads of a row.
+template <bool TRANS_B, int BKT>
+__device__ __forceinline__ void load_tiles(const GemmArgs& g, int m0, int n0, int k0, int kend,
+                                           float4 (&ra)[BKT / 16], float4 (&rb)[BKT / 16]) {
+  constexpr int KQ = BKT / 4;  // quads per K row of a tile
+  const bool kvec = (g.k & 3) == 0;
+#pragma unroll
+  for (int r = 0; r < BKT / 16; ++r) {
+    const int q = threadIdx.x + r * kGemmThreads;
+    const int row = m0 + q / KQ, kk = k0 + (q % KQ) * 4;
+    if (row < g.m && kk + 3 < kend && kvec) {
+      ra[r] = *reinterpret_cast<const float4*>(g.a + (size_t)row * g.k + kk);
     } else {
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = (row < g.m && kk + i < kend) ? g.a[(size_t)row * g.k + kk + i] : 0.0f;
-      ra = make_float4(v[0], v[1], v[2], v[3]);
+      ra[r] = make_float4(v[0], v[1], v[2], v[3]);
     }
   }
-  if constexpr (!TRANS_B) {
-    // B [K, N]: thread -> (k row t/16, n quad t%16)
-    const int kr = k0 + t / 16, col = n0 + (t % 16) * 4;
-    if (kr < kend && col + 3 < g.n && ((g.n & 3) == 0)) {
-      rb = *reinterpret_cast<const float4*>(g.b + (size_t)kr * g.n + col);
-    } else {
-      float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (kr < kend && col + i < g.n) ? g.b[(size_t)kr * g.n + col + i] : 0.0f;
-      rb = make_float4(v[0], v[1], v[2], v[3]);
-    }
-  } else {
-    // B [N, K]: thread -> (n row t/4, k quad t%4)
-    const int col = n0 + t / 4, kk = k0 + (t % 4) * 4;
-    if (col < g.n && kk + 3 < kend && ((g.k & 3) == 0)) {
-      rb = *reinterpret_cast<const float4*>(g.b + (size_t)col * g.k + kk);
-    } else {
-      float v[4];
+  for (int r = 0; r < BKT / 16; ++r) {
+    const int q = threadIdx.x + r * kGemmThreads;
+    if constexpr (!TRANS_B) {
+      // B [K, N]: quad q -> (k row q / 16, n quad q % 16)
+      const int kr = k0 + q / 16, col = n0 + (q % 16) * 4;
+      if (kr < kend && col + 3 < g.n && ((g.n & 3) == 0)) {
+        rb[r] = *reinterpret_cast<const float4*>(g.b + (size_t)kr * g.n + col);
+      } else {
+        float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (col < g.n && kk + i < kend) ? g.b[(size_t)col * g.k + kk + i] : 0.0f;
-      rb = make_float4(v[0], v[1], v[2], v[3]);
+        for (int i = 0; i < 4; ++i) v[i] = (kr < kend && col + i < g.n) ? g.b[(size_t)kr * g.n + col + i] : 0.0f;
+        rb[r] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    } else {
+      // B [N, K]: quad q -> (n row q / (BKT/4), k quad q % (BKT/4))
+      const int col = n0 + q / KQ, kk = k0 + (q % KQ) * 4;
+      if (col < g.n && kk + 3 < kend && kvec) {
+        rb[r] = *reinterpret_cast<const float4*>(g.b + (size_t)col * g.k + kk);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (col < g.n && kk + i < kend) ? g.b[(size_t)col * g.k + kk + i] : 0.0f;
+        rb[r] = make_float4(v[0], v[1], v[2], v[3]);
+      }
     }
   }
 }
 
-template <bool TRANS_B>
-__device__ __forceinline__ void store_tiles(float (*As)[BM + 4], float (*Bs)[BN + 4], const float4& ra,
-                                            const float4& rb) {
-  const int t = threadIdx.x;
-  {
-    const int row = t / 4, kq = (t % 4) * 4;
-    As[kq + 0][row] = ra.x;
-    As[kq + 1][row] = ra.y;
-    As[kq + 2][row] = ra.z;
-    As[kq + 3][row] = ra.w;
-  }
-  if constexpr (!TRANS_B) {
-    const int kr = t / 16, col = (t % 16) * 4;
-    *reinterpret_cast<float4*>(&Bs[kr][col]) = rb;
-  } else {
-    const int col = t / 4, kq = (t % 4) * 4;
-    Bs[kq + 0][col] = rb.x;
-    Bs[kq + 1][col] = rb.y;
-    Bs[kq + 2][col] = rb.z;
-    Bs[kq + 3][col] = rb.w;
+template <bool TRANS_B, int BKT>
+__device__ __forceinline__ void store_tiles(float (*As)[BM + 4], float (*Bs)[BN + 4], const float4 (&ra)[BKT / 16],
+                                            const float4 (&rb)[BKT / 16]) {
+  constexpr int KQ = BKT / 4;
+#pragma unroll
+  for (int r = 0; r < BKT / 16; ++r) {
+    const int q = threadIdx.x + r * kGemmThreads;
+    {
+      const int row = q / KQ, kq = (q % KQ) * 4;
+      As[kq + 0][row] = ra[r].x;
+      As[kq + 1][row] = ra[r].y;
+      As[kq + 2][row] = ra[r].z;
+      As[kq + 3][row] = ra[r].w;
+    }
+    if constexpr (!TRANS_B) {
+      const int kr = q / 16, col = (q % 16) * 4;
+      *reinterpret_cast<float4*>(&Bs[kr][col]) = rb[r];
+    } else {
+      const int col = q / KQ, kq = (q % KQ) * 4;
+      Bs[kq + 0][col] = rb[r].x;
+      Bs[kq + 1][col] = rb[r].y;
+      Bs[kq + 2][col] = rb[r].z;
+      Bs[kq + 3][col] = rb[r].w;
+    }
   }
 }
 
-template <bool TRANS_B, int EPI>
+// BKT = K depth of one LDS stage.
+template <bool TRANS_B, int EPI, int BKT>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
-  __shared__ float As[2][BK][BM + 4];
-  __shared__ float Bs[2][BK][BN + 4];
+  __shared__ float As[2][BKT][BM + 4];
+  __shared__ float Bs[2][BKT][BN + 4];
   const int n_tile = blockIdx.x, m_tile = blockIdx.y, split = blockIdx.z;
   const int m0 = m_tile * BM, n0 = n_tile * BN;
   const int kbeg = split * g.k_chunk;
@@ -119,18 +134,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  float4 ra, rb;
+  float4 ra[BKT / 16], rb[BKT / 16];
   int buf = 0;
   if (kbeg < kend) {
-    load_tiles<TRANS_B>(g, m0, n0, kbeg, kend, ra, rb);
-    store_tiles<TRANS_B>(As[0], Bs[0], ra, rb);
+    load_tiles<TRANS_B, BKT>(g, m0, n0, kbeg, kend, ra, rb);
+    store_tiles<TRANS_B, BKT>(As[0], Bs[0], ra, rb);
   }
   __syncthreads();
-  for (int k0 = kbeg; k0 < kend; k0 += BK) {
-    const bool more = k0 + BK < kend;
-    if (more) load_tiles<TRANS_B>(g, m0, n0, k0 + BK, kend, ra, rb);
+  for (int k0 = kbeg; k0 < kend; k0 += BKT) {
+    const bool more = k0 + BKT < kend;
+    if (more) load_tiles<TRANS_B, BKT>(g, m0, n0, k0 + BKT, kend, ra, rb);
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 4) {
+    for (int kk = 0; kk < BKT; kk += 4) {
       float af[2], bf[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) af[i] = As[buf][kk + lk][wm + i * 16 + li];
@@ -141,7 +156,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_tiles<TRANS_B>(As[buf ^ 1], Bs[buf ^ 1], ra, rb);
+    if (more) store_tiles<TRANS_B, BKT>(As[buf ^ 1], Bs[buf ^ 1], ra, rb);
     __syncthreads();
     buf ^= 1;
   }
@@ -220,13 +235,50 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   }
 }
 
-// out[m, n] = sum over splits (in split order) + bias.
+// out[m, n] = sum over splits (in split order) + bias.  Four columns per thread when `vec`
+// (n a multiple of 4 and out / bias 16-byte aligned; the partials always are).
 __global__ void splitk_reduce_kernel(const float* __restrict__ parts, const float* __restrict__ bias,
-                                     float* __restrict__ out, int m, int n, int splits) {
+                                     float* __restrict__ out, int m, int n, int splits, int vec) {
   const size_t total = (size_t)m * n;
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (; i < total; i += stride) {
+  if (vec) {
+    const size_t quads = total / 4;
+    const float4* __restrict__ p4 = reinterpret_cast<const float4*>(parts);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < quads; i += stride) {
+      float4 s = p4[i];
+      int z = 1;
+      // eight partial loads in flight per step; the sum stays in split order
+      for (; z + 8 <= splits; z += 8) {
+        float4 p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p[u] = p4[(size_t)(z + u) * quads + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          s.x = s.x + p[u].x;
+          s.y = s.y + p[u].y;
+          s.z = s.z + p[u].z;
+          s.w = s.w + p[u].w;
+        }
+      }
+      for (; z < splits; ++z) {
+        const float4 p = p4[(size_t)z * quads + i];
+        s.x = s.x + p.x;
+        s.y = s.y + p.y;
+        s.z = s.z + p.z;
+        s.w = s.w + p.w;
+      }
+      if (bias) {
+        const float4 b = reinterpret_cast<const float4*>(bias)[(i * 4 % n) / 4];
+        s.x = s.x + b.x;
+        s.y = s.y + b.y;
+        s.z = s.z + b.z;
+        s.w = s.w + b.w;
+      }
+      reinterpret_cast<float4*>(out)[i] = s;
+    }
+    return;
+  }
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     float s = parts[i];
     for (int z = 1; z < splits; ++z) s += parts[(size_t)z * total + i];
     if (bias) s = s + bias[i % n];
@@ -234,70 +286,107 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ parts, const floa
   }
 }
 
-// Merges the per-tile (max, index, sum) of each row in tile order; left wins ties.
-__global__ void argmax_merge_kernel(const float* __restrict__ amax, int n_tiles, int m,
-                                    int32_t* __restrict__ token, float* __restrict__ prob) {
-  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+// Combines two (max, index, scaled sum) states.  The larger max wins and on equal maxima the
+// smaller index, so the result is the first maximal index whatever the combination order;
+// the sums are rescaled to the winning max.
+__device__ __forceinline__ void argmax_combine(float& mx, int& best, float& sum, float omx, int obest, float osum) {
+  if (obest < 0) return;
+  if (best < 0) {
+    mx = omx;
+    best = obest;
+    sum = osum;
+  } else if (omx > mx || (omx == mx && obest < best)) {
+    sum = osum + sum * __expf(mx - omx);
+    mx = omx;
+    best = obest;
+  } else {
+    sum = sum + osum * __expf(omx - mx);
+  }
+}
+
+// One workgroup per row merges the row's per-tile (max, index, sum) states: each thread folds
+// a strided subset of tiles, then the wave and the workgroup combine.
+constexpr int kMergeThreads = 256;
+__global__ __launch_bounds__(kMergeThreads) void argmax_merge_kernel(const float* __restrict__ amax, int n_tiles,
+                                                                      int m, int32_t* __restrict__ token,
+                                                                      float* __restrict__ prob) {
+  __shared__ float s_mx[kMergeThreads / 64], s_sum[kMergeThreads / 64];
+  __shared__ int s_best[kMergeThreads / 64];
+  const int row = blockIdx.x;
   if (row >= m) return;
   const float* p = amax + (size_t)row * n_tiles * 3;
-  const int* pi = reinterpret_cast<const int*>(p);
-  float mx = p[0], sum = p[2];
-  int best = pi[1];
-  for (int t = 1; t < n_tiles; ++t) {
-    const float omx = p[t * 3], osum = p[t * 3 + 2];
-    const int obest = pi[t * 3 + 1];
-    if (obest < 0) continue;
-    if (best < 0) {
-      mx = omx;
-      sum = osum;
-      best = obest;
-    } else if (mx >= omx) {
-      sum = sum + osum * __expf(omx - mx);
-    } else {
-      sum = osum + sum * __expf(mx - omx);
-      mx = omx;
-      best = obest;
-    }
+  float mx = -INFINITY, sum = 0.0f;
+  int best = -1;
+  for (int t = threadIdx.x; t < n_tiles; t += kMergeThreads) {
+    argmax_combine(mx, best, sum, p[t * 3], reinterpret_cast<const int*>(p)[t * 3 + 1], p[t * 3 + 2]);
   }
-  token[row] = best;
-  prob[row] = 1.0f / sum;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float omx = __shfl_xor(mx, off, 64);
+    const float osum = __shfl_xor(sum, off, 64);
+    const int obest = __shfl_xor(best, off, 64);
+    argmax_combine(mx, best, sum, omx, obest, osum);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_mx[w] = mx;
+    s_sum[w] = sum;
+    s_best[w] = best;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kMergeThreads / 64; ++i) argmax_combine(mx, best, sum, s_mx[i], s_best[i], s_sum[i]);
+    token[row] = best;
+    prob[row] = 1.0f / sum;
+  }
 }
 
-// Picks the K split so that skinny (decode) shapes still launch enough workgroups to keep
-// all CUs streaming weights: aim for >= 2 workgroups per CU, chunks >= 64 deep.
-int choose_splits(fi_context* ctx, int m, int n, int k) {
+// K range per split: enough workgroups (>= 2 per CU) for skinny shapes to keep every CU
+// streaming weights, in whole stages of the kernel's K depth.
+int choose_k_chunk(fi_context* ctx, int m, int n, int k, int bk) {
   const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
   const int target = 2 * (ctx->compute_units > 0 ? ctx->compute_units : 256);
-  int splits = 1;
-  while (tiles * splits < target && k / (splits * 2) >= 64 && splits < 32) splits *= 2;
-  return splits;
+  if (tiles >= target) return k;
+  const int want = (target + tiles - 1) / tiles;
+  int chunk = (k + want - 1) / want;
+  chunk = std::max(chunk, bk == BK ? 64 : bk);
+  chunk = (chunk + bk - 1) / bk * bk;
+  const int max_splits = 64;
+  if ((k + chunk - 1) / chunk > max_splits) chunk = ((k + max_splits - 1) / max_splits + bk - 1) / bk * bk;
+  return std::min(chunk, k);
 }
 
-template <bool TRANS_B>
-int32_t launch_gemm(fi_context* ctx, GemmArgs g) {
-  const int splits = choose_splits(ctx, g.m, g.n, g.k);
+template <bool TRANS_B, int BKT>
+int32_t launch_gemm_bk(fi_context* ctx, GemmArgs g) {
+  g.k_chunk = choose_k_chunk(ctx, g.m, g.n, g.k, BKT);
+  const int splits = (g.k + g.k_chunk - 1) / g.k_chunk;
   dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, splits);
   if (splits == 1) {
-    g.k_chunk = g.k;
-    hipLaunchKernelGGL((gemm_kernel<TRANS_B, kStore>), grid, dim3(kGemmThreads), 0, ctx->stream, g);
+    hipLaunchKernelGGL((gemm_kernel<TRANS_B, kStore, BKT>), grid, dim3(kGemmThreads), 0, ctx->stream, g);
     FI_CHECK_LAUNCH("gemm_kernel");
     return FI_OK;
   }
-  g.k_chunk = ((g.k + splits - 1) / splits + BK - 1) / BK * BK;
   const size_t part_bytes = (size_t)splits * g.m * g.n * sizeof(float);
   FI_TRY(fi::ensure_workspace(ctx, part_bytes));
   float* parts = static_cast<float*>(ctx->workspace);
   float* out = g.c;
   const float* bias = g.bias;
   g.c = parts;
-  hipLaunchKernelGGL((gemm_kernel<TRANS_B, kPartial>), grid, dim3(kGemmThreads), 0, ctx->stream, g);
+  hipLaunchKernelGGL((gemm_kernel<TRANS_B, kPartial, BKT>), grid, dim3(kGemmThreads), 0, ctx->stream, g);
   FI_CHECK_LAUNCH("gemm_kernel");
-  const size_t total = (size_t)g.m * g.n;
-  unsigned blocks = static_cast<unsigned>((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int vec = (g.n & 3) == 0 && aligned(out) && (bias == nullptr || aligned(bias)) ? 1 : 0;
+  const size_t items = vec ? (size_t)g.m * g.n / 4 : (size_t)g.m * g.n;
+  unsigned blocks = static_cast<unsigned>(std::min<size_t>((items + 255) / 256, 4096));
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, parts, bias, out, g.m, g.n,
-                     splits);
+                     splits, vec);
   FI_CHECK_LAUNCH("splitk_reduce_kernel");
   return FI_OK;
+}
+
+template <bool TRANS_B>
+int32_t launch_gemm(fi_context* ctx, const GemmArgs& g) {
+  return launch_gemm_bk<TRANS_B, BK>(ctx, g);
 }
 
 }  // namespace
@@ -340,9 +429,9 @@ int32_t fi_lm_head_argmax(fi_context* ctx, const float* d_hidden, const float* d
   FI_TRY(fi::ensure_workspace(ctx, (size_t)m * g.n_tiles * 3 * sizeof(float)));
   g.amax = static_cast<float*>(ctx->workspace);
   dim3 grid(g.n_tiles, (m + BM - 1) / BM, 1);
-  hipLaunchKernelGGL((gemm_kernel<true, kArgmax>), grid, dim3(kGemmThreads), 0, ctx->stream, g);
+  hipLaunchKernelGGL((gemm_kernel<true, kArgmax, BK>), grid, dim3(kGemmThreads), 0, ctx->stream, g);
   FI_CHECK_LAUNCH("gemm_kernel(argmax)");
-  hipLaunchKernelGGL(argmax_merge_kernel, dim3((m + 63) / 64), dim3(64), 0, ctx->stream, g.amax, g.n_tiles, m,
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3(m), dim3(kMergeThreads), 0, ctx->stream, g.amax, g.n_tiles, m,
                      d_token, d_prob);
   FI_CHECK_LAUNCH("argmax_merge_kernel");
   return FI_OK;

@@ -171,6 +171,13 @@ int32_t fr_pool_free_count(void* h, int64_t* out) {
   return guard([&] { *out = static_cast<int64_t>(rt(h)->pool->free_count()); });
 }
 
+int32_t fr_last_tick_profile(void* h, double* out) {
+  return guard([&] {
+    const auto p = rt(h)->scheduler_ready().last_tick_profile();
+    for (size_t i = 0; i < p.size(); ++i) out[i] = p[i];
+  });
+}
+
 int32_t fr_last_batch_sizes(void* h, int64_t* sizes) {
   return guard([&] {
     const fr::PackedBatch& b = rt(h)->scheduler_ready().last_batch();

@@ -1,6 +1,7 @@
 // Device-resident model, KV block pool and the batched decoder forward of the host runtime.
 // Every device operation goes through the C ABI of include/ferrisinfer_kernel.h.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 
@@ -226,6 +227,8 @@ void ForwardExecutor::reserve(size_t tokens, size_t seqs) {
 }
 
 std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
+  const auto t_start = std::chrono::steady_clock::now();
+  enqueue_s_ = wait_s_ = 0.0;
   const ModelConfig& c = model_->config();
   const int32_t T = static_cast<int32_t>(b.token_ids.size());
   const int32_t B = static_cast<int32_t>(b.context_lens.size());
@@ -324,11 +327,14 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
   check(fi_rms_norm(ctx_, last_.f32(), model_->norm(), last_norm_.f32(), B, H, c.rms_norm_eps));
   check(fi_lm_head_argmax(ctx_, last_norm_.f32(), model_->output_weight(), B, H, c.vocab_size,
                           static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  const auto t_enqueued = std::chrono::steady_clock::now();
   std::vector<int32_t> tok(B);
   std::vector<float> prob(B);
   check(fi_buf_download(ctx_, tok.data(), B * 4, tok_.get(), B * 4));
   check(fi_buf_download(ctx_, prob.data(), B * 4, prob_.get(), B * 4));
   check(fi_ctx_check_faults(ctx_));
+  enqueue_s_ = std::chrono::duration<double>(t_enqueued - t_start).count();
+  wait_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_enqueued).count();
   std::vector<TokenSample> out(B);
   for (int32_t i = 0; i < B; ++i) out[i] = TokenSample{static_cast<uint32_t>(tok[i]), prob[i]};
   return out;

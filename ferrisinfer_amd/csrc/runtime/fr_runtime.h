@@ -10,6 +10,7 @@
 // partially filled last block is copied.
 #pragma once
 
+#include <array>
 #include <cstdint>
 #include <map>
 #include <optional>
@@ -205,6 +206,8 @@ struct PrefixHandle {
 class PrefixBlockManager {
  public:
   std::vector<ManagedBlockId> update_owned_prefix(uint64_t seq, std::optional<PrefixHandle> h);
+  // update_owned_prefix for callers that drop the release list (scheduler.rs:575-588)
+  void refresh_owned_prefix(uint64_t seq, std::optional<PrefixHandle> h);
   std::vector<ManagedBlockId> update_shared_prefix(uint64_t seq, std::optional<std::pair<uint64_t, PrefixHandle>> a);
   std::vector<ManagedBlockId> remove_sequence(uint64_t seq);
   size_t ref_count(const ManagedBlockId& id) const;
@@ -291,6 +294,9 @@ class ForwardExecutor {
   ForwardExecutor(const DeviceModel* model, BlockPool* pool);
   // Returns one sample per batch sequence (the argmax of its last row).
   std::vector<TokenSample> run(const PackedBatch& batch);
+  // Host seconds of the last run: enqueueing every launch, then waiting for the samples.
+  double last_enqueue_seconds() const { return enqueue_s_; }
+  double last_wait_seconds() const { return wait_s_; }
 
  private:
   void reserve(size_t tokens, size_t seqs);
@@ -300,6 +306,7 @@ class ForwardExecutor {
   fi_context* ctx_;
   DeviceBuffer meta_, hidden_, normed_, q_, k_, v_, attn_, tmp_, h1_, up_, gate_, last_, last_norm_, tok_, prob_;
   size_t cap_tokens_ = 0, cap_seqs_ = 0;
+  double enqueue_s_ = 0.0, wait_s_ = 0.0;
 };
 
 // runtime/scheduler.rs:109-648 over the batched executor.
@@ -312,6 +319,9 @@ class Scheduler {
   bool has_pending() const;
   const Sequence* sequence(uint64_t id) const;
   const PackedBatch& last_batch() const { return last_batch_; }
+  // Host seconds of the last tick: [scheduling and packing, enqueueing the forward, waiting
+  // for its samples, the whole tick].
+  std::array<double, 4> last_tick_profile() const { return tick_profile_; }
   const PrefixBlockManager& block_manager() const { return block_manager_; }
   const BlockPool& pool() const { return *pool_; }
 
@@ -340,6 +350,7 @@ class Scheduler {
   PrefixBlockManager block_manager_;
   std::vector<Sequence> sequences_;
   PackedBatch last_batch_;
+  std::array<double, 4> tick_profile_{};
 };
 
 }  // namespace fr

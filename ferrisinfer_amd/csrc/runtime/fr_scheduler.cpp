@@ -13,6 +13,7 @@
 // whose whole history it shared, session.rs:193-201), and blocks of sequences that finish in
 // the tick return to the pool only after the forward.
 #include <algorithm>
+#include <chrono>
 
 #include "fr_runtime.h"
 
@@ -66,6 +67,18 @@ std::vector<ManagedBlockId> PrefixBlockManager::update_owned_prefix(uint64_t seq
     owned_[seq] = std::move(*h);
   }
   return released;
+}
+
+void PrefixBlockManager::refresh_owned_prefix(uint64_t seq, std::optional<PrefixHandle> h) {
+  // Replacing a handle by an identical one decrements and re-increments the same counts: the
+  // reference discards the release list of this call (scheduler.rs:575-588), so skipping
+  // the round trip leaves every observable count unchanged.
+  auto it = owned_.find(seq);
+  if (h && it != owned_.end() && it->second.token_count == h->token_count && it->second.layers == h->layers &&
+      it->second.blocks == h->blocks) {
+    return;
+  }
+  (void)update_owned_prefix(seq, std::move(h));
 }
 
 std::vector<ManagedBlockId> PrefixBlockManager::update_shared_prefix(
@@ -196,7 +209,6 @@ uint64_t Scheduler::submit(const std::vector<uint32_t>& prompt, size_t max_new_t
   sequences_.push_back(std::move(s));
   block_manager_.update_shared_prefix(id, std::nullopt);
   refresh_prefix_metadata(id);
-  prefix_index_.rebuild(sequences_);
   return id;
 }
 
@@ -268,7 +280,7 @@ void Scheduler::refresh_prefix_metadata(uint64_t id) {
   const Sequence& s = sequences_[index_of(id)];
   std::optional<PrefixHandle> h;
   if (s.phase != Phase::Finished) h = prefix_handle(s, s.cached_prompt_tokens());
-  block_manager_.update_owned_prefix(id, std::move(h));
+  block_manager_.refresh_owned_prefix(id, std::move(h));
 }
 
 void Scheduler::share_blocks(Sequence& target, const Sequence& source, size_t tokens, PackedBatch* batch) {
@@ -294,11 +306,13 @@ void Scheduler::share_blocks(Sequence& target, const Sequence& source, size_t to
 }
 
 size_t Scheduler::maybe_share_prefix(uint64_t id, PackedBatch* batch, uint64_t* source_id) {
-  // scheduler.rs:353-391
-  prefix_index_.rebuild(sequences_);
+  // scheduler.rs:353-391.  The reference rebuilds its prefix index after every sequence
+  // update and again here; only this lookup reads it, so building it here, from the current
+  // sequence states, gives the same matches.
   if (config_.min_prefix_share_tokens == 0) return 0;
   const size_t ti = index_of(id);
   if (sequences_[ti].cached_prompt_tokens() != 0 || sequences_[ti].phase != Phase::Prefill) return 0;
+  prefix_index_.rebuild(sequences_);
   auto cand = prefix_index_.best_match(id, sequences_[ti].prompt);
   if (!cand || cand->second == 0) return 0;
   const size_t si = index_of(cand->first);
@@ -318,7 +332,6 @@ size_t Scheduler::maybe_share_prefix(uint64_t id, PackedBatch* batch, uint64_t* 
   target.record_prefill(shared);
   block_manager_.update_shared_prefix(id, std::move(assignment));
   refresh_prefix_metadata(id);
-  prefix_index_.rebuild(sequences_);
   return shared;
 }
 
@@ -368,6 +381,7 @@ std::vector<ManagedBlockId> Scheduler::release(uint64_t id) {
 
 std::optional<TickReport> Scheduler::execute_next_tick() {
   // scheduler.rs:393-538
+  const auto t0 = std::chrono::steady_clock::now();
   auto plan = plan_next_tick();
   if (!plan) return std::nullopt;
   TickReport report;
@@ -458,14 +472,17 @@ std::optional<TickReport> Scheduler::execute_next_tick() {
       to_release.push_back(id);
     }
     refresh_prefix_metadata(id);
-    prefix_index_.rebuild(sequences_);
     report.updates.push_back(std::move(u));
   }
   consecutive_prefill_ticks_ = plan->first == BatchKind::Prefill ? consecutive_prefill_ticks_ + 1 : 0;
 
   finalize_batch(&batch);
+  const double sched_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  double enqueue_s = 0.0, wait_s = 0.0;
   if (!batch.sequence_ids.empty() || !batch.copy_src.empty()) {
     std::vector<TokenSample> samples = executor_.run(batch);
+    enqueue_s = executor_.last_enqueue_seconds();
+    wait_s = executor_.last_wait_seconds();
     for (size_t i = 0; i < batch.sequence_ids.size(); ++i) {
       sequences_[index_of(batch.sequence_ids[i])].last_sample = samples[i];
     }
@@ -479,6 +496,8 @@ std::optional<TickReport> Scheduler::execute_next_tick() {
     s.blocks.clear();
   }
   last_batch_ = std::move(batch);
+  tick_profile_ = {sched_s, enqueue_s, wait_s,
+                   std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count()};
   return report;
 }
 

@@ -5,6 +5,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import time
 
 import numpy as np
 
@@ -59,6 +60,7 @@ def load() -> C.CDLL:
             "fr_pool_free_count": [_P, C.POINTER(_I64)],
             "fr_last_batch_sizes": [_P, _P],
             "fr_last_batch": [_P] + [_P] * 10,
+            "fr_last_tick_profile": [_P, _P],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -125,10 +127,15 @@ class Runtime:
         return int(out.value)
 
     def execute_next_tick(self):
-        """Returns None or (kind, [update dicts]) in the oracle Scheduler's format."""
+        """Returns None or (kind, [update dicts]) in the oracle Scheduler's format.  The wall
+        time of the native tick (host scheduling, the batched forward, the sample download) is
+        kept in ``last_tick_seconds``."""
         L = load()
         ex = C.c_int32()
-        _check(L.fr_execute_next_tick(self.h, C.byref(ex)))
+        t0 = time.perf_counter()
+        status = L.fr_execute_next_tick(self.h, C.byref(ex))
+        self.last_tick_seconds = time.perf_counter() - t0
+        _check(status)
         if not ex.value:
             return None
         cap = 4096
@@ -169,6 +176,13 @@ class Runtime:
         n = _I64()
         _check(load().fr_pool_free_count(self.h, C.byref(n)))
         return int(n.value)
+
+    def last_tick_profile(self) -> dict:
+        """Host seconds of the last tick: scheduling, enqueue, wait, total."""
+        out = np.zeros(4, np.float64)
+        _check(load().fr_last_tick_profile(self.h, _addr(out)))
+        return dict(schedule=float(out[0]), enqueue=float(out[1]), wait=float(out[2]),
+                    total=float(out[3]))
 
     def last_batch(self) -> dict:
         L = load()

@@ -228,3 +228,76 @@ def c1_requests(seed: int = 0, vocab: int = 4096):
     """C1: 4 prompts of 16/24/32/48 ids ~ U[0, vocab), 32 greedy tokens each."""
     rng = np.random.default_rng(seed + 1)
     return [(rng.integers(0, vocab, size=n).astype(np.uint32), 32) for n in (16, 24, 32, 48)]
+
+
+# ----------------------------------------------------------------------------- C4
+C4_ARRIVAL_RATE = 8.0        # requests per second (Poisson)
+C4_VIRTUAL_TICK_S = 0.05     # one scheduler tick stands for 50 ms of arrival time
+C4_PROMPT_MEDIAN = 512
+C4_PROMPT_SIGMA = 0.5        # lognormal shape (the config names the median only)
+C4_MAX_PROMPT = 2048
+
+
+def c4_requests(seed: int = 0, n: int = 128, vocab: int = 151936) -> list:
+    """C4 workload: ``n`` requests, Poisson arrivals at 8/s mapped to integer ticks of a
+    fixed 50 ms virtual duration (the reference's continuous-batching driver admits requests
+    by integer arrival tick, cli/main.rs:1721-1741), prompt lengths lognormal (median 512,
+    sigma 0.5) clipped to [1, 2048], ids ~ U[0, vocab), output lengths ~ U[64, 256]."""
+    rng = np.random.default_rng(seed + 4)
+    gaps = rng.exponential(1.0 / C4_ARRIVAL_RATE, size=n)
+    arrival_s = np.cumsum(gaps) - gaps[0]
+    ticks = np.floor(arrival_s / C4_VIRTUAL_TICK_S).astype(np.int64)
+    lens = np.exp(np.log(C4_PROMPT_MEDIAN) + C4_PROMPT_SIGMA * rng.standard_normal(n))
+    lens = np.clip(np.rint(lens), 1, C4_MAX_PROMPT).astype(np.int64)
+    outs = rng.integers(64, 257, size=n)
+    return [dict(prompt=rng.integers(0, vocab, size=int(L)).astype(np.uint32),
+                 max_new_tokens=int(o), arrival_tick=int(t))
+            for L, o, t in zip(lens, outs, ticks)]
+
+
+def run_continuous(sched, requests: list, max_ticks: int | None = None) -> dict:
+    """Drives a scheduler (the GPU Runtime or the oracle's ReferenceScheduler) the way the
+    reference's continuous-batching profile does (cli/main.rs:1716-1834): requests arriving
+    at the current tick are submitted before it runs, an idle scheduler jumps to the next
+    arrival, and each tick's wall time is the scheduler's own ``execute_next_tick``.  Returns
+    the tick log and per-request generated tokens; ``decode_tok_s`` is generated tokens over
+    the summed decode-tick time (cli/main.rs:1502-1512, 1619-1622)."""
+    ticks, seq_of = [], []
+    nxt, tick_index = 0, 0
+    while nxt < len(requests) or sched.has_pending():
+        if max_ticks is not None and len(ticks) >= max_ticks:
+            break
+        while (nxt < len(requests) and requests[nxt]["arrival_tick"] < tick_index
+               and not sched.has_pending()):
+            tick_index = requests[nxt]["arrival_tick"]
+        while nxt < len(requests) and requests[nxt]["arrival_tick"] == tick_index:
+            r = requests[nxt]
+            seq_of.append(sched.submit(r["prompt"], max_new_tokens=r["max_new_tokens"]))
+            nxt += 1
+        rep = sched.execute_next_tick()
+        if rep is None:
+            if nxt < len(requests):
+                tick_index = requests[nxt]["arrival_tick"]
+                continue
+            break
+        kind, updates = rep
+        ticks.append(dict(tick=tick_index, kind=kind, batch=len(updates),
+                          generated=sum(u["token"] is not None for u in updates),
+                          appended=sum(u["appended"] for u in updates),
+                          reused=sum(u["reused"] for u in updates),
+                          seconds=sched.last_tick_seconds))
+        if hasattr(sched, "last_tick_profile"):
+            ticks[-1]["profile"] = sched.last_tick_profile()
+        tick_index += 1
+    dec = [t for t in ticks if t["kind"] == 1]
+    pre = [t for t in ticks if t["kind"] == 0]
+    gen = sum(t["generated"] for t in ticks)
+    dec_s = sum(t["seconds"] for t in dec)
+    pre_s = sum(t["seconds"] for t in pre)
+    return dict(ticks=ticks, sequence_ids=seq_of, generated_tokens=gen,
+                decode_ticks=len(dec), prefill_ticks=len(pre), decode_seconds=dec_s,
+                prefill_seconds=pre_s,
+                decode_tok_s=gen / dec_s if dec_s > 0 else 0.0,
+                prefill_tok_s=sum(t["appended"] for t in pre) / pre_s if pre_s > 0 else 0.0,
+                avg_decode_batch=(sum(t["batch"] for t in dec) / len(dec)) if dec else 0.0,
+                max_decode_batch=max((t["batch"] for t in dec), default=0))

@@ -82,6 +82,10 @@ int32_t fr_last_batch(void* runtime, int32_t* token_ids, int32_t* positions, int
                       int32_t* cu_seqlens, int32_t* context_lens, int32_t* block_tables,
                       int32_t* copy_src, int32_t* copy_dst, int32_t* copy_count,
                       uint64_t* sequence_ids);
+/* Host seconds of the last tick: out[4] = [scheduling + packing, enqueueing the batched
+ * forward, waiting for its samples, whole tick].  The reference times whole ticks only
+ * (cli/main.rs:1763-1767); the split shows where a tick's time goes. */
+int32_t fr_last_tick_profile(void* runtime, double* out);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 import subprocess
+import time
 
 import numpy as np
 
@@ -460,9 +461,13 @@ class Scheduler:
         return int(out.value)
 
     def execute_next_tick(self):
-        """Returns None or (kind, [update dicts])."""
+        """Returns None or (kind, [update dicts]); the native call's wall time is kept in
+        ``last_tick_seconds``."""
         ex = C.c_int32()
-        _check(lib().orc_scheduler_execute_next_tick(self.h, C.byref(ex)), True)
+        t0 = time.perf_counter()
+        status = lib().orc_scheduler_execute_next_tick(self.h, C.byref(ex))
+        self.last_tick_seconds = time.perf_counter() - t0
+        _check(status, True)
         if not ex.value:
             return None
         cap = 4096

@@ -9,9 +9,10 @@ from conftest import normwise_error
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [  # (M, K, N)
+SHAPES = [  # (M, K, N); M <= 64 with K, N multiples of 4 take the weight-streaming kernel
     (1, 7, 5), (3, 33, 65), (64, 896, 896), (64, 896, 128), (17, 4864, 896),
     (200, 256, 688), (64, 896, 4864), (130, 64, 70),
+    (1, 4, 4), (5, 100, 1152), (33, 196, 260), (48, 388, 36), (64, 4864, 9728), (7, 2052, 12),
 ]
 
 
@@ -60,7 +61,7 @@ def test_gemm_exact_on_integers(gpu_ctx):
     import torch
 
     rng = np.random.default_rng(1)
-    for m, k, n in [(64, 64, 64), (5, 20, 37), (128, 96, 80)]:
+    for m, k, n in [(64, 64, 64), (5, 20, 37), (128, 96, 80), (64, 384, 256), (3, 1000, 68)]:
         a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
         w = rng.integers(-4, 5, size=(k, n)).astype(np.float32)
         out = torch.empty((m, n), device="cuda")

@@ -146,3 +146,44 @@ def test_runtime_errors(orc):
     with pytest.raises(FerrisError) as e:
         rt2.execute_next_tick()  # 40 tokens need 3 blocks, the pool has 2
     assert e.value.kind == "Runtime"
+
+
+def test_c4_qwen2_shape_matches_reference(orc):
+    """BASELINE config C4's model (Qwen2-0.5B shape: 24 layers, H 896, 14/2 heads, D 64,
+    F 4864, V 151936, tied embeddings, q/k/v biases, theta 1e6; f32 N(0, 0.02) weights) under
+    the continuous-batching driver with Poisson arrival ticks, on a declared subset of the C4
+    workload that the CPU oracle finishes in seconds: its first 3 requests with prompts cut to
+    64 tokens and 4 new tokens each.  Tick log and greedy tokens must match the reference."""
+    from ferrisinfer_amd.runtime import Runtime
+    from ferrisinfer_amd.workloads import (QWEN2_05B_C4, c4_requests, random_weights,
+                                           run_continuous)
+
+    cfg = QWEN2_05B_C4
+    weights = random_weights(cfg, seed=0, qkv_bias=True)
+    reqs = c4_requests(seed=0)[:3]
+    for r in reqs:
+        r["prompt"] = r["prompt"][:64]
+        r["max_new_tokens"] = 4
+    model = orc.Model(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
+                      cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
+                      tie=cfg["tie"])
+    model.set_weights(weights)
+    ref = orc.Scheduler(model, max_batch=64)
+    rrep = run_continuous(ref, reqs)
+    gpu = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
+                  cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
+                  tie=True, max_batch=64, num_blocks=256, block_size=16)
+    gpu.set_weights(weights)
+    del weights
+    grep = run_continuous(gpu, reqs)
+    strip = [{k: t[k] for k in ("tick", "kind", "batch", "generated", "appended")}
+             for t in rrep["ticks"]]
+    assert strip == [{k: t[k] for k in ("tick", "kind", "batch", "generated", "appended")}
+                     for t in grep["ticks"]]
+    for seq, r in zip(rrep["sequence_ids"], reqs):
+        a, b = ref.generated(seq), gpu.generated(seq)
+        assert len(a) == len(b) == 4
+        for i, (x, y) in enumerate(zip(a, b)):
+            if x != y:
+                assert near_tie(model, list(r["prompt"]) + a[:i], None), (seq, i, x, y)
+                break
