@@ -11,59 +11,53 @@
 
 namespace {
 
-// Tunables (compile-time).  The partition size fixes the reduction order for a given context
+// Tunables (compile-time).  The wave chunk fixes the reduction order for a given context
 // length, so it is a constant of the library, not of a launch.
-#ifndef FI_DECODE_PART_TOKENS
-#define FI_DECODE_PART_TOKENS 512
+#ifndef FI_DECODE_WAVE_TOKENS
+#define FI_DECODE_WAVE_TOKENS 128  // context tokens per wave per partition
 #endif
-#ifndef FI_DECODE_KLANES_MAX
-#define FI_DECODE_KLANES_MAX 8  // lanes sharing one K row (8 or 16)
-#endif
-#ifndef FI_DECODE_VUNROLL
-#define FI_DECODE_VUNROLL 2  // V loads per lane per (double-buffered) step
+#ifndef FI_DECODE_INFLIGHT_BYTES
+#define FI_DECODE_INFLIGHT_BYTES 16384  // f32 K or V bytes each wave keeps in flight (bf16: half)
 #endif
 
-constexpr int kPartTokens = FI_DECODE_PART_TOKENS;
-constexpr int kThreads = 256;     // 4 wave64 per workgroup
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kWaveTokens = FI_DECODE_WAVE_TOKENS;
+constexpr int kPartTokens = kWaves * kWaveTokens;
 constexpr int kMaxParts = 256;    // merge weights live in LDS
 constexpr int kMaxContext = kPartTokens * kMaxParts;
 
+constexpr int clamp_int(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// 16-byte K/V vectors: the raw register form stays in flight, widening happens at use.
 template <typename KVT>
 struct KvIO;
 
 template <>
 struct KvIO<float> {
-  static constexpr int kVecElems = 4;  // one 16-byte load
-  __device__ static void load_vec(const float* p, float* out) {
-    float4 v = *reinterpret_cast<const float4*>(p);
+  using Raw = float4;
+  static constexpr int kVecElems = 4;
+  __device__ static Raw load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  __device__ static void widen(const Raw& v, float* out) {
     out[0] = v.x;
     out[1] = v.y;
     out[2] = v.z;
     out[3] = v.w;
   }
-  __device__ static void load_pair(const float* p, float* out) {
-    float2 v = *reinterpret_cast<const float2*>(p);
-    out[0] = v.x;
-    out[1] = v.y;
-  }
 };
 
 template <>
 struct KvIO<uint16_t> {
+  using Raw = uint4;
   static constexpr int kVecElems = 8;
-  __device__ static void load_vec(const uint16_t* p, float* out) {
-    uint4 v = *reinterpret_cast<const uint4*>(p);
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  __device__ static Raw load(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ static void widen(const Raw& v, float* out) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       out[2 * i] = fi::bf16_bits_to_f32(w[i] & 0xffffu);
       out[2 * i + 1] = fi::bf16_bits_to_f32(w[i] >> 16);
     }
-  }
-  __device__ static void load_pair(const uint16_t* p, float* out) {
-    uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-    out[0] = fi::bf16_bits_to_f32(w & 0xffffu);
-    out[1] = fi::bf16_bits_to_f32(w >> 16);
   }
 };
 
@@ -88,49 +82,70 @@ struct DecodeArgs {
   float scale;
 };
 
-// One workgroup = one (sequence, kv_head, partition of kPartTokens tokens).  The GQA group
-// of query heads sharing the kv head is processed together so each K/V byte is read once.
-//   setup: the partition's token -> pool row indices go to LDS once (block-table lookups);
-//   pass 1 (K): KLANES lanes share a token row with 16-byte loads; the next row-step's loads
-//     are issued before the current one is reduced (two register buffers), dot products are
-//     reduced across the row's lanes with DPP, scores go to LDS;
-//   softmax over the partition in LDS (the first V loads are already in flight);
-//   pass 2 (V): D/vec lanes cover a row with 16-byte loads, again double-buffered; per-lane
-//     accumulators are folded across rows with shuffles and across waves in LDS.
-// Rows past the partition end are clamped to its last row: they share addresses with valid
-// lanes (no extra traffic) and are masked out of the scores and weights.
-// A sequence with one partition writes its normalised output directly; otherwise each
-// workgroup stores (max, sum, unnormalised acc) for decode_merge_kernel.
-template <int D, typename KVT, int MAXG>
-__global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a) {
-  constexpr int EPV = KvIO<KVT>::kVecElems;   // elements per 16-byte vector
-  constexpr int VECS = D / EPV;               // vectors per row
-  static_assert(VECS <= 64, "a row must fit one wave of 16-byte loads");
-  constexpr int KLANES = VECS < FI_DECODE_KLANES_MAX ? VECS : FI_DECODE_KLANES_MAX;  // lanes per K row
-  constexpr int KVPL = VECS / KLANES;          // vectors per lane (K)
-  constexpr int KEPL = KVPL * EPV;             // elements per lane (K)
-  constexpr int KROWS_W = 64 / KLANES;         // K rows per wave per step
-  constexpr int KSTEP = 4 * KROWS_W;           // K rows per workgroup per step
-  constexpr int VLANES = VECS;                 // lanes per row in the V pass
-  constexpr int VROWS_W = 64 / VLANES;         // V rows per wave per load
-  constexpr int VU = FI_DECODE_VUNROLL;        // V loads per lane per step
-  constexpr int VSTEP = 4 * VROWS_W * VU;      // V rows per workgroup per step
+// Orders this wave's LDS stores before its later LDS loads by other lanes (a compiler
+// barrier only: a wave's LDS operations execute in order).
+__device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
-  __shared__ float s_q[MAXG][D];
-  __shared__ float s_p[MAXG][kPartTokens];
+// Keeps the instruction scheduler from moving code across this point, so loads issued
+// before it stay ahead of the arithmetic after it (the ring's depth is what stays in flight).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// One workgroup = one (sequence, kv_head, partition of kPartTokens tokens); partitions are
+// numbered fastest across (sequence, kv_head) so the first-dispatched workgroups hold the
+// full leading partitions and the ragged tails come last.  The GQA group of query heads
+// sharing the kv head is processed together so every K/V byte is read once.
+//   setup: the partition's token -> pool row indices go to LDS (block-table lookups) while
+//     each lane loads its slice of the group's query rows into registers;
+//   each wave then owns kWaveTokens consecutive tokens and runs on its own (no workgroup
+//   barrier until the combine):
+//     K: KL lanes share a token row with 16-byte loads, a compile-time ring keeps
+//        ~FI_DECODE_INFLIGHT_BYTES of K in flight, dot products are reduced across the
+//        row's lanes with DPP; each lane keeps the scores of its own query head;
+//     softmax over the wave's tokens in registers (the first V loads are already issued);
+//        probabilities go to the wave's LDS slice;
+//     V: VL lanes cover a row, again through a ring of in-flight loads; accumulators are
+//        folded across the wave's rows with lane shuffles;
+//   combine: the waves' (max, sum, acc) are merged through LDS in wave order.
+// Rows past the end are clamped to the last valid row (same addresses, no extra traffic)
+// and carry probability 0.  A sequence with one partition writes its normalised output;
+// otherwise each workgroup stores (max, sum, unnormalised acc) for decode_merge_kernel.
+template <int D, typename KVT, int G>
+__global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a) {
+  using IO = KvIO<KVT>;
+  using Raw = typename IO::Raw;
+  constexpr int EPV = IO::kVecElems;          // elements per 16-byte vector
+  constexpr int VECS = D / EPV;               // vectors per row
+  static_assert(VECS >= 1 && VECS <= 64 && (VECS & (VECS - 1)) == 0, "row of 16-byte vectors");
+  constexpr int KL = VECS < 8 ? VECS : 8;     // lanes per K row
+  constexpr int KV = VECS / KL;               // vectors per lane per K row
+  constexpr int KE = KV * EPV;                // elements per lane per K row
+  constexpr int KR = 64 / KL;                 // K rows per wave step
+  constexpr int KSTEPS = kWaveTokens / KR;
+  constexpr int HPL = (G + KL - 1) / KL;      // query heads whose scores a lane keeps
+  constexpr int VL = VECS;                    // lanes per V row (one vector each)
+  constexpr int VR = 64 / VL;                 // V rows per wave step
+  constexpr int VSTEPS = kWaveTokens / VR;
+  constexpr int ROWB = D * static_cast<int>(sizeof(KVT));
+  // bf16 rows carry twice the arithmetic per byte: half the bytes in flight keeps the
+  // register ring (and occupancy) the same as for f32.
+  constexpr int INFLIGHT = FI_DECODE_INFLIGHT_BYTES * static_cast<int>(sizeof(KVT)) / 4;
+  constexpr int KDEPTH = clamp_int(INFLIGHT / (KR * ROWB), 1, KSTEPS);
+  constexpr int VDEPTH = clamp_int(INFLIGHT / (VR * ROWB), 1, VSTEPS);
+  static_assert(kWaveTokens % KR == 0 && kWaveTokens % VR == 0, "wave chunk must tile the rows");
+
   __shared__ uint32_t s_row[kPartTokens];
-  __shared__ float s_ml[MAXG][2];
-  __shared__ float s_red[4][MAXG][D];
+  __shared__ float s_p[kWaves][kWaveTokens][G];
+  __shared__ float s_ml[kWaves][G][2];
+  __shared__ float s_acc[kWaves][G][D];
 
   const KVT* __restrict__ k_cache = static_cast<const KVT*>(a.k_cache);
   const KVT* __restrict__ v_cache = static_cast<const KVT*>(a.v_cache);
-  const int parts_per_seq = a.parts_per_seq;
   const int group = a.group;
-  const int wg = blockIdx.x;
-  const int part = wg % parts_per_seq;
-  const int rest = wg / parts_per_seq;
-  const int kvh = rest % a.hkv;
-  const int seq = rest / a.hkv;
+  const int units = a.num_seqs * a.hkv;
+  const int part = blockIdx.x / units;
+  const int unit = blockIdx.x - part * units;
+  const int seq = unit / a.hkv;
+  const int kvh = unit - seq * a.hkv;
   const int ctx = a.context_lens[seq];
   const int tid = threadIdx.x;
   const size_t head0 = (size_t)seq * a.hq + (size_t)kvh * group;  // first query head of the group
@@ -142,160 +157,191 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   }
   const int t0 = part * kPartTokens;
   if (t0 >= ctx) return;  // whole workgroup exits together
-  const int n = min(kPartTokens, ctx - t0);
+  const int n_part = min(kPartTokens, ctx - t0);
   const int nparts = (ctx + kPartTokens - 1) / kPartTokens;
   const int w = tid >> 6;
   const int lane = tid & 63;
+  const int wt0 = w * kWaveTokens;              // the wave's first token within the partition
+  const int n = min(kWaveTokens, n_part - wt0);  // the wave's tokens (<= 0: idle wave)
 
-  for (int i = tid; i < MAXG * D; i += kThreads) {
-    int g = i / D, d = i % D;
-    s_q[g][d] = g < group ? a.q[(head0 + g) * D + d] : 0.0f;  // zero rows keep scores of g >= group at 0
-  }
-  for (int t = tid; t < n; t += kThreads) {
+  // K-pass lane roles: row r of each step, vector column c
+  const int r = lane / KL;
+  const int c = lane % KL;
+  float qreg[G][KE];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+      float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+      if (g < group) {
+        const float* qp = a.q + (head0 + g) * D + (j * KL + c) * EPV;
+        lo = *reinterpret_cast<const float4*>(qp);
+        if constexpr (EPV == 8) hi = *reinterpret_cast<const float4*>(qp + 4);
+      }
+      float* dst = &qreg[g][j * EPV];
+      dst[0] = lo.x;
+      dst[1] = lo.y;
+      dst[2] = lo.z;
+      dst[3] = lo.w;
+      if constexpr (EPV == 8) {
+        dst[4] = hi.x;
+        dst[5] = hi.y;
+        dst[6] = hi.z;
+        dst[7] = hi.w;
+      }
+    }
+  {
     const int bs = a.block_size;
-    const int abs = t0 + t;
-    const int lb = abs / bs;
-    int id = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
-    if (id < 0 || id >= a.num_blocks) {
-      atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
-      id = 0;
-    }
-    s_row[t] = (static_cast<uint32_t>(id) * a.hkv + kvh) * bs + (abs - lb * bs);
-  }
-  __syncthreads();
-
-  // ---- pass 1: scores ----
-  {
-    const int r = lane / KLANES;
-    const int c = lane % KLANES;
-    const int ksteps = (n + KSTEP - 1) / KSTEP;
-    float qreg[MAXG][KEPL];
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-      for (int j = 0; j < KVPL; ++j)
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) qreg[g][j * EPV + e] = s_q[g][(j * KLANES + c) * EPV + e];
-
-    auto load_k = [&](int step, float* buf) {
-      const int tok = min(step * KSTEP + w * KROWS_W + r, n - 1);
-      const KVT* row = k_cache + (size_t)s_row[tok] * D;
-#pragma unroll
-      for (int j = 0; j < KVPL; ++j) KvIO<KVT>::load_vec(row + (j * KLANES + c) * EPV, buf + j * EPV);
-    };
-    auto score_k = [&](int step, const float* buf) {
-      const int tok = step * KSTEP + w * KROWS_W + r;
-#pragma unroll
-      for (int g = 0; g < MAXG; ++g) {
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < KEPL; ++e) dot += qreg[g][e] * buf[e];
-        dot = fi::group_sum<KLANES>(dot);
-        if (g % KLANES == c && tok < n) s_p[g][tok] = dot * a.scale;
+    for (int t = tid; t < n_part; t += kThreads) {
+      const int pos = t0 + t;
+      const int lb = pos / bs;
+      int id = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
+      if (id < 0 || id >= a.num_blocks) {
+        atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
+        id = 0;
       }
-    };
-    float kb0[KEPL], kb1[KEPL];
-    load_k(0, kb0);
-    for (int step = 0; step < ksteps; step += 2) {
-      if (step + 1 < ksteps) load_k(step + 1, kb1);
-      score_k(step, kb0);
-      if (step + 1 < ksteps) {
-        if (step + 2 < ksteps) load_k(step + 2, kb0);
-        score_k(step + 1, kb1);
-      }
-    }
-  }
-
-  // ---- pass 2 prologue: first V loads go out before the softmax ----
-  const int vr = lane / VLANES;
-  const int vc = lane % VLANES;
-  const int vsteps = (n + VSTEP - 1) / VSTEP;
-  auto load_v = [&](int step, float (*buf)[EPV]) {
-#pragma unroll
-    for (int u = 0; u < VU; ++u) {
-      const int tok = min(step * VSTEP + (u * 4 + w) * VROWS_W + vr, n - 1);
-      KvIO<KVT>::load_vec(v_cache + (size_t)s_row[tok] * D + vc * EPV, buf[u]);
-    }
-  };
-  float vb0[VU][EPV], vb1[VU][EPV];
-  load_v(0, vb0);
-  __syncthreads();
-
-  // ---- softmax over the partition ----
-  for (int g = w; g < group; g += 4) {
-    float m = -INFINITY;
-    for (int t = lane; t < n; t += 64) m = fmaxf(m, s_p[g][t]);
-    m = fi::wave_max(m);
-    float l = 0.0f;
-    for (int t = lane; t < n; t += 64) {
-      float p = __expf(s_p[g][t] - m);
-      s_p[g][t] = p;
-      l += p;
-    }
-    l = fi::wave_sum(l);
-    if (lane == 0) {
-      s_ml[g][0] = m;
-      s_ml[g][1] = l;
+      s_row[t] = (static_cast<uint32_t>(id) * a.hkv + kvh) * bs + (pos - lb * bs);
     }
   }
   __syncthreads();
 
-  // ---- pass 2: weighted values ----
-  {
-    float acc[MAXG][EPV];
+  if (n > 0) {  // wave-uniform
+    const uint32_t* rows = s_row + wt0;
+    // ---- K: scores of this lane's rows for its query heads (h * KL + c) ----
+    float sc[KSTEPS][HPL];
+    {
+      Raw kb[KDEPTH][KV];
+      auto issue_k = [&](int s, Raw (&buf)[KV]) {
+        const KVT* p = k_cache + (size_t)rows[min(s * KR + r, n - 1)] * D + c * EPV;
 #pragma unroll
-    for (int g = 0; g < MAXG; ++g)
+        for (int j = 0; j < KV; ++j) buf[j] = IO::load(p + j * KL * EPV);
+      };
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) acc[g][e] = 0.0f;
-    auto accumulate = [&](int step, float (*buf)[EPV]) {
+      for (int s = 0; s < KDEPTH; ++s) issue_k(s, kb[s]);
+      sched_fence();
 #pragma unroll
-      for (int u = 0; u < VU; ++u) {
-        const int tok = step * VSTEP + (u * 4 + w) * VROWS_W + vr;
-        const bool valid = tok < n;
-        const int tt = valid ? tok : 0;
+      for (int s = 0; s < KSTEPS; ++s) {
+        float kf[KE];
 #pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-          const float p = valid ? s_p[g][tt] : 0.0f;
+        for (int j = 0; j < KV; ++j) IO::widen(kb[s % KDEPTH][j], kf + j * EPV);
+        if (s + KDEPTH < KSTEPS) issue_k(s + KDEPTH, kb[s % KDEPTH]);
+        sched_fence();
+        float dot[G];
 #pragma unroll
-          for (int e = 0; e < EPV; ++e) acc[g][e] += p * buf[u][e];
+        for (int g = 0; g < G; ++g) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int e = 0; e < KE; ++e) acc += qreg[g][e] * kf[e];
+          dot[g] = fi::group_sum<KL>(acc);
+        }
+        const bool valid = s * KR + r < n;
+#pragma unroll
+        for (int h = 0; h < HPL; ++h) {
+          float v = dot[h * KL];
+#pragma unroll
+          for (int cc = 1; cc < KL; ++cc)
+            if (h * KL + cc < G) v = c == cc ? dot[h * KL + cc] : v;
+          sc[s][h] = valid ? v * a.scale : -INFINITY;
         }
       }
+    }
+
+    // ---- first V loads go out before the softmax ----
+    const int vr = lane / VL;
+    const int vc = lane % VL;
+    Raw vb[VDEPTH];
+    auto issue_v = [&](int s) {
+      vb[s % VDEPTH] = IO::load(v_cache + (size_t)rows[min(s * VR + vr, n - 1)] * D + vc * EPV);
     };
-    for (int step = 0; step < vsteps; step += 2) {
-      if (step + 1 < vsteps) load_v(step + 1, vb1);
-      accumulate(step, vb0);
-      if (step + 1 < vsteps) {
-        if (step + 2 < vsteps) load_v(step + 2, vb0);
-        accumulate(step + 1, vb1);
+#pragma unroll
+    for (int s = 0; s < VDEPTH; ++s) issue_v(s);
+    sched_fence();
+
+    // ---- softmax over the wave's tokens (lanes sharing c hold one head's scores) ----
+#pragma unroll
+    for (int h = 0; h < HPL; ++h) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) m = fmaxf(m, sc[s][h]);
+#pragma unroll
+      for (int x = KL; x < 64; x <<= 1) m = fmaxf(m, __shfl_xor(m, x, 64));
+      float l = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const float p = sc[s][h] == -INFINITY ? 0.0f : __expf(sc[s][h] - m);
+        sc[s][h] = p;
+        l += p;
+      }
+#pragma unroll
+      for (int x = KL; x < 64; x <<= 1) l += __shfl_xor(l, x, 64);
+      const int g = h * KL + c;
+      if (g < G) {
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) s_p[w][s * KR + r][g] = sc[s][h];
+        if (r == 0) {
+          s_ml[w][g][0] = m;
+          s_ml[w][g][1] = l;
+        }
       }
     }
-    // rows of a wave share columns: fold them with lane shuffles, then waves through LDS
+    wave_lds_sync();
+
+    // ---- V: acc[g][e] = sum_t p[t][g] * V[t][vc * EPV + e] ----
+    float acc[G][EPV];
 #pragma unroll
-    for (int m = VLANES; m < 64; m <<= 1)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int g = 0; g < MAXG; ++g)
+      for (int e = 0; e < EPV; ++e) acc[g][e] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) acc[g][e] += __shfl_xor(acc[g][e], m, 64);
+    for (int s = 0; s < VSTEPS; ++s) {
+      float vf[EPV];
+      IO::widen(vb[s % VDEPTH], vf);
+      if (s + VDEPTH < VSTEPS) issue_v(s + VDEPTH);
+      sched_fence();
+      const float* pp = s_p[w][s * VR + vr];
+      float p[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) p[g] = pp[g];
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[g][e] += p[g] * vf[e];
+    }
+#pragma unroll
+    for (int x = VL; x < 64; x <<= 1)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[g][e] += __shfl_xor(acc[g][e], x, 64);
     if (vr == 0) {
 #pragma unroll
-      for (int g = 0; g < MAXG; ++g)
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) s_red[w][g][vc * EPV + e] = acc[g][e];
+        for (int e = 0; e < EPV; ++e) s_acc[w][g][vc * EPV + e] = acc[g][e];
     }
   }
   __syncthreads();
 
+  // ---- combine the waves (in wave order) ----
+  const int nw = (n_part + kWaveTokens - 1) / kWaveTokens;
   for (int i = tid; i < group * D; i += kThreads) {
-    int g = i / D, d = i % D;
-    float sum = (s_red[0][g][d] + s_red[1][g][d]) + (s_red[2][g][d] + s_red[3][g][d]);
+    const int g = i / D, d = i - (i / D) * D;
+    float mx = s_ml[0][g][0];
+    for (int v = 1; v < nw; ++v) mx = fmaxf(mx, s_ml[v][g][0]);
+    float l = 0.0f, sum = 0.0f;
+    for (int v = 0; v < nw; ++v) {
+      const float wgt = __expf(s_ml[v][g][0] - mx);
+      l += s_ml[v][g][1] * wgt;
+      sum += s_acc[v][g][d] * wgt;
+    }
     if (nparts == 1) {
-      a.out[(head0 + g) * D + d] = sum * (1.0f / s_ml[g][1]);
+      a.out[(head0 + g) * D + d] = sum * (1.0f / l);
     } else {
-      size_t slot = (head0 + g) * parts_per_seq + part;
+      const size_t slot = (head0 + g) * a.parts_per_seq + part;
       a.part_acc[slot * D + d] = sum;
       if (d == 0) {
-        a.part_ml[slot * 2] = s_ml[g][0];
-        a.part_ml[slot * 2 + 1] = s_ml[g][1];
+        a.part_ml[slot * 2] = mx;
+        a.part_ml[slot * 2 + 1] = l;
       }
     }
   }
