@@ -21,6 +21,7 @@ SOURCES = [
     "fi_prefill.hip",
     "fi_ops.hip",
     "fi_gemm.hip",
+    "fi_gemm_packed.hip",
 ]
 
 # gfx950 only; packed-fp32 instructions are disabled (the compiler would otherwise form

@@ -44,6 +44,10 @@ int32_t ensure_workspace(fi_context* ctx, size_t bytes);
 int32_t decode_scratch(fi_context* ctx, int32_t num_seqs, int32_t hq, int32_t parts, int32_t head_dim,
                        float** part_acc, float** part_ml);
 
+// Reduces per-tile greedy-head states [m, n_tiles, 3] (max, index bits, scaled sum) to the
+// first maximal index and 1 / sum per row.
+int32_t argmax_merge(fi_context* ctx, const float* amax, int32_t n_tiles, int32_t m, int32_t* token, float* prob);
+
 }  // namespace fi
 
 #define FI_TRY_HIP(call)                                 \

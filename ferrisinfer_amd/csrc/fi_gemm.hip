@@ -341,6 +341,20 @@ __global__ __launch_bounds__(kMergeThreads) void argmax_merge_kernel(const float
   }
 }
 
+}  // namespace
+
+namespace fi {
+
+int32_t argmax_merge(fi_context* ctx, const float* amax, int32_t n_tiles, int32_t m, int32_t* token, float* prob) {
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3(m), dim3(kMergeThreads), 0, ctx->stream, amax, n_tiles, m, token, prob);
+  FI_CHECK_LAUNCH("argmax_merge_kernel");
+  return FI_OK;
+}
+
+}  // namespace fi
+
+namespace {
+
 // K range per split: enough workgroups (>= 2 per CU) for skinny shapes to keep every CU
 // streaming weights, in whole stages of the kernel's K depth.
 int choose_k_chunk(fi_context* ctx, int m, int n, int k, int bk) {

@@ -1,0 +1,696 @@
+// Weight-streaming projection GEMMs on MFMA (v_mfma_f32_16x16x4_f32) over weights re-laid
+// out once at upload, plus the kernels that consume their split-K partials.  Replaces the
+// decoder block's matmul_f32 / linear_f32_with_bias calls and the elementwise ops around
+// them (kernel/cpu/matmul.rs:46-118, 190-274; runtime/reference.rs:163-370, 712-871,
+// 1103-1191; kernel/cpu/elementwise.rs:48-207; kernel/cpu/reduction.rs:3-73).
+//
+// Packed weight layout.  A weight B [K, N] (the reference's [in, out]) is cut into slabs of
+// 16*PW output columns; each slab stores its K rows (zero-padded to a multiple of 16) in
+// MFMA-fragment order so that one wave reads each 16-row step as four 64*PW-float runs:
+//   packed[((slab * Q + q) * 4 + e) * 64 * PW + lane * PW + p]
+//     = B[16q + 4*(lane/16) + e][slab * 16 * PW + PW * (lane % 16) + p]
+// (Q = ceil(K/16); zero outside [0,K) x [0,N)).  Lane (j, kk) = (lane % 16, lane / 16) loads
+// its PW-vector for step e with one load; element p is the B operand of N-tile p, so tile p's
+// column j is output column slab*16*PW + PW*j + p and a lane finally holds PW adjacent
+// outputs of a row (one vector store).  The A operand is read straight from the row-major
+// activations: lane (i, kk) loads A[row i][16q + 4kk .. +3] and feeds element e to step e,
+// the same k order the packed B uses.
+//
+// Kernel shape: a workgroup of 4 waves owns one (16*MT)-row x (16*PW)-column output tile
+// and a range of K steps; each wave takes a contiguous quarter of the range, keeps a ring of
+// in-flight loads (no LDS, no barrier in the main loop), and the quarters are summed through
+// LDS in wave order.  Workgroups along z split K further; their partials are summed by the
+// consumer kernels in split order.  Every summation order is fixed by the shape, so results
+// are deterministic and independent of the batch composition of other rows.
+#include <algorithm>
+
+#include "fi_common.h"
+#include "fi_device.h"
+
+extern "C" int32_t fi_weight_packed_floats(int32_t k, int32_t n, int32_t pack_width, size_t* floats);
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+template <int PW>
+struct PVec;
+template <>
+struct PVec<1> {
+  using T = float;
+  __device__ static float get(const T& v, int) { return v; }
+};
+template <>
+struct PVec<2> {
+  using T = float2;
+  __device__ static float get(const T& v, int p) { return p == 0 ? v.x : v.y; }
+};
+template <>
+struct PVec<4> {
+  using T = float4;
+  __device__ static float get(const T& v, int p) { return p == 0 ? v.x : (p == 1 ? v.y : (p == 2 ? v.z : v.w)); }
+};
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+enum Epi : int { kEpiPartial = 0, kEpiSwiglu = 1, kEpiArgmax = 2 };
+
+struct PGemmArgs {
+  const float* a;       // [M, lda]
+  const float* bp;      // packed weight
+  float* out;           // partial: [splits, M, N]; swiglu: [M, N]; argmax: [M, slabs, 3]
+  const float* bias0;   // swiglu: bias of the first (up) weight, may be null
+  const float* bias1;   // swiglu: bias of the second (gate) weight, may be null
+  int m, k, n, lda;
+  int q_total;          // ceil(K / 16)
+  int q_per_split;      // K steps per workgroup (z)
+  int slabs;
+};
+
+// A rows are clamped to M-1 (their outputs are never stored).  With K a multiple of 16 every
+// step is a plain 16-byte load; otherwise (KTAIL) each element is loaded from a clamped,
+// always-valid address and zeroed past the row end with a select, so there is no divergent
+// branch (a branch here would force the compiler to drain the load ring).
+template <bool KTAIL>
+__device__ __forceinline__ float4 load_a(const float* row, int k0, int k) {
+  if constexpr (!KTAIL) {
+    return *reinterpret_cast<const float4*>(row + k0);
+  } else {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = row[min(k0 + i, k - 1)];
+      v[i] = k0 + i < k ? x : 0.0f;
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+#ifndef FI_PGEMM_MIN_WAVES
+#define FI_PGEMM_MIN_WAVES 2  // waves per SIMD the register budget must allow
+#endif
+#ifndef FI_PGEMM_RING_REGS
+#define FI_PGEMM_RING_REGS 64  // VGPRs the ring of in-flight loads may hold
+#endif
+
+template <int MT, int PW, int EPI, bool KTAIL>
+__global__ __launch_bounds__(kThreads, FI_PGEMM_MIN_WAVES) void gemm_packed_kernel(PGemmArgs g) {
+  using BV = typename PVec<PW>::T;
+  constexpr int STEP_REGS = 4 * MT + 4 * PW;  // VGPRs one K step of loads occupies
+  constexpr int DEPTH = FI_PGEMM_RING_REGS / STEP_REGS < 2 ? 2 : (FI_PGEMM_RING_REGS / STEP_REGS > 8 ? 8 : FI_PGEMM_RING_REGS / STEP_REGS);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  const int slab = blockIdx.x, mblk = blockIdx.y, z = blockIdx.z;
+  const int m0 = mblk * 16 * MT;
+
+  // this wave's K steps: a contiguous quarter of the workgroup's range
+  const int wq0 = z * g.q_per_split;
+  const int wq1 = min(g.q_total, wq0 + g.q_per_split);
+  const int per = (wq1 - wq0 + kWaves - 1) / kWaves;
+  const int q_beg = min(wq1, wq0 + w * per);
+  const int q_end = min(wq1, q_beg + per);
+
+  const float* arow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) arow[mt] = g.a + (size_t)min(m0 + 16 * mt + li, g.m - 1) * g.lda + 4 * lk;
+  const BV* bbase = reinterpret_cast<const BV*>(g.bp) + (size_t)slab * g.q_total * 4 * 64 + lane;
+
+  v4f acc[MT][PW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int p = 0; p < PW; ++p) acc[mt][p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (q_beg < q_end) {  // wave-uniform
+    // Ring of R = DEPTH + 1 slots: step s lives in slot (s - q_beg) % R.  Before step s is
+    // multiplied, the loads of step s + DEPTH go into the slot step s - 1 has released, so
+    // DEPTH steps stay in flight while the MFMAs of step s run.
+    constexpr int R = DEPTH + 1;
+    float4 ra[R][MT];
+    BV rb[R][4];
+    auto issue = [&](int q, int slot) {
+      q = min(q, q_end - 1);  // clamped refetches hit the cache: no extra HBM traffic
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) ra[slot][mt] = load_a<KTAIL>(arow[mt], 16 * q, g.k - 4 * lk);
+      const BV* bq = bbase + (size_t)q * 4 * 64;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rb[slot][e] = bq[e * 64];
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(q_beg + d, d);
+    for (int q = q_beg; q < q_end; q += R) {
+#pragma unroll
+      for (int d = 0; d < R; ++d) {
+        issue(q + d + DEPTH, (d + DEPTH) % R);
+        sched_fence();
+        if (q + d < q_end) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const float av = e == 0 ? ra[d][mt].x : (e == 1 ? ra[d][mt].y : (e == 2 ? ra[d][mt].z : ra[d][mt].w));
+#pragma unroll
+              for (int p = 0; p < PW; ++p)
+                acc[mt][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, PVec<PW>::get(rb[d][e], p), acc[mt][p], 0, 0, 0);
+            }
+        }
+        sched_fence();
+      }
+    }
+  }
+
+  // ---- sum the four K quarters in wave order through LDS ----
+  __shared__ v4f s_part[kWaves - 1][MT * PW][64];
+  if (w > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < PW; ++p) s_part[w - 1][mt * PW + p][lane] = acc[mt][p];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int src = 0; src < kWaves - 1; ++src)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < PW; ++p) acc[mt][p] += s_part[src][mt * PW + p][lane];
+
+  // acc[mt][p][v] = C[m0 + 16mt + 4lk + v][slab*16*PW + PW*li + p]
+  const int col0 = slab * 16 * PW + PW * li;
+  if constexpr (EPI == kEpiPartial) {
+    float* out = g.out + (size_t)z * g.m * g.n;
+    const bool vec = col0 + PW <= g.n && (g.n % PW) == 0;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + 16 * mt + 4 * lk + v;
+        if (row >= g.m) continue;
+        float* dst = out + (size_t)row * g.n + col0;
+        if (vec) {
+          if constexpr (PW == 4) {
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[mt][0][v], acc[mt][1][v], acc[mt][2][v], acc[mt][3][v]);
+          } else if constexpr (PW == 2) {
+            *reinterpret_cast<float2*>(dst) = make_float2(acc[mt][0][v], acc[mt][1][v]);
+          } else {
+            dst[0] = acc[mt][0][v];
+          }
+        } else {
+#pragma unroll
+          for (int p = 0; p < PW; ++p)
+            if (col0 + p < g.n) dst[p] = acc[mt][p][v];
+        }
+      }
+  } else if constexpr (EPI == kEpiSwiglu) {
+    // pair pack: p = 0 is the up projection (w1), p = 1 the gate (w3) of output column c.
+    // elementwise.rs:118-207 as used at reference.rs:346-360: gate <- gate * (1 / (1 +
+    // exp(-gate))); up <- up * gate.
+    static_assert(PW == 2, "SwiGLU epilogue needs the pair pack");
+    const int c = slab * 16 + li;
+    if (c < g.n) {
+      const float b0 = g.bias0 ? g.bias0[c] : 0.0f;
+      const float b1 = g.bias1 ? g.bias1[c] : 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = m0 + 16 * mt + 4 * lk + v;
+          if (row >= g.m) continue;
+          const float up = g.bias0 ? acc[mt][0][v] + b0 : acc[mt][0][v];
+          float gate = g.bias1 ? acc[mt][1][v] + b1 : acc[mt][1][v];
+          gate = gate * (1.0f / (1.0f + __expf(-gate)));
+          g.out[(size_t)row * g.n + c] = up * gate;
+        }
+    }
+  } else {
+    // Greedy head: per row, the slab's (max, first index of the max, sum of exp(x - max))
+    // over its columns in index order (strict > keeps the first maximum, matmul.rs:532-589);
+    // lanes are combined left to right so ties keep the smaller index.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + 16 * mt + 4 * lk + v;
+        float mx = -INFINITY, sum = 0.0f;
+        int best = -1;
+#pragma unroll
+        for (int p = 0; p < PW; ++p) {
+          const int col = col0 + p;
+          if (col >= g.n) break;
+          const float x = acc[mt][p][v];
+          if (best < 0) {
+            mx = x;
+            sum = 1.0f;
+            best = col;
+          } else if (x > mx) {
+            sum = sum * __expf(mx - x) + 1.0f;
+            mx = x;
+            best = col;
+          } else {
+            sum += __expf(x - mx);
+          }
+        }
+        // combine the 16 lanes li = 0..15 of this row (same lk): lower lanes hold lower columns
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+          const float omx = __shfl_xor(mx, off, 64);
+          const float osum = __shfl_xor(sum, off, 64);
+          const int obest = __shfl_xor(best, off, 64);
+          if (obest >= 0) {
+            if (best < 0) {
+              mx = omx;
+              sum = osum;
+              best = obest;
+            } else if (omx > mx || (omx == mx && obest < best)) {
+              sum = osum + sum * __expf(mx - omx);
+              mx = omx;
+              best = obest;
+            } else {
+              sum = sum + osum * __expf(omx - mx);
+            }
+          }
+        }
+        if (li == 0 && row < g.m) {
+          float* dst = g.out + ((size_t)row * g.slabs + slab) * 3;
+          dst[0] = mx;
+          reinterpret_cast<int*>(dst)[1] = best;
+          dst[2] = sum;
+        }
+      }
+  }
+}
+
+// Up to three source matrices; in column mode they are concatenated along N.
+struct PackSources {
+  const float* src[3];
+  int n[3];     // columns of each source
+  int count;
+};
+
+// One thread per packed float.  Column mode (pair == 0): the packed matrix is the column
+// concatenation of the sources, each [K, n_i] (src_layout 0) or [n_i, K] (src_layout 1).
+// Pair mode (PW = 2): source 0 supplies element p = 0 and source 1 element p = 1 of every
+// lane vector, both [K, n] with n = n[0].
+__global__ void weight_pack_kernel(PackSources s, int pair, int src_layout, int k, int n, int pw, int q_total,
+                                   size_t total, float* __restrict__ dst) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const int slab_cols = pair ? 16 : 16 * pw;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int p = static_cast<int>(i % pw);
+    size_t r = i / pw;
+    const int lane = static_cast<int>(r % 64);
+    r /= 64;
+    const int e = static_cast<int>(r % 4);
+    r /= 4;
+    const int q = static_cast<int>(r % q_total);
+    const int slab = static_cast<int>(r / q_total);
+    const int kk = 16 * q + 4 * (lane / 16) + e;
+    const float* src = s.src[0];
+    int col, ncols;
+    if (pair) {
+      col = slab * slab_cols + (lane % 16);
+      src = s.src[p];
+      ncols = s.n[0];
+    } else {
+      col = slab * slab_cols + pw * (lane % 16) + p;
+      int j = 0;
+      while (j + 1 < s.count && col >= s.n[j]) {
+        col -= s.n[j];
+        ++j;
+      }
+      src = s.src[j];
+      ncols = s.n[j];
+    }
+    float v = 0.0f;
+    if (kk < k && col < ncols) v = src_layout == 0 ? src[(size_t)kk * ncols + col] : src[(size_t)col * k + kk];
+    dst[i] = v;
+  }
+}
+
+int32_t launch_pack(fi_context* ctx, const PackSources& s, int pair, int src_layout, int k, int n, int pw,
+                    float* dst) {
+  size_t total = 0;
+  FI_TRY(fi_weight_packed_floats(k, pair ? 2 * n : n, pw, &total));
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 65536));
+  hipLaunchKernelGGL(weight_pack_kernel, dim3(blocks), dim3(256), 0, ctx->stream, s, pair, src_layout, k, n, pw,
+                     (k + 15) / 16, total, dst);
+  FI_CHECK_LAUNCH("weight_pack_kernel");
+  return FI_OK;
+}
+
+// ---- consumers of split-K partials ----
+
+// One workgroup per row: h = sum_z parts[z][row] (+ bias) + residual -> sum_out; out =
+// rms_norm(h) * w (reduction.rs:3-73: ms = sum(x^2)/H, inv = 1/sqrt(ms + eps), (x*inv)*w).
+constexpr int kRowThreads = 256;
+__global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
+    const float* __restrict__ parts, int splits, const float* __restrict__ bias, const float* __restrict__ residual,
+    float* __restrict__ sum_out, const float* __restrict__ weight, float* __restrict__ out, int rows, int hidden,
+    float eps) {
+  __shared__ float s_red[kRowThreads / 64];
+  const int row = blockIdx.x;
+  const size_t plane = (size_t)rows * hidden;
+  const float* p0 = parts + (size_t)row * hidden;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
+    float x = p0[c];
+    for (int z = 1; z < splits; ++z) x += p0[z * plane + c];
+    if (bias) x = x + bias[c];
+    x = x + residual[(size_t)row * hidden + c];
+    sum_out[(size_t)row * hidden + c] = x;
+    ss += x * x;
+  }
+  ss = fi::wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kRowThreads / 64; ++i) total += s_red[i];
+  const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+  for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
+    const float x = sum_out[(size_t)row * hidden + c];
+    out[(size_t)row * hidden + c] = (x * inv) * weight[c];
+  }
+}
+
+// One workgroup per token: the QKV projection's split partials (+ biases) -> RoPE on q and k
+// at the token's position -> q to q_out, k and v appended to the pool slot (the reference
+// order: rope before attention, KV written for this chunk, reference.rs:163-370).  Columns
+// of the fused projection: [0, Hq*D) q, then Hkv*D of k, then Hkv*D of v.
+template <typename KVT>
+__global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
+    const float* __restrict__ parts, int splits, const float* __restrict__ bias_q, const float* __restrict__ bias_k,
+    const float* __restrict__ bias_v, const int* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rotary_dims, int max_positions,
+    const int64_t* __restrict__ slots, KVT* __restrict__ k_cache, KVT* __restrict__ v_cache, int64_t pool_slots,
+    int block_size, int tokens, int hq, int hkv, int d, float* __restrict__ q_out, uint32_t* __restrict__ faults) {
+  const int t = blockIdx.x;
+  const int width = (hq + 2 * hkv) * d;
+  const size_t plane = (size_t)tokens * width;
+  const float* p0 = parts + (size_t)t * width;
+  const int qw = hq * d, kw = hkv * d;
+  auto value = [&](int col) {
+    float x = p0[col];
+    for (int z = 1; z < splits; ++z) x += p0[z * plane + col];
+    const float* b = col < qw ? bias_q : (col < qw + kw ? bias_k : bias_v);
+    const int bc = col < qw ? col : (col < qw + kw ? col - qw : col - qw - kw);
+    return b ? x + b[bc] : x;
+  };
+  int pos = positions[t];
+  const int half = rotary_dims / 2;
+  if (half > 0 && (pos < 0 || pos >= max_positions)) {
+    if (threadIdx.x == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+    pos = 0;
+  }
+  const int64_t slot = slots[t];
+  const bool write_kv = slot >= 0 && slot < pool_slots;
+  if (slot >= pool_slots && threadIdx.x == 0) atomicOr(faults, FI_FAULT_SLOT_RANGE);
+  const int64_t blk = write_kv ? slot / block_size : 0;
+  const int off = write_kv ? static_cast<int>(slot % block_size) : 0;
+  // q and k heads: rotate pairs (i, i + half) for i < half, copy the rest
+  const int rot_heads = hq + hkv;
+  for (int idx = threadIdx.x; idx < rot_heads * d; idx += kRowThreads) {
+    const int head = idx / d, i = idx - head * d;
+    const int col = head < hq ? head * d + i : hq * d + (head - hq) * d + i;
+    float outv;
+    if (i < half) {
+#pragma clang fp contract(off)
+      const float lo = value(col), hi = value(col + half);
+      const float c = cos_t[(size_t)pos * half + i], s = sin_t[(size_t)pos * half + i];
+      outv = lo * c - hi * s;  // each product rounded before the difference, as Rust does
+    } else if (i < 2 * half) {
+#pragma clang fp contract(off)
+      const int j = i - half;
+      const float lo = value(col - half), hi = value(col);
+      const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
+      outv = hi * c + lo * s;
+    } else {
+      outv = value(col);
+    }
+    if (head < hq) {
+      q_out[(size_t)t * hq * d + col] = outv;
+    } else if (write_kv) {
+      const size_t dst = (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i;
+      if constexpr (sizeof(KVT) == 4) {
+        k_cache[dst] = outv;
+      } else {
+        k_cache[dst] = static_cast<KVT>(fi::f32_to_bf16_bits(outv));
+      }
+    }
+  }
+  if (write_kv) {
+    for (int idx = threadIdx.x; idx < hkv * d; idx += kRowThreads) {
+      const int h = idx / d, i = idx - h * d;
+      const float x = value((hq + hkv) * d + idx);
+      const size_t dst = (((size_t)blk * hkv + h) * block_size + off) * d + i;
+      if constexpr (sizeof(KVT) == 4) {
+        v_cache[dst] = x;
+      } else {
+        v_cache[dst] = static_cast<KVT>(fi::f32_to_bf16_bits(x));
+      }
+    }
+  }
+}
+
+int32_t q_steps(int32_t k) { return (k + 15) / 16; }
+
+int32_t slabs_of(int32_t n, int32_t pw, bool pair) { return pair ? (n + 15) / 16 : (n + 16 * pw - 1) / (16 * pw); }
+
+template <int PW, int EPI>
+int32_t launch_pgemm(fi_context* ctx, const PGemmArgs& g, int splits) {
+  const int mt = g.m <= 16 ? 1 : (g.m <= 32 ? 2 : 4);
+  const unsigned mblocks = static_cast<unsigned>((g.m + 16 * mt - 1) / (16 * mt));
+  dim3 grid(static_cast<unsigned>(g.slabs), mblocks, static_cast<unsigned>(splits));
+  const bool tail = g.k % 16 != 0;
+  switch (mt * 2 + (tail ? 1 : 0)) {
+    case 2:
+      hipLaunchKernelGGL((gemm_packed_kernel<1, PW, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+      break;
+    case 3:
+      hipLaunchKernelGGL((gemm_packed_kernel<1, PW, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gemm_packed_kernel<2, PW, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+      break;
+    case 5:
+      hipLaunchKernelGGL((gemm_packed_kernel<2, PW, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+      break;
+    case 8:
+      hipLaunchKernelGGL((gemm_packed_kernel<4, PW, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_packed_kernel<4, PW, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+      break;
+  }
+  FI_CHECK_LAUNCH("gemm_packed_kernel");
+  return FI_OK;
+}
+
+int32_t check_common(fi_context* ctx, const float* a, int32_t lda, const float* bp, int32_t m, int32_t k, int32_t n) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(m >= 0 && k > 0 && n > 0, FI_ERR_INVALID_SHAPE, "packed gemm: k and n must be positive");
+  FI_REQUIRE(lda >= k && lda % 4 == 0, FI_ERR_INVALID_LAYOUT, "packed gemm: lda must be >= k and a multiple of 4");
+  FI_REQUIRE(m == 0 || (a && bp), FI_ERR_INVALID_CONFIG, "packed gemm: null pointer");
+  FI_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(bp) & 15) == 0,
+             FI_ERR_INVALID_LAYOUT, "packed gemm: operands must be 16-byte aligned");
+  return FI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fi_weight_packed_floats(int32_t k, int32_t n, int32_t pack_width, size_t* floats) {
+  FI_REQUIRE(k > 0 && n > 0, FI_ERR_INVALID_SHAPE, "fi_weight_packed_floats: k and n must be positive");
+  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
+             "fi_weight_packed_floats: pack width must be 1, 2 or 4");
+  FI_REQUIRE(floats != nullptr, FI_ERR_INVALID_CONFIG, "fi_weight_packed_floats: null output");
+  *floats = static_cast<size_t>(slabs_of(n, pack_width, false)) * q_steps(k) * 4 * 64 * pack_width;
+  return FI_OK;
+}
+
+int32_t fi_weight_pack(fi_context* ctx, const float* d_src, int32_t src_layout, int32_t k, int32_t n,
+                       int32_t pack_width, float* d_dst) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(src_layout == 0 || src_layout == 1, FI_ERR_INVALID_LAYOUT, "fi_weight_pack: src_layout must be 0 or 1");
+  size_t total = 0;
+  FI_TRY(fi_weight_packed_floats(k, n, pack_width, &total));
+  FI_REQUIRE(d_src && d_dst, FI_ERR_INVALID_CONFIG, "fi_weight_pack: null pointer");
+  PackSources s{{d_src, nullptr, nullptr}, {n, 0, 0}, 1};
+  return launch_pack(ctx, s, 0, src_layout, k, n, pack_width, d_dst);
+}
+
+int32_t fi_weight_pack_columns(fi_context* ctx, const float* const* d_srcs, const int32_t* ns, int32_t count,
+                               int32_t k, int32_t pack_width, float* d_dst) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(count >= 1 && count <= 3, FI_ERR_INVALID_CONFIG, "fi_weight_pack_columns: 1 to 3 sources");
+  FI_REQUIRE(d_srcs && ns && d_dst, FI_ERR_INVALID_CONFIG, "fi_weight_pack_columns: null pointer");
+  PackSources s{{nullptr, nullptr, nullptr}, {0, 0, 0}, count};
+  int32_t n = 0;
+  for (int i = 0; i < count; ++i) {
+    FI_REQUIRE(d_srcs[i] && ns[i] > 0, FI_ERR_INVALID_CONFIG, "fi_weight_pack_columns: empty source");
+    s.src[i] = d_srcs[i];
+    s.n[i] = ns[i];
+    n += ns[i];
+  }
+  return launch_pack(ctx, s, 0, 0, k, n, pack_width, d_dst);
+}
+
+int32_t fi_weight_pack_pair(fi_context* ctx, const float* d_first, const float* d_second, int32_t k, int32_t n,
+                            float* d_dst) {
+  FI_TRY(fi::enter(ctx));
+  size_t total = 0;
+  FI_TRY(fi_weight_packed_floats(k, 2 * n, 2, &total));
+  FI_REQUIRE(d_first && d_second && d_dst, FI_ERR_INVALID_CONFIG, "fi_weight_pack_pair: null pointer");
+  PackSources s{{d_first, d_second, nullptr}, {n, n, 0}, 2};
+  return launch_pack(ctx, s, 1, 0, k, n, 2, d_dst);
+}
+
+int32_t fi_gemm_packed_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, int32_t pack_width,
+                              int32_t* splits) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(m >= 0 && k > 0 && n > 0, FI_ERR_INVALID_SHAPE, "fi_gemm_packed_splits: bad shape");
+  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
+             "fi_gemm_packed_splits: pack width must be 1, 2 or 4");
+  FI_REQUIRE(splits != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_packed_splits: null output");
+  // enough workgroups for two per CU, each wave keeping at least 4 K steps
+  const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  const long tiles = static_cast<long>(slabs_of(n, pack_width, false)) * std::max(1, (m + 16 * mt - 1) / (16 * mt));
+  const long target = 2L * (ctx->compute_units > 0 ? ctx->compute_units : 256);
+  int s = static_cast<int>(std::max(1L, (target + tiles - 1) / tiles));
+  s = std::min(std::min(s, std::max(1, q_steps(k) / (4 * kWaves))), 16);
+  const int per = (q_steps(k) + s - 1) / s;  // K steps per split; every split non-empty
+  *splits = (q_steps(k) + per - 1) / per;
+  return FI_OK;
+}
+
+int32_t fi_gemm_packed(fi_context* ctx, const float* d_a, int32_t lda, const float* d_bp, int32_t k, int32_t n,
+                       int32_t pack_width, int32_t m, int32_t splits, float* d_out) {
+  FI_TRY(check_common(ctx, d_a, lda, d_bp, m, k, n));
+  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
+             "fi_gemm_packed: pack width must be 1, 2 or 4");
+  FI_REQUIRE(splits >= 1 && splits <= q_steps(k), FI_ERR_INVALID_CONFIG, "fi_gemm_packed: splits out of range");
+  if (m == 0) return FI_OK;
+  FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_packed: null output");
+  PGemmArgs g{};
+  g.a = d_a;
+  g.bp = d_bp;
+  g.out = d_out;
+  g.m = m;
+  g.k = k;
+  g.n = n;
+  g.lda = lda;
+  g.q_total = q_steps(k);
+  g.q_per_split = (g.q_total + splits - 1) / splits;
+  g.slabs = slabs_of(n, pack_width, false);
+  const int used = (g.q_total + g.q_per_split - 1) / g.q_per_split;
+  FI_REQUIRE(used == splits, FI_ERR_INVALID_CONFIG,
+             "fi_gemm_packed: splits must divide the K steps into non-empty ranges (use fi_gemm_packed_splits)");
+  switch (pack_width) {
+    case 1:
+      return launch_pgemm<1, kEpiPartial>(ctx, g, splits);
+    case 2:
+      return launch_pgemm<2, kEpiPartial>(ctx, g, splits);
+    default:
+      return launch_pgemm<4, kEpiPartial>(ctx, g, splits);
+  }
+}
+
+int32_t fi_gemm_packed_swiglu(fi_context* ctx, const float* d_a, int32_t lda, const float* d_bp_pair, int32_t k,
+                              int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate, float* d_out) {
+  FI_TRY(check_common(ctx, d_a, lda, d_bp_pair, m, k, n));
+  if (m == 0) return FI_OK;
+  FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_packed_swiglu: null output");
+  PGemmArgs g{};
+  g.a = d_a;
+  g.bp = d_bp_pair;
+  g.out = d_out;
+  g.bias0 = d_bias_up;
+  g.bias1 = d_bias_gate;
+  g.m = m;
+  g.k = k;
+  g.n = n;
+  g.lda = lda;
+  g.q_total = q_steps(k);
+  g.q_per_split = g.q_total;
+  g.slabs = slabs_of(n, 2, true);
+  return launch_pgemm<2, kEpiSwiglu>(ctx, g, 1);
+}
+
+int32_t fi_lm_head_argmax_packed(fi_context* ctx, const float* d_hidden, int32_t lda, const float* d_bp, int32_t m,
+                                 int32_t hidden, int32_t vocab, int32_t* d_token, float* d_prob) {
+  FI_TRY(check_common(ctx, d_hidden, lda, d_bp, m, hidden, vocab));
+  if (m == 0) return FI_OK;
+  FI_REQUIRE(d_token && d_prob, FI_ERR_INVALID_CONFIG, "fi_lm_head_argmax_packed: null output");
+  PGemmArgs g{};
+  g.a = d_hidden;
+  g.bp = d_bp;
+  g.m = m;
+  g.k = hidden;
+  g.n = vocab;
+  g.lda = lda;
+  g.q_total = q_steps(hidden);
+  g.q_per_split = g.q_total;
+  g.slabs = slabs_of(vocab, 4, false);
+  FI_TRY(fi::ensure_workspace(ctx, (size_t)m * g.slabs * 3 * sizeof(float)));
+  g.out = static_cast<float*>(ctx->workspace);
+  FI_TRY((launch_pgemm<4, kEpiArgmax>(ctx, g, 1)));
+  return fi::argmax_merge(ctx, g.out, g.slabs, m, d_token, d_prob);
+}
+
+int32_t fi_splitk_residual_rms_norm(fi_context* ctx, const float* d_parts, int32_t splits, const float* d_bias,
+                                    const float* d_residual, float* d_sum, const float* d_weight, float* d_out,
+                                    int32_t rows, int32_t hidden, float eps) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(rows >= 0 && hidden > 0 && splits >= 1, FI_ERR_INVALID_SHAPE, "fi_splitk_residual_rms_norm: bad shape");
+  if (rows == 0) return FI_OK;
+  FI_REQUIRE(d_parts && d_residual && d_sum && d_weight && d_out, FI_ERR_INVALID_CONFIG,
+             "fi_splitk_residual_rms_norm: null pointer");
+  hipLaunchKernelGGL(splitk_residual_rms_norm_kernel, dim3(rows), dim3(kRowThreads), 0, ctx->stream, d_parts, splits,
+                     d_bias, d_residual, d_sum, d_weight, d_out, rows, hidden, eps);
+  FI_CHECK_LAUNCH("splitk_residual_rms_norm_kernel");
+  return FI_OK;
+}
+
+int32_t fi_qkv_rope_append(fi_context* ctx, const float* d_parts, int32_t splits, const float* d_bias_q,
+                           const float* d_bias_k, const float* d_bias_v,
+                           const int32_t* d_positions, const float* d_cos, const float* d_sin, int32_t rotary_dims,
+                           int32_t max_positions, const int64_t* d_slot_mapping, void* d_k_cache, void* d_v_cache,
+                           int32_t kv_dtype, int32_t num_blocks, int32_t block_size, int32_t num_tokens,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float* d_q_out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(num_tokens >= 0 && splits >= 1, FI_ERR_INVALID_SHAPE, "fi_qkv_rope_append: bad shape");
+  FI_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && num_q_heads % num_kv_heads == 0,
+             FI_ERR_INVALID_SHAPE, "number of query heads must be divisible by number of KV heads");
+  FI_REQUIRE(rotary_dims >= 0 && rotary_dims <= head_dim && rotary_dims % 2 == 0, FI_ERR_INVALID_CONFIG,
+             "rope.rotary_dims must be even and at most the head dimension");
+  FI_REQUIRE(num_blocks > 0 && block_size > 0, FI_ERR_INVALID_CONFIG, "fi_qkv_rope_append: pool dimensions must be positive");
+  FI_REQUIRE(kv_dtype == FI_DTYPE_F32 || kv_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
+             "fi_qkv_rope_append: KV dtype must be f32 or bf16");
+  if (num_tokens == 0) return FI_OK;
+  FI_REQUIRE(d_parts && d_positions && d_slot_mapping && d_k_cache && d_v_cache && d_q_out, FI_ERR_INVALID_CONFIG,
+             "fi_qkv_rope_append: null pointer");
+  FI_REQUIRE(rotary_dims == 0 || (d_cos && d_sin && max_positions > 0), FI_ERR_INVALID_CONFIG,
+             "fi_qkv_rope_append: rope tables required");
+  const int64_t pool_slots = static_cast<int64_t>(num_blocks) * block_size;
+  if (kv_dtype == FI_DTYPE_F32) {
+    hipLaunchKernelGGL(qkv_rope_append_kernel<float>, dim3(num_tokens), dim3(kRowThreads), 0, ctx->stream, d_parts,
+                       splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions, d_slot_mapping,
+                       static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache), pool_slots, block_size,
+                       num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out, ctx->d_faults);
+  } else {
+    hipLaunchKernelGGL(qkv_rope_append_kernel<uint16_t>, dim3(num_tokens), dim3(kRowThreads), 0, ctx->stream,
+                       d_parts, splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
+                       d_slot_mapping, static_cast<uint16_t*>(d_k_cache), static_cast<uint16_t*>(d_v_cache),
+                       pool_slots, block_size, num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out,
+                       ctx->d_faults);
+  }
+  FI_CHECK_LAUNCH("qkv_rope_append_kernel");
+  return FI_OK;
+}
+
+}  // extern "C"

@@ -122,6 +122,7 @@ void DeviceModel::set_weight(const std::string& name, const float* host, size_t 
 }
 
 void DeviceModel::validate() const {
+  if (finalized_) return;  // checked before packing; the unpacked projections are gone
   // model/decoder.rs:30-52 required_weight_keys
   auto need = [](const DeviceBuffer& b, const std::string& name) {
     if (b.get() == nullptr) fail(ErrorKind::MissingWeight, "missing required tensor: " + name);
@@ -142,6 +143,50 @@ void DeviceModel::validate() const {
   }
   need(norm_, "norm.weight");
   if (!config_.tie_word_embeddings) need(output_, "output.weight");
+}
+
+void DeviceModel::finalize() {
+  if (finalized_) return;
+  validate();
+  const ModelConfig& c = config_;
+  const int32_t h = c.hidden_size, f = c.intermediate_size, kvw = c.num_key_value_heads * c.head_dim();
+  if (h % 4 != 0 || f % 4 != 0) {
+    fail(ErrorKind::Unsupported, "hidden and intermediate sizes must be multiples of 4 for the packed projections");
+  }
+  auto floats = [](int32_t k, int32_t n, int32_t pw) {
+    size_t out = 0;
+    check(fi_weight_packed_floats(k, n, pw, &out));
+    return out;
+  };
+  packed_.resize(c.num_layers);
+  for (int32_t l = 0; l < c.num_layers; ++l) {
+    Layer& w = layers_[l];
+    Packed& p = packed_[l];
+    p.qkv.reserve(ctx_, floats(h, h + 2 * kvw, kQkvPack) * sizeof(float));
+    const float* srcs[3] = {w.wq.f32(), w.wk.f32(), w.wv.f32()};
+    const int32_t ns[3] = {h, kvw, kvw};
+    check(fi_weight_pack_columns(ctx_, srcs, ns, 3, h, kQkvPack, p.qkv.f32()));
+    p.wo.reserve(ctx_, floats(h, h, kWoPack) * sizeof(float));
+    check(fi_weight_pack(ctx_, w.wo.f32(), 0, h, h, kWoPack, p.wo.f32()));
+    p.w13.reserve(ctx_, floats(h, 2 * f, 2) * sizeof(float));
+    check(fi_weight_pack_pair(ctx_, w.w1.f32(), w.w3.f32(), h, f, p.w13.f32()));
+    p.w2.reserve(ctx_, floats(f, h, kW2Pack) * sizeof(float));
+    check(fi_weight_pack(ctx_, w.w2.f32(), 0, f, h, kW2Pack, p.w2.f32()));
+  }
+  lm_packed_.reserve(ctx_, floats(h, c.vocab_size, kLmPack) * sizeof(float));
+  check(fi_weight_pack(ctx_, output_weight(), 1, h, c.vocab_size, kLmPack, lm_packed_.f32()));
+  check(fi_ctx_sync(ctx_));
+  for (Layer& w : layers_) {
+    w.wq = DeviceBuffer();
+    w.wk = DeviceBuffer();
+    w.wv = DeviceBuffer();
+    w.wo = DeviceBuffer();
+    w.w1 = DeviceBuffer();
+    w.w2 = DeviceBuffer();
+    w.w3 = DeviceBuffer();
+  }
+  output_ = DeviceBuffer();
+  finalized_ = true;
 }
 
 // ----------------------------------------------------------------------------- block pool
@@ -209,18 +254,12 @@ void ForwardExecutor::reserve(size_t tokens, size_t seqs) {
   cap_seqs_ = std::max(seqs, cap_seqs_);
   const ModelConfig& c = model_->config();
   const size_t t = cap_tokens_, h = c.hidden_size, f = c.intermediate_size;
-  const size_t kvw = static_cast<size_t>(c.num_key_value_heads) * c.head_dim();
   hidden_.reserve(ctx_, t * h * 4);
   normed_.reserve(ctx_, t * h * 4);
   q_.reserve(ctx_, t * h * 4);
-  k_.reserve(ctx_, t * kvw * 4);
-  v_.reserve(ctx_, t * kvw * 4);
   attn_.reserve(ctx_, t * h * 4);
-  tmp_.reserve(ctx_, t * h * 4);
   h1_.reserve(ctx_, t * h * 4);
-  up_.reserve(ctx_, t * f * 4);
-  gate_.reserve(ctx_, t * f * 4);
-  last_.reserve(ctx_, cap_seqs_ * h * 4);
+  act_.reserve(ctx_, t * f * 4);
   last_norm_.reserve(ctx_, cap_seqs_ * h * 4);
   tok_.reserve(ctx_, cap_seqs_ * 4);
   prob_.reserve(ctx_, cap_seqs_ * 4);
@@ -236,10 +275,23 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
     copy_only(b);
     return {};
   }
+  if (!model_->finalized()) fail(ErrorKind::Runtime, "model weights are not packed (DeviceModel::finalize)");
   reserve(T, B);
   const int32_t H = c.hidden_size, F = c.intermediate_size, hq = c.num_attention_heads;
-  const int32_t hkv = c.num_key_value_heads, D = c.head_dim(), kvw = hkv * D;
+  const int32_t hkv = c.num_key_value_heads, D = c.head_dim(), kvw = hkv * D, W = H + 2 * kvw;
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // attention.rs:659
+
+  // split-K counts of the three partial-output projections; one partials buffer serves all
+  int32_t s_qkv = 1, s_o = 1, s_w2 = 1;
+  check(fi_gemm_packed_splits(ctx_, T, H, W, DeviceModel::kQkvPack, &s_qkv));
+  check(fi_gemm_packed_splits(ctx_, T, H, H, DeviceModel::kWoPack, &s_o));
+  check(fi_gemm_packed_splits(ctx_, T, F, H, DeviceModel::kW2Pack, &s_w2));
+  const size_t parts = std::max({static_cast<size_t>(s_qkv) * T * W, static_cast<size_t>(s_o) * T * H,
+                                 static_cast<size_t>(s_w2) * T * H});
+  if (parts > cap_parts_) {
+    parts_.reserve(ctx_, parts * 4);
+    cap_parts_ = parts;
+  }
 
   // One upload of all integer metadata (8-byte aligned sections).
   std::vector<uint8_t> host;
@@ -274,31 +326,26 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
   float* hidden = hidden_.f32();
   float* normed = normed_.f32();
   float* q = q_.f32();
-  float* k = k_.f32();
-  float* v = v_.f32();
   float* attn = attn_.f32();
-  float* tmp = tmp_.f32();
   float* h1 = h1_.f32();
-  float* up = up_.f32();
-  float* gate = gate_.f32();
+  float* act = act_.f32();
+  float* part = parts_.f32();
 
-  // runtime/reference.rs:372-423 / 664-710: embed, L blocks, final norm, greedy head
+  // runtime/reference.rs:372-423 / 664-710: embed, L blocks, final norm, greedy head.  Block
+  // order as reference.rs:163-370: rmsnorm -> q,k,v (+bias) -> rope -> attention (the chunk's
+  // own K/V appended first, so they are read from the pool) -> wo (+bias) -> +x -> rmsnorm ->
+  // w1, w3 (+bias) -> silu(w3) * w1 -> w2 (+bias) -> +h1.  Each rmsnorm runs fused with the
+  // residual add before it; the last one applies the model's final norm.
   check(fi_embedding(ctx_, model_->tok_embeddings(), c.vocab_size, H, d_ids, T, hidden));
+  check(fi_rms_norm(ctx_, hidden, model_->layer(0).attention_norm.f32(), normed, T, H, c.rms_norm_eps));
   for (int32_t l = 0; l < c.num_layers; ++l) {
     const DeviceModel::Layer& w = model_->layer(l);
-    // runtime/reference.rs:163-370: rmsnorm -> q,k,v (+bias) -> rope -> attention (KV
-    // appended first, so the chunk's own keys come from the pool) -> wo -> +x -> rmsnorm ->
-    // w1, w3 -> silu(w3) * w1 -> w2 -> +h1
-    check(fi_rms_norm(ctx_, hidden, w.attention_norm.f32(), normed, T, H, c.rms_norm_eps));
-    check(fi_gemm(ctx_, normed, w.wq.f32(), w.wq_bias.f32(), q, T, H, H, 0));
-    check(fi_gemm(ctx_, normed, w.wk.f32(), w.wk_bias.f32(), k, T, H, kvw, 0));
-    check(fi_gemm(ctx_, normed, w.wv.f32(), w.wv_bias.f32(), v, T, H, kvw, 0));
-    if (c.rotary_dims > 0) {
-      check(fi_rope(ctx_, q, k, d_pos, model_->rope_cos(), model_->rope_sin(), T, hq, hkv, D, c.rotary_dims,
-                    model_->rope_positions()));
-    }
-    check(fi_kv_append(ctx_, k, v, d_slot, T, pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(),
-                       pool_->block_size(), hkv, D));
+    const DeviceModel::Packed& p = model_->packed(l);
+    check(fi_gemm_packed(ctx_, normed, H, p.qkv.f32(), H, W, DeviceModel::kQkvPack, T, s_qkv, part));
+    check(fi_qkv_rope_append(ctx_, part, s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), d_pos,
+                             model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(), d_slot,
+                             pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(), pool_->block_size(), T,
+                             hq, hkv, D, q));
     if (n_copy > 0) {
       check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(),
                               reinterpret_cast<const int32_t*>(at(o_cs)), reinterpret_cast<const int32_t*>(at(o_cd)),
@@ -314,19 +361,20 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
                                   d_ctx, B, b.max_query_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(),
                                   scale, attn));
     }
-    check(fi_gemm(ctx_, attn, w.wo.f32(), w.wo_bias.f32(), tmp, T, H, H, 0));
-    check(fi_add_rms_norm(ctx_, tmp, hidden, h1, w.ffn_norm.f32(), normed, T, H, c.rms_norm_eps));
-    check(fi_gemm(ctx_, normed, w.w1.f32(), w.w1_bias.f32(), up, T, H, F, 0));
-    check(fi_gemm(ctx_, normed, w.w3.f32(), w.w3_bias.f32(), gate, T, H, F, 0));
-    check(fi_silu_mul(ctx_, up, gate, up, static_cast<int64_t>(T) * F));  // in place over `up`
-    check(fi_gemm(ctx_, up, w.w2.f32(), w.w2_bias.f32(), tmp, T, F, H, 0));
-    check(fi_add(ctx_, tmp, h1, hidden, static_cast<int64_t>(T) * H));
+    check(fi_gemm_packed(ctx_, attn, H, p.wo.f32(), H, H, DeviceModel::kWoPack, T, s_o, part));
+    check(fi_splitk_residual_rms_norm(ctx_, part, s_o, w.wo_bias.f32(), hidden, h1, w.ffn_norm.f32(), normed, T, H,
+                                      c.rms_norm_eps));
+    check(fi_gemm_packed_swiglu(ctx_, normed, H, p.w13.f32(), H, F, T, w.w1_bias.f32(), w.w3_bias.f32(), act));
+    check(fi_gemm_packed(ctx_, act, F, p.w2.f32(), F, H, DeviceModel::kW2Pack, T, s_w2, part));
+    const float* next_norm = l + 1 < c.num_layers ? model_->layer(l + 1).attention_norm.f32() : model_->norm();
+    check(fi_splitk_residual_rms_norm(ctx_, part, s_w2, w.w2_bias.f32(), h1, hidden, next_norm, normed, T, H,
+                                      c.rms_norm_eps));
   }
-  // last row of every sequence -> final norm -> fused greedy head (matmul.rs:190-274)
-  check(fi_embedding(ctx_, hidden, T, H, d_last, B, last_.f32()));
-  check(fi_rms_norm(ctx_, last_.f32(), model_->norm(), last_norm_.f32(), B, H, c.rms_norm_eps));
-  check(fi_lm_head_argmax(ctx_, last_norm_.f32(), model_->output_weight(), B, H, c.vocab_size,
-                          static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  // the final norm ran over every row; each sequence's last row feeds the fused greedy head
+  // (matmul.rs:190-274)
+  check(fi_embedding(ctx_, normed, T, H, d_last, B, last_norm_.f32()));
+  check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, model_->lm_head_packed(), B, H, c.vocab_size,
+                                 static_cast<int32_t*>(tok_.get()), prob_.f32()));
   const auto t_enqueued = std::chrono::steady_clock::now();
   std::vector<int32_t> tok(B);
   std::vector<float> prob(B);

@@ -83,9 +83,22 @@ class DeviceModel {
     DeviceBuffer attention_norm, wq, wq_bias, wk, wk_bias, wv, wv_bias, wo, wo_bias;
     DeviceBuffer ffn_norm, w1, w1_bias, w2, w2_bias, w3, w3_bias;
   };
+  // Projections re-laid out for fi_gemm_packed (include/ferrisinfer_kernel.h): q|k|v as one
+  // column-concatenated matrix, wo, w1/w3 as a SwiGLU pair, w2; pack widths below.
+  struct Packed {
+    DeviceBuffer qkv, wo, w13, w2;
+  };
+  static constexpr int32_t kQkvPack = 1, kWoPack = 1, kW2Pack = 4, kLmPack = 4;
+
   DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions);
   void set_weight(const std::string& name, const float* host, size_t count);
   void validate() const;  // every required tensor present (MissingWeight otherwise)
+  // Packs every projection once the weights are complete and releases the unpacked copies
+  // (the tied embedding stays: the gather reads it).  Idempotent.
+  void finalize();
+  bool finalized() const { return finalized_; }
+  const Packed& packed(int i) const { return packed_.at(i); }
+  const float* lm_head_packed() const { return lm_packed_.f32(); }
   const ModelConfig& config() const { return config_; }
   const Layer& layer(int i) const { return layers_.at(i); }
   const float* tok_embeddings() const { return tok_embeddings_.f32(); }
@@ -102,8 +115,10 @@ class DeviceModel {
   fi_context* ctx_;
   ModelConfig config_;
   std::vector<Layer> layers_;
-  DeviceBuffer tok_embeddings_, norm_, output_, rope_cos_, rope_sin_;
+  std::vector<Packed> packed_;
+  DeviceBuffer tok_embeddings_, norm_, output_, rope_cos_, rope_sin_, lm_packed_;
   int32_t rope_positions_;
+  bool finalized_ = false;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -304,8 +319,8 @@ class ForwardExecutor {
   const DeviceModel* model_;
   BlockPool* pool_;
   fi_context* ctx_;
-  DeviceBuffer meta_, hidden_, normed_, q_, k_, v_, attn_, tmp_, h1_, up_, gate_, last_, last_norm_, tok_, prob_;
-  size_t cap_tokens_ = 0, cap_seqs_ = 0;
+  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, tok_, prob_;
+  size_t cap_tokens_ = 0, cap_seqs_ = 0, cap_parts_ = 0;
   double enqueue_s_ = 0.0, wait_s_ = 0.0;
 };
 

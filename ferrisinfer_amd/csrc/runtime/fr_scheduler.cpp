@@ -158,6 +158,7 @@ Scheduler::Scheduler(DeviceModel* model, BlockPool* pool, const SessionConfig& s
     fail(ErrorKind::InvalidConfig, "scheduler max_consecutive_prefill_ticks must be greater than zero");
   }
   model->validate();
+  model->finalize();
   if (static_cast<size_t>(model->rope_positions()) < session.max_sequence_length &&
       model->config().rotary_dims > 0) {
     fail(ErrorKind::InvalidConfig, "RoPE table shorter than the session max sequence length");

@@ -68,6 +68,17 @@ _SIGNATURES = {
     "fi_add": [_P, _P, _P, _I64],
     "fi_gemm": [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32],
     "fi_lm_head_argmax": [_P, _P, _P, _I32, _I32, _I32, _P, _P],
+    "fi_weight_packed_floats": [_I32, _I32, _I32, C.POINTER(_SZ)],
+    "fi_weight_pack": [_P, _P, _I32, _I32, _I32, _I32, _P],
+    "fi_weight_pack_pair": [_P, _P, _P, _I32, _I32, _P],
+    "fi_gemm_packed_splits": [_P, _I32, _I32, _I32, _I32, C.POINTER(_I32)],
+    "fi_gemm_packed": [_P, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _P],
+    "fi_gemm_packed_swiglu": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P],
+    "fi_lm_head_argmax_packed": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P],
+    "fi_splitk_residual_rms_norm": [_P, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32, _F32],
+    "fi_qkv_rope_append": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I32, _I32,
+                           _I32, _I32, _I32, _I32, _I32, _P],
+    "fi_weight_pack_columns": [_P, C.POINTER(_P), C.POINTER(_I32), _I32, _I32, _I32, _P],
 }
 _RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
 
@@ -250,3 +261,83 @@ class Context:
                                              int(max_query_len), num_q_heads, num_kv_heads,
                                              head_dim, block_size, num_blocks, float(scale),
                                              ptr(out)))
+
+    # ---------------------------------------------------------- packed-weight GEMMs
+    def weight_packed_floats(self, k, n, pack_width):
+        out = _SZ()
+        check(self.lib.fi_weight_packed_floats(int(k), int(n), int(pack_width), C.byref(out)))
+        return int(out.value)
+
+    def weight_pack(self, src, k, n, pack_width, src_layout=0):
+        """Packs a device weight [K, N] (src_layout 0) or [N, K] (1) for fi_gemm_packed."""
+        import torch
+
+        dst = torch.empty(self.weight_packed_floats(k, n, pack_width), dtype=torch.float32,
+                          device=src.device)
+        check(self.lib.fi_weight_pack(self.handle, ptr(src), int(src_layout), int(k), int(n),
+                                      int(pack_width), ptr(dst)))
+        return dst
+
+    def weight_pack_pair(self, first, second, k, n):
+        """SwiGLU pair pack of two [K, N] weights (up = first, gate = second)."""
+        import torch
+
+        dst = torch.empty(self.weight_packed_floats(k, 2 * n, 2), dtype=torch.float32,
+                          device=first.device)
+        check(self.lib.fi_weight_pack_pair(self.handle, ptr(first), ptr(second), int(k), int(n),
+                                           ptr(dst)))
+        return dst
+
+    def gemm_packed_splits(self, m, k, n, pack_width):
+        out = _I32()
+        check(self.lib.fi_gemm_packed_splits(self.handle, int(m), int(k), int(n), int(pack_width),
+                                             C.byref(out)))
+        return int(out.value)
+
+    def gemm_packed(self, a, bp, k, n, pack_width, splits, out):
+        """out [splits, M, N] = split-K partial products of a [M, K] and the packed weight."""
+        check(self.lib.fi_gemm_packed(self.handle, ptr(a), int(a.stride(0)), ptr(bp), int(k), int(n),
+                                      int(pack_width), int(a.shape[0]), int(splits), ptr(out)))
+
+    def gemm_packed_swiglu(self, a, bp_pair, k, n, out, bias_up=None, bias_gate=None):
+        check(self.lib.fi_gemm_packed_swiglu(self.handle, ptr(a), int(a.stride(0)), ptr(bp_pair),
+                                             int(k), int(n), int(a.shape[0]), ptr(bias_up),
+                                             ptr(bias_gate), ptr(out)))
+
+    def lm_head_argmax_packed(self, hidden, bp, vocab, token_out, prob_out):
+        m, h = hidden.shape
+        check(self.lib.fi_lm_head_argmax_packed(self.handle, ptr(hidden), int(hidden.stride(0)),
+                                                ptr(bp), int(m), int(h), int(vocab),
+                                                ptr(token_out), ptr(prob_out)))
+
+    def splitk_residual_rms_norm(self, parts, splits, bias, residual, sum_out, weight, out, eps):
+        rows, hidden = residual.shape
+        check(self.lib.fi_splitk_residual_rms_norm(self.handle, ptr(parts), int(splits), ptr(bias),
+                                                   ptr(residual), ptr(sum_out), ptr(weight),
+                                                   ptr(out), int(rows), int(hidden), float(eps)))
+
+    def weight_pack_columns(self, srcs, k, pack_width):
+        """Packs the column concatenation of up to three device weights [K, n_i]."""
+        import torch
+
+        ns = [int(s.shape[1]) for s in srcs]
+        dst = torch.empty(self.weight_packed_floats(k, sum(ns), pack_width), dtype=torch.float32,
+                          device=srcs[0].device)
+        arr = (_P * len(srcs))(*[ptr(s) for s in srcs])
+        nar = (_I32 * len(srcs))(*ns)
+        check(self.lib.fi_weight_pack_columns(self.handle, arr, nar, len(srcs), int(k),
+                                              int(pack_width), ptr(dst)))
+        return dst
+
+    def qkv_rope_append(self, parts, splits, biases, positions, cos_t, sin_t, rotary_dims,
+                        max_positions, slot_mapping, k_cache, v_cache, kv_dtype, num_blocks,
+                        block_size, num_q_heads, num_kv_heads, head_dim, q_out):
+        bq, bk, bv = biases if biases is not None else (None, None, None)
+        check(self.lib.fi_qkv_rope_append(self.handle, ptr(parts), int(splits), ptr(bq), ptr(bk),
+                                          ptr(bv),
+                                          ptr(positions), ptr(cos_t), ptr(sin_t), int(rotary_dims),
+                                          int(max_positions), ptr(slot_mapping), ptr(k_cache),
+                                          ptr(v_cache), int(kv_dtype), int(num_blocks),
+                                          int(block_size), int(positions.numel()),
+                                          int(num_q_heads), int(num_kv_heads), int(head_dim),
+                                          ptr(q_out)))

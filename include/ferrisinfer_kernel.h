@@ -226,6 +226,80 @@ int32_t fi_lm_head_argmax(fi_context* ctx, const float* d_hidden, const float* d
                           int32_t m, int32_t hidden, int32_t vocab, int32_t* d_token,
                           float* d_prob);
 
+/* ---------------------------------------------------------------- packed-weight path
+ *
+ * The decoder block's projections (matmul_f32 / linear_f32_with_bias over [in, out]
+ * weights, kernel/cpu/matmul.rs:46-118, runtime/reference.rs:1103-1191) on weights re-laid
+ * out once at upload, which the architecture assigns to the GPU backend
+ * (docs/architecture.md:53, 97).  Packed layout: slabs of 16*pack_width output columns, each
+ * holding its K rows (zero-padded to a multiple of 16) in MFMA fragment order, so a wave
+ * streams a slab with contiguous 16-byte loads.  fi_gemm_packed writes split-K partials
+ * [splits, M, N]; the consumers below sum them in split order (deterministic) and fuse the
+ * elementwise ops the reference runs after each projection. */
+
+/* Floats of the packed form of a [K, N] weight. */
+int32_t fi_weight_packed_floats(int32_t k, int32_t n, int32_t pack_width, size_t* floats);
+
+/* Packs a device weight: src_layout 0 = [K, N] ([in, out], model/decoder.rs:76-104),
+ * 1 = [N, K] (the [vocab, hidden] output / tied embedding weight of matmul_rhs_transposed,
+ * kernel/cpu/matmul.rs:120-188).  pack_width 1, 2 or 4. */
+int32_t fi_weight_pack(fi_context* ctx, const float* d_src, int32_t src_layout, int32_t k, int32_t n,
+                       int32_t pack_width, float* d_dst);
+
+/* Packs the column concatenation of up to three [K, ns[i]] weights (the q, k, v projections
+ * of one layer as a single [H, (Hq + 2 Hkv) * D] matrix).  d_srcs is a host array of device
+ * pointers. */
+int32_t fi_weight_pack_columns(fi_context* ctx, const float* const* d_srcs, const int32_t* ns, int32_t count,
+                               int32_t k, int32_t pack_width, float* d_dst);
+
+/* SwiGLU pair pack (pack width 2) of the up (w1) and gate (w3) weights, both [K, N]: each
+ * lane vector holds (up, gate) of one output column. */
+int32_t fi_weight_pack_pair(fi_context* ctx, const float* d_first, const float* d_second, int32_t k, int32_t n,
+                            float* d_dst);
+
+/* The split count fi_gemm_packed should use for an M x K x N product (enough workgroups to
+ * fill the device, every split non-empty). */
+int32_t fi_gemm_packed_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, int32_t pack_width,
+                              int32_t* splits);
+
+/* d_out[z] = A * B restricted to split z's K range, z < splits; A [M, K] row-major with row
+ * stride lda (a multiple of 4, 16-byte aligned rows).  Sum the splits in order (the consumers
+ * do) for matmul_f32 (kernel/cpu/matmul.rs:46-118). */
+int32_t fi_gemm_packed(fi_context* ctx, const float* d_a, int32_t lda, const float* d_bp, int32_t k, int32_t n,
+                       int32_t pack_width, int32_t m, int32_t splits, float* d_out);
+
+/* out[M, N] = (A W1 + b1) * silu(A W3 + b3) with the pair-packed weight: the up / gate
+ * projections, silu_f32_in_place and mul_f32_in_place of the decoder block
+ * (runtime/reference.rs:346-360, kernel/cpu/elementwise.rs:118-207) in one launch. */
+int32_t fi_gemm_packed_swiglu(fi_context* ctx, const float* d_a, int32_t lda, const float* d_bp_pair, int32_t k,
+                              int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate, float* d_out);
+
+/* fi_lm_head_argmax over a weight packed from its [vocab, hidden] layout with pack width 4
+ * (matmul_rhs_transposed_argmax_f32, kernel/cpu/matmul.rs:190-274): first maximal index
+ * and 1 / sum(exp(logit - max)) per row.  Uses the context workspace. */
+int32_t fi_lm_head_argmax_packed(fi_context* ctx, const float* d_hidden, int32_t lda, const float* d_bp, int32_t m,
+                                 int32_t hidden, int32_t vocab, int32_t* d_token, float* d_prob);
+
+/* sum = (sum_z parts[z] + bias) + residual (stored), out = rms_norm(sum) * weight: the
+ * projection's bias add, the residual add_f32_in_place and the next rms_norm_f32 of the
+ * decoder block (runtime/reference.rs:330-343, 362-368; kernel/cpu/reduction.rs:3-73).
+ * parts is [splits, rows, hidden]; bias may be NULL. */
+int32_t fi_splitk_residual_rms_norm(fi_context* ctx, const float* d_parts, int32_t splits, const float* d_bias,
+                                    const float* d_residual, float* d_sum, const float* d_weight, float* d_out,
+                                    int32_t rows, int32_t hidden, float eps);
+
+/* The fused QKV projection's split partials [splits, T, (Hq + 2 Hkv) * D] (+ q/k/v biases,
+ * each may be NULL) -> RoPE of q and k at positions (bit-identical to fi_rope) -> q to
+ * d_q_out [T, Hq, D], k and v appended to the pool by slot_mapping (as fi_kv_append).
+ * Replaces the bias adds, rope_f32 and KvCacheStorage::write_*_f32 of the block
+ * (runtime/reference.rs:163-300, kernel/cpu/attention.rs:165-220, runtime/kv_cache.rs:48-62). */
+int32_t fi_qkv_rope_append(fi_context* ctx, const float* d_parts, int32_t splits, const float* d_bias_q,
+                           const float* d_bias_k, const float* d_bias_v, const int32_t* d_positions,
+                           const float* d_cos, const float* d_sin, int32_t rotary_dims, int32_t max_positions,
+                           const int64_t* d_slot_mapping, void* d_k_cache, void* d_v_cache, int32_t kv_dtype,
+                           int32_t num_blocks, int32_t block_size, int32_t num_tokens, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim, float* d_q_out);
+
 #ifdef __cplusplus
 }
 #endif
