@@ -344,8 +344,39 @@ int32_t launch_pack(fi_context* ctx, const PackSources& s, int pair, int src_lay
 
 // ---- consumers of split-K partials ----
 
+// sum_z parts[z * plane + i] in split order.  The loads of a batch of 8 splits are all issued
+// before the first add (split counts reach 16 for skinny shapes, and a load-add chain would
+// pay one memory latency per split); masked tail loads read split 0 and add exactly 0.
+template <typename T>
+__device__ __forceinline__ T zero_like();
+template <>
+__device__ __forceinline__ float zero_like<float>() { return 0.0f; }
+template <>
+__device__ __forceinline__ float4 zero_like<float4>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+__device__ __forceinline__ float add(float a, float b) { return a + b; }
+__device__ __forceinline__ float4 add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+template <typename T>
+__device__ __forceinline__ T sum_splits(const T* __restrict__ p, size_t plane, int splits) {
+  T x = p[0];
+  for (int z0 = 1; z0 < splits; z0 += 8) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int z = z0 + u;
+      v[u] = p[(size_t)(z < splits ? z : 0) * plane];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (z0 + u < splits) x = add(x, v[u]);
+    }
+  }
+  return x;
+}
+
 // One workgroup per row: h = sum_z parts[z][row] (+ bias) + residual -> sum_out; out =
 // rms_norm(h) * w (reduction.rs:3-73: ms = sum(x^2)/H, inv = 1/sqrt(ms + eps), (x*inv)*w).
+// Four columns per thread when hidden is a multiple of 4.
 constexpr int kRowThreads = 256;
 __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
     const float* __restrict__ parts, int splits, const float* __restrict__ bias, const float* __restrict__ residual,
@@ -354,15 +385,29 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
   __shared__ float s_red[kRowThreads / 64];
   const int row = blockIdx.x;
   const size_t plane = (size_t)rows * hidden;
-  const float* p0 = parts + (size_t)row * hidden;
+  const size_t base = (size_t)row * hidden;
   float ss = 0.0f;
-  for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
-    float x = p0[c];
-    for (int z = 1; z < splits; ++z) x += p0[z * plane + c];
-    if (bias) x = x + bias[c];
-    x = x + residual[(size_t)row * hidden + c];
-    sum_out[(size_t)row * hidden + c] = x;
-    ss += x * x;
+  const bool vec = (hidden & 3) == 0;
+  if (vec) {
+    const int h4 = hidden / 4;
+    for (int c = threadIdx.x; c < h4; c += kRowThreads) {
+      float4 x = sum_splits(reinterpret_cast<const float4*>(parts + base) + c, plane / 4, splits);
+      if (bias) x = add(x, reinterpret_cast<const float4*>(bias)[c]);
+      x = add(x, reinterpret_cast<const float4*>(residual + base)[c]);
+      reinterpret_cast<float4*>(sum_out + base)[c] = x;
+      ss += x.x * x.x;
+      ss += x.y * x.y;
+      ss += x.z * x.z;
+      ss += x.w * x.w;
+    }
+  } else {
+    for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
+      float x = sum_splits(parts + base + c, plane, splits);
+      if (bias) x = x + bias[c];
+      x = x + residual[base + c];
+      sum_out[base + c] = x;
+      ss += x * x;
+    }
   }
   ss = fi::wave_sum(ss);
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
@@ -371,16 +416,34 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
 #pragma unroll
   for (int i = 0; i < kRowThreads / 64; ++i) total += s_red[i];
   const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
-  for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
-    const float x = sum_out[(size_t)row * hidden + c];
-    out[(size_t)row * hidden + c] = (x * inv) * weight[c];
+  if (vec) {
+    const int h4 = hidden / 4;
+    for (int c = threadIdx.x; c < h4; c += kRowThreads) {
+      const float4 x = reinterpret_cast<const float4*>(sum_out + base)[c];
+      const float4 wv = reinterpret_cast<const float4*>(weight)[c];
+      reinterpret_cast<float4*>(out + base)[c] =
+          make_float4((x.x * inv) * wv.x, (x.y * inv) * wv.y, (x.z * inv) * wv.z, (x.w * inv) * wv.w);
+    }
+  } else {
+    for (int c = threadIdx.x; c < hidden; c += kRowThreads) out[base + c] = (sum_out[base + c] * inv) * weight[c];
   }
 }
 
 // One workgroup per token: the QKV projection's split partials (+ biases) -> RoPE on q and k
 // at the token's position -> q to q_out, k and v appended to the pool slot (the reference
 // order: rope before attention, KV written for this chunk, reference.rs:163-370).  Columns
-// of the fused projection: [0, Hq*D) q, then Hkv*D of k, then Hkv*D of v.
+// of the fused projection: [0, Hq*D) q, then Hkv*D of k, then Hkv*D of v.  A thread owns a
+// rotary pair (i, i + rot/2) of one head, or one pass-through / value element, so every
+// partial is read once.
+template <typename KVT>
+__device__ __forceinline__ void put_kv(KVT* cache, size_t idx, float x) {
+  if constexpr (sizeof(KVT) == 4) {
+    cache[idx] = x;
+  } else {
+    cache[idx] = static_cast<KVT>(fi::f32_to_bf16_bits(x));
+  }
+}
+
 template <typename KVT>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float* __restrict__ parts, int splits, const float* __restrict__ bias_q, const float* __restrict__ bias_k,
@@ -394,8 +457,7 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   const float* p0 = parts + (size_t)t * width;
   const int qw = hq * d, kw = hkv * d;
   auto value = [&](int col) {
-    float x = p0[col];
-    for (int z = 1; z < splits; ++z) x += p0[z * plane + col];
+    const float x = sum_splits(p0 + col, plane, splits);
     const float* b = col < qw ? bias_q : (col < qw + kw ? bias_k : bias_v);
     const int bc = col < qw ? col : (col < qw + kw ? col - qw : col - qw - kw);
     return b ? x + b[bc] : x;
@@ -411,47 +473,35 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   if (slot >= pool_slots && threadIdx.x == 0) atomicOr(faults, FI_FAULT_SLOT_RANGE);
   const int64_t blk = write_kv ? slot / block_size : 0;
   const int off = write_kv ? static_cast<int>(slot % block_size) : 0;
-  // q and k heads: rotate pairs (i, i + half) for i < half, copy the rest
-  const int rot_heads = hq + hkv;
-  for (int idx = threadIdx.x; idx < rot_heads * d; idx += kRowThreads) {
-    const int head = idx / d, i = idx - head * d;
-    const int col = head < hq ? head * d + i : hq * d + (head - hq) * d + i;
-    float outv;
-    if (i < half) {
-#pragma clang fp contract(off)
-      const float lo = value(col), hi = value(col + half);
-      const float c = cos_t[(size_t)pos * half + i], s = sin_t[(size_t)pos * half + i];
-      outv = lo * c - hi * s;  // each product rounded before the difference, as Rust does
-    } else if (i < 2 * half) {
-#pragma clang fp contract(off)
-      const int j = i - half;
-      const float lo = value(col - half), hi = value(col);
-      const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
-      outv = hi * c + lo * s;
-    } else {
-      outv = value(col);
-    }
+  auto store = [&](int head, int i, float x) {  // head < hq: q; else k head (head - hq)
     if (head < hq) {
-      q_out[(size_t)t * hq * d + col] = outv;
+      q_out[(size_t)t * qw + head * d + i] = x;
     } else if (write_kv) {
-      const size_t dst = (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i;
-      if constexpr (sizeof(KVT) == 4) {
-        k_cache[dst] = outv;
-      } else {
-        k_cache[dst] = static_cast<KVT>(fi::f32_to_bf16_bits(outv));
-      }
+      put_kv(k_cache, (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i, x);
+    }
+  };
+  const int rot_heads = hq + hkv;
+  const int pass = d - 2 * half;  // dimensions past the rotary ones
+  const int per_head = half + pass;
+  // rotary pairs and pass-through dims of q and k heads
+  for (int idx = threadIdx.x; idx < rot_heads * per_head; idx += kRowThreads) {
+    const int head = idx / per_head, r = idx - head * per_head;
+    const int col0 = head < hq ? head * d : qw + (head - hq) * d;
+    if (r < half) {
+#pragma clang fp contract(off)
+      const float lo = value(col0 + r), hi = value(col0 + r + half);
+      const float c = cos_t[(size_t)pos * half + r], sn = sin_t[(size_t)pos * half + r];
+      store(head, r, lo * c - hi * sn);  // each product rounded before the add, as Rust does
+      store(head, r + half, hi * c + lo * sn);
+    } else {
+      const int i = 2 * half + (r - half);
+      store(head, i, value(col0 + i));
     }
   }
   if (write_kv) {
-    for (int idx = threadIdx.x; idx < hkv * d; idx += kRowThreads) {
+    for (int idx = threadIdx.x; idx < kw; idx += kRowThreads) {
       const int h = idx / d, i = idx - h * d;
-      const float x = value((hq + hkv) * d + idx);
-      const size_t dst = (((size_t)blk * hkv + h) * block_size + off) * d + i;
-      if constexpr (sizeof(KVT) == 4) {
-        v_cache[dst] = x;
-      } else {
-        v_cache[dst] = static_cast<KVT>(fi::f32_to_bf16_bits(x));
-      }
+      put_kv(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i, value(qw + kw + idx));
     }
   }
 }
