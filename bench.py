@@ -49,6 +49,9 @@ def parse_args():
     p.add_argument("--c4-requests", type=int, default=128)
     p.add_argument("--no-kernels", action="store_true",
                    help="skip the C3 prefill/append and projection-GEMM kernel measurements")
+    p.add_argument("--gemm-shapes", action="store_true",
+                   help="only time the projection GEMMs at the C4 shapes (packed-weight path "
+                        "against fi_gemm), one JSON line per shape")
     p.add_argument("--pmc-copy-reference", action="store_true",
                    help="only run a plain 512 MiB device copy (5 launches): the known-size "
                         "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -65,6 +68,63 @@ def pmc_copy_reference():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_copy_reference_bytes_per_launch": n * 4, "launches": 5}))
+
+
+def gemm_shapes(seed):
+    """Projection GEMMs at the C4 (Qwen2-0.5B) shapes: the packed-weight kernel at every
+    pack width against fi_gemm (checked equal within 1e-5 normwise), the SwiGLU pair and the
+    packed greedy head; M = 64 (a decode tick) and M = 1024 (a prefill chunk)."""
+    import torch
+
+    from ferrisinfer_amd import Context
+
+    ctx = Context(0)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+
+    def ms(fn, reps=50):
+        return timed(fn, reps, warmup=5)
+
+    for m in (64, 1024):
+        for name, k, n in (("qkv", 896, 1152), ("wo", 896, 896), ("w2", 4864, 896), ("w13", 896, 9728)):
+            a = torch.randn(m, k, device="cuda", generator=g)
+            w = torch.randn(k, n, device="cuda", generator=g) * 0.02
+            c = torch.empty(m, n, device="cuda")
+            row = {"shape": name, "m": m, "k": k, "n": n,
+                   "fi_gemm_us": round(ms(lambda: ctx.gemm(a, w, c)) * 1e3, 2)}
+            for pw in (1, 2, 4):
+                bp = ctx.weight_pack(w, k, n, pw)
+                s = ctx.gemm_packed_splits(m, k, n, pw)
+                out = torch.empty(s, m, n, device="cuda")
+                us = ms(lambda: ctx.gemm_packed(a, bp, k, n, pw, s, out)) * 1e3
+                err = float((out.sum(0) - c).abs().max() / c.abs().max())
+                assert err < 1e-5, (name, m, pw, err)
+                row[f"packed_pw{pw}"] = {"us": round(us, 2), "splits": s,
+                                         "tflops": round(2 * m * n * k / us / 1e6, 1),
+                                         "weight_gbs": round(4 * k * n / us / 1e3, 1)}
+            print(json.dumps(row), flush=True)
+        k, f = 896, 4864
+        a = torch.randn(m, k, device="cuda", generator=g)
+        w1 = torch.randn(k, f, device="cuda", generator=g) * 0.02
+        w3 = torch.randn(k, f, device="cuda", generator=g) * 0.02
+        bp = ctx.weight_pack_pair(w1, w3, k, f)
+        out = torch.empty(m, f, device="cuda")
+        us = ms(lambda: ctx.gemm_packed_swiglu(a, bp, k, f, out)) * 1e3
+        print(json.dumps({"shape": "w1/w3 pair + swiglu", "m": m, "k": k, "n": f, "us": round(us, 2),
+                          "tflops": round(2 * m * k * 2 * f / us / 1e6, 1)}), flush=True)
+    h, v = 896, 151936
+    w = torch.randn(v, h, device="cuda", generator=g) * 0.02
+    bp = ctx.weight_pack(w, h, v, 4, src_layout=1)
+    for m in (1, 16, 64):
+        hid = torch.randn(m, h, device="cuda", generator=g)
+        tok = torch.empty(m, dtype=torch.int32, device="cuda")
+        prob = torch.empty(m, device="cuda")
+        old = ms(lambda: ctx.lm_head_argmax(hid, w, tok, prob), 20) * 1e3
+        us = ms(lambda: ctx.lm_head_argmax_packed(hid, bp, v, tok, prob), 20) * 1e3
+        print(json.dumps({"shape": "lm_head argmax", "m": m, "k": h, "n": v,
+                          "fi_lm_head_argmax_us": round(old, 2), "packed_us": round(us, 2),
+                          "weight_gbs": round(4 * h * v / us / 1e3, 1),
+                          "tflops": round(2 * m * h * v / us / 1e6, 1)}), flush=True)
+    ctx.close()
 
 
 def traffic_from_profile(kv_dtype):
@@ -128,10 +188,22 @@ def timed(fn, reps, warmup=3):
     return e0.elapsed_time(e1) / reps
 
 
+def gemm_row(m, k, n, ms, splits, pw):
+    """One projection leg: MFMA fraction (2·M·K·N) and weight-stream HBM fraction (4·K·N)."""
+    fl = 2 * m * n * k
+    wb = 4 * k * n
+    return {"m": m, "k": k, "n": n, "pack_width": pw, "splits": splits,
+            "avg_launch_us": round(ms * 1e3, 2),
+            "achieved_tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+            "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / FP32_PEAK_TFS, 4),
+            "weight_gbs": round(wb / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(wb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def kernel_legs(ctx, seed):
     """C3 varlen prefill attention (MFMA f32) and KV append (HBM) at full size, and the
-    projection GEMMs at the C4 shapes: a prefill chunk (M = 1024, MFMA-bound) and a decode
-    tick (M = 64, weight-streaming, HBM-bound)."""
+    packed projection GEMMs at the C4 shapes: a decode tick (M = 64, where f32 weight
+    streaming and MFMA are balanced) and a prefill chunk (M = 1024, MFMA-bound)."""
     import numpy as np
     import torch
 
@@ -174,22 +246,36 @@ def kernel_legs(ctx, seed):
         "frac": round(ab / (ms_a * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del kp, vp, k_new, v_new, slots, q, o
 
+    # the projections as the runtime runs them: packed weights, pack widths of
+    # DeviceModel (q|k|v 1, wo 1, w1/w3 SwiGLU pair, w2 4, lm_head 4), C4 shapes
     g = torch.Generator(device="cuda").manual_seed(seed)
-    for name, m, k, n in (("gemm_c4_prefill_w1", 1024, 896, 4864),
-                          ("gemm_c4_prefill_w2", 1024, 4864, 896),
-                          ("gemm_c4_decode_w1", 64, 896, 4864),
-                          ("gemm_c4_decode_w2", 64, 4864, 896)):
+    for m in (64, 1024):
+        tag = "decode" if m == 64 else "prefill"
+        for name, k, n, pw in (("qkv", 896, 1152, 1), ("wo", 896, 896, 1), ("w2", 4864, 896, 4)):
+            a = torch.randn(m, k, device="cuda", generator=g)
+            w = torch.randn(k, n, device="cuda", generator=g) * 0.02
+            bp = ctx.weight_pack(w, k, n, pw)
+            splits = ctx.gemm_packed_splits(m, k, n, pw)
+            parts = torch.empty(splits, m, n, device="cuda")
+            ms = timed(lambda: ctx.gemm_packed(a, bp, k, n, pw, splits, parts), 50)
+            out[f"gemm_c4_{tag}_{name}"] = gemm_row(m, k, n, ms, splits, pw)
+        k, f = 896, 4864
         a = torch.randn(m, k, device="cuda", generator=g)
-        b = torch.randn(k, n, device="cuda", generator=g)
-        c = torch.empty(m, n, device="cuda")
-        ms = timed(lambda: ctx.gemm(a, b, c), 50)
-        fl = 2 * m * n * k
-        byt = 4 * (m * k + k * n + m * n)
-        out[name] = {"m": m, "k": k, "n": n, "avg_launch_us": round(ms * 1e3, 2),
-                     "achieved_tflops": round(fl / (ms * 1e-3) / 1e12, 2),
-                     "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / FP32_PEAK_TFS, 4),
-                     "achieved_gbs": round(byt / (ms * 1e-3) / 1e9, 1),
-                     "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        w1 = torch.randn(k, f, device="cuda", generator=g) * 0.02
+        w3 = torch.randn(k, f, device="cuda", generator=g) * 0.02
+        bp = ctx.weight_pack_pair(w1, w3, k, f)
+        act = torch.empty(m, f, device="cuda")
+        ms = timed(lambda: ctx.gemm_packed_swiglu(a, bp, k, f, act), 50)
+        out[f"gemm_c4_{tag}_w13_swiglu"] = gemm_row(m, k, 2 * f, ms, 1, 2)
+    h, v = 896, 151936
+    w = torch.randn(v, h, device="cuda", generator=g) * 0.02
+    bp = ctx.weight_pack(w, h, v, 4, src_layout=1)
+    for m in (1, 64):
+        hid = torch.randn(m, h, device="cuda", generator=g)
+        tok = torch.empty(m, dtype=torch.int32, device="cuda")
+        prob = torch.empty(m, device="cuda")
+        ms = timed(lambda: ctx.lm_head_argmax_packed(hid, bp, v, tok, prob), 20)
+        out[f"lm_head_argmax_c4_m{m}"] = gemm_row(m, h, v, ms, 1, 4)
     ctx.check_faults()
     return out
 
@@ -278,6 +364,9 @@ def main():
     args = parse_args()
     if args.pmc_copy_reference:
         pmc_copy_reference()
+        return
+    if args.gemm_shapes:
+        gemm_shapes(args.seed)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
