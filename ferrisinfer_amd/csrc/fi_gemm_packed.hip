@@ -89,97 +89,12 @@ __device__ __forceinline__ float4 load_a(const float* row, int k0, int k) {
   }
 }
 
-#ifndef FI_PGEMM_MIN_WAVES
-#define FI_PGEMM_MIN_WAVES 2  // waves per SIMD the register budget must allow
-#endif
-#ifndef FI_PGEMM_RING_REGS
-#define FI_PGEMM_RING_REGS 64  // VGPRs the ring of in-flight loads may hold
-#endif
-
-template <int MT, int PW, int EPI, bool KTAIL>
-__global__ __launch_bounds__(kThreads, FI_PGEMM_MIN_WAVES) void gemm_packed_kernel(PGemmArgs g) {
-  using BV = typename PVec<PW>::T;
-  constexpr int STEP_REGS = 4 * MT + 4 * PW;  // VGPRs one K step of loads occupies
-  constexpr int DEPTH = FI_PGEMM_RING_REGS / STEP_REGS < 2 ? 2 : (FI_PGEMM_RING_REGS / STEP_REGS > 8 ? 8 : FI_PGEMM_RING_REGS / STEP_REGS);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// Writes one wave's (16*MT) x (16*PW) accumulator tile.  Lane (li, lk) holds
+// acc[mt][p][v] = C[m0 + 16mt + 4lk + v][slab*16*PW + PW*li + p].
+template <int MT, int PW, int EPI>
+__device__ __forceinline__ void store_tile(const PGemmArgs& g, v4f (&acc)[MT][PW], int m0, int slab, int z,
+                                           int lane) {
   const int li = lane & 15, lk = lane >> 4;
-  const int slab = blockIdx.x, mblk = blockIdx.y, z = blockIdx.z;
-  const int m0 = mblk * 16 * MT;
-
-  // this wave's K steps: a contiguous quarter of the workgroup's range
-  const int wq0 = z * g.q_per_split;
-  const int wq1 = min(g.q_total, wq0 + g.q_per_split);
-  const int per = (wq1 - wq0 + kWaves - 1) / kWaves;
-  const int q_beg = min(wq1, wq0 + w * per);
-  const int q_end = min(wq1, q_beg + per);
-
-  const float* arow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) arow[mt] = g.a + (size_t)min(m0 + 16 * mt + li, g.m - 1) * g.lda + 4 * lk;
-  const BV* bbase = reinterpret_cast<const BV*>(g.bp) + (size_t)slab * g.q_total * 4 * 64 + lane;
-
-  v4f acc[MT][PW];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int p = 0; p < PW; ++p) acc[mt][p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  if (q_beg < q_end) {  // wave-uniform
-    // Ring of R = DEPTH + 1 slots: step s lives in slot (s - q_beg) % R.  Before step s is
-    // multiplied, the loads of step s + DEPTH go into the slot step s - 1 has released, so
-    // DEPTH steps stay in flight while the MFMAs of step s run.
-    constexpr int R = DEPTH + 1;
-    float4 ra[R][MT];
-    BV rb[R][4];
-    auto issue = [&](int q, int slot) {
-      q = min(q, q_end - 1);  // clamped refetches hit the cache: no extra HBM traffic
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) ra[slot][mt] = load_a<KTAIL>(arow[mt], 16 * q, g.k - 4 * lk);
-      const BV* bq = bbase + (size_t)q * 4 * 64;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) rb[slot][e] = bq[e * 64];
-    };
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) issue(q_beg + d, d);
-    for (int q = q_beg; q < q_end; q += R) {
-#pragma unroll
-      for (int d = 0; d < R; ++d) {
-        issue(q + d + DEPTH, (d + DEPTH) % R);
-        sched_fence();
-        if (q + d < q_end) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              const float av = e == 0 ? ra[d][mt].x : (e == 1 ? ra[d][mt].y : (e == 2 ? ra[d][mt].z : ra[d][mt].w));
-#pragma unroll
-              for (int p = 0; p < PW; ++p)
-                acc[mt][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, PVec<PW>::get(rb[d][e], p), acc[mt][p], 0, 0, 0);
-            }
-        }
-        sched_fence();
-      }
-    }
-  }
-
-  // ---- sum the four K quarters in wave order through LDS ----
-  __shared__ v4f s_part[kWaves - 1][MT * PW][64];
-  if (w > 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int p = 0; p < PW; ++p) s_part[w - 1][mt * PW + p][lane] = acc[mt][p];
-  }
-  __syncthreads();
-  if (w != 0) return;
-#pragma unroll
-  for (int src = 0; src < kWaves - 1; ++src)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int p = 0; p < PW; ++p) acc[mt][p] += s_part[src][mt * PW + p][lane];
-
-  // acc[mt][p][v] = C[m0 + 16mt + 4lk + v][slab*16*PW + PW*li + p]
   const int col0 = slab * 16 * PW + PW * li;
   if constexpr (EPI == kEpiPartial) {
     float* out = g.out + (size_t)z * g.m * g.n;
@@ -281,6 +196,219 @@ __global__ __launch_bounds__(kThreads, FI_PGEMM_MIN_WAVES) void gemm_packed_kern
           dst[2] = sum;
         }
       }
+  }
+}
+
+#ifndef FI_PGEMM_MIN_WAVES
+#define FI_PGEMM_MIN_WAVES 2  // waves per SIMD the register budget must allow
+#endif
+#ifndef FI_PGEMM_RING_REGS
+#define FI_PGEMM_RING_REGS 64  // VGPRs the ring of in-flight loads may hold
+#endif
+
+template <int MT, int PW, int EPI, bool KTAIL>
+__global__ __launch_bounds__(kThreads, FI_PGEMM_MIN_WAVES) void gemm_packed_kernel(PGemmArgs g) {
+  using BV = typename PVec<PW>::T;
+  constexpr int STEP_REGS = 4 * MT + 4 * PW;  // VGPRs one K step of loads occupies
+  constexpr int DEPTH = FI_PGEMM_RING_REGS / STEP_REGS < 2 ? 2 : (FI_PGEMM_RING_REGS / STEP_REGS > 8 ? 8 : FI_PGEMM_RING_REGS / STEP_REGS);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  const int slab = blockIdx.x, mblk = blockIdx.y, z = blockIdx.z;
+  const int m0 = mblk * 16 * MT;
+
+  // this wave's K steps: a contiguous quarter of the workgroup's range
+  const int wq0 = z * g.q_per_split;
+  const int wq1 = min(g.q_total, wq0 + g.q_per_split);
+  const int per = (wq1 - wq0 + kWaves - 1) / kWaves;
+  const int q_beg = min(wq1, wq0 + w * per);
+  const int q_end = min(wq1, q_beg + per);
+
+  const float* arow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) arow[mt] = g.a + (size_t)min(m0 + 16 * mt + li, g.m - 1) * g.lda + 4 * lk;
+  const BV* bbase = reinterpret_cast<const BV*>(g.bp) + (size_t)slab * g.q_total * 4 * 64 + lane;
+
+  v4f acc[MT][PW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int p = 0; p < PW; ++p) acc[mt][p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (q_beg < q_end) {  // wave-uniform
+    // Ring of R = DEPTH + 1 slots: step s lives in slot (s - q_beg) % R.  Before step s is
+    // multiplied, the loads of step s + DEPTH go into the slot step s - 1 has released, so
+    // DEPTH steps stay in flight while the MFMAs of step s run.
+    constexpr int R = DEPTH + 1;
+    float4 ra[R][MT];
+    BV rb[R][4];
+    auto issue = [&](int q, int slot) {
+      q = min(q, q_end - 1);  // clamped refetches hit the cache: no extra HBM traffic
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) ra[slot][mt] = load_a<KTAIL>(arow[mt], 16 * q, g.k - 4 * lk);
+      const BV* bq = bbase + (size_t)q * 4 * 64;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rb[slot][e] = bq[e * 64];
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(q_beg + d, d);
+    for (int q = q_beg; q < q_end; q += R) {
+#pragma unroll
+      for (int d = 0; d < R; ++d) {
+        issue(q + d + DEPTH, (d + DEPTH) % R);
+        sched_fence();
+        if (q + d < q_end) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const float av = e == 0 ? ra[d][mt].x : (e == 1 ? ra[d][mt].y : (e == 2 ? ra[d][mt].z : ra[d][mt].w));
+#pragma unroll
+              for (int p = 0; p < PW; ++p)
+                acc[mt][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, PVec<PW>::get(rb[d][e], p), acc[mt][p], 0, 0, 0);
+            }
+        }
+        sched_fence();
+      }
+    }
+  }
+
+  // ---- sum the four K quarters in wave order through LDS ----
+  __shared__ v4f s_part[kWaves - 1][MT * PW][64];
+  if (w > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < PW; ++p) s_part[w - 1][mt * PW + p][lane] = acc[mt][p];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int src = 0; src < kWaves - 1; ++src)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < PW; ++p) acc[mt][p] += s_part[src][mt * PW + p][lane];
+
+  store_tile<MT, PW, EPI>(g, acc, m0, slab, z, lane);
+}
+
+// Shared-activation variant: the 4 waves of a workgroup own 4 consecutive weight slabs and
+// one (16*MT)-row block over the workgroup's K range, so the activation rows are read once
+// per workgroup: 64-k chunks of A are staged through double-buffered LDS (one barrier per
+// chunk) in MFMA-fragment order, while each wave streams its own slab through a register ring
+// of B loads issued DEPTH steps ahead.  No cross-wave reduction: each wave stores its tile.
+template <int MT, int PW, int EPI, bool KTAIL>
+__global__ __launch_bounds__(kThreads, 2) void gemm_lds_kernel(PGemmArgs g) {
+  using BV = typename PVec<PW>::T;
+  constexpr int KC = 4;                // K steps (16 k each) per staged A chunk
+  constexpr int R = KC;                // B ring slots: the slot of a step is its index in the chunk
+  constexpr int DEPTH = R - 1;         // B steps in flight ahead of the MFMAs
+  constexpr int A_F4 = KC * MT * 64;   // float4 per A chunk
+  static_assert(A_F4 % kThreads == 0, "A chunk must split evenly over the workgroup");
+  constexpr int A_PER_T = A_F4 / kThreads;
+  __shared__ float4 s_a[2][A_F4];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int slab_id = blockIdx.x * kWaves + w;
+  const int slab = min(slab_id, g.slabs - 1);  // a short last group still loads valid data
+  const int m0 = blockIdx.y * 16 * MT, z = blockIdx.z;
+  const int q0 = z * g.q_per_split;
+  const int q1 = min(g.q_total, q0 + g.q_per_split);
+  const int nchunks = (q1 - q0 + KC - 1) / KC;
+
+  // A chunk slot i = (j * MT + mt) * 64 + ln holds A[m0 + 16mt + ln%16][16(q0+c*KC+j) + 4(ln/16) .. +3]
+  float4 areg[A_PER_T];
+  auto load_a_chunk = [&](int c) {
+#pragma unroll
+    for (int r = 0; r < A_PER_T; ++r) {
+      const int i = tid + r * kThreads;
+      const int j = i / (MT * 64), mt = (i / 64) % MT, ln = i % 64;
+      const int q = min(q0 + c * KC + j, q1 - 1);
+      const int row = min(m0 + 16 * mt + (ln & 15), g.m - 1);
+      areg[r] = load_a<KTAIL>(g.a + (size_t)row * g.lda + 4 * (ln >> 4), 16 * q, g.k - 4 * (ln >> 4));
+    }
+  };
+  auto store_a_chunk = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < A_PER_T; ++r) s_a[buf][tid + r * kThreads] = areg[r];
+  };
+
+  const BV* bbase = reinterpret_cast<const BV*>(g.bp) + (size_t)slab * g.q_total * 4 * 64 + lane;
+  BV rb[R][4];
+  auto issue_b = [&](int q, int slot) {
+    q = min(q, q1 - 1);  // clamped refetches hit the cache: no extra HBM traffic
+    const BV* bq = bbase + (size_t)q * 4 * 64;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rb[slot][e] = bq[e * 64];
+  };
+
+  v4f acc[MT][PW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int p = 0; p < PW; ++p) acc[mt][p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  load_a_chunk(0);
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue_b(q0 + d, d);
+  store_a_chunk(0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;  // workgroup-uniform
+    if (more) load_a_chunk(c + 1);
+    const float4* sa = s_a[c & 1];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int q = q0 + c * KC + j;
+      issue_b(q + DEPTH, (j + DEPTH) % R);
+      sched_fence();
+      if (q < q1) {
+        float4 af[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[mt] = sa[(j * MT + mt) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const float av = e == 0 ? af[mt].x : (e == 1 ? af[mt].y : (e == 2 ? af[mt].z : af[mt].w));
+#pragma unroll
+            for (int p = 0; p < PW; ++p)
+              acc[mt][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, PVec<PW>::get(rb[j][e], p), acc[mt][p], 0, 0, 0);
+          }
+      }
+      sched_fence();
+    }
+    if (more) store_a_chunk((c + 1) & 1);
+    __syncthreads();
+  }
+  if (slab_id < g.slabs) store_tile<MT, PW, EPI>(g, acc, m0, slab, z, lane);
+}
+
+// Pair-pack partials [splits, M, 2N] (up, gate interleaved per column) -> out[M, N] =
+// (sum up + b1) * silu(sum gate + b3), sums in split order (elementwise.rs:118-207).
+__global__ void splitk_swiglu_kernel(const float* __restrict__ parts, int splits, const float* __restrict__ b_up,
+                                     const float* __restrict__ b_gate, int m, int n, float* __restrict__ out) {
+  const size_t total = (size_t)m * n;
+  const size_t plane2 = total;  // float2 elements per split plane
+  const float2* p2 = reinterpret_cast<const float2*>(parts);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    float2 x = p2[i];
+    for (int z0 = 1; z0 < splits; z0 += 8) {
+      float2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p2[(size_t)(z0 + u < splits ? z0 + u : 0) * plane2 + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (z0 + u < splits) {
+          x.x = x.x + v[u].x;
+          x.y = x.y + v[u].y;
+        }
+    }
+    const int c = static_cast<int>(i % n);
+    const float up = b_up ? x.x + b_up[c] : x.x;
+    float gate = b_gate ? x.y + b_gate[c] : x.y;
+    gate = gate * (1.0f / (1.0f + __expf(-gate)));
+    out[i] = up * gate;
   }
 }
 
@@ -510,30 +638,81 @@ int32_t q_steps(int32_t k) { return (k + 15) / 16; }
 
 int32_t slabs_of(int32_t n, int32_t pw, bool pair) { return pair ? (n + 15) / 16 : (n + 16 * pw - 1) / (16 * pw); }
 
+// Row-block height for M rows: 16, 32 or 64.
+int mtiles_for(int m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
+
+// Kernel choice for a launch shape.  The shared-activation kernel (4 slabs per workgroup,
+// activations read once per workgroup) wins whenever there are enough slab groups to fill the
+// device; narrow weights at decode M keep one slab per workgroup (4 waves splitting K), which
+// has 4x the workgroups.  Pack width 4 tiles are too register-heavy for the shared variant.
+struct Plan {
+  bool shared;
+  int mt;
+  int mblocks;
+  int blocks;  // workgroups per split
+};
+
+Plan plan_for(int m, int slabs, int pw) {
+  Plan p{};
+  p.mt = mtiles_for(m);
+  p.mblocks = (m + 16 * p.mt - 1) / (16 * p.mt);
+  const int groups = (slabs + kWaves - 1) / kWaves;
+  p.shared = pw <= 2 && groups * p.mblocks >= 64;
+  p.blocks = (p.shared ? groups : slabs) * p.mblocks;
+  return p;
+}
+
+// Split count: enough workgroups to give every CU two, every split at least 8 (shared) or
+// 16 (per-wave quarters) K steps, and the partials (splits x M x N floats) at most a quarter
+// of the weight bytes (K x N floats) for M >= 16.
+int split_count(fi_context* ctx, int m, int k, int slabs, int pw) {
+  const Plan p = plan_for(m, slabs, pw);
+  const int q = q_steps(k);
+  const long target = 2L * (ctx->compute_units > 0 ? ctx->compute_units : 256);
+  long s = std::max(1L, (target + p.blocks - 1) / p.blocks);
+  s = std::min(s, std::max(1L, static_cast<long>(q / (p.shared ? 8 : 16))));
+  s = std::min(s, std::max(1L, static_cast<long>(k) / (4L * std::max(m, 16))));
+  s = std::min(s, 16L);
+  const int per = (q + static_cast<int>(s) - 1) / static_cast<int>(s);
+  return (q + per - 1) / per;  // every split non-empty
+}
+
+template <int MT, int PW, int EPI, bool KTAIL>
+void launch_one(fi_context* ctx, const PGemmArgs& g, const Plan& p, unsigned splits) {
+  if constexpr (PW <= 2) {
+    if (p.shared) {
+      dim3 grid(static_cast<unsigned>((g.slabs + kWaves - 1) / kWaves), p.mblocks, splits);
+      hipLaunchKernelGGL((gemm_lds_kernel<MT, PW, EPI, KTAIL>), grid, dim3(kThreads), 0, ctx->stream, g);
+      return;
+    }
+  }
+  dim3 grid(static_cast<unsigned>(g.slabs), p.mblocks, splits);
+  hipLaunchKernelGGL((gemm_packed_kernel<MT, PW, EPI, KTAIL>), grid, dim3(kThreads), 0, ctx->stream, g);
+}
+
 template <int PW, int EPI>
 int32_t launch_pgemm(fi_context* ctx, const PGemmArgs& g, int splits) {
-  const int mt = g.m <= 16 ? 1 : (g.m <= 32 ? 2 : 4);
-  const unsigned mblocks = static_cast<unsigned>((g.m + 16 * mt - 1) / (16 * mt));
-  dim3 grid(static_cast<unsigned>(g.slabs), mblocks, static_cast<unsigned>(splits));
+  const Plan p = plan_for(g.m, g.slabs, PW);
+  const unsigned sp = static_cast<unsigned>(splits);
   const bool tail = g.k % 16 != 0;
-  switch (mt * 2 + (tail ? 1 : 0)) {
+  switch (p.mt * 2 + (tail ? 1 : 0)) {
     case 2:
-      hipLaunchKernelGGL((gemm_packed_kernel<1, PW, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+      launch_one<1, PW, EPI, false>(ctx, g, p, sp);
       break;
     case 3:
-      hipLaunchKernelGGL((gemm_packed_kernel<1, PW, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+      launch_one<1, PW, EPI, true>(ctx, g, p, sp);
       break;
     case 4:
-      hipLaunchKernelGGL((gemm_packed_kernel<2, PW, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+      launch_one<2, PW, EPI, false>(ctx, g, p, sp);
       break;
     case 5:
-      hipLaunchKernelGGL((gemm_packed_kernel<2, PW, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+      launch_one<2, PW, EPI, true>(ctx, g, p, sp);
       break;
     case 8:
-      hipLaunchKernelGGL((gemm_packed_kernel<4, PW, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+      launch_one<4, PW, EPI, false>(ctx, g, p, sp);
       break;
     default:
-      hipLaunchKernelGGL((gemm_packed_kernel<4, PW, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+      launch_one<4, PW, EPI, true>(ctx, g, p, sp);
       break;
   }
   FI_CHECK_LAUNCH("gemm_packed_kernel");
@@ -607,14 +786,7 @@ int32_t fi_gemm_packed_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, 
   FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
              "fi_gemm_packed_splits: pack width must be 1, 2 or 4");
   FI_REQUIRE(splits != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_packed_splits: null output");
-  // enough workgroups for two per CU, each wave keeping at least 4 K steps
-  const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-  const long tiles = static_cast<long>(slabs_of(n, pack_width, false)) * std::max(1, (m + 16 * mt - 1) / (16 * mt));
-  const long target = 2L * (ctx->compute_units > 0 ? ctx->compute_units : 256);
-  int s = static_cast<int>(std::max(1L, (target + tiles - 1) / tiles));
-  s = std::min(std::min(s, std::max(1, q_steps(k) / (4 * kWaves))), 16);
-  const int per = (q_steps(k) + s - 1) / s;  // K steps per split; every split non-empty
-  *splits = (q_steps(k) + per - 1) / per;
+  *splits = split_count(ctx, m, k, slabs_of(n, pack_width, false), pack_width);
   return FI_OK;
 }
 
@@ -658,17 +830,32 @@ int32_t fi_gemm_packed_swiglu(fi_context* ctx, const float* d_a, int32_t lda, co
   PGemmArgs g{};
   g.a = d_a;
   g.bp = d_bp_pair;
-  g.out = d_out;
   g.bias0 = d_bias_up;
   g.bias1 = d_bias_gate;
   g.m = m;
   g.k = k;
-  g.n = n;
   g.lda = lda;
   g.q_total = q_steps(k);
-  g.q_per_split = g.q_total;
   g.slabs = slabs_of(n, 2, true);
-  return launch_pgemm<2, kEpiSwiglu>(ctx, g, 1);
+  const int splits = split_count(ctx, m, k, g.slabs, 2);
+  if (splits == 1) {  // the epilogue applies SwiGLU directly
+    g.out = d_out;
+    g.n = n;
+    g.q_per_split = g.q_total;
+    return launch_pgemm<2, kEpiSwiglu>(ctx, g, 1);
+  }
+  // partial (up, gate) pairs per split, then the split sum + SwiGLU
+  FI_TRY(fi::ensure_workspace(ctx, (size_t)splits * m * 2 * n * sizeof(float)));
+  g.out = static_cast<float*>(ctx->workspace);
+  g.n = 2 * n;
+  g.q_per_split = (g.q_total + splits - 1) / splits;
+  FI_TRY((launch_pgemm<2, kEpiPartial>(ctx, g, splits)));
+  const size_t total = (size_t)m * n;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 4096));
+  hipLaunchKernelGGL(splitk_swiglu_kernel, dim3(blocks), dim3(256), 0, ctx->stream, g.out, splits, d_bias_up,
+                     d_bias_gate, m, n, d_out);
+  FI_CHECK_LAUNCH("splitk_swiglu_kernel");
+  return FI_OK;
 }
 
 int32_t fi_lm_head_argmax_packed(fi_context* ctx, const float* d_hidden, int32_t lda, const float* d_bp, int32_t m,
