@@ -12,9 +12,12 @@
 namespace {
 
 // Tunables (compile-time).  The wave chunk fixes the reduction order for a given context
-// length, so it is a constant of the library, not of a launch.
-#ifndef FI_DECODE_WAVE_TOKENS
-#define FI_DECODE_WAVE_TOKENS 128  // context tokens per wave per partition
+// length and model shape, so it is a constant of the library, not of a launch.
+#ifndef FI_DECODE_WIDE_WAVE_TOKENS
+#define FI_DECODE_WIDE_WAVE_TOKENS 128  // context tokens per wave when Hkv * D >= 512
+#endif
+#ifndef FI_DECODE_NARROW_WAVE_TOKENS
+#define FI_DECODE_NARROW_WAVE_TOKENS 64  // narrow KV rows (few, small heads): more workgroups
 #endif
 #ifndef FI_DECODE_INFLIGHT_BYTES
 #define FI_DECODE_INFLIGHT_BYTES 16384  // f32 K or V bytes each wave keeps in flight (bf16: half)
@@ -22,10 +25,12 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kWaveTokens = FI_DECODE_WAVE_TOKENS;
-constexpr int kPartTokens = kWaves * kWaveTokens;
-constexpr int kMaxParts = 256;    // merge weights live in LDS
-constexpr int kMaxContext = kPartTokens * kMaxParts;
+constexpr int kMaxParts = 256;  // merge weights live in LDS
+
+// Tokens per wave for a model shape (never a batch property: outputs stay batch-invariant).
+constexpr int wave_tokens_for(int hkv, int d) {
+  return hkv * d >= 512 ? FI_DECODE_WIDE_WAVE_TOKENS : FI_DECODE_NARROW_WAVE_TOKENS;
+}
 
 constexpr int clamp_int(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
@@ -90,13 +95,13 @@ __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMI
 // before it stay ahead of the arithmetic after it (the ring's depth is what stays in flight).
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// One workgroup = one (sequence, kv_head, partition of kPartTokens tokens); partitions are
+// One workgroup = one (sequence, kv_head, partition of 4*WT tokens); partitions are
 // numbered fastest across (sequence, kv_head) so the first-dispatched workgroups hold the
 // full leading partitions and the ragged tails come last.  The GQA group of query heads
 // sharing the kv head is processed together so every K/V byte is read once.
 //   setup: the partition's token -> pool row indices go to LDS (block-table lookups) while
 //     each lane loads its slice of the group's query rows into registers;
-//   each wave then owns kWaveTokens consecutive tokens and runs on its own (no workgroup
+//   each wave then owns WT consecutive tokens and runs on its own (no workgroup
 //   barrier until the combine):
 //     K: KL lanes share a token row with 16-byte loads, a compile-time ring keeps
 //        ~FI_DECODE_INFLIGHT_BYTES of K in flight, dot products are reduced across the
@@ -109,8 +114,10 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // Rows past the end are clamped to the last valid row (same addresses, no extra traffic)
 // and carry probability 0.  A sequence with one partition writes its normalised output;
 // otherwise each workgroup stores (max, sum, unnormalised acc) for decode_merge_kernel.
-template <int D, typename KVT, int G>
+template <int D, typename KVT, int G, int WT>
 __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a) {
+  constexpr int kWaveTokens = WT;
+  constexpr int kPartTokens = kWaves * WT;
   using IO = KvIO<KVT>;
   using Raw = typename IO::Raw;
   constexpr int EPV = IO::kVecElems;          // elements per 16-byte vector
@@ -352,8 +359,9 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
 // single partition were finished by the partition kernel.  A separate launch orders the
 // partials' stores before these loads.  The first partitions' partials are fetched before
 // the weights are known so the loads overlap.
-template <int D, int MAXG>
+template <int D, int MAXG, int WT>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int kPartTokens = kWaves * WT;
   constexpr int kPrefetch = 8;
   constexpr int kPerThread = (MAXG * D + kThreads - 1) / kThreads;
   __shared__ float s_w[MAXG][kMaxParts];
@@ -483,31 +491,43 @@ int32_t zero_async(fi_context* ctx, void* p, size_t bytes) {
   return FI_OK;
 }
 
-template <int D, typename KVT, int MAXG>
-int32_t launch_decode_group(fi_context* ctx, const DecodeArgs& args, unsigned grid) {
-  hipLaunchKernelGGL((decode_partition_kernel<D, KVT, MAXG>), dim3(grid), dim3(kThreads), 0, ctx->stream, args);
+template <int D, typename KVT, int G>
+int32_t launch_decode_group(fi_context* ctx, const DecodeArgs& args, unsigned grid, int wt) {
+  if (wt == FI_DECODE_WIDE_WAVE_TOKENS) {
+    hipLaunchKernelGGL((decode_partition_kernel<D, KVT, G, FI_DECODE_WIDE_WAVE_TOKENS>), dim3(grid), dim3(kThreads), 0,
+                       ctx->stream, args);
+  } else {
+    hipLaunchKernelGGL((decode_partition_kernel<D, KVT, G, FI_DECODE_NARROW_WAVE_TOKENS>), dim3(grid), dim3(kThreads),
+                       0, ctx->stream, args);
+  }
   FI_CHECK_LAUNCH("decode_partition_kernel");
   if (args.parts_per_seq > 1) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, MAXG>), dim3(static_cast<unsigned>(args.num_seqs) * args.hkv),
-                       dim3(kThreads), 0, ctx->stream, args);
+    const dim3 grid2(static_cast<unsigned>(args.num_seqs) * args.hkv);
+    if (wt == FI_DECODE_WIDE_WAVE_TOKENS) {
+      hipLaunchKernelGGL((decode_merge_kernel<D, G, FI_DECODE_WIDE_WAVE_TOKENS>), grid2, dim3(kThreads), 0, ctx->stream,
+                         args);
+    } else {
+      hipLaunchKernelGGL((decode_merge_kernel<D, G, FI_DECODE_NARROW_WAVE_TOKENS>), grid2, dim3(kThreads), 0,
+                         ctx->stream, args);
+    }
     FI_CHECK_LAUNCH("decode_merge_kernel");
   }
   return FI_OK;
 }
 
 template <int D, typename KVT>
-int32_t launch_decode(fi_context* ctx, const DecodeArgs& args, unsigned grid) {
-  if (args.group <= 1) return launch_decode_group<D, KVT, 1>(ctx, args, grid);
-  if (args.group <= 2) return launch_decode_group<D, KVT, 2>(ctx, args, grid);
-  if (args.group <= 4) return launch_decode_group<D, KVT, 4>(ctx, args, grid);
-  if (args.group <= 8) return launch_decode_group<D, KVT, 8>(ctx, args, grid);
+int32_t launch_decode(fi_context* ctx, const DecodeArgs& args, unsigned grid, int wt) {
+  if (args.group <= 1) return launch_decode_group<D, KVT, 1>(ctx, args, grid, wt);
+  if (args.group <= 2) return launch_decode_group<D, KVT, 2>(ctx, args, grid, wt);
+  if (args.group <= 4) return launch_decode_group<D, KVT, 4>(ctx, args, grid, wt);
+  if (args.group <= 8) return launch_decode_group<D, KVT, 8>(ctx, args, grid, wt);
   return fi::set_error(FI_ERR_UNSUPPORTED, "decode attention supports at most 8 query heads per KV head");
 }
 
 template <int D>
-int32_t launch_decode_dtype(fi_context* ctx, int32_t dtype, const DecodeArgs& args, unsigned grid) {
-  if (dtype == FI_DTYPE_F32) return launch_decode<D, float>(ctx, args, grid);
-  return launch_decode<D, uint16_t>(ctx, args, grid);
+int32_t launch_decode_dtype(fi_context* ctx, int32_t dtype, const DecodeArgs& args, unsigned grid, int wt) {
+  if (dtype == FI_DTYPE_F32) return launch_decode<D, float>(ctx, args, grid, wt);
+  return launch_decode<D, uint16_t>(ctx, args, grid, wt);
 }
 
 }  // namespace
@@ -607,16 +627,18 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
              "fi_attn_decode_paged: pool dimensions must be greater than zero");
   FI_REQUIRE(kv_dtype == FI_DTYPE_F32 || kv_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
              "fi_attn_decode_paged: KV dtype must be f32 or bf16");
-  FI_REQUIRE(max_context_len <= kMaxContext, FI_ERR_UNSUPPORTED,
-             "fi_attn_decode_paged: context longer than " + std::to_string(kMaxContext) + " tokens");
   FI_REQUIRE(static_cast<int64_t>(max_context_len) <= static_cast<int64_t>(max_blocks_per_seq) * block_size,
              FI_ERR_INVALID_SHAPE, "fi_attn_decode_paged: max_context_len exceeds the block-table width");
   FI_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128, FI_ERR_UNSUPPORTED,
              "fi_attn_decode_paged: head_dim must be 32, 64 or 128");
+  const int wt = wave_tokens_for(num_kv_heads, head_dim);
+  const int part_tokens = kWaves * wt;
+  FI_REQUIRE(max_context_len <= part_tokens * kMaxParts, FI_ERR_UNSUPPORTED,
+             "fi_attn_decode_paged: context longer than " + std::to_string(part_tokens * kMaxParts) + " tokens");
   if (num_seqs == 0) return FI_OK;
   FI_REQUIRE(d_q && d_k_cache && d_v_cache && d_block_tables && d_context_lens && d_out,
              FI_ERR_INVALID_CONFIG, "fi_attn_decode_paged: null pointer");
-  const int32_t parts = max_context_len == 0 ? 1 : (max_context_len + kPartTokens - 1) / kPartTokens;
+  const int32_t parts = max_context_len == 0 ? 1 : (max_context_len + part_tokens - 1) / part_tokens;
   DecodeArgs args{};
   args.q = d_q;
   args.k_cache = d_k_cache;
@@ -640,11 +662,11 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
   const unsigned grid = static_cast<unsigned>(num_seqs) * num_kv_heads * parts;
   switch (head_dim) {
     case 32:
-      return launch_decode_dtype<32>(ctx, kv_dtype, args, grid);
+      return launch_decode_dtype<32>(ctx, kv_dtype, args, grid, wt);
     case 64:
-      return launch_decode_dtype<64>(ctx, kv_dtype, args, grid);
+      return launch_decode_dtype<64>(ctx, kv_dtype, args, grid, wt);
     default:
-      return launch_decode_dtype<128>(ctx, kv_dtype, args, grid);
+      return launch_decode_dtype<128>(ctx, kv_dtype, args, grid, wt);
   }
 }
 

@@ -132,8 +132,8 @@ int32_t fi_ctx_check_faults(fi_context* ctx);
 
 /* Paged decode attention, one query token per sequence, all keys [0, context_len) read
  * through the block table (the current token's K/V must already be appended).
- * Split-KV over fixed 512-token partitions with a log-sum-exp merge, so the summation order
- * depends only on context_len.  Replaces, per sequence, read_prefix_f32 +
+ * Split-KV over fixed partitions (512 tokens when Hkv * D >= 512, else 256) with a
+ * log-sum-exp merge, so the summation order depends only on context_len and the model shape.  Replaces, per sequence, read_prefix_f32 +
  * cached_prefixed_causal_attention_f32 (runtime/reference.rs:497-508,
  * runtime/paged_kv.rs:769-791, kernel/cpu/attention.rs:332-518) and
  * decode_causal_attention_f32 (kernel/cpu/attention.rs:520-686).

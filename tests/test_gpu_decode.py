@@ -115,6 +115,32 @@ def test_decode_batch_invariance(gpu_ctx):
         assert np.array_equal(alone[0], full[i])
 
 
+@pytest.mark.parametrize("shape", [(32, 8, 128), (14, 2, 64)])
+def test_decode_split_merge_repeatable(gpu_ctx, shape):
+    """Sequences spanning several partitions go through the split-KV partials and the merge
+    kernel.  Thirty back-to-back launches sharing one workspace must give bit-identical
+    outputs: the partition size depends only on the model shape and every summation order is
+    fixed."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    hq, hkv, d = shape
+    wl = paged_decode_c2(seed=5, num_seqs=48, min_len=600, max_len=2048, num_q_heads=hq,
+                         num_kv_heads=hkv, head_dim=d, num_blocks=8192)
+    kp, vp = _dev(wl.k_pool, torch), _dev(wl.v_pool, torch)
+    q, bt, cl = _dev(wl.q, torch), _dev(wl.block_tables, torch), _dev(wl.context_lens, torch)
+    outs = [torch.empty_like(q) for _ in range(30)]
+    for o in outs:
+        gpu_ctx.attn_decode_paged(q, kp, vp, DTYPE_F32, bt, cl, wl.max_context_len, hkv,
+                                  wl.block_size, wl.num_blocks, wl.scale, o)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 def test_kv_append_scatter_exact(orc, gpu_ctx, kv_dtype):
     """fi_kv_append writes each token row to block_id*bs+offset, bit-exact (bf16: RNE)."""
