@@ -235,7 +235,7 @@ def kernel_legs(ctx, seed):
     flops = wl.attention_flops()
     ab = wl.append_bytes(4)
     out["c3_prefill_attention"] = {
-        "kernel": "prefill_attention_kernel", "bound": "mfma (f32)",
+        "kernel": "prefill_kernel", "bound": "mfma (f32)",
         "tokens": T, "flops_per_launch": flops, "avg_launch_us": round(ms_p * 1e3, 2),
         "achieved_tflops": round(flops / (ms_p * 1e-3) / 1e12, 2), "peak_tflops": FP32_PEAK_TFS,
         "frac": round(flops / (ms_p * 1e-3) / 1e12 / FP32_PEAK_TFS, 4)}

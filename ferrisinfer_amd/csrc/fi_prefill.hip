@@ -6,11 +6,17 @@
 //
 // Sequence b has qlen_b = cu_seqlens[b+1] - cu_seqlens[b] new query tokens at positions
 // [ctx_b - qlen_b, ctx_b); query position p attends keys [0, p] read through the block table
-// (its own K/V rows must already be appended).  One workgroup = (sequence, query head,
-// 64-token query tile): 4 waves x 16 query rows.  Per 32-key tile: K and V are staged in LDS
-// (bf16 widened), S = Q K^T on MFMA with Q held in registers, causal mask + online softmax
-// with row reductions by DPP across the 16 lanes holding a row, P is moved through LDS from
-// the accumulator layout to the A-operand layout, and O += P V on MFMA.
+// (its own K/V rows must already be appended).
+//
+// One workgroup = (sequence, kv head, tile of 64/G query tokens) with all G query heads of the
+// GQA group: 64 (head, token) rows, 16 per wave, so every K/V byte a workgroup stages serves
+// G heads.  Keys are processed in chunks of 32: the chunk's K and V rows are staged in LDS
+// (16-byte loads; bf16 widened), the next chunk's rows are fetched into registers while the
+// current one is multiplied, two barriers per chunk.  Per wave and chunk: S = Q K^T on MFMA
+// with Q held in registers, causal mask + online softmax with DPP row reductions, P through
+// the wave's LDS slice into the A-operand layout, O += P V on MFMA.  The d index of the Q K^T
+// contraction and the key index of the P V contraction are visited in a permuted order so
+// every LDS operand read is one 16-byte read; the sums are the same products.
 #include "fi_common.h"
 #include "fi_device.h"
 
@@ -18,9 +24,9 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kQTile = 64;    // query tokens per workgroup
-constexpr int kKTile = 32;    // keys per LDS tile
 constexpr int kThreads = 256;
+constexpr int kRows = 64;     // (head, token) rows per workgroup
+constexpr int kKeys = 32;     // keys per staged chunk
 
 struct PrefillArgs {
   const float* q;            // [T, Hq, D]
@@ -35,6 +41,7 @@ struct PrefillArgs {
   int hq, hkv, group;
   int block_size, num_blocks;
   float scale;
+  int cu_seqlens_count;      // number of sequences (grid y)
 };
 
 template <int kLanes>
@@ -46,44 +53,81 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
-__device__ __forceinline__ float load_kv(const float* p) { return *p; }
-__device__ __forceinline__ float load_kv(const uint16_t* p) { return fi::bf16_bits_to_f32(*p); }
+// Four consecutive K/V elements of one row as raw registers, widened when staged.
+template <typename KVT>
+struct Quad;
+template <>
+struct Quad<float> {
+  using Raw = float4;
+  __device__ static Raw load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  __device__ static float4 widen(const Raw& r) { return r; }
+  __device__ static Raw zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+};
+template <>
+struct Quad<uint16_t> {
+  using Raw = uint2;
+  __device__ static Raw load(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+  __device__ static float4 widen(const Raw& r) {
+    return make_float4(fi::bf16_bits_to_f32(r.x & 0xffffu), fi::bf16_bits_to_f32(r.x >> 16),
+                       fi::bf16_bits_to_f32(r.y & 0xffffu), fi::bf16_bits_to_f32(r.y >> 16));
+  }
+  __device__ static Raw zero() { return make_uint2(0u, 0u); }
+};
 
-template <int D, typename KVT>
+__device__ __forceinline__ float pick(const float4& v, int e) {
+  return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+}
+
+template <int D, typename KVT, int G>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
-  constexpr int KSTEPS = D / 4;      // MFMA k-steps over the head dimension
-  constexpr int DT = D / 16;         // 16-wide output column tiles
-  __shared__ float Ks[kKTile][D + 1];
-  __shared__ float Vs[kKTile][D + 4];
-  __shared__ float Ps[4][16][kKTile + 1];
-  __shared__ int s_row[kKTile];
+  using QD = Quad<KVT>;
+  constexpr int QT = kRows / G;           // query tokens per workgroup
+  constexpr int DV = D / 4;               // 4-element quads per row
+  constexpr int DS = D / 16;              // 16-wide d steps of the Q K^T contraction
+  constexpr int DH = D / 64 > 0 ? D / 64 : 1;  // 64-wide halves of the output (D = 32: one, masked)
+  constexpr int QUADS = kKeys * DV;       // quads per staged K (or V) chunk
+  constexpr int PER_T = (QUADS + kThreads - 1) / kThreads;
+  static_assert(QUADS % kThreads == 0, "chunk must split evenly over the workgroup");
+  __shared__ float4 Ks[kKeys][DV + 1];
+  __shared__ float4 Vs[kKeys][DV + 1];
+  __shared__ __align__(16) float Ps[4][16][kKeys + 4];
 
   const KVT* __restrict__ k_cache = static_cast<const KVT*>(a.k_cache);
   const KVT* __restrict__ v_cache = static_cast<const KVT*>(a.v_cache);
-  const int qt = blockIdx.x, seq = blockIdx.y, h = blockIdx.z;
+  const int qt = blockIdx.x, seq = blockIdx.y, kvh = blockIdx.z;
   const int qs = a.cu_seqlens[seq];
   const int qlen = a.cu_seqlens[seq + 1] - qs;
-  const int q0 = qt * kQTile;
+  const int q0 = qt * QT;
   if (q0 >= qlen) return;
   const int ctx = a.context_lens[seq];
   const int start = ctx - qlen;  // position of the first query token
-  const int kvh = h / a.group;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lk = lane >> 4;
-  const int r0 = q0 + w * 16;  // first query row (within the sequence) of this wave
 
-  // Q fragment: A[i][k] = Q[r0 + li][4*step + lk]
-  float qreg[KSTEPS];
+  // A operand rows: row i = 16w + li -> (head h, token t) = (i / QT, i % QT)
+  const int arow = 16 * w + li;
+  const int ah = arow / QT, at = arow % QT;
+  const bool a_ok = ah < a.group && q0 + at < qlen;
+  float4 qf[DS];
   {
-    const int row = r0 + li;
-    const float* qp = a.q + ((size_t)(qs + min(row, qlen - 1)) * a.hq + h) * D;
+    const float* qp = a.q + ((size_t)(qs + q0 + (a_ok ? at : 0)) * a.hq + kvh * a.group + (a_ok ? ah : 0)) * D;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) qreg[s] = qp[4 * s + lk];
+    for (int t = 0; t < DS; ++t)
+      qf[t] = a_ok ? *reinterpret_cast<const float4*>(qp + 16 * t + 4 * lk) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
-  v4f o[DT];
+  // accumulator rows of this lane: r = 16w + 4lk + v -> query position
+  int qpos[4];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) o[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int v = 0; v < 4; ++v) {
+    const int r = 16 * w + 4 * lk + v;
+    qpos[v] = start + q0 + r % QT;
+  }
+  v4f o[DH][4];
+#pragma unroll
+  for (int h = 0; h < DH; ++h)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) o[h][p] = v4f{0.f, 0.f, 0.f, 0.f};
   float m_row[4], l_row[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -91,60 +135,75 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     l_row[v] = 0.0f;
   }
 
-  const int kend = start + min(qlen, q0 + kQTile);  // keys needed by the last row of the tile
-  for (int k0 = 0; k0 < kend; k0 += kKTile) {
-    // ---- stage K and V rows [k0, k0 + 32) ----
-    if (tid < kKTile) {
-      const int kp = k0 + tid;
-      int row = -1;
-      if (kp < ctx) {
-        const int lb = kp / a.block_size;
-        int id = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
-        if (id < 0 || id >= a.num_blocks) {
-          atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
-          id = 0;
-        }
-        row = (id * a.hkv + kvh) * a.block_size + (kp - lb * a.block_size);
-      }
-      s_row[tid] = row;
-    }
-    __syncthreads();
-    for (int i = tid; i < kKTile * D; i += kThreads) {
-      const int j = i / D, d = i % D;
-      const int row = s_row[j];
-      float kv = 0.0f, vv = 0.0f;
-      if (row >= 0) {
-        kv = load_kv(k_cache + (size_t)row * D + d);
-        vv = load_kv(v_cache + (size_t)row * D + d);
-      }
-      Ks[j][d] = kv;
-      Vs[j][d] = vv;
-    }
-    __syncthreads();
+  const int kend = start + min(qlen, q0 + QT);  // keys needed by the tile's last token
+  const int nchunks = (kend + kKeys - 1) / kKeys;
 
-    // ---- S = Q K^T for this wave's 16 rows x 32 keys ----
-    v4f s_acc[2] = {v4f{0.0f, 0.0f, 0.0f, 0.0f}, v4f{0.0f, 0.0f, 0.0f, 0.0f}};
+  // chunk staging: quad i = tid + r * kThreads -> key i / DV, quad column i % DV.  Branch-free:
+  // keys past kend re-read the last needed row and are zeroed by a select (a divergent branch
+  // around the loads would make the compiler drain every outstanding load at its merge).
+  typename QD::Raw kr[PER_T], vr[PER_T];
+  bool bad_block = false;
+  auto fetch = [&](int c) {
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
+    for (int r = 0; r < PER_T; ++r) {
+      const int i = tid + r * kThreads;
+      const int key = i / DV, col = i % DV;
+      const int kp = c * kKeys + key;
+      const bool valid = kp < kend;
+      const int kpc = max(valid ? kp : kend - 1, 0);  // kend <= 0 only when ctx < qlen
+      const int lb = kpc / a.block_size;
+      int id = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
+      const bool bad = id < 0 || id >= a.num_blocks;
+      bad_block |= bad;
+      id = bad ? 0 : id;
+      const size_t row = ((size_t)id * a.hkv + kvh) * a.block_size + (kpc - lb * a.block_size);
+      const typename QD::Raw kx = QD::load(k_cache + row * D + 4 * col);
+      const typename QD::Raw vx = QD::load(v_cache + row * D + 4 * col);
+      kr[r] = valid ? kx : QD::zero();
+      vr[r] = valid ? vx : QD::zero();
+    }
+  };
+  auto stage = [&]() {
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        const float b = Ks[jt * 16 + li][4 * s + lk];
-        s_acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[s], b, s_acc[jt], 0, 0, 0);
+    for (int r = 0; r < PER_T; ++r) {
+      const int i = tid + r * kThreads;
+      Ks[i / DV][i % DV] = QD::widen(kr[r]);
+      Vs[i / DV][i % DV] = QD::widen(vr[r]);
+    }
+  };
+
+  fetch(0);
+  stage();
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int k0 = c * kKeys;
+    if (c + 1 < nchunks) fetch(c + 1);
+
+    // ---- S = Q K^T: 16 rows x 32 keys (2 key tiles) ----
+    v4f s_acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+      const float4 kb0 = Ks[li][4 * t + lk];
+      const float4 kb1 = Ks[16 + li][4 * t + lk];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float av = pick(qf[t], e);
+        s_acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pick(kb0, e), s_acc[0], 0, 0, 0);
+        s_acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pick(kb1, e), s_acc[1], 0, 0, 0);
       }
     }
-    // element (jt, v): row r0 + 4*lk + v, key k0 + 16*jt + li
-    float p[2][4];
+    // element (jt, v): row 16w + 4lk + v, key k0 + 16jt + li
+    float pv[2][4];
     float alpha[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int qpos = start + r0 + 4 * lk + v;
       float mx = -INFINITY;
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
         const int kp = k0 + 16 * jt + li;
         const float sv = s_acc[jt][v] * a.scale;
-        p[jt][v] = (kp <= qpos && kp < ctx) ? sv : -INFINITY;
-        mx = fmaxf(mx, p[jt][v]);
+        pv[jt][v] = (kp <= qpos[v] && kp < ctx) ? sv : -INFINITY;
+        mx = fmaxf(mx, pv[jt][v]);
       }
       mx = group_max<16>(mx);
       const float m_new = fmaxf(m_row[v], mx);
@@ -152,56 +211,99 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       float ls = 0.0f;
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
-        p[jt][v] = p[jt][v] == -INFINITY ? 0.0f : __expf(p[jt][v] - m_new);
-        ls += p[jt][v];
+        pv[jt][v] = pv[jt][v] == -INFINITY ? 0.0f : __expf(pv[jt][v] - m_new);
+        ls += pv[jt][v];
       }
       ls = fi::group_sum<16>(ls);
       l_row[v] = l_row[v] * alpha[v] + ls;
       m_row[v] = m_new;
     }
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+    for (int h = 0; h < DH; ++h)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o[t][v] *= alpha[v];
-    // P to LDS in accumulator layout, read back as the A operand
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[h][p][v] *= alpha[v];
+    // P to the wave's LDS slice in accumulator layout; read back as the A operand
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) Ps[w][4 * lk + v][16 * jt + li] = p[jt][v];
-    __syncthreads();
-    // ---- O += P V ----
+      for (int v = 0; v < 4; ++v) Ps[w][4 * lk + v][16 * jt + li] = pv[jt][v];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+    // ---- O += P V: key k-step (u, e) covers keys 16u + 4lk + e ----
 #pragma unroll
-    for (int s = 0; s < kKTile / 4; ++s) {
-      const float pa = Ps[w][li][4 * s + lk];
+    for (int u = 0; u < kKeys / 16; ++u) {
+      const float4 pa = *reinterpret_cast<const float4*>(&Ps[w][li][16 * u + 4 * lk]);
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const float vb = Vs[4 * s + lk][16 * t + li];
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb, o[t], 0, 0, 0);
+      for (int e = 0; e < 4; ++e) {
+        const int key = 16 * u + 4 * lk + e;
+        const float av = pick(pa, e);
+#pragma unroll
+        for (int h = 0; h < DH; ++h) {
+          // output tile (h, p) column li <-> d = 64h + 4li + p
+          const float4 vb = (D >= 64 || h == 0) && (64 * h + 4 * li < D) ? Vs[key][16 * h + li]
+                                                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) o[h][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pick(vb, p), o[h][p], 0, 0, 0);
+        }
       }
     }
-    __syncthreads();
+    __syncthreads();  // every wave is done with this chunk's K/V
+    if (c + 1 < nchunks) {
+      stage();
+      __syncthreads();
+    }
   }
 
+  if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
+
+  // ---- normalise and store: lane holds rows 16w + 4lk + v, d = 64h + 4li + p ----
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const int row = r0 + 4 * lk + v;
-    if (row >= qlen) continue;
+    const int r = 16 * w + 4 * lk + v;
+    const int h = r / QT, t = r % QT;
+    if (h >= a.group || q0 + t >= qlen) continue;
     const float inv = 1.0f / l_row[v];
-    float* op = a.out + ((size_t)(qs + row) * a.hq + h) * D;
+    float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) op[16 * t + li] = o[t][v] * inv;
+    for (int hh = 0; hh < DH; ++hh) {
+      const int d0 = 64 * hh + 4 * li;
+      if (d0 < D) {
+        *reinterpret_cast<float4*>(op + d0) =
+            make_float4(o[hh][0][v] * inv, o[hh][1][v] * inv, o[hh][2][v] * inv, o[hh][3][v] * inv);
+      }
+    }
   }
 }
 
-template <int D>
-int32_t launch_prefill(fi_context* ctx, int32_t dtype, const PrefillArgs& args, dim3 grid) {
-  if (dtype == FI_DTYPE_F32) {
-    hipLaunchKernelGGL((prefill_kernel<D, float>), grid, dim3(kThreads), 0, ctx->stream, args);
-  } else {
-    hipLaunchKernelGGL((prefill_kernel<D, uint16_t>), grid, dim3(kThreads), 0, ctx->stream, args);
+template <int D, typename KVT>
+int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args, int max_query_len) {
+  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
+  const int qt = kRows / g;
+  const dim3 grid((max_query_len + qt - 1) / qt, args.cu_seqlens_count, args.hkv);
+  switch (g) {
+    case 1:
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    case 2:
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 2>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    case 4:
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 4>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    default:
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 8>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
   }
   FI_CHECK_LAUNCH("prefill_kernel");
   return FI_OK;
+}
+
+template <int D>
+int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& args, int max_query_len) {
+  if (dtype == FI_DTYPE_F32) return launch_prefill<D, float>(ctx, args, max_query_len);
+  return launch_prefill<D, uint16_t>(ctx, args, max_query_len);
 }
 
 }  // namespace
@@ -224,6 +326,8 @@ int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k
              "fi_attn_prefill_paged: KV dtype must be f32 or bf16");
   FI_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128, FI_ERR_UNSUPPORTED,
              "fi_attn_prefill_paged: head_dim must be 32, 64 or 128");
+  FI_REQUIRE(num_q_heads / num_kv_heads <= 8, FI_ERR_UNSUPPORTED,
+             "fi_attn_prefill_paged supports at most 8 query heads per KV head");
   if (num_seqs == 0 || max_query_len == 0) return FI_OK;
   FI_REQUIRE(d_q && d_k_cache && d_v_cache && d_block_tables && d_cu_seqlens && d_context_lens && d_out,
              FI_ERR_INVALID_CONFIG, "fi_attn_prefill_paged: null pointer");
@@ -243,14 +347,14 @@ int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k
   args.block_size = block_size;
   args.num_blocks = num_blocks;
   args.scale = scale;
-  dim3 grid((max_query_len + kQTile - 1) / kQTile, num_seqs, num_q_heads);
+  args.cu_seqlens_count = num_seqs;
   switch (head_dim) {
     case 32:
-      return launch_prefill<32>(ctx, kv_dtype, args, grid);
+      return launch_prefill_dtype<32>(ctx, kv_dtype, args, max_query_len);
     case 64:
-      return launch_prefill<64>(ctx, kv_dtype, args, grid);
+      return launch_prefill_dtype<64>(ctx, kv_dtype, args, max_query_len);
     default:
-      return launch_prefill<128>(ctx, kv_dtype, args, grid);
+      return launch_prefill_dtype<128>(ctx, kv_dtype, args, max_query_len);
   }
 }
 

@@ -53,6 +53,7 @@ CASES = [
     (8, 20, 200, 2, 4, 64, 8, 2, 32, 16),     # C1-shaped heads, block-shared prefixes
     (6, 30, 300, 2, 3, 128, 14, 2, 64, 16),   # Qwen2-shaped GQA 7
     (4, 100, 400, 1, 4, 96, 32, 8, 128, 8),   # block size 8
+    (3, 1, 150, 0, 1, 0, 4, 2, 128, 32),      # GQA 2, block size 32, 1-token prompts
 ]
 
 
