@@ -41,7 +41,8 @@ struct PrefillArgs {
   int hq, hkv, group;
   int block_size, num_blocks;
   float scale;
-  int cu_seqlens_count;      // number of sequences (grid y)
+  int num_seqs;
+  int max_query_len;
 };
 
 template <int kLanes>
@@ -94,7 +95,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
   const KVT* __restrict__ k_cache = static_cast<const KVT*>(a.k_cache);
   const KVT* __restrict__ v_cache = static_cast<const KVT*>(a.v_cache);
-  const int qt = blockIdx.x, seq = blockIdx.y, kvh = blockIdx.z;
+  // The 1-D grid is padded to a multiple of 8.  Hardware workgroup L runs on XCD L % 8; the
+  // logical tile (L % 8) * (grid / 8) + L / 8 gives each XCD a contiguous range of the order
+  // (tile fastest, then sequence, then KV head), so the tiles that re-read one sequence's K/V
+  // rows share an L2.
+  const int ntiles = (a.max_query_len + QT - 1) / QT;
+  const int logical = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+  if (logical >= ntiles * a.num_seqs * a.hkv) return;
+  const int qt = logical % ntiles;
+  const int seq = (logical / ntiles) % a.num_seqs, kvh = logical / (ntiles * a.num_seqs);
   const int qs = a.cu_seqlens[seq];
   const int qlen = a.cu_seqlens[seq + 1] - qs;
   const int q0 = qt * QT;
@@ -136,27 +145,39 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 
   const int kend = start + min(qlen, q0 + QT);  // keys needed by the tile's last token
-  const int nchunks = (kend + kKeys - 1) / kKeys;
+  const int nchunks = max((kend + kKeys - 1) / kKeys, 1);
 
-  // chunk staging: quad i = tid + r * kThreads -> key i / DV, quad column i % DV.  Branch-free:
-  // keys past kend re-read the last needed row and are zeroed by a select (a divergent branch
-  // around the loads would make the compiler drain every outstanding load at its merge).
+  // Chunk staging: quad i = tid + r * kThreads -> key i / DV, quad column i % DV.  The block
+  // ids of chunk c + 2 are loaded while chunk c is multiplied and the K/V rows of chunk c + 1
+  // are in flight, so no load waits on another.  Every load is unconditional (chunk index and
+  // key clamped, padding keys zeroed by a select): a divergent branch around a load makes the
+  // compiler drain all outstanding loads where the paths merge.
   typename QD::Raw kr[PER_T], vr[PER_T];
+  int ids[PER_T], offs[PER_T];
   bool bad_block = false;
-  auto fetch = [&](int c) {
+  auto lookup = [&](int c) {  // block ids and in-block rows of chunk c's keys
+    c = min(c, nchunks - 1);
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) {
+      const int key = (tid + r * kThreads) / DV;
+      const int kpc = max(min(c * kKeys + key, kend - 1), 0);  // kend <= 0 only when ctx < qlen
+      const int lb = kpc / a.block_size;
+      const bool in_table = lb < a.max_blocks;
+      ids[r] = a.block_tables[(size_t)seq * a.max_blocks + (in_table ? lb : 0)];
+      ids[r] = in_table ? ids[r] : -1;
+      offs[r] = kpc - lb * a.block_size;
+    }
+  };
+  auto fetch = [&](int c) {  // K/V quads of chunk c from the ids of the last lookup
+    c = min(c, nchunks - 1);
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int i = tid + r * kThreads;
       const int key = i / DV, col = i % DV;
-      const int kp = c * kKeys + key;
-      const bool valid = kp < kend;
-      const int kpc = max(valid ? kp : kend - 1, 0);  // kend <= 0 only when ctx < qlen
-      const int lb = kpc / a.block_size;
-      int id = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
-      const bool bad = id < 0 || id >= a.num_blocks;
+      const bool valid = c * kKeys + key < kend;
+      const bool bad = ids[r] < 0 || ids[r] >= a.num_blocks;
       bad_block |= bad;
-      id = bad ? 0 : id;
-      const size_t row = ((size_t)id * a.hkv + kvh) * a.block_size + (kpc - lb * a.block_size);
+      const size_t row = ((size_t)(bad ? 0 : ids[r]) * a.hkv + kvh) * a.block_size + offs[r];
       const typename QD::Raw kx = QD::load(k_cache + row * D + 4 * col);
       const typename QD::Raw vx = QD::load(v_cache + row * D + 4 * col);
       kr[r] = valid ? kx : QD::zero();
@@ -172,12 +193,16 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     }
   };
 
+  lookup(0);
   fetch(0);
+  lookup(1);
   stage();
   __syncthreads();
   for (int c = 0; c < nchunks; ++c) {
     const int k0 = c * kKeys;
-    if (c + 1 < nchunks) fetch(c + 1);
+    fetch(c + 1);   // the last chunk re-reads itself: the loads stay unconditional
+    lookup(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- S = Q K^T: 16 rows x 32 keys (2 key tiles) ----
     v4f s_acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
@@ -278,10 +303,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 }
 
 template <int D, typename KVT>
-int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args, int max_query_len) {
+int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args) {
+  const int max_query_len = args.max_query_len;
   const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
   const int qt = kRows / g;
-  const dim3 grid((max_query_len + qt - 1) / qt, args.cu_seqlens_count, args.hkv);
+  const long total = (long)((max_query_len + qt - 1) / qt) * args.num_seqs * args.hkv;
+  FI_REQUIRE(total <= 0x7fffffffL - 7, FI_ERR_INVALID_SHAPE, "fi_attn_prefill_paged: grid too large");
+  const dim3 grid((unsigned)((total + 7) / 8 * 8));
   switch (g) {
     case 1:
       hipLaunchKernelGGL((prefill_kernel<D, KVT, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
@@ -301,9 +329,9 @@ int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args, int max_query_l
 }
 
 template <int D>
-int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& args, int max_query_len) {
-  if (dtype == FI_DTYPE_F32) return launch_prefill<D, float>(ctx, args, max_query_len);
-  return launch_prefill<D, uint16_t>(ctx, args, max_query_len);
+int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& args) {
+  if (dtype == FI_DTYPE_F32) return launch_prefill<D, float>(ctx, args);
+  return launch_prefill<D, uint16_t>(ctx, args);
 }
 
 }  // namespace
@@ -347,14 +375,15 @@ int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k
   args.block_size = block_size;
   args.num_blocks = num_blocks;
   args.scale = scale;
-  args.cu_seqlens_count = num_seqs;
+  args.num_seqs = num_seqs;
+  args.max_query_len = max_query_len;
   switch (head_dim) {
     case 32:
-      return launch_prefill_dtype<32>(ctx, kv_dtype, args, max_query_len);
+      return launch_prefill_dtype<32>(ctx, kv_dtype, args);
     case 64:
-      return launch_prefill_dtype<64>(ctx, kv_dtype, args, max_query_len);
+      return launch_prefill_dtype<64>(ctx, kv_dtype, args);
     default:
-      return launch_prefill_dtype<128>(ctx, kv_dtype, args, max_query_len);
+      return launch_prefill_dtype<128>(ctx, kv_dtype, args);
   }
 }
 
