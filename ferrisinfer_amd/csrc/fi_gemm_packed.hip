@@ -557,12 +557,13 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
   }
 }
 
-// One workgroup per token: the QKV projection's split partials (+ biases) -> RoPE on q and k
-// at the token's position -> q to q_out, k and v appended to the pool slot (the reference
-// order: rope before attention, KV written for this chunk, reference.rs:163-370).  Columns
-// of the fused projection: [0, Hq*D) q, then Hkv*D of k, then Hkv*D of v.  A thread owns a
-// rotary pair (i, i + rot/2) of one head, or one pass-through / value element, so every
-// partial is read once.
+// The QKV projection's split partials (+ biases) -> RoPE on q and k at the token's position
+// -> q to q_out, k and v appended to the pool slot (the reference order: rope before
+// attention, KV written for this chunk, reference.rs:163-370).  Columns of the fused
+// projection: [0, Hq*D) q, then Hkv*D of k, then Hkv*D of v.  One flat grid over (token,
+// item): an item is a rotary pair (i, i + rot/2) of a q or k head, one pass-through element
+// of such a head, or one value element, so every partial is read once and a decode tick of a
+// few dozen tokens still spreads its loads over many workgroups.
 template <typename KVT>
 __device__ __forceinline__ void put_kv(KVT* cache, size_t idx, float x) {
   if constexpr (sizeof(KVT) == 4) {
@@ -579,26 +580,28 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rotary_dims, int max_positions,
     const int64_t* __restrict__ slots, KVT* __restrict__ k_cache, KVT* __restrict__ v_cache, int64_t pool_slots,
     int block_size, int tokens, int hq, int hkv, int d, float* __restrict__ q_out, uint32_t* __restrict__ faults) {
-  const int t = blockIdx.x;
-  const int width = (hq + 2 * hkv) * d;
+  const int half = rotary_dims / 2;
+  const int pass = d - 2 * half;  // dimensions past the rotary ones
+  const int per_head = half + pass;
+  const int rot_items = (hq + hkv) * per_head;
+  const int qw = hq * d, kw = hkv * d;
+  const int items = rot_items + kw;
+  const int gid = blockIdx.x * kRowThreads + threadIdx.x;
+  const int t = gid / items;
+  if (t >= tokens) return;
+  const int idx = gid - t * items;
+  const int width = qw + 2 * kw;
   const size_t plane = (size_t)tokens * width;
   const float* p0 = parts + (size_t)t * width;
-  const int qw = hq * d, kw = hkv * d;
   auto value = [&](int col) {
     const float x = sum_splits(p0 + col, plane, splits);
     const float* b = col < qw ? bias_q : (col < qw + kw ? bias_k : bias_v);
     const int bc = col < qw ? col : (col < qw + kw ? col - qw : col - qw - kw);
     return b ? x + b[bc] : x;
   };
-  int pos = positions[t];
-  const int half = rotary_dims / 2;
-  if (half > 0 && (pos < 0 || pos >= max_positions)) {
-    if (threadIdx.x == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
-    pos = 0;
-  }
   const int64_t slot = slots[t];
   const bool write_kv = slot >= 0 && slot < pool_slots;
-  if (slot >= pool_slots && threadIdx.x == 0) atomicOr(faults, FI_FAULT_SLOT_RANGE);
+  if (idx == 0 && slot >= pool_slots) atomicOr(faults, FI_FAULT_SLOT_RANGE);
   const int64_t blk = write_kv ? slot / block_size : 0;
   const int off = write_kv ? static_cast<int>(slot % block_size) : 0;
   auto store = [&](int head, int i, float x) {  // head < hq: q; else k head (head - hq)
@@ -608,15 +611,16 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
       put_kv(k_cache, (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i, x);
     }
   };
-  const int rot_heads = hq + hkv;
-  const int pass = d - 2 * half;  // dimensions past the rotary ones
-  const int per_head = half + pass;
-  // rotary pairs and pass-through dims of q and k heads
-  for (int idx = threadIdx.x; idx < rot_heads * per_head; idx += kRowThreads) {
+  if (idx < rot_items) {
     const int head = idx / per_head, r = idx - head * per_head;
     const int col0 = head < hq ? head * d : qw + (head - hq) * d;
     if (r < half) {
 #pragma clang fp contract(off)
+      int pos = positions[t];
+      if (pos < 0 || pos >= max_positions) {
+        if (idx == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+        pos = 0;
+      }
       const float lo = value(col0 + r), hi = value(col0 + r + half);
       const float c = cos_t[(size_t)pos * half + r], sn = sin_t[(size_t)pos * half + r];
       store(head, r, lo * c - hi * sn);  // each product rounded before the add, as Rust does
@@ -625,12 +629,10 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
       const int i = 2 * half + (r - half);
       store(head, i, value(col0 + i));
     }
-  }
-  if (write_kv) {
-    for (int idx = threadIdx.x; idx < kw; idx += kRowThreads) {
-      const int h = idx / d, i = idx - h * d;
-      put_kv(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i, value(qw + kw + idx));
-    }
+  } else if (write_kv) {
+    const int v = idx - rot_items;
+    const int h = v / d, i = v - h * d;
+    put_kv(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i, value(qw + kw + v));
   }
 }
 
@@ -914,13 +916,18 @@ int32_t fi_qkv_rope_append(fi_context* ctx, const float* d_parts, int32_t splits
   FI_REQUIRE(rotary_dims == 0 || (d_cos && d_sin && max_positions > 0), FI_ERR_INVALID_CONFIG,
              "fi_qkv_rope_append: rope tables required");
   const int64_t pool_slots = static_cast<int64_t>(num_blocks) * block_size;
+  const int64_t items = static_cast<int64_t>(num_q_heads + num_kv_heads) * (head_dim - rotary_dims / 2) +
+                        static_cast<int64_t>(num_kv_heads) * head_dim;
+  FI_REQUIRE(items * num_tokens < 0x7fffffffLL - kRowThreads, FI_ERR_INVALID_SHAPE,
+             "fi_qkv_rope_append: too many tokens for one launch");
+  const dim3 grid(static_cast<unsigned>((items * num_tokens + kRowThreads - 1) / kRowThreads));
   if (kv_dtype == FI_DTYPE_F32) {
-    hipLaunchKernelGGL(qkv_rope_append_kernel<float>, dim3(num_tokens), dim3(kRowThreads), 0, ctx->stream, d_parts,
+    hipLaunchKernelGGL(qkv_rope_append_kernel<float>, grid, dim3(kRowThreads), 0, ctx->stream, d_parts,
                        splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions, d_slot_mapping,
                        static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache), pool_slots, block_size,
                        num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out, ctx->d_faults);
   } else {
-    hipLaunchKernelGGL(qkv_rope_append_kernel<uint16_t>, dim3(num_tokens), dim3(kRowThreads), 0, ctx->stream,
+    hipLaunchKernelGGL(qkv_rope_append_kernel<uint16_t>, grid, dim3(kRowThreads), 0, ctx->stream,
                        d_parts, splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
                        d_slot_mapping, static_cast<uint16_t*>(d_k_cache), static_cast<uint16_t*>(d_v_cache),
                        pool_slots, block_size, num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out,
