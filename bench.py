@@ -31,6 +31,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
 FP32_PEAK_TFS = 157.3  # MI355X dense fp32 (vector and MFMA), AMD public spec
+BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, AMD public spec
 METRIC = "decode tokens/sec @ ragged batch 64; paged-attn achieved HBM GB/s (% peak)"
 
 
@@ -47,6 +48,9 @@ def parse_args():
     p.add_argument("--no-c4", action="store_true",
                    help="skip the C4 (Qwen2-0.5B-shaped) continuous-batching measurement")
     p.add_argument("--c4-requests", type=int, default=128)
+    p.add_argument("--no-c5", action="store_true",
+                   help="skip the C5 (Llama-3-8B-shaped, bf16 weights and KV) decode-step measurement")
+    p.add_argument("--c5-steps", type=int, default=5)
     p.add_argument("--no-kernels", action="store_true",
                    help="skip the C3 prefill/append and projection-GEMM kernel measurements")
     p.add_argument("--gemm-shapes", action="store_true",
@@ -330,6 +334,125 @@ def c4_continuous(seed, n_requests):
     return out
 
 
+def c5_step(seed, steps):
+    """C5: the Llama-3-8B-shaped decoder (32 layers, hidden 4096, Hq 32 / Hkv 8, D 128, FFN
+    14336, vocab 128256, untied head) with random N(0, 0.02) bf16 weights and a bf16 KV pool per
+    layer sized for the step's 257 sequences (about 147 GB over the 32 layers, N(0, 1) contents).
+    One step = 256 decode tokens (contexts U[512, 8192]) + one 2048-token prefill chunk (2048
+    tokens already cached) through every layer and the greedy head.  Also times layer 0's ops
+    one by one for their roofline fractions."""
+    import numpy as np
+    import torch
+
+    from ferrisinfer_amd import Context
+    from ferrisinfer_amd.bf16_decoder import LLAMA3_8B_C5, Bf16Decoder, build_step_batch, c5_step_shape
+
+    cfg = LLAMA3_8B_C5
+    h, f, v, hq, hkv = cfg["hidden"], cfg["intermediate"], cfg["vocab"], cfg["heads"], cfg["kv_heads"]
+    d = h // hq
+    bs = 16
+    decode_ctx, prefill = c5_step_shape(seed)
+    lens = list(decode_ctx) + [p + n for p, n in prefill]
+    num_blocks = sum((n + bs - 1) // bs for n in lens)
+    t = len(decode_ctx) + sum(n for _, n in prefill)
+    ctx = Context(0)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dec = Bf16Decoder(ctx, cfg, num_blocks, bs, max_tokens=t, max_last_rows=len(lens))
+
+    def w(*shape):
+        return (torch.randn(*shape, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+
+    ones = torch.ones(h, device="cuda")
+    for _ in range(cfg["layers"]):
+        dec.set_layer(w(h, h), w(h, hkv * d), w(h, hkv * d), w(h, h), w(h, f), w(f, h), w(h, f), ones, ones)
+    dec.set_head(ones, w(v, h))
+    for pool in dec.k_pools + dec.v_pools:
+        pool.view(torch.bfloat16).normal_(generator=g)
+    kv_bytes = sum(p.numel() * 2 for p in dec.k_pools + dec.v_pools)
+    batch, _ = build_step_batch(decode_ctx, prefill, bs, num_blocks, seed)
+    x = torch.randn(t, h, device="cuda", generator=g) * 0.02  # synthetic embeddings of the step's tokens
+    torch.cuda.synchronize()
+
+    dec.step(x, batch)  # warm-up
+    torch.cuda.synchronize()
+    ctx.check_faults()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        dec.step(x, batch)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ctx.check_faults()
+    step_ms = e0.elapsed_time(e1) / steps
+
+    # layer 0's ops one by one (repeated launches; the K/V append rewrites the same slots)
+    nd = batch.num_decode
+    lw = dec.layers[0]
+    normed, q, attn, act = dec.normed[:t], dec.q[:t], dec.attn[:t], dec.act[:t]
+    ops = {}
+    s_qkv = ctx.gemm_bf16_splits(t, h, dec.nqkv)
+    parts = dec._parts(t, dec.nqkv, s_qkv)
+    ops["qkv_gemm"] = (timed(lambda: ctx.gemm_bf16(normed, lw["qkv"], h, dec.nqkv, s_qkv, parts), 10),
+                       2.0 * t * h * dec.nqkv, "mfma")
+    ops["qkv_rope_append"] = (timed(lambda: ctx.qkv_rope_append(
+        parts, s_qkv, None, batch.positions, dec.cos, dec.sin, d, dec.max_pos, batch.slot_mapping,
+        dec.k_pools[0], dec.v_pools[0], 1, num_blocks, bs, hq, hkv, d, q), 10), None, None)
+    scale = 1.0 / d ** 0.5
+    dec_bytes = sum(decode_ctx) * hkv * d * 2 * 2 + nd * hq * d * 8 + sum((c + bs - 1) // bs for c in decode_ctx) * 4
+    ops["decode_attention"] = (timed(lambda: ctx.attn_decode_paged(
+        q[:nd], dec.k_pools[0], dec.v_pools[0], 1, batch.dec_block_tables, batch.dec_context_lens,
+        batch.dec_max_context, hkv, bs, num_blocks, scale, attn[:nd]), 10), dec_bytes, "hbm")
+    pf_flops = sum(4.0 * hq * d * sum(range(p + 1, p + n + 1)) for p, n in prefill)
+    ops["prefill_attention"] = (timed(lambda: ctx.attn_prefill_paged(
+        q[nd:], dec.k_pools[0], dec.v_pools[0], 1, batch.pf_block_tables, batch.pf_cu_seqlens,
+        batch.pf_context_lens, batch.pf_max_query, hkv, bs, num_blocks, scale, attn[nd:]), 10),
+        pf_flops, "mfma_f32")
+    s_o = ctx.gemm_bf16_splits(t, h, h)
+    parts = dec._parts(t, h, s_o)
+    ops["wo_gemm"] = (timed(lambda: ctx.gemm_bf16(attn.view(t, h), lw["wo"], h, h, s_o, parts), 10),
+                      2.0 * t * h * h, "mfma")
+    ops["w13_swiglu_gemm"] = (timed(lambda: ctx.gemm_bf16_swiglu(normed, lw["w13"], h, f, act), 10),
+                              4.0 * t * h * f, "mfma")
+    s_w2 = ctx.gemm_bf16_splits(t, f, h)
+    parts = dec._parts(t, h, s_w2)
+    ops["w2_gemm"] = (timed(lambda: ctx.gemm_bf16(act, lw["w2"], f, h, s_w2, parts), 10),
+                      2.0 * t * f * h, "mfma")
+    r = int(batch.last_rows.numel())
+    ops["lm_head_argmax"] = (timed(lambda: ctx.lm_head_argmax_bf16(dec.last[:r], dec.lm_head, v, dec.tok[:r],
+                                                                   dec.prob[:r]), 10), 2.0 * r * h * v, "mfma")
+    ctx.check_faults()
+    out_ops = {}
+    for name, (ms, work, bound) in ops.items():
+        row = {"avg_launch_us": round(ms * 1e3, 1)}
+        if bound == "hbm":
+            row.update(bytes_per_launch=int(work), achieved_gbs=round(work / (ms * 1e-3) / 1e9, 1),
+                       hbm_frac=round(work / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        elif bound == "mfma":
+            tf = work / (ms * 1e-3) / 1e12
+            row.update(flops=work, achieved_tflops=round(tf, 1), bf16_mfma_frac=round(tf / BF16_PEAK_TFS, 4))
+        elif bound == "mfma_f32":
+            tf = work / (ms * 1e-3) / 1e12
+            row.update(flops=work, achieved_tflops=round(tf, 1), f32_mfma_frac=round(tf / FP32_PEAK_TFS, 4))
+        out_ops[name] = row
+    res = {
+        "workload": f"C5 Llama-3-8B shape, bf16 weights (random N(0,0.02)) and bf16 KV; step = {nd} decode "
+                    f"tokens (ctx U[512,8192], sum {sum(decode_ctx)}) + {sum(n for _, n in prefill)}-token "
+                    "prefill chunk after a 2048-token cached prefix; 32 layers + greedy head; block 16",
+        "kv_pool_gb": round(kv_bytes / 1e9, 1),
+        "ms_per_step": round(step_ms, 3),
+        "decode_tok_s": round(nd / (step_ms * 1e-3), 1),
+        "step_tok_s": round(t / (step_ms * 1e-3), 1),
+        "steps": steps,
+        "layer0_ops": out_ops,
+    }
+    del dec, x, batch
+    ctx.close()
+    torch.cuda.empty_cache()
+    return res
+
+
 def c4_cpu_baseline(seed, threads):
     """The oracle's restatement of the reference (per-sequence sessions, its thread fan-out)
     on a declared C4 subset: the first 4 requests, prompts cut to 64 tokens, 8 new tokens."""
@@ -477,6 +600,9 @@ def main():
         if not args.no_cpu_baseline:
             print("bench: C4 CPU baseline (oracle, declared subset)", file=sys.stderr, flush=True)
             result["c4"]["cpu_baseline"] = c4_cpu_baseline(args.seed, min(16, os.cpu_count() or 1))
+    if not args.no_c5:
+        print("bench: C5 bf16 decoder step", file=sys.stderr, flush=True)
+        result["c5"] = c5_step(args.seed, args.c5_steps)
     print(json.dumps(result), flush=True)
 
 

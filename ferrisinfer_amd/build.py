@@ -22,6 +22,7 @@ SOURCES = [
     "fi_ops.hip",
     "fi_gemm.hip",
     "fi_gemm_packed.hip",
+    "fi_gemm_bf16.hip",
 ]
 
 # gfx950 only; packed-fp32 instructions are disabled (the compiler would otherwise form

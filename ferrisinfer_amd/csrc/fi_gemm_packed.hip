@@ -733,6 +733,20 @@ int32_t check_common(fi_context* ctx, const float* a, int32_t lda, const float* 
 
 }  // namespace
 
+namespace fi {
+
+int32_t splitk_swiglu(fi_context* ctx, const float* parts, int32_t splits, const float* bias_up,
+                      const float* bias_gate, int32_t m, int32_t n, float* out) {
+  const size_t total = (size_t)m * n;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 4096));
+  hipLaunchKernelGGL(splitk_swiglu_kernel, dim3(blocks), dim3(256), 0, ctx->stream, parts, splits, bias_up, bias_gate,
+                     m, n, out);
+  FI_CHECK_LAUNCH("splitk_swiglu_kernel");
+  return FI_OK;
+}
+
+}  // namespace fi
+
 extern "C" {
 
 int32_t fi_weight_packed_floats(int32_t k, int32_t n, int32_t pack_width, size_t* floats) {
@@ -852,12 +866,7 @@ int32_t fi_gemm_packed_swiglu(fi_context* ctx, const float* d_a, int32_t lda, co
   g.n = 2 * n;
   g.q_per_split = (g.q_total + splits - 1) / splits;
   FI_TRY((launch_pgemm<2, kEpiPartial>(ctx, g, splits)));
-  const size_t total = (size_t)m * n;
-  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 4096));
-  hipLaunchKernelGGL(splitk_swiglu_kernel, dim3(blocks), dim3(256), 0, ctx->stream, g.out, splits, d_bias_up,
-                     d_bias_gate, m, n, d_out);
-  FI_CHECK_LAUNCH("splitk_swiglu_kernel");
-  return FI_OK;
+  return fi::splitk_swiglu(ctx, g.out, splits, d_bias_up, d_bias_gate, m, n, d_out);
 }
 
 int32_t fi_lm_head_argmax_packed(fi_context* ctx, const float* d_hidden, int32_t lda, const float* d_bp, int32_t m,

@@ -79,6 +79,14 @@ _SIGNATURES = {
     "fi_qkv_rope_append": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I32, _I32,
                            _I32, _I32, _I32, _I32, _I32, _P],
     "fi_weight_pack_columns": [_P, C.POINTER(_P), C.POINTER(_I32), _I32, _I32, _I32, _P],
+    "fi_weight_packed_bf16_elems": [_I32, _I32, _I32, C.POINTER(_SZ)],
+    "fi_weight_pack_bf16": [_P, _P, _I32, _I32, _I32, _I32, _P],
+    "fi_weight_pack_bf16_columns": [_P, C.POINTER(_P), C.POINTER(_I32), _I32, _I32, _I32, _P],
+    "fi_weight_pack_bf16_pair": [_P, _P, _P, _I32, _I32, _I32, _P],
+    "fi_gemm_bf16_splits": [_P, _I32, _I32, _I32, C.POINTER(_I32)],
+    "fi_gemm_bf16": [_P, _P, _I32, _P, _I32, _I32, _I32, _I32, _P],
+    "fi_gemm_bf16_swiglu": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P],
+    "fi_lm_head_argmax_bf16": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P],
 }
 _RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
 
@@ -328,6 +336,76 @@ class Context:
         check(self.lib.fi_weight_pack_columns(self.handle, arr, nar, len(srcs), int(k),
                                               int(pack_width), ptr(dst)))
         return dst
+
+    # ---- bf16-stored weights ----
+
+    @staticmethod
+    def _src_dtype(t):
+        import torch
+
+        if t.dtype == torch.float32:
+            return DTYPE_F32
+        if t.dtype in (torch.bfloat16, torch.int16):
+            return DTYPE_BF16
+        raise FerrisError(5, f"bf16 weight pack: unsupported source dtype {t.dtype}")
+
+    def weight_packed_bf16_elems(self, k, n, pair=False):
+        out = _SZ()
+        check(self.lib.fi_weight_packed_bf16_elems(int(k), int(n), int(bool(pair)), C.byref(out)))
+        return int(out.value)
+
+    def weight_pack_bf16(self, src, k, n, src_layout=0):
+        """Packs a device weight (f32, bf16 or raw bf16 bits as int16), [K, N] (src_layout 0) or
+        [N, K] (1), for fi_gemm_bf16; returns the packed bf16 bits as int16."""
+        import torch
+
+        dst = torch.empty(self.weight_packed_bf16_elems(k, n), dtype=torch.int16, device=src.device)
+        check(self.lib.fi_weight_pack_bf16(self.handle, ptr(src), self._src_dtype(src),
+                                           int(src_layout), int(k), int(n), ptr(dst)))
+        return dst
+
+    def weight_pack_bf16_columns(self, srcs, k):
+        import torch
+
+        ns = [int(t.shape[1]) for t in srcs]
+        dst = torch.empty(self.weight_packed_bf16_elems(k, sum(ns)), dtype=torch.int16,
+                          device=srcs[0].device)
+        arr = (_P * len(srcs))(*[ptr(t) for t in srcs])
+        nar = (_I32 * len(srcs))(*ns)
+        check(self.lib.fi_weight_pack_bf16_columns(self.handle, arr, nar, len(srcs),
+                                                   self._src_dtype(srcs[0]), int(k), ptr(dst)))
+        return dst
+
+    def weight_pack_bf16_pair(self, up, gate, k, n):
+        import torch
+
+        dst = torch.empty(self.weight_packed_bf16_elems(k, n, pair=True), dtype=torch.int16,
+                          device=up.device)
+        check(self.lib.fi_weight_pack_bf16_pair(self.handle, ptr(up), ptr(gate), self._src_dtype(up),
+                                                int(k), int(n), ptr(dst)))
+        return dst
+
+    def gemm_bf16_splits(self, m, k, n):
+        out = _I32()
+        check(self.lib.fi_gemm_bf16_splits(self.handle, int(m), int(k), int(n), C.byref(out)))
+        return int(out.value)
+
+    def gemm_bf16(self, a, bp, k, n, splits, out):
+        """out [splits, M, N] = split-K partial products of a [M, K] (f32) and the packed bf16
+        weight."""
+        check(self.lib.fi_gemm_bf16(self.handle, ptr(a), int(a.stride(0)), ptr(bp), int(k), int(n),
+                                    int(a.shape[0]), int(splits), ptr(out)))
+
+    def gemm_bf16_swiglu(self, a, bp_pair, k, n, out, bias_up=None, bias_gate=None):
+        check(self.lib.fi_gemm_bf16_swiglu(self.handle, ptr(a), int(a.stride(0)), ptr(bp_pair),
+                                           int(k), int(n), int(a.shape[0]), ptr(bias_up),
+                                           ptr(bias_gate), ptr(out)))
+
+    def lm_head_argmax_bf16(self, hidden, bp, vocab, token_out, prob_out):
+        m, h = hidden.shape
+        check(self.lib.fi_lm_head_argmax_bf16(self.handle, ptr(hidden), int(hidden.stride(0)),
+                                              ptr(bp), int(m), int(h), int(vocab), ptr(token_out),
+                                              ptr(prob_out)))
 
     def qkv_rope_append(self, parts, splits, biases, positions, cos_t, sin_t, rotary_dims,
                         max_positions, slot_mapping, k_cache, v_cache, kv_dtype, num_blocks,

@@ -300,6 +300,52 @@ int32_t fi_qkv_rope_append(fi_context* ctx, const float* d_parts, int32_t splits
                            int32_t num_blocks, int32_t block_size, int32_t num_tokens, int32_t num_q_heads,
                            int32_t num_kv_heads, int32_t head_dim, float* d_q_out);
 
+/* ---- Projections over bf16-stored weights (bf16 configurations) ----
+ * The reference loads bf16 weights by exact widening (io/safetensors.rs:540-542) and runs the
+ * f32 kernels; this path keeps the weights bf16 in HBM, packed for v_mfma_f32_16x16x32_bf16,
+ * rounds the f32 activations to bf16 (nearest even) and accumulates in f32.  The outputs use
+ * the formats of the f32 packed path above, so the same consumers sum the split partials. */
+
+/* bf16 elements of the packed form of a [K, N] weight (pair != 0: the up/gate pair of two
+ * [K, N] weights). */
+int32_t fi_weight_packed_bf16_elems(int32_t k, int32_t n, int32_t pair, size_t* elems);
+
+/* Packs a device weight given as f32 (rounded to nearest even) or bf16 bits (src_dtype):
+ * src_layout 0 = [K, N] ([in, out], model/decoder.rs:76-104), 1 = [N, K] (the tied
+ * [vocab, hidden] weight of matmul_rhs_transposed, kernel/cpu/matmul.rs:120-188). */
+int32_t fi_weight_pack_bf16(fi_context* ctx, const void* d_src, int32_t src_dtype, int32_t src_layout, int32_t k,
+                            int32_t n, uint16_t* d_dst);
+
+/* Column concatenation of up to three [K, ns[i]] weights (the fused q|k|v projection).  d_srcs
+ * is a host array of device pointers. */
+int32_t fi_weight_pack_bf16_columns(fi_context* ctx, const void* const* d_srcs, const int32_t* ns, int32_t count,
+                                    int32_t src_dtype, int32_t k, uint16_t* d_dst);
+
+/* SwiGLU pair pack of the up (w1) and gate (w3) weights, both [K, N]. */
+int32_t fi_weight_pack_bf16_pair(fi_context* ctx, const void* d_up, const void* d_gate, int32_t src_dtype, int32_t k,
+                                 int32_t n, uint16_t* d_dst);
+
+/* The split count fi_gemm_bf16 should use for an M x K x N product. */
+int32_t fi_gemm_bf16_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, int32_t* splits);
+
+/* d_out[z] = A * W over split z's K range (as fi_gemm_packed): matmul_f32 / linear_f32_with_bias
+ * (kernel/cpu/matmul.rs:46-118, 424-499) with bf16 operands and f32 accumulation.  A [M, K] f32
+ * with row stride lda (a multiple of 4, at least K rounded up to 4; 16-byte aligned rows). */
+int32_t fi_gemm_bf16(fi_context* ctx, const float* d_a, int32_t lda, const uint16_t* d_bp, int32_t k, int32_t n,
+                     int32_t m, int32_t splits, float* d_out);
+
+/* out[M, N] = (A W1 + b1) * silu(A W3 + b3) over the pair-packed bf16 weight (the decoder
+ * block's up/gate projections and SwiGLU, runtime/reference.rs:346-360,
+ * kernel/cpu/elementwise.rs:118-207).  Uses the context workspace when K is split. */
+int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const float* d_a, int32_t lda, const uint16_t* d_bp_pair, int32_t k,
+                            int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate, float* d_out);
+
+/* Greedy head over a bf16 weight packed from its [vocab, hidden] layout
+ * (matmul_rhs_transposed_argmax_f32, kernel/cpu/matmul.rs:190-274): first maximal index and
+ * 1 / sum(exp(logit - max)) per row.  Uses the context workspace. */
+int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const float* d_hidden, int32_t lda, const uint16_t* d_bp, int32_t m,
+                               int32_t hidden, int32_t vocab, int32_t* d_token, float* d_prob);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,184 @@
+"""GPU parity of the bf16-weight projection path (bf16 configurations, e.g. C5 Llama-3-8B).
+
+Two checks per op:
+* tight: against the oracle's linear_f32_with_bias / SwiGLU / greedy head evaluated on the
+  bf16-rounded operands (activations rounded to nearest even, weights widened exactly).  A
+  product of two bf16 values is exact in f32, so only the summation order differs: 1e-5
+  normwise.  This pins the packing, the MFMA fragment layout and the activation rounding;
+* reference: against the reference semantics (f32 activations, weights widened from bf16 as
+  io/safetensors.rs:540-542 loads them), within the bf16-storage tolerance 2e-2.
+"""
+import numpy as np
+import pytest
+
+from conftest import normwise_error
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def bf16_weights(rng, shape, scale=0.02):
+    """Random weights as bf16 bits (RNE of N(0, scale))."""
+    import oracle
+
+    return oracle.f32_to_bf16((rng.standard_normal(shape, dtype=np.float32) * scale).astype(np.float32))
+
+
+def round_bf16(orc, x):
+    return orc.bf16_to_f32(orc.f32_to_bf16(x))
+
+
+def sum_splits(parts):
+    acc = parts[0].copy()
+    for z in range(1, parts.shape[0]):
+        acc = acc + parts[z]
+    return acc
+
+
+def padded(a):
+    """Device copy of a [M, K] f32 array with rows padded to a multiple of 4 floats (NaN in the
+    padding: the kernel must not read past K)."""
+    import torch
+
+    m, k = a.shape
+    lda = (k + 3) // 4 * 4
+    d = torch.full((m, lda), float("nan"), device="cuda")
+    d[:, :k] = dev(a)
+    return d[:, :k]
+
+
+SHAPES = [  # (M, K, N): C5 decode / prefill tiles, C1 and C4 shapes, ragged tails
+    (256, 4096, 1024), (300, 512, 520), (64, 896, 1152), (8, 256, 688), (37, 96, 300),
+    (1, 64, 40), (17, 100, 33), (130, 4096, 256), (5, 2, 3),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bf16_gemm_matches_linear(orc, gpu_ctx, shape):
+    import torch
+
+    m, k, n = shape
+    print(f"bf16 gemm shape={shape}", flush=True)
+    rng = np.random.default_rng(m + 3 * k + 7 * n)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    wb = bf16_weights(rng, (k, n))
+    w = orc.bf16_to_f32(wb)
+    bp = gpu_ctx.weight_pack_bf16(dev(wb.view(np.int16)), k, n)
+    for splits in sorted({1, gpu_ctx.gemm_bf16_splits(m, k, n)}):
+        q = (k + 31) // 32
+        per = (q + splits - 1) // splits
+        if (q + per - 1) // per != splits:
+            continue
+        out = torch.full((splits, m, n), float("nan"), device="cuda")
+        gpu_ctx.gemm_bf16(padded(a), bp, k, n, splits, out)
+        torch.cuda.synchronize()
+        got = sum_splits(out.cpu().numpy())
+        tight = orc.linear_with_bias(round_bf16(orc, a), w, None)
+        assert normwise_error(got, tight) <= 1e-5, (shape, splits)
+        ref = orc.linear_with_bias(a, w, None)
+        assert normwise_error(got, ref) <= 2e-2, (shape, splits)
+
+
+def test_bf16_pack_sources_agree(gpu_ctx):
+    """Packing from f32 (rounded on the device) equals packing the RNE bf16 bits; the column
+    concatenation pack equals packing the concatenated matrix; the [N, K] source layout equals
+    the transposed [K, N] one."""
+    import torch
+
+    import oracle
+
+    rng = np.random.default_rng(7)
+    k = 96
+    parts = [(rng.standard_normal((k, n), dtype=np.float32) * 0.05).astype(np.float32) for n in (64, 16, 48)]
+    cat = np.concatenate(parts, axis=1)
+    bits = oracle.f32_to_bf16(cat).view(np.int16)
+    p_f32 = gpu_ctx.weight_pack_bf16(dev(cat), k, 128)
+    p_bits = gpu_ctx.weight_pack_bf16(dev(bits), k, 128)
+    assert torch.equal(p_f32, p_bits)
+    p_cols = gpu_ctx.weight_pack_bf16_columns([dev(p) for p in parts], k)
+    assert torch.equal(p_cols, p_bits)
+    p_t = gpu_ctx.weight_pack_bf16(dev(np.ascontiguousarray(bits.T)), k, 128, src_layout=1)
+    assert torch.equal(p_t, p_bits)
+
+
+@pytest.mark.parametrize("m,k,f,bias", [(8, 4096, 1024, False), (300, 256, 688, True), (64, 896, 4864, False),
+                                        (3, 64, 40, True)])
+def test_bf16_swiglu(orc, gpu_ctx, m, k, f, bias):
+    import torch
+
+    print(f"bf16 swiglu m={m} k={k} f={f}", flush=True)
+    rng = np.random.default_rng(m + k + f)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    w1b, w3b = bf16_weights(rng, (k, f)), bf16_weights(rng, (k, f))
+    w1, w3 = orc.bf16_to_f32(w1b), orc.bf16_to_f32(w3b)
+    b1 = rng.standard_normal(f, dtype=np.float32) * 0.1 if bias else None
+    b3 = rng.standard_normal(f, dtype=np.float32) * 0.1 if bias else None
+    bp = gpu_ctx.weight_pack_bf16_pair(dev(w1b.view(np.int16)), dev(w3b.view(np.int16)), k, f)
+    out = torch.full((m, f), float("nan"), device="cuda")
+    gpu_ctx.gemm_bf16_swiglu(padded(a), bp, k, f, out, None if b1 is None else dev(b1),
+                             None if b3 is None else dev(b3))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+
+    def swiglu(x):
+        up = orc.linear_with_bias(x, w1, b1)
+        gate = orc.linear_with_bias(x, w3, b3)
+        return orc.mul(up, orc.silu(gate))
+
+    assert normwise_error(got, swiglu(round_bf16(orc, a))) <= 1e-5
+    assert normwise_error(got, swiglu(a)) <= 2e-2
+
+
+@pytest.mark.parametrize("m,h,v", [(1, 64, 129), (4, 256, 4096), (257, 512, 3000), (8, 2048, 32000)])
+def test_bf16_lm_head_argmax(orc, gpu_ctx, m, h, v):
+    import torch
+
+    print(f"bf16 lm_head m={m} h={h} v={v}", flush=True)
+    rng = np.random.default_rng(h + v)
+    hid = rng.standard_normal((m, h), dtype=np.float32)
+    wb = bf16_weights(rng, (v, h), 0.05)
+    w = orc.bf16_to_f32(wb)
+    bp = gpu_ctx.weight_pack_bf16(dev(wb.view(np.int16)), h, v, src_layout=1)
+    tok = torch.empty(m, dtype=torch.int32, device="cuda")
+    prob = torch.empty(m, device="cuda")
+    gpu_ctx.lm_head_argmax_bf16(padded(hid), bp, v, tok, prob)
+    torch.cuda.synchronize()
+    hr = round_bf16(orc, hid)
+    logits = hr.astype(np.float64) @ w.T.astype(np.float64)
+    rows = range(m) if m <= 64 else list(range(32)) + [m - 1]
+    for r in rows:
+        top2 = np.sort(logits[r])[-2:]
+        if top2[1] - top2[0] < 1e-4 * max(1.0, abs(top2[1])):
+            continue  # near tie: the summation order may pick the other index
+        ridx, rprob = orc.matmul_rhs_transposed_argmax(hr[r:r + 1], w)
+        assert int(tok[r]) == ridx, r
+        assert abs(float(prob[r]) - rprob) <= 1e-4 * max(rprob, 1e-30) + 1e-7
+
+
+def test_bf16_lm_head_reference_vector_and_ties(gpu_ctx):
+    """matmul.rs:745-758: lhs [1,2], rhs [[1,0],[0,1],[1,1]] -> (2, 0.66524094) (all values
+    exact in bf16); equal logits across slabs keep the first index."""
+    import torch
+
+    tok = torch.empty(1, dtype=torch.int32, device="cuda")
+    prob = torch.empty(1, device="cuda")
+    hid = torch.zeros((1, 4), device="cuda")
+    hid[0, :2] = torch.tensor([1.0, 2.0])
+    w = np.array([[1, 0], [0, 1], [1, 1]], np.float32)
+    bp = gpu_ctx.weight_pack_bf16(dev(w), 2, 3, src_layout=1)
+    gpu_ctx.lm_head_argmax_bf16(hid[:, :2], bp, 3, tok, prob)
+    torch.cuda.synchronize()
+    assert int(tok[0]) == 2
+    assert abs(float(prob[0]) - 0.66524094) <= 1e-6
+    v, h = 300, 4
+    w = np.zeros((v, h), np.float32)
+    w[[70, 5, 200, 71, 6], 0] = 1.0  # max logit 1.0 at 5, 6, 70, 71, 200 -> first is 5
+    bp = gpu_ctx.weight_pack_bf16(dev(w), h, v, src_layout=1)
+    gpu_ctx.lm_head_argmax_bf16(dev(np.array([[1, 0, 0, 0]], np.float32)), bp, v, tok, prob)
+    torch.cuda.synchronize()
+    assert int(tok[0]) == 5
