@@ -211,7 +211,7 @@ def kernel_legs(ctx, seed):
     import numpy as np
     import torch
 
-    from ferrisinfer_amd import DTYPE_F32
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
     from ferrisinfer_amd.workloads import prefill_c3
 
     out = {}
@@ -243,6 +243,24 @@ def kernel_legs(ctx, seed):
         "tokens": T, "flops_per_launch": flops, "avg_launch_us": round(ms_p * 1e3, 2),
         "achieved_tflops": round(flops / (ms_p * 1e-3) / 1e12, 2), "peak_tflops": FP32_PEAK_TFS,
         "frac": round(flops / (ms_p * 1e-3) / 1e12 / FP32_PEAK_TFS, 4)}
+    # the same workload on a bf16 pool through the bf16-MFMA variant
+    kb = torch.zeros(shape, dtype=torch.int16, device="cuda")
+    vb = torch.zeros(shape, dtype=torch.int16, device="cuda")
+    ctx.kv_append(k_new, v_new, slots, kb, vb, DTYPE_BF16, wl.num_blocks, wl.block_size,
+                  wl.num_kv_heads, wl.head_dim)
+
+    def prefill_bf16():
+        ctx.attn_prefill_paged_bf16(q, kb, vb, bt, cu, cl, int(wl.query_lens.max()), wl.num_kv_heads,
+                                    wl.block_size, wl.num_blocks, wl.scale, o)
+
+    ms_b = timed(prefill_bf16, 20)
+    ctx.check_faults()
+    out["c3_prefill_attention_bf16_mfma"] = {
+        "kernel": "prefill_bf16_kernel", "bound": "mfma (bf16)", "kv_dtype": "bf16",
+        "tokens": T, "flops_per_launch": flops, "avg_launch_us": round(ms_b * 1e3, 2),
+        "achieved_tflops": round(flops / (ms_b * 1e-3) / 1e12, 2), "peak_tflops": BF16_PEAK_TFS,
+        "frac": round(flops / (ms_b * 1e-3) / 1e12 / BF16_PEAK_TFS, 4)}
+    del kb, vb
     out["c3_kv_append"] = {
         "kernel": "kv_append_kernel", "bound": "hbm", "tokens": T,
         "bytes_per_launch": ab, "avg_launch_us": round(ms_a * 1e3, 2),
@@ -405,10 +423,10 @@ def c5_step(seed, steps):
         q[:nd], dec.k_pools[0], dec.v_pools[0], 1, batch.dec_block_tables, batch.dec_context_lens,
         batch.dec_max_context, hkv, bs, num_blocks, scale, attn[:nd]), 10), dec_bytes, "hbm")
     pf_flops = sum(4.0 * hq * d * sum(range(p + 1, p + n + 1)) for p, n in prefill)
-    ops["prefill_attention"] = (timed(lambda: ctx.attn_prefill_paged(
-        q[nd:], dec.k_pools[0], dec.v_pools[0], 1, batch.pf_block_tables, batch.pf_cu_seqlens,
+    ops["prefill_attention_bf16_mfma"] = (timed(lambda: ctx.attn_prefill_paged_bf16(
+        q[nd:], dec.k_pools[0], dec.v_pools[0], batch.pf_block_tables, batch.pf_cu_seqlens,
         batch.pf_context_lens, batch.pf_max_query, hkv, bs, num_blocks, scale, attn[nd:]), 10),
-        pf_flops, "mfma_f32")
+        pf_flops, "mfma")
     s_o = ctx.gemm_bf16_splits(t, h, h)
     parts = dec._parts(t, h, s_o)
     ops["wo_gemm"] = (timed(lambda: ctx.gemm_bf16(attn.view(t, h), lw["wo"], h, h, s_o, parts), 10),

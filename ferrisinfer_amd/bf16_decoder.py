@@ -6,9 +6,9 @@ Per layer, in the order of the reference decoder block (runtime/reference.rs:163
 
     attention_norm -> q|k|v projection (fi_gemm_bf16, split-K partials)
     -> fi_qkv_rope_append (split sum, RoPE, K/V appended to the layer's bf16 pool by slot)
-    -> paged attention: fi_attn_decode_paged over the decode rows, fi_attn_prefill_paged over
-       the prefill chunk (the reference's decode / cached-prefixed attention per sequence,
-       kernel/cpu/attention.rs:332-686)
+    -> paged attention: fi_attn_decode_paged over the decode rows, fi_attn_prefill_paged_bf16
+       (bf16 MFMA) over the prefill chunk (the reference's decode / cached-prefixed attention
+       per sequence, kernel/cpu/attention.rs:332-686)
     -> wo projection -> fi_splitk_residual_rms_norm (residual add + ffn_norm)
     -> fi_gemm_bf16_swiglu (w1, w3, silu * mul) -> w2 projection
     -> fi_splitk_residual_rms_norm (residual add + the next layer's attention_norm, or the
@@ -19,13 +19,14 @@ matmul_rhs_transposed_argmax_f32, kernel/cpu/matmul.rs:190-274).
 
 The reference loads bf16 weights by exact widening (io/safetensors.rs:540-542) and runs f32
 math; the projections here multiply bf16-rounded activations by the bf16 weights with f32
-accumulation, the rest (norms, RoPE, attention, SwiGLU) stays f32 with bf16 K/V storage.
+accumulation; the prefill chunk's attention multiplies bf16-rounded queries and probabilities
+by the bf16 K/V; the rest (norms, RoPE, decode attention, softmax, SwiGLU) stays f32.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
 
-from .kernel import DTYPE_BF16, DTYPE_F32, FerrisError
+from .kernel import DTYPE_BF16, FerrisError
 
 LLAMA3_8B_C5 = dict(hidden=4096, intermediate=14336, layers=32, heads=32, kv_heads=8, vocab=128256,
                     max_pos=8192 + 2048, eps=1e-6, theta=500000.0, tie=False)
@@ -141,9 +142,9 @@ class Bf16Decoder:
                                     b.dec_block_tables, b.dec_context_lens, b.dec_max_context, self.hkv,
                                     self.block_size, self.num_blocks, scale, attn[:nd])
             if t > nd:
-                c.attn_prefill_paged(q[nd:], self.k_pools[li], self.v_pools[li], DTYPE_BF16,
-                                     b.pf_block_tables, b.pf_cu_seqlens, b.pf_context_lens, b.pf_max_query,
-                                     self.hkv, self.block_size, self.num_blocks, scale, attn[nd:])
+                c.attn_prefill_paged_bf16(q[nd:], self.k_pools[li], self.v_pools[li], b.pf_block_tables,
+                                          b.pf_cu_seqlens, b.pf_context_lens, b.pf_max_query, self.hkv,
+                                          self.block_size, self.num_blocks, scale, attn[nd:])
             parts = self._parts(t, h, s_o)
             c.gemm_bf16(attn.view(t, h), w["wo"], h, h, s_o, parts)
             c.splitk_residual_rms_norm(parts, s_o, None, res, other, w["ffn_norm"], normed, eps)

@@ -334,6 +334,285 @@ int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& 
   return launch_prefill<D, uint16_t>(ctx, args);
 }
 
+// ---- bf16-MFMA variant for a bf16 pool (fi_attn_prefill_paged_bf16) ----
+// Same workgroup shape, tile order and chunk pipeline as prefill_kernel, on
+// v_mfma_f32_16x16x32_bf16: K and V stay bf16 in LDS (V transposed on the way in so both
+// operands are 16-byte fragment reads), Q and the softmax probabilities are rounded to bf16
+// (nearest even), scores, softmax and accumulation stay f32.  64-key chunks.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
+  constexpr int QT = kRows / G;
+  constexpr int KB = 64;                 // keys per chunk
+  constexpr int DS = D / 32;             // 32-wide d steps of Q K^T
+  constexpr int DT = D / 16;             // 16-wide output d tiles of P V
+  constexpr int JT = KB / 16;            // 16-key score tiles per chunk
+  constexpr int KS = KB / 32;            // 32-key steps of P V
+  constexpr int RV = D / 8;              // 16-byte vectors per K/V row
+  constexpr int PER_T = KB * RV / kThreads;
+  static_assert(KB * RV % kThreads == 0 && kThreads % KB == 0, "chunk must split over the workgroup");
+  constexpr int KP = D + 8;              // padded LDS rows (conflict-free fragment reads)
+  constexpr int VP = KB + 8;
+  __shared__ __align__(16) uint16_t Ks[KB][KP];
+  __shared__ __align__(16) uint16_t Vt[D][VP];
+  __shared__ __align__(16) uint16_t Ps[4][16][VP];
+
+  const uint16_t* __restrict__ k_cache = static_cast<const uint16_t*>(a.k_cache);
+  const uint16_t* __restrict__ v_cache = static_cast<const uint16_t*>(a.v_cache);
+  const int ntiles = (a.max_query_len + QT - 1) / QT;
+  const int logical = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+  if (logical >= ntiles * a.num_seqs * a.hkv) return;
+  const int qt = logical % ntiles;
+  const int seq = (logical / ntiles) % a.num_seqs, kvh = logical / (ntiles * a.num_seqs);
+  const int qs = a.cu_seqlens[seq];
+  const int qlen = a.cu_seqlens[seq + 1] - qs;
+  const int q0 = qt * QT;
+  if (q0 >= qlen) return;
+  const int ctx = a.context_lens[seq];
+  const int start = ctx - qlen;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int li = lane & 15, lk = lane >> 4;
+
+  // Q fragments (A operand): row 16w + li, d = 32 t + 8 lk + e
+  const int arow = 16 * w + li;
+  const int ah = arow / QT, at = arow % QT;
+  const bool a_ok = ah < a.group && q0 + at < qlen;
+  bf16x8 qf[DS];
+  {
+    const float* qp = a.q + ((size_t)(qs + q0 + (a_ok ? at : 0)) * a.hq + kvh * a.group + (a_ok ? ah : 0)) * D;
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+      const float4 lo = *reinterpret_cast<const float4*>(qp + 32 * t + 8 * lk);
+      const float4 hi = *reinterpret_cast<const float4*>(qp + 32 * t + 8 * lk + 4);
+      const f32x8 v = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const f32x8 z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      qf[t] = __builtin_convertvector(a_ok ? v : z, bf16x8);
+    }
+  }
+  int qpos[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) qpos[v] = start + q0 + (16 * w + 4 * lk + v) % QT;
+  v4f o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_row[4], l_row[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    m_row[v] = -INFINITY;
+    l_row[v] = 0.0f;
+  }
+
+  const int kend = start + min(qlen, q0 + QT);
+  const int nchunks = max((kend + KB - 1) / KB, 1);
+
+  // staging: thread owns key `lane` of the chunk and row vectors w + 4 r; one block lookup per
+  // chunk, looked up a chunk ahead, loads unconditional (clamped key, padding keys zeroed)
+  uint4 kr[PER_T], vr[PER_T];
+  int id_next = 0, off_next = 0;
+  bool bad_block = false;
+  auto lookup = [&](int c) {
+    c = min(c, nchunks - 1);
+    const int kpc = max(min(c * KB + lane, kend - 1), 0);
+    const int lb = kpc / a.block_size;
+    const bool in_table = lb < a.max_blocks;
+    const int id = a.block_tables[(size_t)seq * a.max_blocks + (in_table ? lb : 0)];
+    id_next = in_table ? id : -1;
+    off_next = kpc - lb * a.block_size;
+  };
+  auto fetch = [&](int c) {
+    c = min(c, nchunks - 1);
+    const bool valid = c * KB + lane < kend;
+    const bool bad = id_next < 0 || id_next >= a.num_blocks;
+    bad_block |= bad;
+    const size_t row = ((size_t)(bad ? 0 : id_next) * a.hkv + kvh) * a.block_size + off_next;
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) {
+      const int dv = w + 4 * r;
+      const uint4 kx = *reinterpret_cast<const uint4*>(k_cache + row * D + 8 * dv);
+      const uint4 vx = *reinterpret_cast<const uint4*>(v_cache + row * D + 8 * dv);
+      kr[r] = valid ? kx : make_uint4(0u, 0u, 0u, 0u);
+      vr[r] = valid ? vx : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) {
+      const int dv = w + 4 * r;
+      *reinterpret_cast<uint4*>(&Ks[lane][8 * dv]) = kr[r];
+      const uint32_t x[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Vt[8 * dv + 2 * e][lane] = static_cast<uint16_t>(x[e] & 0xffffu);
+        Vt[8 * dv + 2 * e + 1][lane] = static_cast<uint16_t>(x[e] >> 16);
+      }
+    }
+  };
+
+  lookup(0);
+  fetch(0);
+  lookup(1);
+  stage();
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int k0 = c * KB;
+    fetch(c + 1);
+    lookup(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- S = Q K^T: 16 rows x 64 keys ----
+    v4f s_acc[JT];
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      s_acc[jt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < DS; ++t) {
+        const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[16 * jt + li][32 * t + 8 * lk]);
+        s_acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t], kb, s_acc[jt], 0, 0, 0);
+      }
+    }
+    // element (jt, v): row 16w + 4lk + v, key k0 + 16jt + li
+    float pv[JT][4];
+    float alpha[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const int kp = k0 + 16 * jt + li;
+        const float sv = s_acc[jt][v] * a.scale;
+        pv[jt][v] = (kp <= qpos[v] && kp < ctx) ? sv : -INFINITY;
+        mx = fmaxf(mx, pv[jt][v]);
+      }
+      mx = group_max<16>(mx);
+      const float m_new = fmaxf(m_row[v], mx);
+      alpha[v] = m_new == -INFINITY ? 1.0f : __expf(m_row[v] - m_new);
+      float ls = 0.0f;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        pv[jt][v] = pv[jt][v] == -INFINITY ? 0.0f : __expf(pv[jt][v] - m_new);
+        ls += pv[jt][v];
+      }
+      ls = fi::group_sum<16>(ls);
+      l_row[v] = l_row[v] * alpha[v] + ls;
+      m_row[v] = m_new;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[dt][v] *= alpha[v];
+    // P (bf16) to the wave's LDS slice in accumulator layout; read back as the A operand
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        Ps[w][4 * lk + v][16 * jt + li] = static_cast<uint16_t>(fi::f32_to_bf16_bits(pv[jt][v]));
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+    // ---- O += P V: keys 32 u + 8 lk + e, output d = 16 dt + li ----
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&Ps[w][li][32 * u + 8 * lk]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&Vt[16 * dt + li][32 * u + 8 * lk]);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[dt], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // every wave is done with this chunk's K/V
+    if (c + 1 < nchunks) {
+      stage();
+      __syncthreads();
+    }
+  }
+
+  if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
+
+  // ---- normalise and store: lane holds rows 16w + 4lk + v, d = 16 dt + li ----
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 16 * w + 4 * lk + v;
+    const int h = r / QT, t = r % QT;
+    if (h >= a.group || q0 + t >= qlen) continue;
+    const float inv = 1.0f / l_row[v];
+    float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) op[16 * dt + li] = o[dt][v] * inv;
+  }
+}
+
+template <int D>
+int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args) {
+  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
+  const int qt = kRows / g;
+  const long total = (long)((args.max_query_len + qt - 1) / qt) * args.num_seqs * args.hkv;
+  FI_REQUIRE(total <= 0x7fffffffL - 7, FI_ERR_INVALID_SHAPE, "fi_attn_prefill_paged_bf16: grid too large");
+  const dim3 grid((unsigned)((total + 7) / 8 * 8));
+  switch (g) {
+    case 1:
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    case 2:
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 2>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    case 4:
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 4>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    default:
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 8>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+  }
+  FI_CHECK_LAUNCH("prefill_bf16_kernel");
+  return FI_OK;
+}
+
+// Checks the arguments of a prefill entry point and fills the kernel arguments; *empty when
+// there is nothing to compute.
+int32_t prefill_args(fi_context* ctx, const char* name, const float* d_q, const void* d_k_cache,
+                     const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
+                     int32_t max_blocks_per_seq, const int32_t* d_cu_seqlens, const int32_t* d_context_lens,
+                     int32_t num_seqs, int32_t max_query_len, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale, float* d_out,
+                     PrefillArgs* args, bool* empty) {
+  const std::string n(name);
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(num_seqs >= 0 && max_query_len >= 0, FI_ERR_INVALID_SHAPE, n + ": negative sizes");
+  FI_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, FI_ERR_INVALID_SHAPE,
+             "number of query heads must be divisible by number of KV heads");
+  FI_REQUIRE(block_size > 0 && num_blocks > 0 && max_blocks_per_seq > 0, FI_ERR_INVALID_CONFIG,
+             n + ": pool dimensions must be greater than zero");
+  FI_REQUIRE(kv_dtype == FI_DTYPE_F32 || kv_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
+             n + ": KV dtype must be f32 or bf16");
+  FI_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128, FI_ERR_UNSUPPORTED,
+             n + ": head_dim must be 32, 64 or 128");
+  FI_REQUIRE(num_q_heads / num_kv_heads <= 8, FI_ERR_UNSUPPORTED, n + " supports at most 8 query heads per KV head");
+  *empty = num_seqs == 0 || max_query_len == 0;
+  if (*empty) return FI_OK;
+  FI_REQUIRE(d_q && d_k_cache && d_v_cache && d_block_tables && d_cu_seqlens && d_context_lens && d_out,
+             FI_ERR_INVALID_CONFIG, n + ": null pointer");
+  PrefillArgs& g = *args;
+  g = PrefillArgs{};
+  g.q = d_q;
+  g.k_cache = d_k_cache;
+  g.v_cache = d_v_cache;
+  g.cu_seqlens = d_cu_seqlens;
+  g.context_lens = d_context_lens;
+  g.block_tables = d_block_tables;
+  g.out = d_out;
+  g.faults = ctx->d_faults;
+  g.max_blocks = max_blocks_per_seq;
+  g.hq = num_q_heads;
+  g.hkv = num_kv_heads;
+  g.group = num_q_heads / num_kv_heads;
+  g.block_size = block_size;
+  g.num_blocks = num_blocks;
+  g.scale = scale;
+  g.num_seqs = num_seqs;
+  g.max_query_len = max_query_len;
+  return FI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -344,39 +623,12 @@ int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k
                               const int32_t* d_context_lens, int32_t num_seqs, int32_t max_query_len,
                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                               int32_t block_size, int32_t num_blocks, float scale, float* d_out) {
-  FI_TRY(fi::enter(ctx));
-  FI_REQUIRE(num_seqs >= 0 && max_query_len >= 0, FI_ERR_INVALID_SHAPE, "fi_attn_prefill_paged: negative sizes");
-  FI_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, FI_ERR_INVALID_SHAPE,
-             "number of query heads must be divisible by number of KV heads");
-  FI_REQUIRE(block_size > 0 && num_blocks > 0 && max_blocks_per_seq > 0, FI_ERR_INVALID_CONFIG,
-             "fi_attn_prefill_paged: pool dimensions must be greater than zero");
-  FI_REQUIRE(kv_dtype == FI_DTYPE_F32 || kv_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
-             "fi_attn_prefill_paged: KV dtype must be f32 or bf16");
-  FI_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128, FI_ERR_UNSUPPORTED,
-             "fi_attn_prefill_paged: head_dim must be 32, 64 or 128");
-  FI_REQUIRE(num_q_heads / num_kv_heads <= 8, FI_ERR_UNSUPPORTED,
-             "fi_attn_prefill_paged supports at most 8 query heads per KV head");
-  if (num_seqs == 0 || max_query_len == 0) return FI_OK;
-  FI_REQUIRE(d_q && d_k_cache && d_v_cache && d_block_tables && d_cu_seqlens && d_context_lens && d_out,
-             FI_ERR_INVALID_CONFIG, "fi_attn_prefill_paged: null pointer");
   PrefillArgs args{};
-  args.q = d_q;
-  args.k_cache = d_k_cache;
-  args.v_cache = d_v_cache;
-  args.cu_seqlens = d_cu_seqlens;
-  args.context_lens = d_context_lens;
-  args.block_tables = d_block_tables;
-  args.out = d_out;
-  args.faults = ctx->d_faults;
-  args.max_blocks = max_blocks_per_seq;
-  args.hq = num_q_heads;
-  args.hkv = num_kv_heads;
-  args.group = num_q_heads / num_kv_heads;
-  args.block_size = block_size;
-  args.num_blocks = num_blocks;
-  args.scale = scale;
-  args.num_seqs = num_seqs;
-  args.max_query_len = max_query_len;
+  bool empty = false;
+  FI_TRY(prefill_args(ctx, "fi_attn_prefill_paged", d_q, d_k_cache, d_v_cache, kv_dtype, d_block_tables,
+                      max_blocks_per_seq, d_cu_seqlens, d_context_lens, num_seqs, max_query_len, num_q_heads,
+                      num_kv_heads, head_dim, block_size, num_blocks, scale, d_out, &args, &empty));
+  if (empty) return FI_OK;
   switch (head_dim) {
     case 32:
       return launch_prefill_dtype<32>(ctx, kv_dtype, args);
@@ -384,6 +636,28 @@ int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k
       return launch_prefill_dtype<64>(ctx, kv_dtype, args);
     default:
       return launch_prefill_dtype<128>(ctx, kv_dtype, args);
+  }
+}
+
+int32_t fi_attn_prefill_paged_bf16(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                                   const void* d_v_cache, const int32_t* d_block_tables,
+                                   int32_t max_blocks_per_seq, const int32_t* d_cu_seqlens,
+                                   const int32_t* d_context_lens, int32_t num_seqs, int32_t max_query_len,
+                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t block_size, int32_t num_blocks, float scale, float* d_out) {
+  PrefillArgs args{};
+  bool empty = false;
+  FI_TRY(prefill_args(ctx, "fi_attn_prefill_paged_bf16", d_q, d_k_cache, d_v_cache, FI_DTYPE_BF16,
+                      d_block_tables, max_blocks_per_seq, d_cu_seqlens, d_context_lens, num_seqs, max_query_len,
+                      num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, scale, d_out, &args, &empty));
+  if (empty) return FI_OK;
+  switch (head_dim) {
+    case 32:
+      return launch_prefill_bf16<32>(ctx, args);
+    case 64:
+      return launch_prefill_bf16<64>(ctx, args);
+    default:
+      return launch_prefill_bf16<128>(ctx, args);
   }
 }
 

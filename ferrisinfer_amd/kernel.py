@@ -79,6 +79,8 @@ _SIGNATURES = {
     "fi_qkv_rope_append": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I32, _I32,
                            _I32, _I32, _I32, _I32, _I32, _P],
     "fi_weight_pack_columns": [_P, C.POINTER(_P), C.POINTER(_I32), _I32, _I32, _I32, _P],
+    "fi_attn_prefill_paged_bf16": [_P, _P, _P, _P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
+                                   _I32, _F32, _P],
     "fi_weight_packed_bf16_elems": [_I32, _I32, _I32, C.POINTER(_SZ)],
     "fi_weight_pack_bf16": [_P, _P, _I32, _I32, _I32, _I32, _P],
     "fi_weight_pack_bf16_columns": [_P, C.POINTER(_P), C.POINTER(_I32), _I32, _I32, _I32, _P],
@@ -269,6 +271,17 @@ class Context:
                                              int(max_query_len), num_q_heads, num_kv_heads,
                                              head_dim, block_size, num_blocks, float(scale),
                                              ptr(out)))
+
+    def attn_prefill_paged_bf16(self, q, k_cache, v_cache, block_tables, cu_seqlens, context_lens,
+                                max_query_len, num_kv_heads, block_size, num_blocks, scale, out):
+        """fi_attn_prefill_paged over a bf16 pool on bf16 MFMA (Q and P rounded to bf16)."""
+        t, num_q_heads, head_dim = q.shape
+        check(self.lib.fi_attn_prefill_paged_bf16(self.handle, ptr(q), ptr(k_cache), ptr(v_cache),
+                                                  ptr(block_tables), int(block_tables.shape[1]),
+                                                  ptr(cu_seqlens), ptr(context_lens),
+                                                  int(context_lens.numel()), int(max_query_len),
+                                                  num_q_heads, num_kv_heads, head_dim, block_size,
+                                                  num_blocks, float(scale), ptr(out)))
 
     # ---------------------------------------------------------- packed-weight GEMMs
     def weight_packed_floats(self, k, n, pack_width):

@@ -161,6 +161,18 @@ int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k
                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                               int32_t num_blocks, float scale, float* d_out);
 
+/* fi_attn_prefill_paged over a bf16 pool on bf16 MFMA (v_mfma_f32_16x16x32_bf16): the queries
+ * and the softmax probabilities are rounded to bf16 (nearest even) for the two products;
+ * scores, softmax and accumulation stay f32.  The bf16-storage counterpart of the same
+ * reference attention (within the bf16 tolerance of the f32-math path above), for callers
+ * that store K/V in bf16 and want the bf16 MFMA rate. */
+int32_t fi_attn_prefill_paged_bf16(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                                   const void* d_v_cache, const int32_t* d_block_tables,
+                                   int32_t max_blocks_per_seq, const int32_t* d_cu_seqlens,
+                                   const int32_t* d_context_lens, int32_t num_seqs, int32_t max_query_len,
+                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t block_size, int32_t num_blocks, float scale, float* d_out);
+
 /* ---------------------------------------------------------------- decoder-block ops */
 
 /* out[r, :] = table[ids[r], :].  Replaces embedding_gather_f32

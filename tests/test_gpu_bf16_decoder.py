@@ -5,9 +5,10 @@ on a bf16 KV pool, against the oracle's restatement of the reference decoder blo
 residual adds) with the same bf16 weights widened to f32 and K/V stored as bf16.
 
 Checks:
-* the attention stage exactly: the oracle's cached-prefixed attention on the step's own rotated
-  queries and the pool contents after the append (prefix rows + the appended rows, read back
-  through the block tables) matches the step's attention output within 1e-4;
+* the attention stage on the step's own inputs: the oracle's cached-prefixed attention on the
+  step's rotated queries and the pool contents after the append (prefix rows + the appended
+  rows, read back through the block tables) matches the decode rows within 1e-4 (f32 math) and
+  the prefill chunk within 1e-2 (bf16 MFMA: queries and probabilities rounded to bf16);
 * the whole layer within the bf16-storage bound 2e-2 normwise of the reference semantics (f32
   activations), and within 5e-3 of the oracle run with the projection inputs and the appended
   K/V rounded to bf16 as the GPU path does.  That second bound cannot be tight: the two
@@ -120,7 +121,7 @@ def test_bf16_decoder_layer_matches_reference(orc):
         kk, vv = got_pool[0][ids, :, offs, :], got_pool[1][ids, :, offs, :]
         want = orc.cached_prefixed_causal_attention(got_q[r0:r1], kk[:start], vv[:start], start,
                                                     kk[start:], vv[start:])
-        assert normwise_error(got_attn[r0:r1], want) <= 1e-4, s
+        assert normwise_error(got_attn[r0:r1], want) <= (1e-4 if s < nd else 1e-2), s
 
     ref = layer(x, round_inputs=False)
     tight = layer(x, round_inputs=True)

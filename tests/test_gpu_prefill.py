@@ -10,7 +10,7 @@ from conftest import normwise_error
 pytestmark = pytest.mark.gpu
 
 
-def run_prefill(ctx, wl, kv_dtype):
+def run_prefill(ctx, wl, kv_dtype, bf16_mfma=False):
     import torch
 
     from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
@@ -25,9 +25,14 @@ def run_prefill(ctx, wl, kv_dtype):
                   wl.block_size, wl.num_kv_heads, wl.head_dim)
     q = d(wl.q)
     out = torch.empty_like(q)
-    ctx.attn_prefill_paged(q, kp, vp, dt, d(wl.block_tables), d(wl.cu_seqlens),
-                           d(wl.context_lens), int(wl.query_lens.max()), wl.num_kv_heads,
-                           wl.block_size, wl.num_blocks, wl.scale, out)
+    if bf16_mfma:
+        ctx.attn_prefill_paged_bf16(q, kp, vp, d(wl.block_tables), d(wl.cu_seqlens),
+                                    d(wl.context_lens), int(wl.query_lens.max()), wl.num_kv_heads,
+                                    wl.block_size, wl.num_blocks, wl.scale, out)
+    else:
+        ctx.attn_prefill_paged(q, kp, vp, dt, d(wl.block_tables), d(wl.cu_seqlens),
+                               d(wl.context_lens), int(wl.query_lens.max()), wl.num_kv_heads,
+                               wl.block_size, wl.num_blocks, wl.scale, out)
     torch.cuda.synchronize()
     ctx.check_faults()
     return out.cpu().numpy()
@@ -84,6 +89,35 @@ def test_prefill_c3_full_size(orc, gpu_ctx, kv_dtype):
     got = run_prefill(gpu_ctx, wl, kv_dtype)
     err = normwise_error(got, oracle_prefill(orc, wl, kv_dtype))
     assert err <= (1e-4 if kv_dtype == "f32" else 2e-2), err
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_prefill_bf16_mfma_small(orc, gpu_ctx, case):
+    """fi_attn_prefill_paged_bf16 (bf16 MFMA, Q and P rounded to bf16) on a bf16 pool: within
+    the bf16-storage bound of the oracle, and within 5e-3 of the f32-math kernel on the same
+    pool (the rounding of Q and of the probabilities is the only difference)."""
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    b, lo, hi, g, gs, sh, hq, hkv, d, bs = case
+    print(f"prefill bf16 mfma case={case}", flush=True)
+    wl = prefill_c3(seed=5, num_seqs=b, min_len=lo, max_len=hi, groups=g, group_size=gs,
+                    shared_prefix=sh, num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                    block_size=bs, num_blocks=1024)
+    got = run_prefill(gpu_ctx, wl, "bf16", bf16_mfma=True)
+    f32_math = run_prefill(gpu_ctx, wl, "bf16")
+    assert normwise_error(got, f32_math) <= 5e-3
+    assert normwise_error(got, oracle_prefill(orc, wl, "bf16")) <= 2e-2
+
+
+def test_prefill_bf16_mfma_c3_full_size(orc, gpu_ctx):
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    print("prefill bf16 mfma C3 full", flush=True)
+    wl = prefill_c3(seed=0)
+    got = run_prefill(gpu_ctx, wl, "bf16", bf16_mfma=True)
+    f32_math = run_prefill(gpu_ctx, wl, "bf16")
+    assert normwise_error(got, f32_math) <= 5e-3
+    assert normwise_error(got, oracle_prefill(orc, wl, "bf16")) <= 2e-2
 
 
 def test_prefill_one_token_matches_decode(gpu_ctx):
