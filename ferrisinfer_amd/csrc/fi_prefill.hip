@@ -17,6 +17,10 @@
 // the wave's LDS slice into the A-operand layout, O += P V on MFMA.  The d index of the Q K^T
 // contraction and the key index of the P V contraction are visited in a permuted order so
 // every LDS operand read is one 16-byte read; the sums are the same products.
+//
+// Tiles run largest first: a one-workgroup planning kernel sorts the (sequence, tile) pairs by
+// the number of key chunks they attend, so the long tiles of long sequences do not start last
+// and leave the device idle behind them.
 #include "fi_common.h"
 #include "fi_device.h"
 
@@ -43,7 +47,44 @@ struct PrefillArgs {
   float scale;
   int num_seqs;
   int max_query_len;
+  const int* order;          // (sequence, query tile) pairs, largest first
 };
+
+// One workgroup sorts the (sequence, query tile) pairs by the number of kb-key chunks they
+// attend, largest first (counting sort over 1024 buckets; order within a bucket arbitrary,
+// which no result depends on; tiles past a sequence's end sort last).
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(const int* __restrict__ cu, const int* __restrict__ ctxl,
+                                                            int num_seqs, int ntiles, int qt_rows, int kb,
+                                                            int* __restrict__ order) {
+  __shared__ int hist[1024];
+  __shared__ int part[1024];
+  const int tid = threadIdx.x;
+  const int total = num_seqs * ntiles;
+  hist[tid] = 0;
+  __syncthreads();
+  auto bucket = [&](int t) {  // 0 = past the sequence's end, else chunks + 1 (capped)
+    const int seq = t / ntiles, qt = t - (t / ntiles) * ntiles;
+    const int qs = cu[seq], qlen = cu[seq + 1] - qs;
+    const int q0 = qt * qt_rows;
+    if (q0 >= qlen) return 0;
+    const int kend = ctxl[seq] - qlen + min(qlen, q0 + qt_rows);
+    return min(max((kend + kb - 1) / kb, 0) + 1, 1023);
+  };
+  for (int t = tid; t < total; t += 1024) atomicAdd(&hist[1023 - bucket(t)], 1);
+  __syncthreads();
+  const int v = hist[tid];  // exclusive scan of the bucket counts (Hillis-Steele)
+  part[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int x = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += x;
+    __syncthreads();
+  }
+  hist[tid] = part[tid] - v;
+  __syncthreads();
+  for (int t = tid; t < total; t += 1024) order[atomicAdd(&hist[1023 - bucket(t)], 1)] = t;
+}
 
 template <int kLanes>
 __device__ __forceinline__ float group_max(float v) {
@@ -95,15 +136,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
   const KVT* __restrict__ k_cache = static_cast<const KVT*>(a.k_cache);
   const KVT* __restrict__ v_cache = static_cast<const KVT*>(a.v_cache);
-  // The 1-D grid is padded to a multiple of 8.  Hardware workgroup L runs on XCD L % 8; the
-  // logical tile (L % 8) * (grid / 8) + L / 8 gives each XCD a contiguous range of the order
-  // (tile fastest, then sequence, then KV head), so the tiles that re-read one sequence's K/V
-  // rows share an L2.
+  // Workgroup L takes the (L / Hkv)-th largest (sequence, tile) pair for kv head L % Hkv:
+  // the heaviest tiles start first, and hardware workgroup L runs on XCD L % 8, so each XCD
+  // keeps to one kv head's K/V (Hkv = 8) or a fixed subset of heads.
   const int ntiles = (a.max_query_len + QT - 1) / QT;
-  const int logical = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
-  if (logical >= ntiles * a.num_seqs * a.hkv) return;
-  const int qt = logical % ntiles;
-  const int seq = (logical / ntiles) % a.num_seqs, kvh = logical / (ntiles * a.num_seqs);
+  const int rank = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
+  const int tile = a.order[rank];
+  const int qt = tile % ntiles, seq = tile / ntiles;
   const int qs = a.cu_seqlens[seq];
   const int qlen = a.cu_seqlens[seq + 1] - qs;
   const int q0 = qt * QT;
@@ -302,14 +341,29 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 }
 
+// Sorts the tiles largest first into the context workspace (one small launch before the
+// attention kernel) and sizes the grid: one workgroup per (tile, kv head).
+int32_t plan_tiles(fi_context* ctx, PrefillArgs& args, int qt, int kb, const char* name, dim3* grid) {
+  const int ntiles = (args.max_query_len + qt - 1) / qt;
+  const long pairs = (long)ntiles * args.num_seqs;
+  FI_REQUIRE(pairs * args.hkv <= 0x7fffffffL, FI_ERR_INVALID_SHAPE, std::string(name) + ": grid too large");
+  FI_TRY(fi::ensure_workspace(ctx, (size_t)pairs * sizeof(int)));
+  int* order = static_cast<int*>(ctx->workspace);
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, ctx->stream, args.cu_seqlens, args.context_lens,
+                     args.num_seqs, ntiles, qt, kb, order);
+  FI_CHECK_LAUNCH("prefill_plan_kernel");
+  args.order = order;
+  *grid = dim3(static_cast<unsigned>(pairs * args.hkv));
+  return FI_OK;
+}
+
 template <int D, typename KVT>
-int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args) {
-  const int max_query_len = args.max_query_len;
+int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args_in) {
+  PrefillArgs args = args_in;
   const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
   const int qt = kRows / g;
-  const long total = (long)((max_query_len + qt - 1) / qt) * args.num_seqs * args.hkv;
-  FI_REQUIRE(total <= 0x7fffffffL - 7, FI_ERR_INVALID_SHAPE, "fi_attn_prefill_paged: grid too large");
-  const dim3 grid((unsigned)((total + 7) / 8 * 8));
+  dim3 grid;
+  FI_TRY(plan_tiles(ctx, args, qt, kKeys, "fi_attn_prefill_paged", &grid));
   switch (g) {
     case 1:
       hipLaunchKernelGGL((prefill_kernel<D, KVT, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
@@ -362,10 +416,9 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
   const uint16_t* __restrict__ k_cache = static_cast<const uint16_t*>(a.k_cache);
   const uint16_t* __restrict__ v_cache = static_cast<const uint16_t*>(a.v_cache);
   const int ntiles = (a.max_query_len + QT - 1) / QT;
-  const int logical = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
-  if (logical >= ntiles * a.num_seqs * a.hkv) return;
-  const int qt = logical % ntiles;
-  const int seq = (logical / ntiles) % a.num_seqs, kvh = logical / (ntiles * a.num_seqs);
+  const int rank = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
+  const int tile = a.order[rank];
+  const int qt = tile % ntiles, seq = tile / ntiles;
   const int qs = a.cu_seqlens[seq];
   const int qlen = a.cu_seqlens[seq + 1] - qs;
   const int q0 = qt * QT;
@@ -543,12 +596,12 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
 }
 
 template <int D>
-int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args) {
+int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
+  PrefillArgs args = args_in;
   const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
   const int qt = kRows / g;
-  const long total = (long)((args.max_query_len + qt - 1) / qt) * args.num_seqs * args.hkv;
-  FI_REQUIRE(total <= 0x7fffffffL - 7, FI_ERR_INVALID_SHAPE, "fi_attn_prefill_paged_bf16: grid too large");
-  const dim3 grid((unsigned)((total + 7) / 8 * 8));
+  dim3 grid;
+  FI_TRY(plan_tiles(ctx, args, qt, 64, "fi_attn_prefill_paged_bf16", &grid));
   switch (g) {
     case 1:
       hipLaunchKernelGGL((prefill_bf16_kernel<D, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
