@@ -57,6 +57,8 @@ _SIGS = {
     "orc_matmul_rhs_transposed_argmax_f32": [F32P, F32P, I64, I64, C.POINTER(C.c_uint32),
                                              C.POINTER(C.c_float)],
     "orc_argmax_last_token": [F32P, I64, I64, C.POINTER(C.c_uint32), C.POINTER(C.c_float)],
+    "orc_sample_last_token": [F32P, I64, I64, C.c_float, I64, C.c_float, C.POINTER(C.c_uint64),
+                              C.POINTER(C.c_uint32), C.POINTER(C.c_float)],
     "orc_rope_f32": [F32P, F32P, I64, I64, I64, I64, I64, I64, C.c_float],
     "orc_prefixed_causal_attention_f32": [F32P, F32P, F32P, I64, I64, I64, I64, I64, F32P],
     "orc_cached_prefixed_causal_attention_f32": [F32P, F32P, F32P, I64, F32P, F32P, I64, I64,
@@ -109,6 +111,10 @@ def lib():
             fn.restype = C.c_int32
         L.orc_last_error.restype = C.c_char_p
         L.orc_runtime_last_error.restype = C.c_char_p
+        L.orc_sampler_state_new.argtypes = [C.c_uint64]
+        L.orc_sampler_state_new.restype = C.c_uint64
+        L.orc_sampler_next_f32.argtypes = [C.POINTER(C.c_uint64)]
+        L.orc_sampler_next_f32.restype = C.c_float
         L.orc_set_threads.argtypes = [I64]
         L.orc_set_threads.restype = None
         L.orc_threads.restype = I64
@@ -213,6 +219,32 @@ def matmul_rhs_transposed_argmax(h, w):
     _check(lib().orc_matmul_rhs_transposed_argmax_f32(h, w, w.shape[1], w.shape[0],
                                                       C.byref(idx), C.byref(prob)))
     return int(idx.value), float(prob.value)
+
+
+def sampler_state_new(seed: int) -> int:
+    """SamplerState::new (runtime/sampler.rs:55-63)."""
+    return int(lib().orc_sampler_state_new(C.c_uint64(seed)))
+
+
+def sampler_next_f32(state: int):
+    """SamplerState::next_f32 (runtime/sampler.rs:65-74): returns (value, new_state)."""
+    st = C.c_uint64(state)
+    v = lib().orc_sampler_next_f32(C.byref(st))
+    return float(v), int(st.value)
+
+
+def sample_last_token(logits, temperature, top_k, top_p, state):
+    """sample_last_token (runtime/sampler.rs:121-241) on the last row of logits [seq, vocab]:
+    returns (token, probability, new_state)."""
+    logits = f32(logits)
+    if logits.ndim == 1:
+        logits = logits[None, :]
+    st = C.c_uint64(state)
+    idx = C.c_uint32()
+    prob = C.c_float()
+    _check(lib().orc_sample_last_token(logits, logits.shape[0], logits.shape[1], float(temperature), int(top_k),
+                                       float(top_p), C.byref(st), C.byref(idx), C.byref(prob)))
+    return int(idx.value), float(prob.value), int(st.value)
 
 
 def argmax_last_token(logits):

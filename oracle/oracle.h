@@ -81,6 +81,11 @@ void mul_f32_in_place(float* out, const float* rhs, size_t count);
 void add_f32_in_place(float* out, const float* rhs, size_t count);
 void argmax_last_token(const float* logits, size_t seq_len, size_t vocab, uint32_t* token_id,
                        float* probability);
+uint64_t sampler_state_new(uint64_t seed);
+float sampler_next_f32(uint64_t* state);
+bool sampler_is_greedy(float temperature, size_t top_k, float top_p);
+void sample_last_token(const float* logits, size_t seq_len, size_t vocab, float temperature, size_t top_k,
+                       float top_p, uint64_t* state, uint32_t* token_id, float* probability);
 
 // bf16 storage helpers: widening is exact (crates/ferrisinfer-io/src/safetensors.rs:540-542);
 // narrowing is round-to-nearest-even (the GPU KV-append rule; the reference has no bf16 KV).

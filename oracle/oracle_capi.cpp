@@ -67,6 +67,18 @@ int32_t orc_argmax_last_token(const float* logits, int64_t seq_len, int64_t voca
   return guard([&] { orc::argmax_last_token(logits, seq_len, vocab, id, prob); });
 }
 
+uint64_t orc_sampler_state_new(uint64_t seed) { return orc::sampler_state_new(seed); }
+
+float orc_sampler_next_f32(uint64_t* state) { return orc::sampler_next_f32(state); }
+
+int32_t orc_sample_last_token(const float* logits, int64_t seq_len, int64_t vocab, float temperature, int64_t top_k,
+                              float top_p, uint64_t* state, uint32_t* id, float* prob) {
+  return guard([&] {
+    orc::sample_last_token(logits, seq_len, vocab, temperature, static_cast<size_t>(top_k < 0 ? 0 : top_k), top_p,
+                           state, id, prob);
+  });
+}
+
 int32_t orc_rope_f32(float* q, float* k, int64_t seq_len, int64_t hq, int64_t hkv, int64_t d,
                      int64_t position_offset, int64_t rotary_dims, float theta) {
   return guard([&] { orc::rope_f32(q, k, seq_len, hq, hkv, d, position_offset, rotary_dims, theta); });

@@ -6,6 +6,7 @@
 // thread count except the fused-argmax probability (matmul.rs:232-270), exactly as in
 // the reference.
 #include <algorithm>
+#include <cfloat>
 #include <cmath>
 #include <cstring>
 #include <functional>
@@ -344,6 +345,97 @@ void argmax_last_token(const float* logits, size_t seq_len, size_t vocab, uint32
   }
   *token_id = static_cast<uint32_t>(best);
   *probability = 1.0f / denominator;
+}
+
+// runtime/sampler.rs:55-75 SamplerState: seed 0 becomes the golden-ratio constant; next_f32
+// is one xorshift64 step, then the xorshift64* multiplier, keeping the top 24 bits / 2^24.
+uint64_t sampler_state_new(uint64_t seed) { return seed == 0 ? 0x9e3779b97f4a7c15ULL : seed; }
+
+float sampler_next_f32(uint64_t* state) {
+  uint64_t x = *state;
+  x ^= x >> 12;
+  x ^= x << 25;
+  x ^= x >> 27;
+  *state = x;
+  const uint64_t value = x * 0x2545F4914F6CDD1DULL;
+  const uint32_t upper = static_cast<uint32_t>(value >> 40);
+  return static_cast<float>(upper) / static_cast<float>(1u << 24);
+}
+
+// runtime/sampler.rs:40-42 SamplerConfig::is_greedy
+bool sampler_is_greedy(float temperature, size_t top_k, float top_p) {
+  return temperature <= 0.0f || top_k == 1 || top_p <= 0.0f;
+}
+
+// runtime/sampler.rs:121-241 sample_last_token.  The top-k candidates are kept by streaming
+// replacement (the first minimum in list order, by total_cmp, is replaced by a strictly larger
+// logit); the list is stably sorted by total_cmp descending; weights exp(l/T - l0/T), the top-p
+// prefix and the threshold walk are sequential f32 sums in list order.
+void sample_last_token(const float* logits, size_t seq_len, size_t vocab, float temperature, size_t top_k,
+                       float top_p, uint64_t* state, uint32_t* token_id, float* probability) {
+  if (sampler_is_greedy(temperature, top_k, top_p)) {
+    argmax_last_token(logits, seq_len, vocab, token_id, probability);
+    return;
+  }
+  if (seq_len == 0 || vocab == 0) fail(ErrorKind::InvalidShape, "sample_last_token requires non-empty logits");
+  const float* row = logits + (seq_len - 1) * vocab;
+  const size_t k = std::min(std::max(top_k, static_cast<size_t>(1)), vocab);
+  std::vector<std::pair<size_t, float>> cand;
+  cand.reserve(k);
+  if (k == vocab) {
+    for (size_t i = 0; i < vocab; ++i) cand.emplace_back(i, row[i]);
+  } else {
+    for (size_t i = 0; i < vocab; ++i) {
+      if (cand.size() < k) {
+        cand.emplace_back(i, row[i]);
+        continue;
+      }
+      size_t min_pos = 0;  // Iterator::min_by keeps the first of equal minima
+      for (size_t j = 1; j < cand.size(); ++j) {
+        if (total_cmp_key(cand[j].second) < total_cmp_key(cand[min_pos].second)) min_pos = j;
+      }
+      if (row[i] > cand[min_pos].second) cand[min_pos] = {i, row[i]};
+    }
+  }
+  std::stable_sort(cand.begin(), cand.end(), [](const std::pair<size_t, float>& a, const std::pair<size_t, float>& b) {
+    return total_cmp_key(a.second) > total_cmp_key(b.second);
+  });
+  const float temp = std::fmax(temperature, FLT_EPSILON);  // f32::max ignores a NaN operand
+  const float scaled_max = cand[0].second / temp;
+  std::vector<float> weight(cand.size());
+  float total_weight = 0.0f;
+  for (size_t i = 0; i < cand.size(); ++i) {
+    weight[i] = std::exp((cand[i].second / temp) - scaled_max);
+    total_weight = total_weight + weight[i];
+  }
+  if (!std::isfinite(total_weight) || total_weight <= 0.0f) {
+    fail(ErrorKind::Runtime, "failed to build a finite sampling distribution");
+  }
+  float p = top_p;  // f32::clamp(0, 1); a NaN stays NaN
+  if (p < 0.0f) p = 0.0f;
+  if (p > 1.0f) p = 1.0f;
+  const float cutoff = p >= 1.0f ? total_weight : total_weight * p;
+  float retained_weight = 0.0f;
+  size_t retained = 0;
+  for (size_t i = 0; i < cand.size(); ++i) {
+    retained_weight = retained_weight + weight[i];
+    ++retained;
+    if (retained_weight >= cutoff) break;
+  }
+  retained = std::max(retained, static_cast<size_t>(1));
+  float retained_total = 0.0f;
+  for (size_t i = 0; i < retained; ++i) retained_total = retained_total + weight[i];
+  float threshold = sampler_next_f32(state) * retained_total;
+  size_t selected = 0;
+  for (size_t i = 0; i < retained; ++i) {
+    threshold = threshold - weight[i];
+    if (threshold <= 0.0f) {
+      selected = i;
+      break;
+    }
+  }
+  *token_id = static_cast<uint32_t>(cand[selected].first);
+  *probability = weight[selected] / retained_total;
 }
 
 // ---------------------------------------------------------------------------

@@ -307,3 +307,102 @@ def test_bf16_widening_and_rne(orc):
     assert orc.bf16_to_f32(bits).tolist() == [1.0, -1.0, 3.140625, 0.0, -0.0]
     vals = np.array([0x3F808000, 0x3F818000, 0x3F808001, 0x3F807FFF], np.uint32).view(np.float32)
     assert orc.f32_to_bf16(vals).tolist() == [0x3F80, 0x3F82, 0x3F81, 0x3F80]
+
+
+# ---- sampler (runtime/sampler.rs) ----
+MASK64 = (1 << 64) - 1
+
+
+def _xorshift_star(x):
+    """One SamplerState::next_f32 step written from the published xorshift64* recurrence."""
+    x ^= x >> 12
+    x ^= (x << 25) & MASK64
+    x ^= x >> 27
+    value = (x * 0x2545F4914F6CDD1D) & MASK64
+    return np.float32((value >> 40) / float(1 << 24)), x
+
+
+def test_sampler_rng_matches_xorshift64_star(orc):
+    assert orc.sampler_state_new(0) == 0x9E3779B97F4A7C15  # sampler.rs:57-61
+    assert orc.sampler_state_new(123) == 123
+    for seed in (0, 42, 123):
+        st = orc.sampler_state_new(seed)
+        x = st
+        for _ in range(1000):
+            v, st = orc.sampler_next_f32(st)
+            want, x = _xorshift_star(x)
+            assert st == x and np.float32(v) == want
+
+
+def test_sampler_reference_unit_tests(orc):
+    # sampler.rs:247-260: argmax of the last row [1, 3, 2] is 1
+    tok, prob = orc.argmax_last_token(np.array([[0, 1, 2], [1, 3, 2]], np.float32))
+    assert tok == 1 and 0.0 < prob <= 1.0
+    # sampler.rs:262-284: top_k = 2 over [1, 3, 2, 0.5] samples 1 or 2
+    tok, prob, _ = orc.sample_last_token(np.array([[1.0, 3.0, 2.0, 0.5]], np.float32), 1.0, 2, 1.0,
+                                         orc.sampler_state_new(123))
+    assert tok in (1, 2) and 0.0 < prob <= 1.0
+
+
+def test_sampler_greedy_configs_take_argmax_and_keep_the_state(orc):
+    row = np.array([[0.5, 2.0, 2.0, -1.0]], np.float32)  # ties: the last maximum (max_by)
+    for t, k, p in ((0.0, 20, 0.9), (0.7, 1, 0.9), (0.7, 20, 0.0)):
+        tok, prob, st = orc.sample_last_token(row, t, k, p, 77)
+        assert (tok, prob) == orc.argmax_last_token(row) and tok == 2 and st == 77
+
+
+def _draws(orc, row, t, k, p, n, seed=1):
+    st = orc.sampler_state_new(seed)
+    counts = np.zeros(row.shape[-1], np.int64)
+    for _ in range(n):
+        tok, _, st = orc.sample_last_token(row, t, k, p, st)
+        counts[tok] += 1
+    return counts
+
+
+def test_sampler_frequencies_follow_the_weights(orc):
+    row = np.array([[0.0, 1.0, 2.0, 3.0]], np.float32)
+    n = 20000
+    for t, k, keep in ((1.0, 4, [0, 1, 2, 3]), (0.5, 4, [0, 1, 2, 3]), (1.0, 2, [2, 3])):
+        counts = _draws(orc, row, t, k, 1.0, n)
+        w = np.zeros(4)
+        w[keep] = np.exp(row[0, keep] / t)
+        w /= w.sum()
+        assert all(counts[i] == 0 for i in range(4) if i not in keep)
+        sigma = np.sqrt(n * w * (1 - w)) + 1e-9
+        assert np.all(np.abs(counts - n * w) <= 5 * sigma), (t, k, counts, n * w)
+
+
+def test_sampler_top_p_keeps_the_shortest_reaching_prefix(orc):
+    # sorted weights exp(l - 3): 1, e^-1, e^-2, e^-3 (total 1.553); top_p 0.7 -> cutoff 1.087:
+    # the prefix {3, 2} is the first to reach it
+    row = np.array([[0.0, 1.0, 2.0, 3.0]], np.float32)
+    counts = _draws(orc, row, 1.0, 4, 0.7, 4000)
+    assert counts[0] == 0 and counts[1] == 0 and counts[2] > 0 and counts[3] > 0
+    counts = _draws(orc, row, 1.0, 4, 0.5, 500)  # 1 / 1.553 = 0.644 >= 0.5: only token 3
+    assert counts[3] == 500
+
+
+def test_sampler_top_k_replacement_order(orc):
+    # sampler.rs:168-183: a full candidate list replaces its FIRST minimum (list order) only by
+    # a strictly larger logit.  [1, 1, 5, 1], k = 2: (0,1),(1,1) -> 5 replaces position 0 ->
+    # (2,5),(1,1); the last 1 is not larger -> candidates {2, 1}, never 0 or 3.
+    counts = _draws(orc, np.array([[1.0, 1.0, 5.0, 1.0]], np.float32), 100.0, 2, 1.0, 400)
+    assert counts[0] == 0 and counts[3] == 0 and counts[1] > 0 and counts[2] > 0
+    # [3, 1, 1, 2], k = 2: the second 1 does not replace, 2 replaces the 1 at position 1 -> {0, 3}
+    counts = _draws(orc, np.array([[3.0, 1.0, 1.0, 2.0]], np.float32), 100.0, 2, 1.0, 400)
+    assert counts[1] == 0 and counts[2] == 0 and counts[0] > 0 and counts[3] > 0
+
+
+def test_sampler_threshold_walk_and_stable_order(orc):
+    # [2, 2, 0], k = V: stable sort keeps (0, 2) before (1, 2); weights 1, 1, e^-2 (T = 1);
+    # threshold = u * total, subtracted in list order: token 0 iff u * total <= 1
+    row = np.array([[2.0, 2.0, 0.0]], np.float32)
+    st = orc.sampler_state_new(9)
+    for _ in range(200):
+        u, nxt = orc.sampler_next_f32(st)
+        total = np.float32(1.0) + np.float32(1.0) + np.float32(np.exp(np.float32(-2.0)))
+        thr = np.float32(np.float32(u) * total)
+        want = 0 if thr - np.float32(1.0) <= 0 else (1 if thr - np.float32(1.0) - np.float32(1.0) <= 0 else 2)
+        tok, prob, st = orc.sample_last_token(row, 1.0, 3, 1.0, st)
+        assert st == nxt and tok == want
