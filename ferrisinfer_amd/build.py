@@ -23,6 +23,7 @@ SOURCES = [
     "fi_gemm.hip",
     "fi_gemm_packed.hip",
     "fi_gemm_bf16.hip",
+    "fi_sample.hip",
 ]
 
 # gfx950 only; packed-fp32 instructions are disabled (the compiler would otherwise form

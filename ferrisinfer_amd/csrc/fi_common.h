@@ -13,6 +13,8 @@ enum : uint32_t {
   FI_FAULT_SLOT_RANGE = 1u << 0,   // kv append: slot beyond the pool
   FI_FAULT_TOKEN_RANGE = 1u << 1,  // embedding: token id beyond the vocabulary
   FI_FAULT_BLOCK_RANGE = 1u << 2,  // attention: block id beyond the pool
+  FI_FAULT_SAMPLE_TOPK = 1u << 3,       // sampling: top_k (after clamping to the vocabulary) above 1024
+  FI_FAULT_SAMPLE_NONFINITE = 1u << 4,  // sampling: the candidate weights do not sum to a finite, positive total
 };
 
 struct fi_context {

@@ -185,6 +185,8 @@ int32_t fi_ctx_check_faults(fi_context* ctx) {
   if (bits & FI_FAULT_SLOT_RANGE) msg += " KV slot beyond the block pool;";
   if (bits & FI_FAULT_TOKEN_RANGE) msg += " token id out of vocabulary range;";
   if (bits & FI_FAULT_BLOCK_RANGE) msg += " block id beyond the block pool;";
+  if (bits & FI_FAULT_SAMPLE_TOPK) msg += " sampling top_k above the device limit of 1024;";
+  if (bits & FI_FAULT_SAMPLE_NONFINITE) msg += " failed to build a finite sampling distribution;";
   return fi::set_error(FI_ERR_RUNTIME, msg);
 }
 

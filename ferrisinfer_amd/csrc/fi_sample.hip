@@ -1,0 +1,776 @@
+// Device-side token sampling: sample_last_token (runtime/sampler.rs:121-241) and, for greedy
+// configurations, argmax_last_token (sampler.rs:77-119), one workgroup of 8 waves per logits
+// row.
+//
+// Top-k.  The reference keeps its k candidates by streaming replacement: the first k logits
+// fill the list; a later logit that is strictly larger (IEEE >) than the list's minimum
+// replaces the FIRST minimum in list order (Iterator::min_by over total_cmp).  Replacement
+// keeps the list's values equal to the k largest values of the prefix scanned so far, so:
+//   * fast path, one pass: a logit below the k+1-th largest value of some part of the row
+//     cannot be among the k + 1 largest.  Each wave buffers in LDS only the logits at or above
+//     its running bound (the k+1-th largest of what it has buffered, raised to the other
+//     waves' bounds) and compacts the buffer by radix selection when it fills.  When the k+1
+//     largest values of the row are strictly decreasing and the row holds no NaN, the final
+//     list is exactly the k largest logits, in value order;
+//   * otherwise (equal values among the top k + 1, signed zeros, NaN) list positions decide
+//     which equal logit is kept and how equal candidates are ordered, and the replacement is
+//     replayed: in rounds of one 1024-logit step per wave, every wave keeps the logits of its step
+//     above the list minimum published at the round's start (the minimum never falls, so a
+//     logit not above it cannot enter later), in index order; wave 0, holding the list in
+//     registers, applies them one by one against the current minimum.  The list is then
+//     sorted stably by total_cmp descending.
+// Weights exp(l / T - l0 / T) are computed in parallel; one lane then forms the total, the
+// top-p prefix, the retained total, the xorshift64* draw and the threshold walk, sequentially
+// in f32 in list order.  The exponential is the device expf; the reference's is the host
+// libm's, so a weight may differ in its last bit.
+#include "fi_common.h"
+#include "fi_device.h"
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxTopK = 1024;
+constexpr int kPerLane = 16;          // logits per lane per wave step
+constexpr int kStep = 64 * kPerLane;  // logits per wave step
+constexpr int kGroup = 256;           // logits per wave appended between buffer checks
+constexpr int kRegion = 1536;         // buffered candidates per wave: k + 1 (at most 1025), equal ones, one group
+constexpr int kSortMax = 2048;        // fast-path candidates sorted at the end
+constexpr int kRankSortMax = 256;     // at most this many: rank counting, else a bitonic sort
+constexpr int kIntMin = static_cast<int>(0x80000000u);
+
+// total_cmp as a signed-integer order
+__device__ __forceinline__ int32_t total_key(float v) {
+  const int32_t b = __float_as_int(v);
+  return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
+}
+
+__device__ __forceinline__ float key_value(int32_t key) {
+  return __int_as_float(key ^ static_cast<int32_t>(static_cast<uint32_t>(key >> 31) >> 1));
+}
+
+__device__ __forceinline__ int lanes_below(uint64_t ballot) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ballot >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ballot), 0)));
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_vec(const float* p, float (&v)[VEC]) {
+  if constexpr (VEC == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+    v[3] = t.w;
+  } else {
+    v[0] = *p;
+  }
+}
+
+// Logit e (0..kPerLane) of this lane in wave step s: groups of VEC consecutive logits, lanes
+// ascending within a group, groups ascending.
+template <int VEC>
+__device__ __forceinline__ int step_index(int s, int lane, int e) {
+  return s * kStep + ((e / VEC) * 64 + lane) * VEC + (e % VEC);
+}
+
+// The kPerLane logits of wave step s (addresses clamped into the row; step_index < vocab
+// tells which are real).
+template <int VEC>
+__device__ __forceinline__ void load_step(const float* row, int vocab, int s, int lane, float (&v)[kPerLane]) {
+  const int last = vocab - VEC;  // last vector start (vocab % VEC == 0)
+#pragma unroll
+  for (int j = 0; j < kPerLane / VEC; ++j) {
+    float t[VEC];
+    load_vec<VEC>(row + min(step_index<VEC>(s, lane, j * VEC), last), t);
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) v[j * VEC + u] = t[u];
+  }
+}
+
+// Runs f(logits, s) over wave steps first, first + stride, ... with a ring of four step
+// buffers: three steps of loads are in flight while one is processed.  Every call is made
+// unconditionally (steps at or past nsteps hold no real logit; f masks them by index) so that
+// no load is sunk into a branch next to its use.
+template <int VEC, typename F>
+__device__ __forceinline__ void stream_steps(const float* row, int vocab, int first, int stride, int nsteps, int lane,
+                                             F&& f) {
+  float b0[kPerLane], b1[kPerLane], b2[kPerLane], b3[kPerLane];
+  load_step<VEC>(row, vocab, first, lane, b0);
+  load_step<VEC>(row, vocab, first + stride, lane, b1);
+  load_step<VEC>(row, vocab, first + 2 * stride, lane, b2);
+  for (int s = first; s < nsteps; s += 4 * stride) {
+    load_step<VEC>(row, vocab, s + 3 * stride, lane, b3);
+    f(b0, s);
+    load_step<VEC>(row, vocab, s + 4 * stride, lane, b0);
+    f(b1, s + stride);
+    load_step<VEC>(row, vocab, s + 5 * stride, lane, b1);
+    f(b2, s + 2 * stride);
+    load_step<VEC>(row, vocab, s + 6 * stride, lane, b2);
+    f(b3, s + 3 * stride);
+  }
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Radix selection, one 8-bit digit: hist[256] holds the counts of the candidates matching the
+// digits chosen so far; returns the digit of the element of descending rank `want` among them
+// and makes `want` its rank within that digit (one wave).
+__device__ __forceinline__ int pick_digit_desc(const int* hist, int lane, int& want) {
+  int c[4];
+  int tot = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    c[q] = hist[255 - (4 * lane + q)];  // lanes ascending = digits descending
+    tot += c[q];
+  }
+  int incl = tot;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += t;
+  }
+  const int excl = incl - tot;
+  const bool here = excl <= want && want < incl;
+  int digit = 0, below = 0, acc = excl;
+  bool found = false;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (here && !found && want < acc + c[q]) {
+      digit = 255 - (4 * lane + q);
+      below = acc;
+      found = true;
+    }
+    acc += c[q];
+  }
+  const int src = __builtin_ctzll(__ballot(here));
+  digit = __builtin_amdgcn_readlane(digit, src);
+  below = __builtin_amdgcn_readlane(below, src);
+  want -= below;
+  return digit;
+}
+
+// Key of descending rank `rank` among key[0, n) (one wave; n > rank).
+__device__ int wave_select_desc(const int* key, int n, int rank, int* hist, int lane) {
+  uint32_t prefix = 0, mask = 0;
+  int want = rank;
+  for (int d = 24; d >= 0; d -= 8) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hist[lane + 64 * q] = 0;
+    wave_sync();
+    for (int i = lane; i < n; i += 64) {
+      const uint32_t u = static_cast<uint32_t>(key[i]) ^ 0x80000000u;
+      if ((u & mask) == prefix) atomicAdd(&hist[(u >> d) & 255u], 1);
+    }
+    wave_sync();
+    const int digit = pick_digit_desc(hist, lane, want);
+    prefix |= static_cast<uint32_t>(digit) << d;
+    mask |= 255u << d;
+    wave_sync();
+  }
+  return static_cast<int>(prefix ^ 0x80000000u);
+}
+
+// Keeps the entries of key/idx[0, n) with key >= bound, in place; returns their count (one wave).
+__device__ int wave_compact(int* key, int* idx, int n, int bound, int lane) {
+  int out = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const bool in = i < n;
+    const int kk = in ? key[i] : 0;
+    const int ii = in ? idx[i] : 0;
+    const bool keep = in && kk >= bound;
+    const uint64_t b = __ballot(keep);
+    wave_sync();  // the chunk is read before any of it is overwritten
+    if (keep) {
+      const int pos = out + lanes_below(b);
+      key[pos] = kk;
+      idx[pos] = ii;
+    }
+    out += __popcll(b);
+    wave_sync();
+  }
+  return out;
+}
+
+// (key, id) before (key', id') in (key descending, id ascending) order.
+__device__ __forceinline__ bool before(int ka, int ia, int kb, int ib) { return ka > kb || (ka == kb && ia < ib); }
+
+// Sorts key/id[0, n) into (key descending, id ascending) order in place (whole workgroup;
+// the arrays hold at least the next power of two >= n entries).
+__device__ void block_bitonic_sort(int* key, int* id, int n, int tid) {
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + tid; i < n2; i += kThreads) {
+    key[i] = kIntMin;
+    id[i] = 0x7fffffff;
+  }
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < (n2 >> 1); t += kThreads) {
+        const int i = 2 * t - (t & (stride - 1));
+        const int j = i + stride;
+        const int ka = key[i], ia = id[i], kb = key[j], ib = id[j];
+        const bool up = (i & size) == 0;
+        if (up ? before(kb, ib, ka, ia) : before(ka, ia, kb, ib)) {
+          key[i] = kb;
+          id[i] = ib;
+          key[j] = ka;
+          id[j] = ia;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Minimum of wave 0's register list by total_cmp, first list position among equal minima.
+template <int NS>
+__device__ __forceinline__ void list_min(const float (&val)[NS], int k, int lane, int* pos, float* minv) {
+  int best_key = 0x7fffffff, best_pos = 0x7fffffff;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int p = s * 64 + lane;
+    const int key = total_key(val[s]);
+    if (p < k && key < best_key) {  // slots ascend, so the first equal minimum stays
+      best_key = key;
+      best_pos = p;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int ok = __shfl_xor(best_key, off, 64);
+    const int op = __shfl_xor(best_pos, off, 64);
+    if (ok < best_key || (ok == best_key && op < best_pos)) {
+      best_key = ok;
+      best_pos = op;
+    }
+  }
+  *pos = best_pos;
+  float v = 0.0f;  // the owner lane's slot value (every slot is read so the list stays in registers)
+#pragma unroll
+  for (int s = 0; s < NS; ++s) v = (s == (best_pos >> 6)) ? val[s] : v;
+  *minv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), best_pos & 63));
+}
+
+struct SampleShared {
+  int key[kWaves][kRegion];  // per-wave candidate buffers (fast path: total_cmp keys; replay: logit bits)
+  int idx[kWaves][kRegion];  // their logit indices
+  int hist[kWaves][256];
+  union {
+    struct {
+      int key[kSortMax];
+      int idx[kSortMax];
+    } fast;  // candidates at or above the k+1-th largest logit, then sorted
+    struct {
+      float val[kMaxTopK];
+      int idx[kMaxTopK];
+    } list;  // the replayed list, by position
+  } u;
+  float s_val[kMaxTopK + 1];  // the sorted list
+  int s_idx[kMaxTopK + 1];
+  alignas(16) float wts[kMaxTopK];  // its weights (zero past k)
+  int bound[kWaves];    // each wave's current lower bound (a total_cmp key)
+  int count[kWaves];
+  int flags;  // bit 0: NaN seen, bit 1: buffer overflow, bit 2: not strictly decreasing
+  int sel[2];
+  int m;
+  float pub_min;  // replay: the list minimum at the start of the round
+  float red_f[kWaves][2];
+  int red_i[kWaves][3];
+};
+
+// The reference's replacement over the whole row, replayed exactly (whole workgroup; wave 0
+// holds the list, NS slots per lane).  Leaves list position p in sh.u.list.val[p] / idx[p].
+template <int VEC, int NS>
+__device__ __forceinline__ void replay_top_k(const float* row, int vocab, int k, int w, int lane, SampleShared& sh) {
+  float val[NS];
+  int idx[NS];
+  int min_pos = 0;
+  float min_val = 0.0f;
+  if (w == 0) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int p = s * 64 + lane;
+      val[s] = p < k ? row[p] : 0.0f;
+      idx[s] = p;
+    }
+    list_min<NS>(val, k, lane, &min_pos, &min_val);
+    if (lane == 0) sh.pub_min = min_val;
+  }
+  __syncthreads();
+  const int nsteps = (vocab + kStep - 1) / kStep;
+  const int first = k / kStep;  // the first step holding an index >= k
+  float cur[kPerLane], nxt[kPerLane];
+  load_step<VEC>(row, vocab, first + w, lane, cur);
+  for (int r0 = first; r0 < nsteps; r0 += kWaves) {
+    const int s = r0 + w;
+    load_step<VEC>(row, vocab, s + kWaves, lane, nxt);
+    // this wave's step: logits above the published minimum, in index order
+    const float bound = sh.pub_min;
+    const bool full = s * kStep >= k && (s + 1) * kStep <= vocab;
+    int cnt = 0;
+#pragma unroll
+    for (int g = 0; g < kPerLane / VEC; ++g) {
+      uint64_t b[VEC];
+      int before_lane = 0;
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) {
+        const int i = step_index<VEC>(s, lane, g * VEC + u);
+        b[u] = __ballot((full || (i >= k && i < vocab)) && cur[g * VEC + u] > bound);
+        before_lane += lanes_below(b[u]);
+      }
+      int within = 0;
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) {
+        if ((b[u] >> lane) & 1) {
+          const int pos = cnt + before_lane + within;
+          sh.key[w][pos] = __float_as_int(cur[g * VEC + u]);
+          sh.idx[w][pos] = step_index<VEC>(s, lane, g * VEC + u);
+          ++within;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) cnt += __popcll(b[u]);
+    }
+    if (lane == 0) sh.count[w] = cnt;
+    __syncthreads();
+    if (w == 0) {
+      for (int q = 0; q < kWaves; ++q) {
+        const int c = sh.count[q];
+        for (int base = 0; base < c; base += 64) {
+          const int i = base + lane;
+          const bool in = i < c;
+          const float x = in ? __int_as_float(sh.key[q][i]) : 0.0f;
+          const int id = in ? sh.idx[q][i] : 0;
+          uint64_t ball = __ballot(in && x > min_val);
+          while (ball) {  // wave-uniform, in index order
+            const int j = __builtin_ctzll(ball);
+            ball &= ball - 1;
+            const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+            if (xj > min_val) {
+              const int idj = __builtin_amdgcn_readlane(id, j);
+              const int slot = min_pos >> 6, owner = min_pos & 63;
+#pragma unroll
+              for (int t = 0; t < NS; ++t) {
+                if (t == slot && lane == owner) {
+                  val[t] = xj;
+                  idx[t] = idj;
+                }
+              }
+              list_min<NS>(val, k, lane, &min_pos, &min_val);
+            }
+          }
+        }
+      }
+      if (lane == 0) sh.pub_min = min_val;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kPerLane; ++e) cur[e] = nxt[e];
+  }
+  if (w == 0) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int p = s * 64 + lane;
+      if (p < k) {
+        sh.u.list.val[p] = val[s];
+        sh.u.list.idx[p] = idx[s];
+      }
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint64_t xorshift_step(uint64_t x) {
+  x ^= x >> 12;
+  x ^= x << 25;
+  x ^= x >> 27;
+  return x;
+}
+
+__device__ __forceinline__ void sampling_fault(uint32_t* faults, uint32_t bit, int32_t* token, float* prob, int r) {
+  atomicOr(faults, bit);
+  token[r] = -1;
+  prob[r] = 0.0f;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Combines two (running maximum, sum of 2^(x - maximum)) pairs in log2 units; a maximum of
+// -inf carries no mass.
+__device__ __forceinline__ void merge_softmax(float& m, float& sum, float om, float os) {
+  const float nm = fmaxf(m, om);
+  sum = (m > -INFINITY ? sum * __builtin_amdgcn_exp2f(m - nm) : 0.0f) +
+        (om > -INFINITY ? os * __builtin_amdgcn_exp2f(om - nm) : 0.0f);
+  m = nm;
+}
+
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restrict__ logits, int ld, int vocab,
+                                                          const float* __restrict__ temperature,
+                                                          const int32_t* __restrict__ top_k,
+                                                          const float* __restrict__ top_p, uint64_t* __restrict__ rng,
+                                                          int32_t* __restrict__ token, float* __restrict__ prob,
+                                                          uint32_t* __restrict__ faults) {
+  __shared__ SampleShared sh;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float* row = logits + (size_t)r * ld;
+  const float T = temperature[r];
+  const int K = top_k[r];
+  const float P = top_p[r];
+  const int nsteps = (vocab + kStep - 1) / kStep;
+
+  if (T <= 0.0f || K == 1 || P <= 0.0f) {  // SamplerConfig::is_greedy (sampler.rs:40-42)
+    // Last maximal index by total_cmp (Iterator::max_by) and 1 / sum exp(l - max) in one pass,
+    // the sum over finite logits against a running maximum raised once per 16 logits (base-2
+    // exponentials of log2e-scaled logits: within 1e-6 of the exact sum, where the reference's
+    // own sequential f32 sum is within (vocab - 1) * 2^-24); a NaN, a +inf or a row of -inf
+    // makes the reference's sum NaN.
+    int bk = kIntMin, bi = -1;
+    float m = -INFINITY, sum = 0.0f;
+    bool bad = false;
+    stream_steps<VEC>(row, vocab, w, kWaves, nsteps, lane, [&](const float (&v)[kPerLane], int s) {
+      const int valid = vocab - s * kStep;
+      float xs[kPerLane];
+      float smax = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) {
+        const int off = step_index<VEC>(0, lane, e);
+        const bool in = off < valid;
+        const float x = v[e];
+        const int key = total_key(x);
+        const bool take = in && key >= bk;  // indices ascend per lane: a later equal maximum wins
+        bk = take ? key : bk;
+        bi = take ? s * kStep + off : bi;
+        bad = bad || (in && !(x < INFINITY));
+        xs[e] = (in && x > -INFINITY && x < INFINITY) ? x * kLog2e : -INFINITY;
+        smax = fmaxf(smax, xs[e]);
+      }
+      // m and xs in log2 units: sum of 2^(xs - m) = sum of exp(x - max)
+      const float nm = fmaxf(m, smax);
+      sum = (nm > m) ? sum * __builtin_amdgcn_exp2f(m - nm) : sum;  // m = -inf: sum is 0
+      m = nm;
+      const float base = m > -INFINITY ? m : 0.0f;
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) sum += __builtin_amdgcn_exp2f(xs[e] - base);
+    });
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const int ok = __shfl_xor(bk, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ok > bk || (ok == bk && oi > bi)) {
+        bk = ok;
+        bi = oi;
+      }
+      merge_softmax(m, sum, __shfl_xor(m, off, 64), __shfl_xor(sum, off, 64));
+    }
+    bad = __ballot(bad) != 0;
+    if (lane == 0) {
+      sh.red_i[w][0] = bk;
+      sh.red_i[w][1] = bi;
+      sh.red_i[w][2] = bad;
+      sh.red_f[w][0] = m;
+      sh.red_f[w][1] = sum;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 1; i < kWaves; ++i) {
+        if (sh.red_i[i][0] > bk || (sh.red_i[i][0] == bk && sh.red_i[i][1] > bi)) {
+          bk = sh.red_i[i][0];
+          bi = sh.red_i[i][1];
+        }
+        merge_softmax(m, sum, sh.red_f[i][0], sh.red_f[i][1]);
+        bad = bad || sh.red_i[i][2];
+      }
+      token[r] = bi;
+      prob[r] = (bad || !(sum > 0.0f)) ? __int_as_float(0x7fc00000) : 1.0f / sum;
+    }
+    return;
+  }
+
+  const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
+  if (k > kMaxTopK) {
+    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
+    return;
+  }
+  if (tid < kWaves) sh.bound[tid] = kIntMin;
+  if (tid == 0) {
+    sh.flags = 0;
+    sh.m = 0;
+  }
+  __syncthreads();
+
+  bool sorted = false;  // s_val / s_idx hold the sorted list
+  if (k < vocab) {
+    // ---- one pass: buffer the logits that can be among the k+1 largest ----
+    int* rkey = sh.key[w];
+    int* ridx = sh.idx[w];
+    int bound = kIntMin, cnt = 0;
+    uint32_t nan_bits = 0;  // max of |bits|: above 0x7f800000 when a NaN was seen
+    stream_steps<VEC>(row, vocab, w, kWaves, nsteps, lane, [&](const float (&v)[kPerLane], int s) {
+      const int valid = vocab - s * kStep;  // logits of this step below vocab: step_index offsets < valid
+      int hits = 0;
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) {
+        const bool in = step_index<VEC>(0, lane, e) < valid;
+        const uint32_t bits = __float_as_uint(v[e]);
+        nan_bits = max(nan_bits, in ? bits & 0x7fffffffu : 0u);
+        hits += (in && total_key(v[e]) >= bound) ? 1 : 0;
+      }
+      if (__ballot(hits > 0)) {  // rare once the bound has risen: append a group at a time
+#pragma unroll
+        for (int g = 0; g < kPerLane / (kGroup / 64); ++g) {
+#pragma unroll
+          for (int e = g * (kGroup / 64); e < (g + 1) * (kGroup / 64); ++e) {
+            const bool pass = step_index<VEC>(0, lane, e) < valid && total_key(v[e]) >= bound;
+            const uint64_t ball = __ballot(pass);
+            if (pass) {
+              const int pos = cnt + lanes_below(ball);
+              rkey[pos] = total_key(v[e]);
+              ridx[pos] = step_index<VEC>(s, lane, e);
+            }
+            cnt += __popcll(ball);
+          }
+          if (cnt > kRegion - kGroup) {
+            wave_sync();
+            bound = max(bound, wave_select_desc(rkey, cnt, k, sh.hist[w], lane));
+            cnt = wave_compact(rkey, ridx, cnt, bound, lane);
+            if (lane == 0) atomicMax(&sh.bound[w], bound);
+            if (cnt > kRegion - kGroup) {  // equal logits fill the buffer: the row is replayed
+              if (lane == 0) atomicOr(&sh.flags, 2);
+              cnt = 0;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) {
+        bound = max(bound, __hip_atomic_load(&sh.bound[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      }
+    });
+    if (__ballot(nan_bits > 0x7f800000u) && lane == 0) atomicOr(&sh.flags, 1);
+    if (lane == 0) sh.count[w] = cnt;
+    __syncthreads();
+
+    if (sh.flags == 0) {
+      // ---- the k+1-th largest over all buffers (radix selection, 8 bits a round) ----
+      uint32_t prefix = 0, mask = 0;
+      int want = k;
+      for (int d = 24; d >= 0; d -= 8) {
+        if (tid < 256) sh.hist[0][tid] = 0;
+        __syncthreads();
+        for (int q = 0; q < kWaves; ++q) {
+          for (int i = tid; i < sh.count[q]; i += kThreads) {
+            const uint32_t u = static_cast<uint32_t>(sh.key[q][i]) ^ 0x80000000u;
+            if ((u & mask) == prefix) atomicAdd(&sh.hist[0][(u >> d) & 255u], 1);
+          }
+        }
+        __syncthreads();
+        if (w == 0) {
+          const int digit = pick_digit_desc(sh.hist[0], lane, want);
+          if (lane == 0) {
+            sh.sel[0] = digit;
+            sh.sel[1] = want;
+          }
+        }
+        __syncthreads();
+        prefix |= static_cast<uint32_t>(sh.sel[0]) << d;
+        mask |= 255u << d;
+        want = sh.sel[1];
+        __syncthreads();
+      }
+      const int kth = static_cast<int>(prefix ^ 0x80000000u);
+      // ---- gather the candidates at or above it ----
+      for (int q = 0; q < kWaves; ++q) {
+        for (int i = tid; i < sh.count[q]; i += kThreads) {
+          if (sh.key[q][i] >= kth) {
+            const int pos = atomicAdd(&sh.m, 1);
+            if (pos < kSortMax) {
+              sh.u.fast.key[pos] = sh.key[q][i];
+              sh.u.fast.idx[pos] = sh.idx[q][i];
+            }
+          }
+        }
+      }
+      __syncthreads();
+      const int m = sh.m;
+      if (m <= kSortMax) {
+        // ---- ranks 0..k by (key descending, index ascending) ----
+        if (m <= kRankSortMax) {
+          for (int i = tid; i < m; i += kThreads) {
+            const int key = sh.u.fast.key[i], id = sh.u.fast.idx[i];
+            int rank = 0;
+            for (int j = 0; j < m; ++j) rank += before(sh.u.fast.key[j], sh.u.fast.idx[j], key, id);
+            if (rank <= k) {
+              sh.s_val[rank] = key_value(key);
+              sh.s_idx[rank] = id;
+            }
+          }
+        } else {
+          block_bitonic_sort(sh.u.fast.key, sh.u.fast.idx, m, tid);
+          for (int i = tid; i <= k; i += kThreads) {
+            sh.s_val[i] = key_value(sh.u.fast.key[i]);
+            sh.s_idx[i] = sh.u.fast.idx[i];
+          }
+        }
+        __syncthreads();
+        for (int i = tid; i < k; i += kThreads) {
+          if (!(sh.s_val[i] > sh.s_val[i + 1])) atomicOr(&sh.flags, 4);
+        }
+        __syncthreads();
+        sorted = sh.flags == 0;
+      }
+    }
+  }
+
+  if (!sorted) {
+    // ---- the reference's replacement, replayed; then a stable sort by total_cmp ----
+    if (k < vocab) {
+      if (k <= 64) {
+        replay_top_k<VEC, 1>(row, vocab, k, w, lane, sh);
+      } else if (k <= 256) {
+        replay_top_k<VEC, 4>(row, vocab, k, w, lane, sh);
+      } else {
+        replay_top_k<VEC, 16>(row, vocab, k, w, lane, sh);
+      }
+    } else {
+      for (int p = tid; p < k; p += kThreads) {
+        sh.u.list.val[p] = row[p];
+        sh.u.list.idx[p] = p;
+      }
+      __syncthreads();
+    }
+    if (k <= kRankSortMax) {
+      for (int i = tid; i < k; i += kThreads) {
+        const int key = total_key(sh.u.list.val[i]);
+        int rank = 0;
+        for (int j = 0; j < k; ++j) rank += before(total_key(sh.u.list.val[j]), j, key, i);
+        sh.s_val[rank] = sh.u.list.val[i];
+        sh.s_idx[rank] = sh.u.list.idx[i];
+      }
+    } else {  // (key, list position) pairs in the first wave buffer
+      for (int i = tid; i < k; i += kThreads) {
+        sh.key[0][i] = total_key(sh.u.list.val[i]);
+        sh.idx[0][i] = i;
+      }
+      __syncthreads();
+      block_bitonic_sort(sh.key[0], sh.idx[0], k, tid);
+      for (int i = tid; i < k; i += kThreads) {
+        sh.s_val[i] = sh.u.list.val[sh.idx[0][i]];
+        sh.s_idx[i] = sh.u.list.idx[sh.idx[0][i]];
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- weights (parallel), then total, top-p, draw and threshold walk (one lane, in order) ----
+  const float temp = fmaxf(T, 1.1920929e-7f);  // max(f32::EPSILON); a NaN temperature gives EPSILON
+  const float scaled_max = sh.s_val[0] / temp;
+  for (int i = tid; i < kMaxTopK; i += kThreads) sh.wts[i] = i < k ? expf((sh.s_val[i] / temp) - scaled_max) : 0.0f;
+  __syncthreads();
+  if (tid == 0) {
+#pragma clang fp contract(off)
+    const float* wv = sh.wts;
+    const float4* w4 = reinterpret_cast<const float4*>(sh.wts);  // zero past k: + 0.0f leaves a sum >= +0 unchanged
+    float total = 0.0f;
+    for (int i = 0; i < k; i += 8) {
+      const float4 a = w4[i / 4], b = w4[i / 4 + 1];
+      total = total + a.x;
+      total = total + a.y;
+      total = total + a.z;
+      total = total + a.w;
+      total = total + b.x;
+      total = total + b.y;
+      total = total + b.z;
+      total = total + b.w;
+    }
+    if (!(total <= 3.402823466e+38f) || total <= 0.0f) {  // not finite, or no mass
+      sampling_fault(faults, FI_FAULT_SAMPLE_NONFINITE, token, prob, r);
+      return;
+    }
+    float p = P;  // f32::clamp(0, 1): a NaN stays NaN
+    if (p < 0.0f) p = 0.0f;
+    if (p > 1.0f) p = 1.0f;
+    const float cutoff = p >= 1.0f ? total : total * p;
+    float kept = 0.0f;
+    int retained = 0;
+    for (int i = 0; i < k; i += 4) {
+      const float4 a = w4[i / 4];
+      const float t[4] = {a.x, a.y, a.z, a.w};
+      bool reached = false;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (!reached && i + j < k) {
+          kept = kept + t[j];
+          ++retained;
+          reached = kept >= cutoff;
+        }
+      }
+      if (reached) break;
+    }
+    retained = max(retained, 1);
+    float retained_total = 0.0f;
+    for (int i = 0; i < retained; i += 4) {
+      const float4 a = w4[i / 4];
+      const float t[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) retained_total = retained_total + (i + j < retained ? t[j] : 0.0f);
+    }
+    const uint64_t x = xorshift_step(rng[r]);  // SamplerState::next_u64 / next_f32 (sampler.rs:62-75)
+    rng[r] = x;
+    const uint32_t upper = static_cast<uint32_t>((x * 0x2545F4914F6CDD1DULL) >> 40);
+    float threshold = (static_cast<float>(upper) / 16777216.0f) * retained_total;
+    int sel = 0;
+    for (int i = 0; i < retained; i += 4) {
+      const float4 a = w4[i / 4];
+      const float t[4] = {a.x, a.y, a.z, a.w};
+      bool hit = false;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (!hit && i + j < retained) {
+          threshold = threshold - t[j];
+          if (threshold <= 0.0f) {
+            sel = i + j;
+            hit = true;
+          }
+        }
+      }
+      if (hit) break;
+    }
+    token[r] = sh.s_idx[sel];
+    prob[r] = wv[sel] / retained_total;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fi_sample_tokens(fi_context* ctx, const float* d_logits, int32_t ld, int32_t rows, int32_t vocab,
+                         const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                         uint64_t* d_rng_state, int32_t* d_token, float* d_prob) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(rows >= 0 && vocab > 0 && ld >= vocab, FI_ERR_INVALID_SHAPE,
+             "fi_sample_tokens: requires non-empty logits rows (vocab > 0, ld >= vocab)");
+  if (rows == 0) return FI_OK;
+  FI_REQUIRE(d_logits && d_temperature && d_top_k && d_top_p && d_rng_state && d_token && d_prob,
+             FI_ERR_INVALID_CONFIG, "fi_sample_tokens: null pointer");
+  const bool vec4 = vocab % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(d_logits) % 16 == 0;
+  if (vec4) {
+    hipLaunchKernelGGL(sample_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                       d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+  } else {
+    hipLaunchKernelGGL(sample_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                       d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+  }
+  FI_CHECK_LAUNCH("sample_kernel");
+  return FI_OK;
+}
+
+}  // extern "C"

@@ -89,6 +89,7 @@ _SIGNATURES = {
     "fi_gemm_bf16": [_P, _P, _I32, _P, _I32, _I32, _I32, _I32, _P],
     "fi_gemm_bf16_swiglu": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P],
     "fi_lm_head_argmax_bf16": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P],
+    "fi_sample_tokens": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
 
@@ -419,6 +420,15 @@ class Context:
         check(self.lib.fi_lm_head_argmax_bf16(self.handle, ptr(hidden), int(hidden.stride(0)),
                                               ptr(bp), int(m), int(h), int(vocab), ptr(token_out),
                                               ptr(prob_out)))
+
+    def sample_tokens(self, logits, temperature, top_k, top_p, rng_state, token_out, prob_out):
+        """One token per row of logits [rows, vocab] (f32, row stride logits.stride(0)) under the
+        per-row configuration (temperature f32, top_k int32, top_p f32) and xorshift64* states
+        (uint64 stored as int64, advanced in place for sampled rows)."""
+        rows, vocab = logits.shape
+        check(self.lib.fi_sample_tokens(self.handle, ptr(logits), int(logits.stride(0)), int(rows),
+                                        int(vocab), ptr(temperature), ptr(top_k), ptr(top_p),
+                                        ptr(rng_state), ptr(token_out), ptr(prob_out)))
 
     def qkv_rope_append(self, parts, splits, biases, positions, cos_t, sin_t, rotary_dims,
                         max_positions, slot_mapping, k_cache, v_cache, kv_dtype, num_blocks,

@@ -358,6 +358,25 @@ int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const float* d_a, int32_t lda, cons
 int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const float* d_hidden, int32_t lda, const uint16_t* d_bp, int32_t m,
                                int32_t hidden, int32_t vocab, int32_t* d_token, float* d_prob);
 
+/* ---------------------------------------------------------------- sampling */
+
+/* Samples one token per logits row on the device: sample_last_token
+ * (runtime/sampler.rs:121-241) for row r's configuration (d_temperature[r], d_top_k[r],
+ * d_top_p[r]), or argmax_last_token (sampler.rs:77-119) when that configuration is greedy
+ * (SamplerConfig::is_greedy, sampler.rs:40-42: temperature <= 0, top_k == 1 or top_p <= 0).
+ * d_logits [rows, ld] f32 holds each sequence's last-token logits (the row the reference takes
+ * from [seq_len, vocab]); d_rng_state[r] is row r's SamplerState (sampler.rs:51-75; seed 0 maps
+ * to 0x9e3779b97f4a7c15 when the state is created), advanced by one draw for a sampled row and
+ * left as it is for a greedy row.  Writes the token id and its probability (weight / retained
+ * total, or 1 / sum exp(l - max) when greedy).  top_k below 1 counts as 1 (usize::max(1)); a
+ * top_k that stays above 1024 after clamping to the vocabulary, and a distribution whose total
+ * weight is not finite and positive (sampler.rs:195-200, Runtime), write token -1 and are
+ * reported as Runtime by the next fi_ctx_check_faults().  Probabilities may differ from the
+ * host's in the last bits (device expf); tokens are the reference's. */
+int32_t fi_sample_tokens(fi_context* ctx, const float* d_logits, int32_t ld, int32_t rows, int32_t vocab,
+                         const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
+                         uint64_t* d_rng_state, int32_t* d_token, float* d_prob);
+
 #ifdef __cplusplus
 }
 #endif
