@@ -68,6 +68,15 @@ int32_t fr_create(int32_t ordinal, const fr_model_config* mc, const fr_runtime_c
     c.tie_word_embeddings = mc->tie_word_embeddings != 0;
     r->session.max_sequence_length = rc->max_sequence_length;
     r->session.max_generated_tokens = rc->max_generated_tokens;
+    if (rc->top_k < 0) fr::fail(fr::ErrorKind::InvalidConfig, "sampler top_k must not be negative");
+    r->session.sampler.temperature = rc->temperature;
+    r->session.sampler.top_k = rc->top_k;
+    r->session.sampler.top_p = rc->top_p;
+    r->session.sampler.repetition_penalty = rc->repetition_penalty;
+    r->session.sampler.seed = rc->seed;
+    if (!r->session.sampler.is_greedy() && std::min<int64_t>(std::max<int64_t>(rc->top_k, 1), mc->vocab_size) > 1024) {
+      fr::fail(fr::ErrorKind::Unsupported, "sampler top_k above 1024 is not supported by the device sampler");
+    }
     r->sched.max_batch_size = rc->max_batch_size;
     r->sched.max_prefill_chunk_tokens = rc->max_prefill_chunk_tokens;
     r->sched.max_prefill_batch_tokens = rc->max_prefill_batch_tokens;

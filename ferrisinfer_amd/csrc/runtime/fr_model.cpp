@@ -265,7 +265,17 @@ void ForwardExecutor::reserve(size_t tokens, size_t seqs) {
   prob_.reserve(ctx_, cap_seqs_ * 4);
 }
 
-std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
+uint64_t sampler_state_new(uint64_t seed) { return seed == 0 ? 0x9e3779b97f4a7c15ULL : seed; }
+
+uint64_t sampler_state_next(uint64_t x) {
+  x ^= x >> 12;
+  x ^= x << 25;
+  x ^= x >> 27;
+  return x;
+}
+
+std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const SamplerConfig& sampler,
+                                              std::vector<uint64_t>* states) {
   const auto t_start = std::chrono::steady_clock::now();
   enqueue_s_ = wait_s_ = 0.0;
   const ModelConfig& c = model_->config();
@@ -370,16 +380,45 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b) {
     check(fi_splitk_residual_rms_norm(ctx_, part, s_w2, w.w2_bias.f32(), h1, hidden, next_norm, normed, T, H,
                                       c.rms_norm_eps));
   }
-  // the final norm ran over every row; each sequence's last row feeds the fused greedy head
-  // (matmul.rs:190-274)
+  // the final norm ran over every row; each sequence's last row feeds the head
   check(fi_embedding(ctx_, normed, T, H, d_last, B, last_norm_.f32()));
-  check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, model_->lm_head_packed(), B, H, c.vocab_size,
-                                 static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  const bool greedy = sampler.is_greedy();
+  if (greedy) {
+    // fused greedy head (matmul_rhs_transposed_argmax_f32, matmul.rs:190-274), as the
+    // reference session's greedy path (session.rs:349-356, 393-398)
+    check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, model_->lm_head_packed(), B, H, c.vocab_size,
+                                   static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  } else {
+    // last-row logits (matmul_rhs_transposed, one K split) and sample_last_token per row
+    // (session.rs:357-373, 399-406) with each sequence's sampler state
+    if (states == nullptr || states->size() != static_cast<size_t>(B)) {
+      fail(ErrorKind::InvalidShape, "sampled batch requires one sampler state per sequence");
+    }
+    logits_.reserve(ctx_, static_cast<size_t>(B) * c.vocab_size * 4);
+    check(fi_gemm_packed(ctx_, last_norm_.f32(), H, model_->lm_head_packed(), H, c.vocab_size, DeviceModel::kLmPack,
+                         B, 1, logits_.f32()));
+    // one upload: states [B] u64, temperature [B] f32, top_k [B] i32, top_p [B] f32
+    std::vector<uint8_t> cfg(static_cast<size_t>(B) * 20);
+    std::memcpy(cfg.data(), states->data(), static_cast<size_t>(B) * 8);
+    const int32_t k32 = static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(sampler.top_k, 0), INT32_MAX));
+    for (int32_t i = 0; i < B; ++i) {
+      std::memcpy(cfg.data() + B * 8 + i * 4, &sampler.temperature, 4);
+      std::memcpy(cfg.data() + B * 12 + i * 4, &k32, 4);
+      std::memcpy(cfg.data() + B * 16 + i * 4, &sampler.top_p, 4);
+    }
+    samp_.reserve(ctx_, cfg.size());
+    check(fi_buf_upload(ctx_, samp_.get(), cfg.size(), cfg.data(), cfg.size()));
+    uint8_t* d = static_cast<uint8_t*>(samp_.get());
+    check(fi_sample_tokens(ctx_, logits_.f32(), c.vocab_size, B, c.vocab_size, reinterpret_cast<const float*>(d + B * 8),
+                           reinterpret_cast<const int32_t*>(d + B * 12), reinterpret_cast<const float*>(d + B * 16),
+                           reinterpret_cast<uint64_t*>(d), static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  }
   const auto t_enqueued = std::chrono::steady_clock::now();
   std::vector<int32_t> tok(B);
   std::vector<float> prob(B);
   check(fi_buf_download(ctx_, tok.data(), B * 4, tok_.get(), B * 4));
   check(fi_buf_download(ctx_, prob.data(), B * 4, prob_.get(), B * 4));
+  if (!greedy) check(fi_buf_download(ctx_, states->data(), B * 8, samp_.get(), B * 8));
   check(fi_ctx_check_faults(ctx_));
   enqueue_s_ = std::chrono::duration<double>(t_enqueued - t_start).count();
   wait_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_enqueued).count();

@@ -179,6 +179,7 @@ struct Sequence {
   size_t position = 0;
   std::vector<uint32_t> history;
   std::optional<TokenSample> last_sample;
+  uint64_t sampler_state = 0;  // SamplerState of the session (session.rs:100, 138)
   // KV: logical block i -> pool block blocks[i]
   std::vector<int32_t> blocks;
 
@@ -261,9 +262,22 @@ struct SchedulerConfig {
   size_t min_prefix_share_tokens = 64;
 };
 
+// runtime/sampler.rs:3-43: SamplerConfig (greedy by default) and SamplerState (xorshift64*).
+struct SamplerConfig {
+  float temperature = 0.0f;
+  int64_t top_k = 1;
+  float top_p = 1.0f;
+  float repetition_penalty = 1.0f;
+  uint64_t seed = 0;
+  bool is_greedy() const { return temperature <= 0.0f || top_k == 1 || top_p <= 0.0f; }  // sampler.rs:40-42
+};
+uint64_t sampler_state_new(uint64_t seed);   // SamplerState::new (sampler.rs:55-63)
+uint64_t sampler_state_next(uint64_t state);  // the state after one draw (sampler.rs:65-70)
+
 struct SessionConfig {
   size_t max_sequence_length = 4096;
   size_t max_generated_tokens = 512;
+  SamplerConfig sampler;  // every session's sampler (session.rs:29-46)
 };
 
 // runtime/scheduler.rs:54-71
@@ -307,8 +321,10 @@ struct PackedBatch {
 class ForwardExecutor {
  public:
   ForwardExecutor(const DeviceModel* model, BlockPool* pool);
-  // Returns one sample per batch sequence (the argmax of its last row).
-  std::vector<TokenSample> run(const PackedBatch& batch);
+  // Returns one sample per batch sequence from its last row: the fused argmax head for a
+  // greedy sampler, else the row's logits through the device sampler with states[i]
+  // (advanced in place by one draw per sequence).
+  std::vector<TokenSample> run(const PackedBatch& batch, const SamplerConfig& sampler, std::vector<uint64_t>* states);
   // Host seconds of the last run: enqueueing every launch, then waiting for the samples.
   double last_enqueue_seconds() const { return enqueue_s_; }
   double last_wait_seconds() const { return wait_s_; }
@@ -319,7 +335,7 @@ class ForwardExecutor {
   const DeviceModel* model_;
   BlockPool* pool_;
   fi_context* ctx_;
-  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, tok_, prob_;
+  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, tok_, prob_, logits_, samp_;
   size_t cap_tokens_ = 0, cap_seqs_ = 0, cap_parts_ = 0;
   double enqueue_s_ = 0.0, wait_s_ = 0.0;
 };

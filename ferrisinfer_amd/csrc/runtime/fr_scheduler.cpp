@@ -206,6 +206,7 @@ uint64_t Scheduler::submit(const std::vector<uint32_t>& prompt, size_t max_new_t
   s.requested_max_new_tokens = max_new_tokens;
   s.max_new_tokens = std::min(max_new_tokens, session_.max_generated_tokens);
   s.stop_token = stop_token;
+  s.sampler_state = sampler_state_new(session_.sampler.seed);  // Session::new (session.rs:110, 138)
   const uint64_t id = s.sequence_id;
   sequences_.push_back(std::move(s));
   block_manager_.update_shared_prefix(id, std::nullopt);
@@ -328,8 +329,15 @@ size_t Scheduler::maybe_share_prefix(uint64_t id, PackedBatch* batch, uint64_t* 
   share_blocks(target, source, shared, batch);
   target.position = shared;
   target.history.assign(source.history.begin(), source.history.begin() + shared);
+  // import_prefix_from (session.rs:188-211): reset, then the source's last sample and sampler
+  // state when the whole source history is imported (every session has the same sampler);
+  // either may still be produced by this tick's forward (see execute_next_tick)
   target.last_sample.reset();
-  if (shared == source.position) target.last_sample = source.last_sample;  // may be filled after the forward
+  target.sampler_state = sampler_state_new(session_.sampler.seed);
+  if (shared == source.position) {
+    target.last_sample = source.last_sample;
+    target.sampler_state = source.sampler_state;
+  }
   target.record_prefill(shared);
   block_manager_.update_shared_prefix(id, std::move(assignment));
   refresh_prefix_metadata(id);
@@ -406,11 +414,17 @@ std::optional<TickReport> Scheduler::execute_next_tick() {
       const size_t reused = maybe_share_prefix(id, &batch, &source_id);
       Sequence& s = sequences_[index_of(id)];
       const size_t appended = s.next_prefill_chunk_len(config_.max_prefill_chunk_tokens);
-      if (appended == 0 && reused > 0 && reused == sequences_[index_of(source_id)].position &&
+      if (reused > 0 && reused == sequences_[index_of(source_id)].position &&
           std::find(computed.begin(), computed.end(), source_id) != computed.end()) {
         // The whole history was shared from a source that ran earlier in this tick: in
-        // sequential order its new last sample is the one copied, so take it after the forward.
-        copy_sample.emplace_back(id, source_id);
+        // sequential order the source had already drawn its new sample, so the copied
+        // sampler state is the one after that draw; its last sample is taken after the forward
+        // (when this sequence adds no rows of its own).
+        if (!session_.sampler.is_greedy()) {
+          Sequence& t = sequences_[index_of(id)];
+          t.sampler_state = sampler_state_next(t.sampler_state);
+        }
+        if (appended == 0) copy_sample.emplace_back(id, source_id);
       }
       if (appended > 0) {
         // session.rs:220-244 / 381-412
@@ -481,15 +495,22 @@ std::optional<TickReport> Scheduler::execute_next_tick() {
   const double sched_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   double enqueue_s = 0.0, wait_s = 0.0;
   if (!batch.sequence_ids.empty() || !batch.copy_src.empty()) {
-    std::vector<TokenSample> samples = executor_.run(batch);
+    std::vector<uint64_t> states(batch.sequence_ids.size());
+    for (size_t i = 0; i < states.size(); ++i) states[i] = sequences_[index_of(batch.sequence_ids[i])].sampler_state;
+    std::vector<TokenSample> samples = executor_.run(batch, session_.sampler, &states);
     enqueue_s = executor_.last_enqueue_seconds();
     wait_s = executor_.last_wait_seconds();
     for (size_t i = 0; i < batch.sequence_ids.size(); ++i) {
-      sequences_[index_of(batch.sequence_ids[i])].last_sample = samples[i];
+      Sequence& s = sequences_[index_of(batch.sequence_ids[i])];
+      s.last_sample = samples[i];
+      s.sampler_state = states[i];
     }
   }
   for (auto& [target, source] : copy_sample) {
-    sequences_[index_of(target)].last_sample = sequences_[index_of(source)].last_sample;
+    Sequence& t = sequences_[index_of(target)];
+    const Sequence& src = sequences_[index_of(source)];
+    t.last_sample = src.last_sample;
+    t.sampler_state = src.sampler_state;
   }
   for (uint64_t id : to_release) {
     Sequence& s = sequences_[index_of(id)];

@@ -110,6 +110,14 @@ def load() -> C.CDLL:
         if not os.path.exists(LIB_PATH):
             raise FerrisError(8, f"HIP backend {LIB_PATH} is not built; run "
                                  "`python -m ferrisinfer_amd.build` (or __graft_entry__.build())")
+        # torch bundles its own libamdhip64 (soname libamdhip64.so.7) and binds its libraries to
+        # it by path.  Loaded first, it also satisfies this library's libamdhip64.so.7
+        # dependency, so the process holds a single HIP runtime; loaded after this library, it
+        # would bring a second one, whose initialisation fails.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = C.CDLL(LIB_PATH)
         for name, args in _SIGNATURES.items():
             fn = getattr(lib, name, None)

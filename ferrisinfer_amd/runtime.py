@@ -29,7 +29,9 @@ class RuntimeConfig(C.Structure):
                 ("max_prefill_batch_tokens", C.c_int64),
                 ("max_consecutive_prefill_ticks", C.c_int64),
                 ("min_prefix_share_tokens", C.c_int64), ("num_blocks", C.c_int32),
-                ("block_size", C.c_int32), ("kv_dtype", C.c_int32)]
+                ("block_size", C.c_int32), ("kv_dtype", C.c_int32),
+                ("temperature", C.c_float), ("top_k", C.c_int64), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
 
 
 _P = C.c_void_p
@@ -87,14 +89,18 @@ class Runtime:
                  eps=1e-6, theta=10000.0, rotary_dims=None, tie=False, max_seq=4096,
                  max_gen=512, max_batch=16, max_chunk=256, max_batch_tokens=1024,
                  max_consecutive_prefill=2, min_share=64, num_blocks=4096, block_size=16,
-                 kv_dtype="f32", ordinal=0):
+                 kv_dtype="f32", ordinal=0, sampler=None):
+        """sampler: None (greedy) or (temperature, top_k, top_p, seed), the SamplerConfig of
+        every session (runtime/sampler.rs:3-43)."""
         L = load()
+        temperature, top_k, top_p, seed = (0.0, 1, 1.0, 0) if sampler is None else sampler
         head_dim = hidden // heads
         mc = ModelConfig(hidden, intermediate, layers, heads, kv_heads, vocab, max_pos, eps, theta,
                          head_dim if rotary_dims is None else rotary_dims, 1 if tie else 0)
         rc = RuntimeConfig(max_seq, max_gen, max_batch, max_chunk, max_batch_tokens,
                            max_consecutive_prefill, min_share, num_blocks, block_size,
-                           DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16)
+                           DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16,
+                           temperature, top_k, top_p, 1.0, seed)
         h = _P()
         _check(L.fr_create(ordinal, C.byref(mc), C.byref(rc), C.byref(h)))
         self.h = h

@@ -44,6 +44,16 @@ typedef struct fr_runtime_config {
   int32_t num_blocks;
   int32_t block_size;
   int32_t kv_dtype; /* FI_DTYPE_F32 or FI_DTYPE_BF16 */
+  /* SamplerConfig of every session (sampler.rs:3-43, session.rs:29-46).  Greedy when
+   * temperature <= 0, top_k == 1 or top_p <= 0 (a zero-filled struct is greedy): the fused
+   * argmax head.  Otherwise sample_last_token on the device (fi_sample_tokens) with one
+   * SamplerState per sequence started from `seed`; top_k, clamped to the vocabulary, must not
+   * exceed 1024 (Unsupported at fr_create). */
+  float temperature;
+  int64_t top_k;
+  float top_p;
+  float repetition_penalty; /* carried, unused by the sampler (as in the reference) */
+  uint64_t seed;
 } fr_runtime_config;
 
 const char* fr_last_error(void);

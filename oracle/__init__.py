@@ -148,6 +148,11 @@ def lib():
         L.orc_scheduler_destroy.restype = None
         L.orc_scheduler_has_pending.argtypes = [VP]
         L.orc_scheduler_has_pending.restype = C.c_int32
+        for name in ("orc_session_set_sampler", "orc_scheduler_set_sampler"):
+            getattr(L, name).argtypes = [VP, C.c_float, I64, C.c_float, C.c_uint64]
+            getattr(L, name).restype = C.c_int32
+        L.orc_session_sampler_state.argtypes = [VP, C.POINTER(C.c_uint64)]
+        L.orc_session_sampler_state.restype = C.c_int32
         _lib = L
     return _lib
 
@@ -468,16 +473,31 @@ class Session:
     def copy_prefix_from(self, source: "Session", tokens: int):
         _check(lib().orc_session_copy_prefix(self.h, source.h, tokens), True)
 
+    def set_sampler(self, temperature=0.0, top_k=1, top_p=1.0, seed=0):
+        """SamplerConfig (runtime/sampler.rs:3-43); restarts the sampler state."""
+        _check(lib().orc_session_set_sampler(self.h, temperature, top_k, top_p, seed), True)
+
+    @property
+    def sampler_state(self) -> int:
+        out = C.c_uint64()
+        _check(lib().orc_session_sampler_state(self.h, C.byref(out)), True)
+        return int(out.value)
+
 
 class Scheduler:
     def __init__(self, model: Model, max_seq=4096, max_gen=512, page_size=16, max_batch=16,
-                 max_chunk=256, max_batch_tokens=1024, max_consecutive_prefill=2, min_share=64):
+                 max_chunk=256, max_batch_tokens=1024, max_consecutive_prefill=2, min_share=64,
+                 sampler=None):
+        """sampler: None (greedy) or (temperature, top_k, top_p, seed), the SessionConfig
+        sampler of every submitted request."""
         self.model = model
         self.h = lib().orc_scheduler_create(model.h, max_seq, max_gen, page_size, max_batch,
                                             max_chunk, max_batch_tokens, max_consecutive_prefill,
                                             min_share)
         if not self.h:
             raise OracleError(6, lib().orc_runtime_last_error().decode())
+        if sampler is not None:
+            _check(lib().orc_scheduler_set_sampler(self.h, *sampler), True)
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -641,8 +641,35 @@ static KvCache make_session_kv(const Model& m, const SessionConfig& sc) {
   return sc.page_size == 0 ? KvCache::contiguous(kc) : KvCache::paged(kc, sc.page_size);
 }
 
+bool SamplerConfig::is_greedy() const { return sampler_is_greedy(temperature, top_k, top_p); }
+
+bool SamplerConfig::operator==(const SamplerConfig& o) const {
+  return temperature == o.temperature && top_k == o.top_k && top_p == o.top_p &&
+         repetition_penalty == o.repetition_penalty && seed == o.seed;
+}
+
+// session.rs:104-139: the sampler state starts from the configuration's seed
 Session::Session(std::shared_ptr<const Model> model, const SessionConfig& config)
-    : model_(std::move(model)), config_(config), kv_(make_session_kv(*model_, config)) {}
+    : model_(std::move(model)), config_(config), kv_(make_session_kv(*model_, config)),
+      sampler_state_(sampler_state_new(config.sampler.seed)) {}
+
+void Session::set_sampler(const SamplerConfig& sampler) {
+  config_.sampler = sampler;
+  sampler_state_ = sampler_state_new(sampler.seed);
+}
+
+// session.rs:349-373, 393-406: a greedy configuration takes the fused argmax head
+// (matmul_rhs_transposed_argmax); otherwise the last row's logits go through
+// sample_last_token with the session's sampler state.
+TokenSample Session::sample_hidden_row(const float* hidden_row) {
+  if (config_.sampler.is_greedy()) return sample_from_hidden_row(*model_, hidden_row);
+  const std::vector<float> logits = logits_from_hidden_row(*model_, hidden_row);
+  const SamplerConfig& c = config_.sampler;
+  TokenSample t{};
+  sample_last_token(logits.data(), 1, logits.size(), c.temperature, c.top_k, c.top_p, &sampler_state_, &t.token_id,
+                    &t.probability);
+  return t;
+}
 
 std::optional<PrefixHandle> Session::prefix_handle(size_t token_count) const {
   if (token_count > position_) {
@@ -660,9 +687,10 @@ void Session::copy_prefix_from_session(const Session& source, size_t token_count
   kv_.copy_prefix_from(source.kv_, token_count);
   position_ = token_count;
   history_.assign(source.history_.begin(), source.history_.begin() + token_count);
-  if (token_count == source.position_ && model_ == source.model_) {
+  if (token_count == source.position_ && model_ == source.model_ && config_.sampler == source.config_.sampler) {
     last_sample_ = source.last_sample_;
     last_hidden_ = source.last_hidden_;
+    sampler_state_ = source.sampler_state_;  // session.rs:195-201
   }
 }
 
@@ -672,6 +700,7 @@ void Session::reset() {
   history_.clear();
   last_sample_.reset();
   last_hidden_.clear();
+  sampler_state_ = sampler_state_new(config_.sampler.seed);  // session.rs:206-212
 }
 
 void Session::prefill_tokens(const std::vector<uint32_t>& ids) {
@@ -696,7 +725,7 @@ void Session::process_token(uint32_t token) {
   if (position_ >= config_.max_sequence_length) fail(ErrorKind::Runtime, "cannot process tokens beyond max sequence length");
   if (position_ != kv_.used_tokens()) fail(ErrorKind::Runtime, "session position and KV cache usage diverged");
   std::vector<float> hidden = token_hidden_with_kv_cache(*model_, token, &kv_, position_);
-  TokenSample s = sample_from_hidden_row(*model_, hidden.data());
+  TokenSample s = sample_hidden_row(hidden.data());
   kv_.advance(1);
   position_ += 1;
   history_.push_back(token);
@@ -711,7 +740,7 @@ void Session::process_prefill(const std::vector<uint32_t>& ids) {
   std::vector<float> hidden = prefill_hidden_with_kv_capture(*model_, ids, &kv_);
   size_t h = model_->config.hidden_size;
   const float* last = hidden.data() + (ids.size() - 1) * h;
-  TokenSample s = sample_from_hidden_row(*model_, last);
+  TokenSample s = sample_hidden_row(last);
   kv_.advance(ids.size());
   position_ += ids.size();
   history_.insert(history_.end(), ids.begin(), ids.end());

@@ -190,11 +190,23 @@ std::vector<float> token_hidden_with_kv_cache(const Model& m, uint32_t token, Kv
 TokenSample sample_from_hidden_row(const Model& m, const float* hidden_row);
 std::vector<float> logits_from_hidden_row(const Model& m, const float* hidden_row);
 
-// ---- runtime/session.rs:92-413 Session (greedy sampler only) ----
+// ---- runtime/sampler.rs:3-43 SamplerConfig (greedy by default) ----
+struct SamplerConfig {
+  float temperature = 0.0f;
+  size_t top_k = 1;
+  float top_p = 1.0f;
+  float repetition_penalty = 1.0f;
+  uint64_t seed = 0;
+  bool is_greedy() const;
+  bool operator==(const SamplerConfig& o) const;  // sampler_configs_match (session.rs:415-421)
+};
+
+// ---- runtime/session.rs:92-413 Session ----
 struct SessionConfig {
   size_t max_sequence_length = 4096;
   size_t max_generated_tokens = 512;
   size_t page_size = 0;  // 0 = contiguous KV, else paged with this page size
+  SamplerConfig sampler;
 };
 
 class Session {
@@ -205,6 +217,10 @@ class Session {
   const KvCache& kv_cache() const { return kv_; }
   const std::vector<uint32_t>& token_history() const { return history_; }
   std::optional<TokenSample> last_sample() const { return last_sample_; }
+  uint64_t sampler_state() const { return sampler_state_; }
+  // Replaces the session's sampler configuration and restarts its state (a test hook; the
+  // reference fixes it at construction).
+  void set_sampler(const SamplerConfig& sampler);
   std::optional<PrefixHandle> prefix_handle(size_t token_count) const;
   void copy_prefix_from_session(const Session& source, size_t token_count);
   void reset();
@@ -216,12 +232,14 @@ class Session {
  private:
   void process_token(uint32_t token);
   void process_prefill(const std::vector<uint32_t>& ids);
+  TokenSample sample_hidden_row(const float* hidden_row);
   std::shared_ptr<const Model> model_;
   SessionConfig config_;
   KvCache kv_;
   size_t position_ = 0;
   std::vector<uint32_t> history_;
   std::optional<TokenSample> last_sample_;
+  uint64_t sampler_state_;
   std::vector<float> last_hidden_;
 };
 
@@ -373,6 +391,8 @@ class ReferenceScheduler {
   const SequenceState* sequence_state(uint64_t seq) const;
   const Session* session(uint64_t seq) const;
   const PrefixBlockManager& block_manager() const { return block_manager_; }
+  // The sampler configuration of the sessions submitted from now on (SessionConfig::sampler).
+  void set_sampler(const SamplerConfig& sampler) { session_config_.sampler = sampler; }
 
  private:
   struct Entry {

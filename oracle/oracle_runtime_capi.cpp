@@ -161,6 +161,19 @@ void* orc_session_create(void* m, int64_t max_seq, int64_t max_gen, int64_t page
   return s;
 }
 void orc_session_destroy(void* s) { delete static_cast<OrcSession*>(s); }
+int32_t orc_session_set_sampler(void* s, float temperature, int64_t top_k, float top_p, uint64_t seed) {
+  return guard([&] {
+    SamplerConfig c;
+    c.temperature = temperature;
+    c.top_k = static_cast<size_t>(top_k);
+    c.top_p = top_p;
+    c.seed = seed;
+    static_cast<OrcSession*>(s)->session->set_sampler(c);
+  });
+}
+int32_t orc_session_sampler_state(void* s, uint64_t* out) {
+  return guard([&] { *out = static_cast<OrcSession*>(s)->session->sampler_state(); });
+}
 int32_t orc_session_prefill(void* s, const uint32_t* ids, int64_t n) {
   return guard([&] { static_cast<OrcSession*>(s)->session->prefill_tokens(std::vector<uint32_t>(ids, ids + n)); });
 }
@@ -229,6 +242,16 @@ void* orc_scheduler_create(void* m, int64_t max_seq, int64_t max_gen, int64_t pa
   return s;
 }
 void orc_scheduler_destroy(void* s) { delete static_cast<OrcScheduler*>(s); }
+int32_t orc_scheduler_set_sampler(void* s, float temperature, int64_t top_k, float top_p, uint64_t seed) {
+  return guard([&] {
+    SamplerConfig c;
+    c.temperature = temperature;
+    c.top_k = static_cast<size_t>(top_k);
+    c.top_p = top_p;
+    c.seed = seed;
+    static_cast<OrcScheduler*>(s)->sched->set_sampler(c);
+  });
+}
 int32_t orc_scheduler_submit(void* s, const uint32_t* ids, int64_t n, int64_t max_new, int64_t stop,
                              uint64_t* seq_out) {
   return guard([&] {

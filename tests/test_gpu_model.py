@@ -11,19 +11,19 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-def build_pair(orc, cfg, weights, sched_kw, num_blocks=4096, kv_dtype="f32"):
+def build_pair(orc, cfg, weights, sched_kw, num_blocks=4096, kv_dtype="f32", sampler=None):
     from ferrisinfer_amd.runtime import Runtime
 
     model = orc.Model(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
                       cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
                       tie=cfg["tie"])
     model.set_weights(weights)
-    ref = orc.Scheduler(model, page_size=16, **sched_kw)
+    ref = orc.Scheduler(model, page_size=16, sampler=sampler, **sched_kw)
     ref.attach_packer(num_blocks, 16)
     gpu = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
                   cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
                   tie=cfg["tie"], num_blocks=num_blocks, block_size=16, kv_dtype=kv_dtype,
-                  **sched_kw)
+                  sampler=sampler, **sched_kw)
     gpu.set_weights(weights)
     return model, ref, gpu
 
@@ -120,6 +120,63 @@ def test_prefix_sharing_and_chunking_match_reference(orc):
     ticks, ties = compare(model, ref, gpu, reqs)
     assert any(u["reused"] > 0 for _, us in ticks for u in us)
     assert gpu.pool_free_count() == 4096
+
+
+SAMPLERS = [(0.8, 20, 0.9, 42), (1.3, 50, 1.0, 0)]
+
+
+@pytest.mark.parametrize("sampler", SAMPLERS)
+def test_sampled_ticks_match_reference(orc, sampler):
+    """A sampling SessionConfig (runtime/sampler.rs:121-241 per sequence, xorshift64* state
+    per session): the C1 requests and the prefix-sharing set under the same scheduler limits
+    as above.  Every sequence's tokens must equal the reference's exactly: the draws consume
+    the per-sequence states in the reference's order, including a whole-history import from a
+    source that drew earlier in the same tick."""
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1, c1_requests, random_weights
+
+    print(f"sampled ticks sampler={sampler}", flush=True)
+    cfg = dict(TINY_LLAMA_C1, layers=2)
+    weights = random_weights(cfg, seed=3, std=0.05)
+    rng = np.random.default_rng(7)
+    base = rng.integers(0, cfg["vocab"], size=40).astype(np.uint32)
+    sharing = [
+        (base.copy(), 6),
+        (np.concatenate([base[:37], rng.integers(0, 4096, 9)]).astype(np.uint32), 5),
+        (base.copy(), 3),
+        (rng.integers(0, 4096, 23).astype(np.uint32), 7),
+    ]
+    cases = [(c1_requests(0), {}),
+             (sharing, dict(max_batch=3, max_chunk=20, max_batch_tokens=50, min_share=16))]
+    for requests, kw in cases:
+        model, ref, gpu = build_pair(orc, cfg, weights, kw, sampler=sampler)
+        rid, rticks = drive(ref, requests)
+        gid, gticks = drive(gpu, requests)
+        assert rid == gid and len(rticks) == len(gticks)
+        for (rk, ru), (gk, gu) in zip(rticks, gticks):
+            assert rk == gk
+            for a, b in zip(ru, gu):
+                for key in ("sequence_id", "reused", "appended", "phase", "finish_reason", "token"):
+                    assert a[key] == b[key], (key, a, b)
+                if a["token"] is not None:
+                    assert abs(a["probability"] - b["probability"]) <= 1e-4 * a["probability"]
+        for seq in rid:
+            assert ref.generated(seq) == gpu.generated(seq), seq
+        assert gpu.pool_free_count() == 4096
+
+
+def test_sampler_config_limits(orc):
+    from ferrisinfer_amd import FerrisError
+    from ferrisinfer_amd.runtime import Runtime
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1
+
+    cfg = TINY_LLAMA_C1
+    with pytest.raises(FerrisError, match="top_k above 1024"):
+        Runtime(cfg["hidden"], cfg["intermediate"], 1, cfg["heads"], cfg["kv_heads"], cfg["vocab"],
+                sampler=(0.8, 2000, 0.9, 0))
+    Runtime(cfg["hidden"], cfg["intermediate"], 1, cfg["heads"], cfg["kv_heads"], 1000,
+            sampler=(0.8, 2000, 0.9, 0)).close()  # clamps to the 1000-token vocabulary
+    Runtime(cfg["hidden"], cfg["intermediate"], 1, cfg["heads"], cfg["kv_heads"], cfg["vocab"],
+            sampler=(0.0, 2000, 0.9, 0)).close()  # greedy: top_k unused
 
 
 def test_runtime_errors(orc):
