@@ -298,16 +298,39 @@ def kernel_legs(ctx, seed):
         prob = torch.empty(m, device="cuda")
         ms = timed(lambda: ctx.lm_head_argmax_packed(hid, bp, v, tok, prob), 20)
         out[f"lm_head_argmax_c4_m{m}"] = gemm_row(m, h, v, ms, 1, 4)
+    del w, bp
+    # device sampling (sample_last_token per row, one workgroup per row): the logits are
+    # read once, so the bound is HBM at rows * vocab * 4 bytes per launch; N(0, 2.5) logits
+    # under the reference's chat_default sampler (top-k 20) and a greedy configuration
+    for tag, rows, vocab, cfg in (("c4_m64_topk20", 64, 151936, (0.7, 20, 0.9)),
+                                  ("c5_m257_topk20", 257, 128256, (0.7, 20, 0.9)),
+                                  ("c4_m64_greedy", 64, 151936, (0.0, 1, 1.0))):
+        logits = torch.randn(rows, vocab, device="cuda", generator=g) * 2.5
+        temp = torch.full((rows,), cfg[0], device="cuda")
+        topk = torch.full((rows,), cfg[1], dtype=torch.int32, device="cuda")
+        topp = torch.full((rows,), cfg[2], device="cuda")
+        st = torch.arange(1, rows + 1, dtype=torch.int64, device="cuda")
+        tok = torch.empty(rows, dtype=torch.int32, device="cuda")
+        prob = torch.empty(rows, device="cuda")
+        ms = timed(lambda: ctx.sample_tokens(logits, temp, topk, topp, st, tok, prob), 20)
+        b = rows * vocab * 4
+        out[f"sample_tokens_{tag}"] = {
+            "kernel": "sample_kernel<4>", "bound": "hbm", "rows": rows, "vocab": vocab,
+            "temperature": cfg[0], "top_k": cfg[1], "top_p": cfg[2], "bytes_per_launch": b,
+            "avg_launch_us": round(ms * 1e3, 2), "achieved_gbs": round(b / (ms * 1e-3) / 1e9, 1),
+            "peak_gbs": HBM_PEAK_GBS, "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del logits
     ctx.check_faults()
     return out
 
 
-def c4_continuous(seed, n_requests):
+def c4_continuous(seed, n_requests, sampler=None):
     """C4: the Qwen2-0.5B-shaped model (f32, tied, q/k/v biases, random N(0, 0.02) weights)
     served by the GPU runtime under continuous batching (max batch 64, block 16, the
     reference scheduler's other defaults), Poisson arrivals at 8 req/s on 50 ms virtual
     ticks.  Decode tok/s = generated tokens / summed decode-tick wall time, the reference's
-    continuous-batching definition (cli/main.rs:1502-1512, 1619-1622)."""
+    continuous-batching definition (cli/main.rs:1502-1512, 1619-1622).  sampler: None for
+    greedy sessions, or (temperature, top_k, top_p, seed) for sampled ones."""
     import numpy as np
 
     from ferrisinfer_amd.runtime import Runtime
@@ -317,7 +340,7 @@ def c4_continuous(seed, n_requests):
     weights = random_weights(cfg, seed=seed, qkv_bias=True)
     rt = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
                  cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"], tie=True, max_seq=4096,
-                 max_gen=512, max_batch=64, num_blocks=16384, block_size=16)
+                 max_gen=512, max_batch=64, num_blocks=16384, block_size=16, sampler=sampler)
     rt.set_weights(weights)
     del weights
     # warm-up: one short request through prefill and decode (module load, first launches)
@@ -335,7 +358,9 @@ def c4_continuous(seed, n_requests):
     out = {
         "workload": f"C4 Qwen2-0.5B shape, {n_requests} requests, Poisson 8/s on 50 ms virtual "
                     "ticks, prompts lognormal(median 512, sigma 0.5) clipped [1,2048], outputs "
-                    "U[64,256], greedy, max batch 64, block 16, f32 weights+KV",
+                    "U[64,256], " + ("greedy" if sampler is None else
+                                     "sampled (temperature, top_k, top_p, seed) = " + str(sampler))
+                    + ", max batch 64, block 16, f32 weights+KV",
         "decode_tok_s": round(rep["decode_tok_s"], 1),
         "decode_tok_s_at_batch_64": round(64 * len(full) / full_s, 1) if full_s > 0 else None,
         "ms_per_decode_tick_at_batch_64": round(full_s / len(full) * 1e3, 3) if full else None,
@@ -615,6 +640,13 @@ def main():
     if not args.no_c4:
         print("bench: C4 continuous batching on the GPU runtime", file=sys.stderr, flush=True)
         result["c4"] = c4_continuous(args.seed, args.c4_requests)
+        # the same requests under the reference's chat_default sampler (sampler.rs:30-37):
+        # logits head + device sampling in every tick
+        sampled = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42))
+        result["c4"]["sampled_chat_default"] = {
+            k: sampled[k] for k in ("workload", "decode_tok_s", "decode_tok_s_at_batch_64",
+                                    "ms_per_decode_tick_at_batch_64", "prefill_tok_s",
+                                    "generated_tokens", "decode_tick_host_ms")}
         if not args.no_cpu_baseline:
             print("bench: C4 CPU baseline (oracle, declared subset)", file=sys.stderr, flush=True)
             result["c4"]["cpu_baseline"] = c4_cpu_baseline(args.seed, min(16, os.cpu_count() or 1))
