@@ -24,6 +24,7 @@ SOURCES = [
     "fi_gemm_packed.hip",
     "fi_gemm_bf16.hip",
     "fi_sample.hip",
+    "fi_convert.hip",
 ]
 
 # gfx950 only; packed-fp32 instructions are disabled (the compiler would otherwise form
@@ -50,7 +51,8 @@ def hipcc() -> str:
 
 RUNTIME_LIB = "libferrisinfer_runtime.so"
 RUNTIME_PATH = os.path.join(PKG_DIR, RUNTIME_LIB)
-RUNTIME_SOURCES = ["runtime/fr_model.cpp", "runtime/fr_scheduler.cpp", "runtime/fr_capi.cpp"]
+RUNTIME_SOURCES = ["runtime/fr_model.cpp", "runtime/fr_scheduler.cpp", "runtime/fr_capi.cpp",
+                   "runtime/fr_json.cpp", "runtime/fr_checkpoint.cpp"]
 
 
 def build_runtime(verbose: bool = False) -> str:

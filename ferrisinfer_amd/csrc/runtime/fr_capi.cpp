@@ -4,6 +4,7 @@
 #include <string>
 
 #include "../../../include/ferrisinfer_runtime.h"
+#include "fr_checkpoint.h"
 #include "fr_runtime.h"
 
 namespace {
@@ -97,6 +98,80 @@ int32_t fr_set_weight(void* h, const char* name, const float* data, int64_t coun
   return guard([&] {
     if (rt(h)->scheduler) fr::fail(fr::ErrorKind::Runtime, "weights are frozen once requests were submitted");
     rt(h)->model->set_weight(name, data, static_cast<size_t>(count));
+  });
+}
+
+int32_t fr_hf_read_config(const char* model_dir, fr_model_config* out) {
+  return guard([&] {
+    if (!model_dir || !out) fr::fail(fr::ErrorKind::InvalidConfig, "fr_hf_read_config: null argument");
+    const fr::ModelConfig c = fr::read_hf_config(model_dir);
+    out->hidden_size = c.hidden_size;
+    out->intermediate_size = c.intermediate_size;
+    out->num_layers = c.num_layers;
+    out->num_attention_heads = c.num_attention_heads;
+    out->num_key_value_heads = c.num_key_value_heads;
+    out->vocab_size = c.vocab_size;
+    out->max_position_embeddings = c.max_position_embeddings;
+    out->rms_norm_eps = c.rms_norm_eps;
+    out->rope_theta = c.rope_theta;
+    out->rotary_dims = c.rotary_dims;
+    out->tie_word_embeddings = c.tie_word_embeddings ? 1 : 0;
+  });
+}
+
+int32_t fr_hf_inspect(const char* model_dir, int64_t* counts) {
+  return guard([&] {
+    if (!model_dir || !counts) fr::fail(fr::ErrorKind::InvalidConfig, "fr_hf_inspect: null argument");
+    const fr::HfInspection r = fr::inspect_hf(model_dir);
+    counts[0] = static_cast<int64_t>(r.shard_count);
+    counts[1] = static_cast<int64_t>(r.tensor_count);
+    counts[2] = static_cast<int64_t>(r.total_data_bytes);
+    counts[3] = static_cast<int64_t>(r.mapped_required);
+    counts[4] = static_cast<int64_t>(r.mapped_optional);
+    counts[5] = static_cast<int64_t>(r.missing_required.size());
+    counts[6] = static_cast<int64_t>(r.missing_optional.size());
+    counts[7] = static_cast<int64_t>(r.shape_mismatches.size());
+  });
+}
+
+int32_t fr_safetensors_info(const char* model_dir, int64_t* tensors, int64_t* shards, int64_t* total_bytes) {
+  return guard([&] {
+    if (!model_dir || !tensors || !shards || !total_bytes) fr::fail(fr::ErrorKind::InvalidConfig, "fr_safetensors_info: null argument");
+    const fr::SafeTensorsRepository repo = fr::SafeTensorsRepository::open(model_dir);
+    *tensors = static_cast<int64_t>(repo.tensor_count());
+    *shards = static_cast<int64_t>(repo.shard_count());
+    *total_bytes = static_cast<int64_t>(repo.total_data_bytes());
+  });
+}
+
+int32_t fr_safetensors_entry(const char* model_dir, const char* name, int32_t* dtype, int64_t* shape, int32_t capacity,
+                             int32_t* rank, char* path, int64_t path_capacity, int64_t* offset, int64_t* byte_len) {
+  return guard([&] {
+    if (!model_dir || !name || !dtype || !shape || !rank || !path || !offset || !byte_len) {
+      fr::fail(fr::ErrorKind::InvalidConfig, "fr_safetensors_entry: null argument");
+    }
+    const fr::SafeTensorsRepository repo = fr::SafeTensorsRepository::open(model_dir);
+    const fr::StEntry* e = repo.get(name);
+    if (e == nullptr) {
+      fr::fail(fr::ErrorKind::MissingWeight, std::string("tensor '") + name + "' was not found in safetensors repository");
+    }
+    if (static_cast<int64_t>(e->shape.size()) > capacity) fr::fail(fr::ErrorKind::InvalidShape, "shape capacity too small");
+    if (static_cast<int64_t>(e->path.size()) + 1 > path_capacity) fr::fail(fr::ErrorKind::InvalidShape, "path capacity too small");
+    *dtype = e->dtype == fr::StDType::F32 ? FI_DTYPE_F32 : (e->dtype == fr::StDType::BF16 ? FI_DTYPE_BF16 : FI_DTYPE_F16);
+    *rank = static_cast<int32_t>(e->shape.size());
+    for (size_t i = 0; i < e->shape.size(); ++i) shape[i] = static_cast<int64_t>(e->shape[i]);
+    std::memcpy(path, e->path.c_str(), e->path.size() + 1);
+    *offset = static_cast<int64_t>(e->absolute_offset());
+    *byte_len = static_cast<int64_t>(e->byte_len());
+  });
+}
+
+int32_t fr_load_hf_weights(void* h, const char* model_dir, int64_t* loaded) {
+  return guard([&] {
+    if (!model_dir) fr::fail(fr::ErrorKind::InvalidConfig, "fr_load_hf_weights: null directory");
+    if (rt(h)->scheduler) fr::fail(fr::ErrorKind::Runtime, "weights are frozen once requests were submitted");
+    const size_t n = fr::load_hf_weights(rt(h)->model.get(), model_dir);
+    if (loaded) *loaded = static_cast<int64_t>(n);
   });
 }
 

@@ -81,6 +81,12 @@ DeviceModel::DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rop
 }
 
 void DeviceModel::set_weight(const std::string& name, const float* host, size_t count) {
+  DeviceBuffer* dst = weight_slot(name, count);
+  check(fi_buf_upload(ctx_, dst->get(), count * sizeof(float), host, count * sizeof(float)));
+}
+
+DeviceBuffer* DeviceModel::weight_slot(const std::string& name, size_t count) {
+  if (finalized_) fail(ErrorKind::Runtime, "weights are packed; tensor " + name + " can no longer be set");
   const ModelConfig& c = config_;
   const size_t h = c.hidden_size, f = c.intermediate_size, kvw = static_cast<size_t>(c.num_key_value_heads) * c.head_dim();
   auto put = [&](DeviceBuffer* dst, size_t expected) {
@@ -89,7 +95,7 @@ void DeviceModel::set_weight(const std::string& name, const float* host, size_t 
                                         std::to_string(expected));
     }
     dst->reserve(ctx_, count * sizeof(float));
-    check(fi_buf_upload(ctx_, dst->get(), count * sizeof(float), host, count * sizeof(float)));
+    return dst;
   };
   if (name == "tok_embeddings.weight") return put(&tok_embeddings_, static_cast<size_t>(c.vocab_size) * h);
   if (name == "norm.weight") return put(&norm_, h);
@@ -97,8 +103,13 @@ void DeviceModel::set_weight(const std::string& name, const float* host, size_t 
   const std::string prefix = "layers.";
   if (name.compare(0, prefix.size(), prefix) == 0) {
     const size_t dot = name.find('.', prefix.size());
-    const int layer = std::stoi(name.substr(prefix.size(), dot - prefix.size()));
-    if (layer < 0 || layer >= c.num_layers) fail(ErrorKind::InvalidShape, "layer index out of range in " + name);
+    const std::string index = name.substr(prefix.size(), dot == std::string::npos ? std::string::npos : dot - prefix.size());
+    if (dot == std::string::npos || index.empty() || index.size() > 9 ||
+        index.find_first_not_of("0123456789") != std::string::npos) {
+      fail(ErrorKind::MissingWeight, "unknown tensor name: " + name);
+    }
+    const int layer = std::stoi(index);
+    if (layer >= c.num_layers) fail(ErrorKind::InvalidShape, "layer index out of range in " + name);
     const std::string rest = name.substr(dot + 1);
     Layer& w = layers_[layer];
     if (rest == "attention_norm.weight") return put(&w.attention_norm, h);

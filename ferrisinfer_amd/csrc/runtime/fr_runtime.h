@@ -92,6 +92,10 @@ class DeviceModel {
 
   DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions);
   void set_weight(const std::string& name, const float* host, size_t count);
+  // The device buffer of weight `name` sized for `count` floats (contents undefined until
+  // written); InvalidShape when count is not the tensor's size, MissingWeight for an unknown
+  // name.  set_weight uploads into it; the checkpoint loader converts into it on the device.
+  DeviceBuffer* weight_slot(const std::string& name, size_t count);
   void validate() const;  // every required tensor present (MissingWeight otherwise)
   // Packs every projection once the weights are complete and releases the unpacked copies
   // (the tied embedding stays: the gather reads it).  Idempotent.

@@ -21,6 +21,7 @@ ERROR_KINDS = ["Io", "Parse", "InvalidShape", "InvalidLayout", "InvalidType", "I
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
 
 
 class FerrisError(RuntimeError):
@@ -42,6 +43,7 @@ _SZ = C.c_size_t
 # name -> argtypes; every function returns int32 status unless listed in _RESTYPES.
 _SIGNATURES = {
     "fi_ctx_create": [_I32, C.POINTER(_P)],
+    "fi_convert_to_f32": [_P, _P, _I32, _I64, _I64, _I32, _P],
     "fi_ctx_destroy": [_P],
     "fi_ctx_sync": [_P],
     "fi_ctx_set_stream": [_P, _P],
@@ -437,6 +439,13 @@ class Context:
         check(self.lib.fi_sample_tokens(self.handle, ptr(logits), int(logits.stride(0)), int(rows),
                                         int(vocab), ptr(temperature), ptr(top_k), ptr(top_p),
                                         ptr(rng_state), ptr(token_out), ptr(prob_out)))
+
+    def convert_to_f32(self, src, src_dtype, rows, cols, transpose, dst):
+        """dst (f32) = the widening of src, a [rows, cols] row-major tensor of src_dtype
+        (DTYPE_F32 / DTYPE_BF16 / DTYPE_F16 raw bits in any torch dtype of that width), or its
+        [cols, rows] transpose when transpose is true."""
+        check(self.lib.fi_convert_to_f32(self.handle, ptr(src), int(src_dtype), int(rows), int(cols),
+                                         1 if transpose else 0, ptr(dst)))
 
     def qkv_rope_append(self, parts, splits, biases, positions, cos_t, sin_t, rotary_dims,
                         max_positions, slot_mapping, k_cache, v_cache, kv_dtype, num_blocks,

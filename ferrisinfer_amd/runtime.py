@@ -9,7 +9,7 @@ import time
 
 import numpy as np
 
-from .kernel import DTYPE_BF16, DTYPE_F32, FerrisError, PKG_DIR, load as load_kernel
+from .kernel import DTYPE_BF16, DTYPE_F16, DTYPE_F32, FerrisError, PKG_DIR, load as load_kernel
 
 LIB_PATH = os.path.join(PKG_DIR, "libferrisinfer_runtime.so")
 
@@ -63,6 +63,12 @@ def load() -> C.CDLL:
             "fr_last_batch_sizes": [_P, _P],
             "fr_last_batch": [_P] + [_P] * 10,
             "fr_last_tick_profile": [_P, _P],
+            "fr_hf_read_config": [C.c_char_p, C.POINTER(ModelConfig)],
+            "fr_hf_inspect": [C.c_char_p, _P],
+            "fr_safetensors_info": [C.c_char_p, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)],
+            "fr_safetensors_entry": [C.c_char_p, C.c_char_p, C.POINTER(_I32), _P, _I32, C.POINTER(_I32),
+                                     C.c_char_p, _I64, C.POINTER(_I64), C.POINTER(_I64)],
+            "fr_load_hf_weights": [_P, C.c_char_p, C.POINTER(_I64)],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -80,6 +86,50 @@ def _check(status):
 
 def _addr(a: np.ndarray) -> int:
     return a.ctypes.data
+
+
+def _path(p) -> bytes:
+    return os.fsencode(os.fspath(p))
+
+
+def read_hf_config(model_dir) -> dict:
+    """config.json of a Qwen2 checkpoint as Runtime keyword arguments (io/hf.rs:306-369)."""
+    mc = ModelConfig()
+    _check(load().fr_hf_read_config(_path(model_dir), C.byref(mc)))
+    return {"hidden": mc.hidden_size, "intermediate": mc.intermediate_size, "layers": mc.num_layers,
+            "heads": mc.num_attention_heads, "kv_heads": mc.num_key_value_heads, "vocab": mc.vocab_size,
+            "max_pos": mc.max_position_embeddings, "eps": mc.rms_norm_eps, "theta": mc.rope_theta,
+            "rotary_dims": mc.rotary_dims, "tie": bool(mc.tie_word_embeddings)}
+
+
+def hf_inspect(model_dir) -> dict:
+    """io/hf.rs:66-118 HfSource::inspect counts (the tokenizer is not read)."""
+    c = np.zeros(8, np.int64)
+    _check(load().fr_hf_inspect(_path(model_dir), _addr(c)))
+    keys = ("shard_count", "tensor_count", "total_data_bytes", "mapped_required", "mapped_optional",
+            "missing_required", "missing_optional", "shape_mismatches")
+    out = {k: int(v) for k, v in zip(keys, c)}
+    out["compatible"] = out["missing_required"] == 0 and out["shape_mismatches"] == 0
+    return out
+
+
+def safetensors_info(model_dir) -> dict:
+    """io/safetensors.rs SafeTensorsRepository::open + tensor_count / shard_count / total_data_bytes."""
+    t, s, b = _I64(), _I64(), _I64()
+    _check(load().fr_safetensors_info(_path(model_dir), C.byref(t), C.byref(s), C.byref(b)))
+    return {"tensors": t.value, "shards": s.value, "total_data_bytes": b.value}
+
+
+def safetensors_entry(model_dir, name) -> dict:
+    """One tensor's entry: dtype code, shape, shard path, absolute data offset and length."""
+    dtype, rank = _I32(), _I32()
+    shape = np.zeros(16, np.int64)
+    path = C.create_string_buffer(4096)
+    off, n = _I64(), _I64()
+    _check(load().fr_safetensors_entry(_path(model_dir), name.encode(), C.byref(dtype), _addr(shape), 16,
+                                       C.byref(rank), path, 4096, C.byref(off), C.byref(n)))
+    return {"dtype": dtype.value, "shape": [int(x) for x in shape[:rank.value]],
+            "path": os.fsdecode(path.value), "offset": off.value, "byte_len": n.value}
 
 
 class Runtime:
@@ -120,6 +170,23 @@ class Runtime:
     def set_weight(self, name, array):
         a = np.ascontiguousarray(np.asarray(array, dtype=np.float32)).reshape(-1)
         _check(load().fr_set_weight(self.h, name.encode(), _addr(a), a.size))
+
+    @classmethod
+    def from_hf(cls, model_dir, **kwargs):
+        """A runtime for the Qwen2 checkpoint under model_dir: config.json gives the model
+        shape, every planned tensor is loaded on the device (fr_load_hf_weights); kwargs are
+        the runtime options of __init__."""
+        cfg = read_hf_config(model_dir)
+        cfg["max_pos"] = kwargs.pop("max_pos", cfg["max_pos"])
+        rt = cls(**cfg, **kwargs)
+        rt.load_hf_weights(model_dir)
+        return rt
+
+    def load_hf_weights(self, model_dir) -> int:
+        """Every planned tensor of the checkpoint into this runtime's model; returns the count."""
+        n = _I64()
+        _check(load().fr_load_hf_weights(self.h, _path(model_dir), C.byref(n)))
+        return n.value
 
     def set_weights(self, weights: dict):
         for k, v in weights.items():

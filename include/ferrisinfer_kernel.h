@@ -53,8 +53,9 @@ enum {
   FI_ERR_RUNTIME = 9
 };
 
-/* KV storage dtypes (core/dtype.rs:1-42 F32 / BF16). */
-enum { FI_DTYPE_F32 = 0, FI_DTYPE_BF16 = 1 };
+/* Element dtypes: KV storage (core/dtype.rs:1-42 F32 / BF16) and, with F16, the safetensors
+ * payloads fi_convert_to_f32 imports (io/safetensors.rs:11-16). */
+enum { FI_DTYPE_F32 = 0, FI_DTYPE_BF16 = 1, FI_DTYPE_F16 = 2 };
 
 typedef struct fi_context fi_context;
 
@@ -376,6 +377,16 @@ int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const float* d_hidden, int32_t l
 int32_t fi_sample_tokens(fi_context* ctx, const float* d_logits, int32_t ld, int32_t rows, int32_t vocab,
                          const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
                          uint64_t* d_rng_state, int32_t* d_token, float* d_prob);
+
+/* ---------------------------------------------------------------- checkpoint import
+ * d_dst = the f32 widening of d_src, a [rows, cols] row-major tensor of src_dtype (FI_DTYPE_F32,
+ * _BF16 or _F16; rank-1 tensors as rows = 1); transpose != 0 writes the [cols, rows] transpose
+ * (dst[c * rows + r] = src[r * cols + c]).  BF16 widens as bits << 16; F16 by the IEEE rule
+ * (subnormals normalised, infinities and NaN payloads kept).  Replaces the host conversion of
+ * io/safetensors.rs:437-471 (convert_to_f32_vec, transpose_2d) and :538-568 (bf16_to_f32,
+ * f16_to_f32).  d_src and d_dst must not overlap. */
+int32_t fi_convert_to_f32(fi_context* ctx, const void* d_src, int32_t src_dtype, int64_t rows, int64_t cols,
+                          int32_t transpose, float* d_dst);
 
 #ifdef __cplusplus
 }

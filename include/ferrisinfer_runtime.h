@@ -67,6 +67,34 @@ int32_t fr_destroy(void* runtime);
 int32_t fr_set_weight(void* runtime, const char* name, const float* data, int64_t count);
 
 /* ReferenceScheduler::submit (scheduler.rs:204-250); stop < 0 means no stop token. */
+/* ---------------------------------------------------------------- checkpoint import
+ * HF Qwen2 checkpoints (config.json + model.safetensors or a sharded
+ * model.safetensors.index.json) with F32 / BF16 / F16 tensors.
+ *
+ * fr_hf_read_config: config.json -> model config (io/hf.rs:306-369 parse_qwen2_config;
+ * model_type must be "qwen2"; hidden_act silu / swish, other activations Unsupported: the
+ * device decoder is silu-gated).  rotary_dims = round(head_dim * partial_rotary_factor). */
+int32_t fr_hf_read_config(const char* model_dir, fr_model_config* out);
+/* io/hf.rs:66-118 HfSource::inspect: counts[8] = shard count, tensor count, total data bytes,
+ * mapped required, mapped optional, missing required, missing optional, shape mismatches. */
+int32_t fr_hf_inspect(const char* model_dir, int64_t* counts);
+/* io/safetensors.rs:87-187 SafeTensorsRepository::open / tensor_count / shard_count /
+ * total_data_bytes, with the header validation of :225-397 (Io, Parse, InvalidType,
+ * Unsupported and Runtime errors as the reference raises them). */
+int32_t fr_safetensors_info(const char* model_dir, int64_t* tensors, int64_t* shards, int64_t* total_bytes);
+/* One tensor's entry: dtype (FI_DTYPE_F32 / _BF16 / _F16), shape (rank <= capacity), the
+ * shard file path (NUL-terminated) and the absolute byte offset and length of its data
+ * (safetensors.rs:47-83 SafeTensorEntry). */
+int32_t fr_safetensors_entry(const char* model_dir, const char* name, int32_t* dtype, int64_t* shape, int32_t capacity,
+                             int32_t* rank, char* path, int64_t path_capacity, int64_t* offset, int64_t* byte_len);
+/* Loads every planned tensor (io/hf.rs:208-304, 380-500: names, expected shapes, [out, in] ->
+ * [in, out] transposes, optional q/k/v biases, lm_head unless tied) into the runtime's model:
+ * each tensor's raw bytes go to HBM and are widened / transposed there (fi_convert_to_f32).
+ * The runtime's model config must be the checkpoint's (fr_hf_read_config); shape mismatches
+ * are InvalidShape, absent required tensors MissingWeight.  loaded (may be NULL) = tensors
+ * loaded. */
+int32_t fr_load_hf_weights(void* runtime, const char* model_dir, int64_t* loaded);
+
 int32_t fr_submit(void* runtime, const uint32_t* prompt, int64_t n, int64_t max_new_tokens,
                   int64_t stop, uint64_t* sequence_id);
 /* ReferenceScheduler::execute_next_tick (scheduler.rs:393-415); *executed = 0 when idle. */
