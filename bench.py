@@ -53,6 +53,8 @@ def parse_args():
     p.add_argument("--c5-steps", type=int, default=5)
     p.add_argument("--no-kernels", action="store_true",
                    help="skip the C3 prefill/append and projection-GEMM kernel measurements")
+    p.add_argument("--hf-load", action="store_true",
+                   help="also time importing a Qwen2-0.5B-shaped BF16 HF checkpoint")
     p.add_argument("--gemm-shapes", action="store_true",
                    help="only time the projection GEMMs at the C4 shapes (packed-weight path "
                         "against fi_gemm), one JSON line per shape")
@@ -320,8 +322,60 @@ def kernel_legs(ctx, seed):
             "avg_launch_us": round(ms * 1e3, 2), "achieved_gbs": round(b / (ms * 1e-3) / 1e9, 1),
             "peak_gbs": HBM_PEAK_GBS, "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del logits
+    # checkpoint import (fi_convert_to_f32): HBM-bound, 2 bytes read + 4 written per element;
+    # a Qwen2 MLP weight [4864, 896] bf16 transposed to [896, 4864] f32, and the [151936, 896]
+    # embedding widened in place order
+    from ferrisinfer_amd import DTYPE_F16
+    for tag, rows, cols, dt, tr in (("bf16_t_4864x896", 4864, 896, DTYPE_BF16, True),
+                                    ("f16_t_4864x896", 4864, 896, DTYPE_F16, True),
+                                    ("bf16_151936x896", 151936, 896, DTYPE_BF16, False)):
+        src = torch.randint(-32768, 32767, (rows * cols,), dtype=torch.int16, device="cuda", generator=g)
+        dst = torch.empty(rows * cols, device="cuda")
+        ms = timed(lambda: ctx.convert_to_f32(src, dt, rows, cols, tr, dst), 20)
+        b = rows * cols * 6
+        out[f"convert_to_f32_{tag}"] = {
+            "kernel": "widen_transpose_kernel" if tr else "widen_kernel", "bound": "hbm",
+            "bytes_per_launch": b, "avg_launch_us": round(ms * 1e3, 2),
+            "achieved_gbs": round(b / (ms * 1e-3) / 1e9, 1), "peak_gbs": HBM_PEAK_GBS,
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del src, dst
     ctx.check_faults()
     return out
+
+
+def hf_load(seed):
+    """A Qwen2-0.5B-shaped checkpoint (BF16, tied, q/k/v biases, random values; 988 MB of
+    safetensors in 2 shards) written to a temporary directory, then imported by the runtime:
+    config + every tensor to HBM with on-device widening / transposes (Runtime.from_hf), and
+    the first submit, which packs the projections for the GEMM kernels."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from ferrisinfer_amd.runtime import Runtime
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, write_qwen2_checkpoint
+
+    cfg = dict(QWEN2_05B_C4)
+    tmp = tempfile.mkdtemp(prefix="fi_hf_")
+    try:
+        t0 = time.perf_counter()
+        written = write_qwen2_checkpoint(tmp, cfg, "BF16", seed=seed, shards=2, biases=True, std=0.02)
+        t_write = time.perf_counter() - t0
+        nbytes = sum(len(raw) for *_, raw in written.values())
+        del written
+        t0 = time.perf_counter()
+        rt = Runtime.from_hf(tmp, num_blocks=64, block_size=16)
+        t_load = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        rt.submit(np.arange(8, dtype=np.uint32), max_new_tokens=1)
+        t_pack = time.perf_counter() - t0
+        rt.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return {"workload": "Qwen2-0.5B-shaped HF checkpoint, BF16, 2 shards, tied, q/k/v biases",
+            "safetensors_bytes": nbytes, "write_s": round(t_write, 2), "load_s": round(t_load, 3),
+            "load_gbs": round(nbytes / t_load / 1e9, 2), "first_submit_pack_s": round(t_pack, 3)}
 
 
 def c4_continuous(seed, n_requests, sampler=None):
@@ -653,6 +707,9 @@ def main():
     if not args.no_c5:
         print("bench: C5 bf16 decoder step", file=sys.stderr, flush=True)
         result["c5"] = c5_step(args.seed, args.c5_steps)
+    if args.hf_load:
+        print("bench: hf checkpoint import", file=sys.stderr, flush=True)
+        result["hf_load"] = hf_load(args.seed)
     print(json.dumps(result), flush=True)
 
 

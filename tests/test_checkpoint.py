@@ -11,7 +11,7 @@ import struct
 import numpy as np
 import pytest
 
-from ckpt_writer import encode, write_qwen2_checkpoint, write_safetensors
+from ferrisinfer_amd.workloads import encode, write_qwen2_checkpoint, write_safetensors
 from oracle.checkpoint import (bf16_bits_to_f32_bits, convert_to_f32, f16_bits_to_f32_bits,
                                internal_weights, qwen2_plans)
 

@@ -6,7 +6,7 @@ the same files (io/safetensors.rs, io/hf.rs)."""
 import numpy as np
 import pytest
 
-from ckpt_writer import write_qwen2_checkpoint
+from ferrisinfer_amd.workloads import write_qwen2_checkpoint
 from oracle.checkpoint import bf16_bits_to_f32_bits, f16_bits_to_f32_bits, internal_weights
 
 pytestmark = pytest.mark.gpu
