@@ -395,10 +395,16 @@ int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& 
 // (nearest even), scores, softmax and accumulation stay f32.  64-key chunks.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+#ifndef FI_PREFILL_BF16_RG
+#define FI_PREFILL_BF16_RG 2  // 16-row groups per wave
+#endif
+#ifndef FI_PREFILL_BF16_WAVES
+#define FI_PREFILL_BF16_WAVES 2  // waves per SIMD the register budget must allow
+#endif
 
-template <int D, int G>
-__global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
-  constexpr int QT = kRows / G;
+template <int D, int G, int RG>
+__global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_kernel(PrefillArgs a) {
+  constexpr int QT = kRows * RG / G;    // query tokens per workgroup (RG 16-row groups a wave)
   constexpr int KB = 64;                 // keys per chunk
   constexpr int DS = D / 32;             // 32-wide d steps of Q K^T
   constexpr int DT = D / 16;             // 16-wide output d tiles of P V
@@ -411,7 +417,6 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
   constexpr int VP = KB + 8;
   __shared__ __align__(16) uint16_t Ks[KB][KP];
   __shared__ __align__(16) uint16_t Vt[D][VP];
-  __shared__ __align__(16) uint16_t Ps[4][16][VP];
 
   const uint16_t* __restrict__ k_cache = static_cast<const uint16_t*>(a.k_cache);
   const uint16_t* __restrict__ v_cache = static_cast<const uint16_t*>(a.v_cache);
@@ -428,12 +433,20 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lk = lane >> 4;
 
-  // Q fragments (A operand): row 16w + li, d = 32 t + 8 lk + e
-  const int arow = 16 * w + li;
-  const int ah = arow / QT, at = arow % QT;
-  const bool a_ok = ah < a.group && q0 + at < qlen;
-  bf16x8 qf[DS];
-  {
+  // Transposed products: S^T = K Q^T leaves each lane the scores of one row (row li of each
+  // of the wave's row groups, keys 16 jt + 4 lk + v of score tile jt), so the row statistics
+  // need only the four lanes li + 16 lk, and O^T = V^T P^T takes those scores as its B operand
+  // straight from registers: MFMA k index 8 lk + e of 32-key step u stands for key
+  // 32 u + 4 lk + e (e < 4) or 32 u + 16 + 4 lk + (e - 4), and V^T is read at the same keys.
+  // Every K and V fragment read from LDS serves the wave's RG row groups.
+  int row_r[RG], qpos[RG];
+  bf16x8 qf[RG][DS];  // B operand: row li of group g, d = 32 t + 8 lk + e
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    row_r[g] = 16 * (w + 4 * g) + li;
+    qpos[g] = start + q0 + row_r[g] % QT;
+    const int ah = row_r[g] / QT, at = row_r[g] % QT;
+    const bool a_ok = ah < a.group && q0 + at < qlen;
     const float* qp = a.q + ((size_t)(qs + q0 + (a_ok ? at : 0)) * a.hq + kvh * a.group + (a_ok ? ah : 0)) * D;
 #pragma unroll
     for (int t = 0; t < DS; ++t) {
@@ -441,21 +454,19 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
       const float4 hi = *reinterpret_cast<const float4*>(qp + 32 * t + 8 * lk + 4);
       const f32x8 v = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       const f32x8 z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      qf[t] = __builtin_convertvector(a_ok ? v : z, bf16x8);
+      qf[g][t] = __builtin_convertvector(a_ok ? v : z, bf16x8);
     }
   }
-  int qpos[4];
+  v4f o[RG][DT];  // O^T tile dt of group g: d = 16 dt + 4 lk + v, row li
+  float m_row[RG], l_part[RG];  // running max (log2 units); this lane's share of the row sum
 #pragma unroll
-  for (int v = 0; v < 4; ++v) qpos[v] = start + q0 + (16 * w + 4 * lk + v) % QT;
-  v4f o[DT];
+  for (int g = 0; g < RG; ++g) {
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
-  float m_row[4], l_row[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    m_row[v] = -INFINITY;
-    l_row[v] = 0.0f;
+    for (int dt = 0; dt < DT; ++dt) o[g][dt] = v4f{0.f, 0.f, 0.f, 0.f};
+    m_row[g] = -INFINITY;
+    l_part[g] = 0.0f;
   }
+  const float c2 = a.scale * 1.4426950408889634f;  // scores -> log2 units
 
   const int kend = start + min(qlen, q0 + QT);
   const int nchunks = max((kend + KB - 1) / KB, 1);
@@ -514,63 +525,74 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
     lookup(c + 2);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- S = Q K^T: 16 rows x 64 keys ----
-    v4f s_acc[JT];
+    // ---- S^T = K Q^T: 64 keys x 16 rows per group ----
+    v4f s_acc[RG][JT];
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt) {
-      s_acc[jt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int g = 0; g < RG; ++g) s_acc[g][jt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < DS; ++t) {
         const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[16 * jt + li][32 * t + 8 * lk]);
-        s_acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t], kb, s_acc[jt], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+          s_acc[g][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qf[g][t], s_acc[g][jt], 0, 0, 0);
       }
     }
-    // element (jt, v): row 16w + 4lk + v, key k0 + 16jt + li
-    float pv[JT][4];
-    float alpha[4];
+    // causal / context mask only where the chunk reaches past the tile's first query position
+    const bool full = k0 + KB - 1 <= start + q0;  // workgroup-uniform
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int g = 0; g < RG; ++g) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) {
-        const int kp = k0 + 16 * jt + li;
-        const float sv = s_acc[jt][v] * a.scale;
-        pv[jt][v] = (kp <= qpos[v] && kp < ctx) ? sv : -INFINITY;
-        mx = fmaxf(mx, pv[jt][v]);
-      }
-      mx = group_max<16>(mx);
-      const float m_new = fmaxf(m_row[v], mx);
-      alpha[v] = m_new == -INFINITY ? 1.0f : __expf(m_row[v] - m_new);
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float x = s_acc[g][jt][v] * c2;
+          if (!full) {
+            const int kp = k0 + 16 * jt + 4 * lk + v;
+            x = (kp <= qpos[g] && kp < ctx) ? x : -INFINITY;
+          }
+          s_acc[g][jt][v] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_row[g], mx);  // finite: key 0 of chunk 0 is visible to every row
+      const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
+      m_row[g] = m_new;
       float ls = 0.0f;
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) {
-        pv[jt][v] = pv[jt][v] == -INFINITY ? 0.0f : __expf(pv[jt][v] - m_new);
-        ls += pv[jt][v];
-      }
-      ls = fi::group_sum<16>(ls);
-      l_row[v] = l_row[v] * alpha[v] + ls;
-      m_row[v] = m_new;
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float pexp = __builtin_amdgcn_exp2f(s_acc[g][jt][v] - m_new);
+          s_acc[g][jt][v] = pexp;
+          ls += pexp;
+        }
+      l_part[g] = l_part[g] * alpha + ls;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[g][dt] *= alpha;
     }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) o[dt][v] *= alpha[v];
-    // P (bf16) to the wave's LDS slice in accumulator layout; read back as the A operand
-#pragma unroll
-    for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        Ps[w][4 * lk + v][16 * jt + li] = static_cast<uint16_t>(fi::f32_to_bf16_bits(pv[jt][v]));
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-    // ---- O += P V: keys 32 u + 8 lk + e, output d = 16 dt + li ----
+    // ---- O^T += V^T P^T over the chunk's 32-key steps ----
 #pragma unroll
     for (int u = 0; u < KS; ++u) {
-      const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&Ps[w][li][32 * u + 8 * lk]);
+      bf16x8 pb[RG];
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        const f32x8 pf = {s_acc[g][2 * u][0], s_acc[g][2 * u][1], s_acc[g][2 * u][2], s_acc[g][2 * u][3],
+                          s_acc[g][2 * u + 1][0], s_acc[g][2 * u + 1][1], s_acc[g][2 * u + 1][2],
+                          s_acc[g][2 * u + 1][3]};
+        pb[g] = __builtin_convertvector(pf, bf16x8);  // nearest even
+      }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&Vt[16 * dt + li][32 * u + 8 * lk]);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[dt], 0, 0, 0);
+        const uint2 lo = *reinterpret_cast<const uint2*>(&Vt[16 * dt + li][32 * u + 4 * lk]);
+        const uint2 hi = *reinterpret_cast<const uint2*>(&Vt[16 * dt + li][32 * u + 16 + 4 * lk]);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+        for (int g = 0; g < RG; ++g) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], o[g][dt], 0, 0, 0);
       }
     }
     __syncthreads();  // every wave is done with this chunk's K/V
@@ -582,16 +604,21 @@ __global__ __launch_bounds__(kThreads) void prefill_bf16_kernel(PrefillArgs a) {
 
   if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
 
-  // ---- normalise and store: lane holds rows 16w + 4lk + v, d = 16 dt + li ----
+  // ---- normalise and store: lane holds row li of each group, d = 16 dt + 4 lk + v ----
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int r = 16 * w + 4 * lk + v;
-    const int h = r / QT, t = r % QT;
-    if (h >= a.group || q0 + t >= qlen) continue;
-    const float inv = 1.0f / l_row[v];
-    float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
+  for (int g = 0; g < RG; ++g) {
+    float l_row = l_part[g] + __shfl_xor(l_part[g], 16, 64);
+    l_row += __shfl_xor(l_row, 32, 64);
+    const int h = row_r[g] / QT, t = row_r[g] % QT;
+    if (h < a.group && q0 + t < qlen) {
+      const float inv = 1.0f / l_row;
+      float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) op[16 * dt + li] = o[dt][v] * inv;
+      for (int dt = 0; dt < DT; ++dt) {
+        *reinterpret_cast<float4*>(op + 16 * dt + 4 * lk) =
+            make_float4(o[g][dt][0] * inv, o[g][dt][1] * inv, o[g][dt][2] * inv, o[g][dt][3] * inv);
+      }
+    }
   }
 }
 
@@ -599,21 +626,22 @@ template <int D>
 int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
   PrefillArgs args = args_in;
   const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
-  const int qt = kRows / g;
+  constexpr int RG = FI_PREFILL_BF16_RG;
+  const int qt = kRows * RG / g;
   dim3 grid;
   FI_TRY(plan_tiles(ctx, args, qt, 64, "fi_attn_prefill_paged_bf16", &grid));
   switch (g) {
     case 1:
-      hipLaunchKernelGGL((prefill_bf16_kernel<D, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 1, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
     case 2:
-      hipLaunchKernelGGL((prefill_bf16_kernel<D, 2>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 2, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
     case 4:
-      hipLaunchKernelGGL((prefill_bf16_kernel<D, 4>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 4, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
     default:
-      hipLaunchKernelGGL((prefill_bf16_kernel<D, 8>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, 8, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
   }
   FI_CHECK_LAUNCH("prefill_bf16_kernel");
@@ -644,6 +672,9 @@ int32_t prefill_args(fi_context* ctx, const char* name, const float* d_q, const 
   if (*empty) return FI_OK;
   FI_REQUIRE(d_q && d_k_cache && d_v_cache && d_block_tables && d_cu_seqlens && d_context_lens && d_out,
              FI_ERR_INVALID_CONFIG, n + ": null pointer");
+  FI_REQUIRE((reinterpret_cast<uintptr_t>(d_q) & 15) == 0 && (reinterpret_cast<uintptr_t>(d_out) & 15) == 0 &&
+                 (reinterpret_cast<uintptr_t>(d_k_cache) & 15) == 0 && (reinterpret_cast<uintptr_t>(d_v_cache) & 15) == 0,
+             FI_ERR_INVALID_LAYOUT, n + ": q, out and the K/V pools must be 16-byte aligned (vector accesses)");
   PrefillArgs& g = *args;
   g = PrefillArgs{};
   g.q = d_q;

@@ -153,7 +153,8 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
  * block_tables (the chunk's own K/V rows must already be appended).  Replaces
  * causal_self_attention_f32 / cached_prefixed_causal_attention_f32 with the paged prefix
  * gather (kernel/cpu/attention.rs:222-518, runtime/reference.rs:425-465,
- * runtime/paged_kv.rs:769-791).  max_query_len must bound every qlen_b (it sizes the grid). */
+ * runtime/paged_kv.rs:769-791).  max_query_len must bound every qlen_b (it sizes the grid);
+ * q, out and the pools must be 16-byte aligned (InvalidLayout otherwise). */
 int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
                               const void* d_v_cache, int32_t kv_dtype,
                               const int32_t* d_block_tables, int32_t max_blocks_per_seq,
