@@ -395,6 +395,13 @@ int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& 
 // (nearest even), scores, softmax and accumulation stay f32.  64-key chunks.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+// ds_read_b64_tr_b16 at an LDS address (8-byte aligned)
+__device__ __forceinline__ v4s lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p));
+}
 #ifndef FI_PREFILL_BF16_RG
 #define FI_PREFILL_BF16_RG 2  // 16-row groups per wave
 #endif
@@ -414,9 +421,8 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
   constexpr int PER_T = KB * RV / kThreads;
   static_assert(KB * RV % kThreads == 0 && kThreads % KB == 0, "chunk must split over the workgroup");
   constexpr int KP = D + 8;              // padded LDS rows (conflict-free fragment reads)
-  constexpr int VP = KB + 8;
   __shared__ __align__(16) uint16_t Ks[KB][KP];
-  __shared__ __align__(16) uint16_t Vt[D][VP];
+  __shared__ __align__(16) uint16_t Vs[KB][KP];  // row-major like K; read through transpose loads
 
   const uint16_t* __restrict__ k_cache = static_cast<const uint16_t*>(a.k_cache);
   const uint16_t* __restrict__ v_cache = static_cast<const uint16_t*>(a.v_cache);
@@ -505,12 +511,7 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
     for (int r = 0; r < PER_T; ++r) {
       const int dv = w + 4 * r;
       *reinterpret_cast<uint4*>(&Ks[lane][8 * dv]) = kr[r];
-      const uint32_t x[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Vt[8 * dv + 2 * e][lane] = static_cast<uint16_t>(x[e] & 0xffffu);
-        Vt[8 * dv + 2 * e + 1][lane] = static_cast<uint16_t>(x[e] >> 16);
-      }
+      *reinterpret_cast<uint4*>(&Vs[lane][8 * dv]) = vr[r];
     }
   };
 
@@ -586,11 +587,16 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
                           s_acc[g][2 * u + 1][3]};
         pb[g] = __builtin_convertvector(pf, bf16x8);  // nearest even
       }
+      // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of the
+      // 8-byte reads of lanes 4 e + i / 4 (e = 0..3).  Lane (li, lk) points at key
+      // 32 u + 4 lk + li / 4 (+ 16 for the upper half), d 16 dt + 4 (li % 4) .. + 3, so it
+      // receives V at d = 16 dt + li for keys 32 u + 4 lk + e (+ 16): the keys its P holds.
+      const int vrow = 32 * u + 4 * lk + (li >> 2), vcol = 4 * (li & 3);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(&Vt[16 * dt + li][32 * u + 4 * lk]);
-        const uint2 hi = *reinterpret_cast<const uint2*>(&Vt[16 * dt + li][32 * u + 16 + 4 * lk]);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        const v4s lo = lds_read_tr16(&Vs[vrow][16 * dt + vcol]);
+        const v4s hi = lds_read_tr16(&Vs[vrow + 16][16 * dt + vcol]);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int g = 0; g < RG; ++g) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], o[g][dt], 0, 0, 0);
       }
