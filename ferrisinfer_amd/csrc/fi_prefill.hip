@@ -31,6 +31,9 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kRows = 64;     // (head, token) rows per workgroup
 constexpr int kKeys = 32;     // keys per staged chunk
+#ifndef FI_PREFILL_F32_RG
+#define FI_PREFILL_F32_RG 2  // 16-row groups per wave of the f32 kernel
+#endif
 
 struct PrefillArgs {
   const float* q;            // [T, Hq, D]
@@ -120,10 +123,10 @@ __device__ __forceinline__ float pick(const float4& v, int e) {
   return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
 }
 
-template <int D, typename KVT, int G>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+template <int D, typename KVT, int G, int RG>
+__global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   using QD = Quad<KVT>;
-  constexpr int QT = kRows / G;           // query tokens per workgroup
+  constexpr int QT = kRows * RG / G;      // query tokens per workgroup (RG 16-row groups a wave)
   constexpr int DV = D / 4;               // 4-element quads per row
   constexpr int DS = D / 16;              // 16-wide d steps of the Q K^T contraction
   constexpr int DH = D / 64 > 0 ? D / 64 : 1;  // 64-wide halves of the output (D = 32: one, masked)
@@ -132,7 +135,6 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   static_assert(QUADS % kThreads == 0, "chunk must split evenly over the workgroup");
   __shared__ float4 Ks[kKeys][DV + 1];
   __shared__ float4 Vs[kKeys][DV + 1];
-  __shared__ __align__(16) float Ps[4][16][kKeys + 4];
 
   const KVT* __restrict__ k_cache = static_cast<const KVT*>(a.k_cache);
   const KVT* __restrict__ v_cache = static_cast<const KVT*>(a.v_cache);
@@ -152,36 +154,37 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lk = lane >> 4;
 
-  // A operand rows: row i = 16w + li -> (head h, token t) = (i / QT, i % QT)
-  const int arow = 16 * w + li;
-  const int ah = arow / QT, at = arow % QT;
-  const bool a_ok = ah < a.group && q0 + at < qlen;
-  float4 qf[DS];
-  {
+  // Transposed products on v_mfma_f32_16x16x4_f32.  S^T = K Q^T: MFMA step (t, e) contracts
+  // d = 16 t + 4 lk + e, so both operands are float4 LDS / register reads; the accumulator
+  // gives lane (li, lk) the scores of row li (of each row group) at keys 16 jt + 4 lk + v.
+  // O^T = V^T P^T: MFMA step (jt, v) contracts key 16 jt + 4 lk + v, exactly the key whose
+  // probability the lane holds, so P is the B operand straight from registers; output tile
+  // (h, p) has d rows 64 h + 4 li + p, so one float4 V read feeds four MFMAs.
+  int row_r[RG], qpos[RG];
+  float4 qf[RG][DS];  // row li of group g, d = 16 t + 4 lk .. + 3
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    row_r[g] = 16 * (w + 4 * g) + li;
+    qpos[g] = start + q0 + row_r[g] % QT;
+    const int ah = row_r[g] / QT, at = row_r[g] % QT;
+    const bool a_ok = ah < a.group && q0 + at < qlen;
     const float* qp = a.q + ((size_t)(qs + q0 + (a_ok ? at : 0)) * a.hq + kvh * a.group + (a_ok ? ah : 0)) * D;
 #pragma unroll
     for (int t = 0; t < DS; ++t)
-      qf[t] = a_ok ? *reinterpret_cast<const float4*>(qp + 16 * t + 4 * lk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qf[g][t] = a_ok ? *reinterpret_cast<const float4*>(qp + 16 * t + 4 * lk) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-
-  // accumulator rows of this lane: r = 16w + 4lk + v -> query position
-  int qpos[4];
+  v4f o[RG][DH][4];  // O^T tile (h, p) of group g: d = 64 h + 4 (4 lk + v) + p, row li
+  float m_row[RG], l_part[RG];  // running max (log2 units); this lane's share of the row sum
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int r = 16 * w + 4 * lk + v;
-    qpos[v] = start + q0 + r % QT;
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int h = 0; h < DH; ++h)
+#pragma unroll
+      for (int p = 0; p < 4; ++p) o[g][h][p] = v4f{0.f, 0.f, 0.f, 0.f};
+    m_row[g] = -INFINITY;
+    l_part[g] = 0.0f;
   }
-  v4f o[DH][4];
-#pragma unroll
-  for (int h = 0; h < DH; ++h)
-#pragma unroll
-    for (int p = 0; p < 4; ++p) o[h][p] = v4f{0.f, 0.f, 0.f, 0.f};
-  float m_row[4], l_row[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    m_row[v] = -INFINITY;
-    l_row[v] = 0.0f;
-  }
+  const float c2 = a.scale * 1.4426950408889634f;  // scores -> log2 units
 
   const int kend = start + min(qlen, q0 + QT);  // keys needed by the tile's last token
   const int nchunks = max((kend + kKeys - 1) / kKeys, 1);
@@ -243,76 +246,78 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     lookup(c + 2);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- S = Q K^T: 16 rows x 32 keys (2 key tiles) ----
-    v4f s_acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    // ---- S^T = K Q^T: 32 keys (2 key tiles) x 16 rows per group ----
+    v4f s_acc[RG][2];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) s_acc[g][0] = s_acc[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < DS; ++t) {
       const float4 kb0 = Ks[li][4 * t + lk];
       const float4 kb1 = Ks[16 + li][4 * t + lk];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float av = pick(qf[t], e);
-        s_acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pick(kb0, e), s_acc[0], 0, 0, 0);
-        s_acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pick(kb1, e), s_acc[1], 0, 0, 0);
-      }
-    }
-    // element (jt, v): row 16w + 4lk + v, key k0 + 16jt + li
-    float pv[2][4];
-    float alpha[4];
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+        for (int g = 0; g < RG; ++g) {
+          const float bv = pick(qf[g][t], e);
+          s_acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(kb0, e), bv, s_acc[g][0], 0, 0, 0);
+          s_acc[g][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(kb1, e), bv, s_acc[g][1], 0, 0, 0);
+        }
+    }
+    // causal / context mask only where the chunk reaches past the tile's first query position
+    const bool full = k0 + kKeys - 1 <= start + q0;  // workgroup-uniform
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        const int kp = k0 + 16 * jt + li;
-        const float sv = s_acc[jt][v] * a.scale;
-        pv[jt][v] = (kp <= qpos[v] && kp < ctx) ? sv : -INFINITY;
-        mx = fmaxf(mx, pv[jt][v]);
-      }
-      mx = group_max<16>(mx);
-      const float m_new = fmaxf(m_row[v], mx);
-      alpha[v] = m_new == -INFINITY ? 1.0f : __expf(m_row[v] - m_new);
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float x = s_acc[g][jt][v] * c2;
+          if (!full) {
+            const int kp = k0 + 16 * jt + 4 * lk + v;
+            x = (kp <= qpos[g] && kp < ctx) ? x : -INFINITY;
+          }
+          s_acc[g][jt][v] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_row[g], mx);  // finite: key 0 of chunk 0 is visible to every row
+      const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
+      m_row[g] = m_new;
       float ls = 0.0f;
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        pv[jt][v] = pv[jt][v] == -INFINITY ? 0.0f : __expf(pv[jt][v] - m_new);
-        ls += pv[jt][v];
-      }
-      ls = fi::group_sum<16>(ls);
-      l_row[v] = l_row[v] * alpha[v] + ls;
-      m_row[v] = m_new;
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float pexp = __builtin_amdgcn_exp2f(s_acc[g][jt][v] - m_new);
+          s_acc[g][jt][v] = pexp;
+          ls += pexp;
+        }
+      l_part[g] = l_part[g] * alpha + ls;
+#pragma unroll
+      for (int h = 0; h < DH; ++h)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) o[g][h][p] *= alpha;
     }
-#pragma unroll
-    for (int h = 0; h < DH; ++h)
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[h][p][v] *= alpha[v];
-    // P to the wave's LDS slice in accumulator layout; read back as the A operand
+
+    // ---- O^T += V^T P^T: MFMA step (jt, v) is key 16 jt + 4 lk + v ----
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) Ps[w][4 * lk + v][16 * jt + li] = pv[jt][v];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-
-    // ---- O += P V: key k-step (u, e) covers keys 16u + 4lk + e ----
-#pragma unroll
-    for (int u = 0; u < kKeys / 16; ++u) {
-      const float4 pa = *reinterpret_cast<const float4*>(&Ps[w][li][16 * u + 4 * lk]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = 16 * u + 4 * lk + e;
-        const float av = pick(pa, e);
+      for (int v = 0; v < 4; ++v) {
+        const int key = 16 * jt + 4 * lk + v;
 #pragma unroll
         for (int h = 0; h < DH; ++h) {
-          // output tile (h, p) column li <-> d = 64h + 4li + p
-          const float4 vb = (D >= 64 || h == 0) && (64 * h + 4 * li < D) ? Vs[key][16 * h + li]
+          const float4 va = (D >= 64 || h == 0) && (64 * h + 4 * li < D) ? Vs[key][16 * h + li]
                                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-          for (int p = 0; p < 4; ++p) o[h][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pick(vb, p), o[h][p], 0, 0, 0);
+          for (int p = 0; p < 4; ++p)
+#pragma unroll
+            for (int g = 0; g < RG; ++g)
+              o[g][h][p] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(va, p), s_acc[g][jt][v], o[g][h][p], 0, 0, 0);
         }
       }
-    }
     __syncthreads();  // every wave is done with this chunk's K/V
     if (c + 1 < nchunks) {
       stage();
@@ -322,21 +327,25 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
   if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
 
-  // ---- normalise and store: lane holds rows 16w + 4lk + v, d = 64h + 4li + p ----
+  // ---- normalise and store: lane holds row li of each group, d = 64 h + 16 lk + 4 v + p ----
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int r = 16 * w + 4 * lk + v;
-    const int h = r / QT, t = r % QT;
-    if (h >= a.group || q0 + t >= qlen) continue;
-    const float inv = 1.0f / l_row[v];
-    float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
+  for (int g = 0; g < RG; ++g) {
+    float l_row = l_part[g] + __shfl_xor(l_part[g], 16, 64);
+    l_row += __shfl_xor(l_row, 32, 64);
+    const int hd = row_r[g] / QT, t = row_r[g] % QT;
+    if (hd < a.group && q0 + t < qlen) {
+      const float inv = 1.0f / l_row;
+      float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + hd) * D;
 #pragma unroll
-    for (int hh = 0; hh < DH; ++hh) {
-      const int d0 = 64 * hh + 4 * li;
-      if (d0 < D) {
-        *reinterpret_cast<float4*>(op + d0) =
-            make_float4(o[hh][0][v] * inv, o[hh][1][v] * inv, o[hh][2][v] * inv, o[hh][3][v] * inv);
-      }
+      for (int h = 0; h < DH; ++h)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int d0 = 64 * h + 16 * lk + 4 * v;
+          if (d0 < D) {
+            *reinterpret_cast<float4*>(op + d0) = make_float4(o[g][h][0][v] * inv, o[g][h][1][v] * inv,
+                                                              o[g][h][2][v] * inv, o[g][h][3][v] * inv);
+          }
+        }
     }
   }
 }
@@ -361,21 +370,22 @@ template <int D, typename KVT>
 int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args_in) {
   PrefillArgs args = args_in;
   const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
-  const int qt = kRows / g;
+  constexpr int RG = FI_PREFILL_F32_RG;
+  const int qt = kRows * RG / g;
   dim3 grid;
   FI_TRY(plan_tiles(ctx, args, qt, kKeys, "fi_attn_prefill_paged", &grid));
   switch (g) {
     case 1:
-      hipLaunchKernelGGL((prefill_kernel<D, KVT, 1>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 1, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
     case 2:
-      hipLaunchKernelGGL((prefill_kernel<D, KVT, 2>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 2, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
     case 4:
-      hipLaunchKernelGGL((prefill_kernel<D, KVT, 4>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 4, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
     default:
-      hipLaunchKernelGGL((prefill_kernel<D, KVT, 8>), grid, dim3(kThreads), 0, ctx->stream, args);
+      hipLaunchKernelGGL((prefill_kernel<D, KVT, 8, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
       break;
   }
   FI_CHECK_LAUNCH("prefill_kernel");
