@@ -31,9 +31,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kRows = 64;     // (head, token) rows per workgroup
 constexpr int kKeys = 32;     // keys per staged chunk
-#ifndef FI_PREFILL_F32_RG
-#define FI_PREFILL_F32_RG 2  // 16-row groups per wave of the f32 kernel
-#endif
 
 struct PrefillArgs {
   const float* q;            // [T, Hq, D]
@@ -366,11 +363,18 @@ int32_t plan_tiles(fi_context* ctx, PrefillArgs& args, int qt, int kb, const cha
   return FI_OK;
 }
 
-template <int D, typename KVT>
-int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args_in) {
-  PrefillArgs args = args_in;
-  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
-  constexpr int RG = FI_PREFILL_F32_RG;
+// Row groups per wave: two when the grid still gives every CU two workgroups (every K/V
+// fragment read from LDS then feeds two MFMAs), one for launches with few (sequence, tile,
+// kv head) triples, such as a prefill chunk over two kv heads.
+int row_groups(fi_context* ctx, const PrefillArgs& args, int g) {
+  const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  const int qt2 = kRows * 2 / g;
+  const long tiles2 = (long)((args.max_query_len + qt2 - 1) / qt2) * args.num_seqs * args.hkv;
+  return tiles2 >= 2 * cus ? 2 : 1;
+}
+
+template <int D, typename KVT, int RG>
+int32_t launch_prefill_rg(fi_context* ctx, PrefillArgs& args, int g) {
   const int qt = kRows * RG / g;
   dim3 grid;
   FI_TRY(plan_tiles(ctx, args, qt, kKeys, "fi_attn_prefill_paged", &grid));
@@ -390,6 +394,14 @@ int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args_in) {
   }
   FI_CHECK_LAUNCH("prefill_kernel");
   return FI_OK;
+}
+
+template <int D, typename KVT>
+int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args_in) {
+  PrefillArgs args = args_in;
+  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
+  return row_groups(ctx, args, g) == 2 ? launch_prefill_rg<D, KVT, 2>(ctx, args, g)
+                                       : launch_prefill_rg<D, KVT, 1>(ctx, args, g);
 }
 
 template <int D>
@@ -412,9 +424,6 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 __device__ __forceinline__ v4s lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p));
 }
-#ifndef FI_PREFILL_BF16_RG
-#define FI_PREFILL_BF16_RG 2  // 16-row groups per wave
-#endif
 #ifndef FI_PREFILL_BF16_WAVES
 #define FI_PREFILL_BF16_WAVES 2  // waves per SIMD the register budget must allow
 #endif
@@ -638,11 +647,8 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
   }
 }
 
-template <int D>
-int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
-  PrefillArgs args = args_in;
-  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
-  constexpr int RG = FI_PREFILL_BF16_RG;
+template <int D, int RG>
+int32_t launch_prefill_bf16_rg(fi_context* ctx, PrefillArgs& args, int g) {
   const int qt = kRows * RG / g;
   dim3 grid;
   FI_TRY(plan_tiles(ctx, args, qt, 64, "fi_attn_prefill_paged_bf16", &grid));
@@ -662,6 +668,14 @@ int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
   }
   FI_CHECK_LAUNCH("prefill_bf16_kernel");
   return FI_OK;
+}
+
+template <int D>
+int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
+  PrefillArgs args = args_in;
+  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
+  return row_groups(ctx, args, g) == 2 ? launch_prefill_bf16_rg<D, 2>(ctx, args, g)
+                                       : launch_prefill_bf16_rg<D, 1>(ctx, args, g);
 }
 
 // Checks the arguments of a prefill entry point and fills the kernel arguments; *empty when
