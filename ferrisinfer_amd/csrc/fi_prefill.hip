@@ -8,15 +8,17 @@
 // [ctx_b - qlen_b, ctx_b); query position p attends keys [0, p] read through the block table
 // (its own K/V rows must already be appended).
 //
-// One workgroup = (sequence, kv head, tile of 64/G query tokens) with all G query heads of the
-// GQA group: 64 (head, token) rows, 16 per wave, so every K/V byte a workgroup stages serves
-// G heads.  Keys are processed in chunks of 32: the chunk's K and V rows are staged in LDS
-// (16-byte loads; bf16 widened), the next chunk's rows are fetched into registers while the
-// current one is multiplied, two barriers per chunk.  Per wave and chunk: S = Q K^T on MFMA
-// with Q held in registers, causal mask + online softmax with DPP row reductions, P through
-// the wave's LDS slice into the A-operand layout, O += P V on MFMA.  The d index of the Q K^T
-// contraction and the key index of the P V contraction are visited in a permuted order so
-// every LDS operand read is one 16-byte read; the sums are the same products.
+// One workgroup = (sequence, kv head, tile of 64·RG/G query tokens) with all G query heads of
+// the GQA group: RG 16-row groups per wave (RG = 1 or 2, chosen per launch from the grid
+// size), so every K/V byte a workgroup stages serves G heads and, with RG = 2, every LDS
+// fragment read feeds two MFMAs.  Keys are processed in chunks (32 keys f32, 64 bf16): the
+// chunk's K and V rows are staged in LDS (16-byte loads; bf16 widened for the f32 kernel),
+// the next chunk's rows are fetched into registers while the current one is multiplied, two
+// barriers per chunk.  The products are taken transposed: S^T = K Q^T leaves each lane the
+// scores of one row, so the online softmax needs two cross-lane steps for the row maximum
+// and none for the sum until the end, and O^T = V^T P^T takes the probabilities as its B
+// operand straight from registers (the key order of its k index is matched in the V reads).
+// The causal mask is applied only on chunks that reach past a tile's first query.
 //
 // Tiles run largest first: a one-workgroup planning kernel sorts the (sequence, tile) pairs by
 // the number of key chunks they attend, so the long tiles of long sequences do not start last
@@ -84,15 +86,6 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int* __restric
   hist[tid] = part[tid] - v;
   __syncthreads();
   for (int t = tid; t < total; t += 1024) order[atomicAdd(&hist[1023 - bucket(t)], 1)] = t;
-}
-
-template <int kLanes>
-__device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, fi::dpp_mov<0xB1>(v));
-  v = fmaxf(v, fi::dpp_mov<0x4E>(v));
-  v = fmaxf(v, fi::dpp_mov<0x141>(v));
-  v = fmaxf(v, fi::dpp_mov<0x140>(v));
-  return v;
 }
 
 // Four consecutive K/V elements of one row as raw registers, widened when staged.
@@ -412,9 +405,9 @@ int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& 
 
 // ---- bf16-MFMA variant for a bf16 pool (fi_attn_prefill_paged_bf16) ----
 // Same workgroup shape, tile order and chunk pipeline as prefill_kernel, on
-// v_mfma_f32_16x16x32_bf16: K and V stay bf16 in LDS (V transposed on the way in so both
-// operands are 16-byte fragment reads), Q and the softmax probabilities are rounded to bf16
-// (nearest even), scores, softmax and accumulation stay f32.  64-key chunks.
+// v_mfma_f32_16x16x32_bf16: K and V stay bf16 in LDS, row-major (V^T fragments come from
+// ds_read_b64_tr_b16), Q and the softmax probabilities are rounded to bf16 (nearest even);
+// scores, softmax and accumulation stay f32.  64-key chunks.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
