@@ -119,7 +119,7 @@ def gemm_shapes(seed):
                           "tflops": round(2 * m * k * 2 * f / us / 1e6, 1)}), flush=True)
     h, v = 896, 151936
     w = torch.randn(v, h, device="cuda", generator=g) * 0.02
-    bp = ctx.weight_pack(w, h, v, 4, src_layout=1)
+    bp = ctx.weight_pack(w, h, v, 2, src_layout=1)
     for m in (1, 16, 64):
         hid = torch.randn(m, h, device="cuda", generator=g)
         tok = torch.empty(m, dtype=torch.int32, device="cuda")
@@ -293,7 +293,7 @@ def kernel_legs(ctx, seed):
         out[f"gemm_c4_{tag}_w13_swiglu"] = gemm_row(m, k, 2 * f, ms, 1, 2)
     h, v = 896, 151936
     w = torch.randn(v, h, device="cuda", generator=g) * 0.02
-    bp = ctx.weight_pack(w, h, v, 4, src_layout=1)
+    bp = ctx.weight_pack(w, h, v, 2, src_layout=1)
     for m in (1, 64):
         hid = torch.randn(m, h, device="cuda", generator=g)
         tok = torch.empty(m, dtype=torch.int32, device="cuda")

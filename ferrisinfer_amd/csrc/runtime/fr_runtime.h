@@ -88,7 +88,7 @@ class DeviceModel {
   struct Packed {
     DeviceBuffer qkv, wo, w13, w2;
   };
-  static constexpr int32_t kQkvPack = 1, kWoPack = 1, kW2Pack = 4, kLmPack = 4;
+  static constexpr int32_t kQkvPack = 1, kWoPack = 1, kW2Pack = 4, kLmPack = 2;
 
   DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions);
   void set_weight(const std::string& name, const float* host, size_t count);

@@ -337,6 +337,7 @@ class Context:
                                              ptr(bias_gate), ptr(out)))
 
     def lm_head_argmax_packed(self, hidden, bp, vocab, token_out, prob_out):
+        """Greedy head over a weight packed from [vocab, hidden] at pack width 2."""
         m, h = hidden.shape
         check(self.lib.fi_lm_head_argmax_packed(self.handle, ptr(hidden), int(hidden.stride(0)),
                                                 ptr(bp), int(m), int(h), int(vocab),

@@ -288,7 +288,7 @@ int32_t fi_gemm_packed(fi_context* ctx, const float* d_a, int32_t lda, const flo
 int32_t fi_gemm_packed_swiglu(fi_context* ctx, const float* d_a, int32_t lda, const float* d_bp_pair, int32_t k,
                               int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate, float* d_out);
 
-/* fi_lm_head_argmax over a weight packed from its [vocab, hidden] layout with pack width 4
+/* fi_lm_head_argmax over a weight packed from its [vocab, hidden] layout with pack width 2
  * (matmul_rhs_transposed_argmax_f32, kernel/cpu/matmul.rs:190-274): first maximal index
  * and 1 / sum(exp(logit - max)) per row.  Uses the context workspace. */
 int32_t fi_lm_head_argmax_packed(fi_context* ctx, const float* d_hidden, int32_t lda, const float* d_bp, int32_t m,

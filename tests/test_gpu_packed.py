@@ -131,7 +131,7 @@ def test_packed_lm_head_argmax(orc, gpu_ctx, m, h, v):
     lda = (h + 3) // 4 * 4
     hid_dev = torch.zeros((m, lda), device="cuda")
     hid_dev[:, :h] = dev(hid)
-    bp = gpu_ctx.weight_pack(dev(w), h, v, 4, src_layout=1)
+    bp = gpu_ctx.weight_pack(dev(w), h, v, 2, src_layout=1)
     tok = torch.empty(m, dtype=torch.int32, device="cuda")
     prob = torch.empty(m, device="cuda")
     gpu_ctx.lm_head_argmax_packed(hid_dev[:, :h], bp, v, tok, prob)
@@ -156,7 +156,7 @@ def test_packed_lm_head_reference_vector_and_ties(gpu_ctx):
     hid = torch.zeros((1, 4), device="cuda")
     hid[0, :2] = torch.tensor([1.0, 2.0])
     w = np.array([[1, 0], [0, 1], [1, 1]], np.float32)
-    bp = gpu_ctx.weight_pack(dev(w), 2, 3, 4, src_layout=1)
+    bp = gpu_ctx.weight_pack(dev(w), 2, 3, 2, src_layout=1)
     gpu_ctx.lm_head_argmax_packed(hid[:, :2], bp, 3, tok, prob)
     torch.cuda.synchronize()
     assert int(tok[0]) == 2
@@ -164,7 +164,7 @@ def test_packed_lm_head_reference_vector_and_ties(gpu_ctx):
     v, h = 300, 4
     w = np.zeros((v, h), np.float32)
     w[[70, 5, 200, 71, 6], 0] = 1.0  # max logit 1.0 at 5, 6, 70, 71, 200 -> first is 5
-    bp = gpu_ctx.weight_pack(dev(w), h, v, 4, src_layout=1)
+    bp = gpu_ctx.weight_pack(dev(w), h, v, 2, src_layout=1)
     hid = dev(np.array([[1, 0, 0, 0]], np.float32))
     gpu_ctx.lm_head_argmax_packed(hid, bp, v, tok, prob)
     torch.cuda.synchronize()
