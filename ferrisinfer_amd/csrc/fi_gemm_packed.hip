@@ -636,6 +636,87 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   }
 }
 
+// Four consecutive columns per thread: the same per-element arithmetic as
+// qkv_rope_append_kernel (splits summed in order, bias added, RoPE with each product rounded
+// before the add) on 16-byte loads and stores.  Needs rotary_dims / 2, the pass-through width
+// and D to be multiples of 4 and 16-byte aligned operands (checked by the entry point).
+template <typename KVT>
+__global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
+    const float* __restrict__ parts, int splits, const float* __restrict__ bias_q, const float* __restrict__ bias_k,
+    const float* __restrict__ bias_v, const int* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rotary_dims, int max_positions,
+    const int64_t* __restrict__ slots, KVT* __restrict__ k_cache, KVT* __restrict__ v_cache, int64_t pool_slots,
+    int block_size, int tokens, int hq, int hkv, int d, float* __restrict__ q_out, uint32_t* __restrict__ faults) {
+  const int half = rotary_dims / 2;
+  const int pass = d - 2 * half;
+  const int quads_per_head = (half + pass) / 4;
+  const int rot_items = (hq + hkv) * quads_per_head;
+  const int qw = hq * d, kw = hkv * d;
+  const int items = rot_items + kw / 4;
+  const int gid = blockIdx.x * kRowThreads + threadIdx.x;
+  const int t = gid / items;
+  if (t >= tokens) return;
+  const int idx = gid - t * items;
+  const int width = qw + 2 * kw;
+  const size_t plane4 = (size_t)tokens * width / 4;
+  const float* p0 = parts + (size_t)t * width;
+  auto value4 = [&](int col) {
+    const float4 x = sum_splits(reinterpret_cast<const float4*>(p0 + col), plane4, splits);
+    const float* b = col < qw ? bias_q : (col < qw + kw ? bias_k : bias_v);
+    const int bc = col < qw ? col : (col < qw + kw ? col - qw : col - qw - kw);
+    if (!b) return x;
+    const float4 bv = *reinterpret_cast<const float4*>(b + bc);
+    return make_float4(x.x + bv.x, x.y + bv.y, x.z + bv.z, x.w + bv.w);
+  };
+  const int64_t slot = slots[t];
+  const bool write_kv = slot >= 0 && slot < pool_slots;
+  if (idx == 0 && slot >= pool_slots) atomicOr(faults, FI_FAULT_SLOT_RANGE);
+  const int64_t blk = write_kv ? slot / block_size : 0;
+  const int off = write_kv ? static_cast<int>(slot % block_size) : 0;
+  auto store4 = [&](int head, int i, const float4& x) {  // head < hq: q; else k head (head - hq)
+    if (head < hq) {
+      *reinterpret_cast<float4*>(q_out + (size_t)t * qw + head * d + i) = x;
+    } else if (write_kv) {
+      const size_t base = (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i;
+      put_kv(k_cache, base, x.x);
+      put_kv(k_cache, base + 1, x.y);
+      put_kv(k_cache, base + 2, x.z);
+      put_kv(k_cache, base + 3, x.w);
+    }
+  };
+  if (idx < rot_items) {
+    const int head = idx / quads_per_head, r = 4 * (idx - head * quads_per_head);
+    const int col0 = head < hq ? head * d : qw + (head - hq) * d;
+    if (r < half) {
+#pragma clang fp contract(off)
+      int pos = positions[t];
+      if (pos < 0 || pos >= max_positions) {
+        if (idx == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+        pos = 0;
+      }
+      const float4 lo = value4(col0 + r), hi = value4(col0 + r + half);
+      const float4 c = *reinterpret_cast<const float4*>(cos_t + (size_t)pos * half + r);
+      const float4 sn = *reinterpret_cast<const float4*>(sin_t + (size_t)pos * half + r);
+      store4(head, r, make_float4(lo.x * c.x - hi.x * sn.x, lo.y * c.y - hi.y * sn.y, lo.z * c.z - hi.z * sn.z,
+                                  lo.w * c.w - hi.w * sn.w));
+      store4(head, r + half, make_float4(hi.x * c.x + lo.x * sn.x, hi.y * c.y + lo.y * sn.y,
+                                         hi.z * c.z + lo.z * sn.z, hi.w * c.w + lo.w * sn.w));
+    } else {
+      const int i = 2 * half + (r - half);
+      store4(head, i, value4(col0 + i));
+    }
+  } else if (write_kv) {
+    const int v = 4 * (idx - rot_items);
+    const int h = v / d, i = v - h * d;
+    const float4 x = value4(qw + kw + v);
+    const size_t base = (((size_t)blk * hkv + h) * block_size + off) * d + i;
+    put_kv(v_cache, base, x.x);
+    put_kv(v_cache, base + 1, x.y);
+    put_kv(v_cache, base + 2, x.z);
+    put_kv(v_cache, base + 3, x.w);
+  }
+}
+
 int32_t q_steps(int32_t k) { return (k + 15) / 16; }
 
 // Pack width of the greedy head's weight: width 2 runs on the shared-activation kernel (four
@@ -929,19 +1010,38 @@ int32_t fi_qkv_rope_append(fi_context* ctx, const float* d_parts, int32_t splits
   FI_REQUIRE(rotary_dims == 0 || (d_cos && d_sin && max_positions > 0), FI_ERR_INVALID_CONFIG,
              "fi_qkv_rope_append: rope tables required");
   const int64_t pool_slots = static_cast<int64_t>(num_blocks) * block_size;
+  auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int32_t half = rotary_dims / 2, pass = head_dim - 2 * half;
+  const bool vec4 = half % 4 == 0 && pass % 4 == 0 && head_dim % 4 == 0 && aligned16(d_parts) && aligned16(d_q_out) &&
+                    (!d_bias_q || aligned16(d_bias_q)) && (!d_bias_k || aligned16(d_bias_k)) &&
+                    (!d_bias_v || aligned16(d_bias_v)) && (rotary_dims == 0 || (aligned16(d_cos) && aligned16(d_sin)));
   const int64_t items = static_cast<int64_t>(num_q_heads + num_kv_heads) * (head_dim - rotary_dims / 2) +
                         static_cast<int64_t>(num_kv_heads) * head_dim;
-  FI_REQUIRE(items * num_tokens < 0x7fffffffLL - kRowThreads, FI_ERR_INVALID_SHAPE,
+  const int64_t launch_items = vec4 ? items / 4 : items;
+  FI_REQUIRE(launch_items * num_tokens < 0x7fffffffLL - kRowThreads, FI_ERR_INVALID_SHAPE,
              "fi_qkv_rope_append: too many tokens for one launch");
-  const dim3 grid(static_cast<unsigned>((items * num_tokens + kRowThreads - 1) / kRowThreads));
+  const dim3 grid(static_cast<unsigned>((launch_items * num_tokens + kRowThreads - 1) / kRowThreads));
   if (kv_dtype == FI_DTYPE_F32) {
-    hipLaunchKernelGGL(qkv_rope_append_kernel<float>, grid, dim3(kRowThreads), 0, ctx->stream, d_parts,
-                       splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions, d_slot_mapping,
-                       static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache), pool_slots, block_size,
-                       num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out, ctx->d_faults);
+    if (vec4) {
+      hipLaunchKernelGGL(qkv_rope_append4_kernel<float>, grid, dim3(kRowThreads), 0, ctx->stream, d_parts, splits,
+                         d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
+                         d_slot_mapping, static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache), pool_slots,
+                         block_size, num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out, ctx->d_faults);
+    } else {
+      hipLaunchKernelGGL(qkv_rope_append_kernel<float>, grid, dim3(kRowThreads), 0, ctx->stream, d_parts, splits,
+                         d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
+                         d_slot_mapping, static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache), pool_slots,
+                         block_size, num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out, ctx->d_faults);
+    }
+  } else if (vec4) {
+    hipLaunchKernelGGL(qkv_rope_append4_kernel<uint16_t>, grid, dim3(kRowThreads), 0, ctx->stream, d_parts, splits,
+                       d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
+                       d_slot_mapping, static_cast<uint16_t*>(d_k_cache), static_cast<uint16_t*>(d_v_cache),
+                       pool_slots, block_size, num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out,
+                       ctx->d_faults);
   } else {
-    hipLaunchKernelGGL(qkv_rope_append_kernel<uint16_t>, grid, dim3(kRowThreads), 0, ctx->stream,
-                       d_parts, splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
+    hipLaunchKernelGGL(qkv_rope_append_kernel<uint16_t>, grid, dim3(kRowThreads), 0, ctx->stream, d_parts, splits,
+                       d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin, rotary_dims, max_positions,
                        d_slot_mapping, static_cast<uint16_t*>(d_k_cache), static_cast<uint16_t*>(d_v_cache),
                        pool_slots, block_size, num_tokens, num_q_heads, num_kv_heads, head_dim, d_q_out,
                        ctx->d_faults);

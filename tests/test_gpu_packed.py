@@ -194,7 +194,8 @@ def test_splitk_residual_rms_norm(orc, gpu_ctx, rows, hidden, splits, bias):
 
 
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
-@pytest.mark.parametrize("hq,hkv,d,rot,splits", [(14, 2, 64, 64, 3), (8, 2, 32, 32, 1), (4, 2, 64, 32, 2)])
+@pytest.mark.parametrize("hq,hkv,d,rot,splits", [(14, 2, 64, 64, 3), (8, 2, 32, 32, 1), (4, 2, 64, 32, 2),
+                                                  (4, 2, 32, 6, 2)])  # last: scalar path (rot / 2 = 3)
 def test_qkv_rope_append_matches_standalone_ops(gpu_ctx, kv, hq, hkv, d, rot, splits):
     """Fused consumer == split sum + bias, then fi_rope, then fi_kv_append, bit for bit."""
     import torch
