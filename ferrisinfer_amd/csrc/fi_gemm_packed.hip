@@ -516,18 +516,31 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
   const size_t base = (size_t)row * hidden;
   float ss = 0.0f;
   const bool vec = (hidden & 3) == 0;
-  if (vec) {
-    const int h4 = hidden / 4;
-    for (int c = threadIdx.x; c < h4; c += kRowThreads) {
-      float4 x = sum_splits(reinterpret_cast<const float4*>(parts + base) + c, plane / 4, splits);
-      if (bias) x = add(x, reinterpret_cast<const float4*>(bias)[c]);
-      x = add(x, reinterpret_cast<const float4*>(residual + base)[c]);
-      reinterpret_cast<float4*>(sum_out + base)[c] = x;
-      ss += x.x * x.x;
-      ss += x.y * x.y;
-      ss += x.z * x.z;
-      ss += x.w * x.w;
+  // rows up to kRowQuads float4 per thread keep their sums in registers for the second pass
+  // (no re-read of sum_out); wider rows loop and re-read
+  constexpr int kRowQuads = 8;
+  const int h4 = hidden / 4;
+  const bool held = vec && h4 <= kRowQuads * kRowThreads;
+  float4 xs[kRowQuads];
+  auto sum_quad = [&](int c) {
+    float4 x = sum_splits(reinterpret_cast<const float4*>(parts + base) + c, plane / 4, splits);
+    if (bias) x = add(x, reinterpret_cast<const float4*>(bias)[c]);
+    x = add(x, reinterpret_cast<const float4*>(residual + base)[c]);
+    reinterpret_cast<float4*>(sum_out + base)[c] = x;
+    ss += x.x * x.x;
+    ss += x.y * x.y;
+    ss += x.z * x.z;
+    ss += x.w * x.w;
+    return x;
+  };
+  if (held) {
+#pragma unroll
+    for (int i = 0; i < kRowQuads; ++i) {
+      const int c = threadIdx.x + i * kRowThreads;
+      if (c < h4) xs[i] = sum_quad(c);
     }
+  } else if (vec) {
+    for (int c = threadIdx.x; c < h4; c += kRowThreads) (void)sum_quad(c);
   } else {
     for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
       float x = sum_splits(parts + base + c, plane, splits);
@@ -544,14 +557,19 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
 #pragma unroll
   for (int i = 0; i < kRowThreads / 64; ++i) total += s_red[i];
   const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
-  if (vec) {
-    const int h4 = hidden / 4;
-    for (int c = threadIdx.x; c < h4; c += kRowThreads) {
-      const float4 x = reinterpret_cast<const float4*>(sum_out + base)[c];
-      const float4 wv = reinterpret_cast<const float4*>(weight)[c];
-      reinterpret_cast<float4*>(out + base)[c] =
-          make_float4((x.x * inv) * wv.x, (x.y * inv) * wv.y, (x.z * inv) * wv.z, (x.w * inv) * wv.w);
+  auto norm_quad = [&](int c, const float4& x) {
+    const float4 wv = reinterpret_cast<const float4*>(weight)[c];
+    reinterpret_cast<float4*>(out + base)[c] =
+        make_float4((x.x * inv) * wv.x, (x.y * inv) * wv.y, (x.z * inv) * wv.z, (x.w * inv) * wv.w);
+  };
+  if (held) {
+#pragma unroll
+    for (int i = 0; i < kRowQuads; ++i) {
+      const int c = threadIdx.x + i * kRowThreads;
+      if (c < h4) norm_quad(c, xs[i]);
     }
+  } else if (vec) {
+    for (int c = threadIdx.x; c < h4; c += kRowThreads) norm_quad(c, reinterpret_cast<const float4*>(sum_out + base)[c]);
   } else {
     for (int c = threadIdx.x; c < hidden; c += kRowThreads) out[base + c] = (sum_out[base + c] * inv) * weight[c];
   }
