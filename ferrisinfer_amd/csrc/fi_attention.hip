@@ -153,8 +153,12 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   const int unit = blockIdx.x - part * units;
   const int seq = unit / a.hkv;
   const int kvh = unit - seq * a.hkv;
-  const int ctx = a.context_lens[seq];
   const int tid = threadIdx.x;
+  int ctx = a.context_lens[seq];
+  if (ctx > a.parts_per_seq * kPartTokens) {  // beyond the grid: clamp and report
+    if (part == 0 && tid == 0) atomicOr(a.faults, FI_FAULT_CONTEXT_RANGE);
+    ctx = a.parts_per_seq * kPartTokens;
+  }
   const size_t head0 = (size_t)seq * a.hq + (size_t)kvh * group;  // first query head of the group
   if (ctx <= 0) {  // no keys: defined output of zeros
     if (part == 0) {
@@ -369,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   const int pair = blockIdx.x;
   const int seq = pair / a.hkv;
   const int kvh = pair % a.hkv;
-  const int ctx = a.context_lens[seq];
+  const int ctx = min(a.context_lens[seq], a.parts_per_seq * kPartTokens);  // clamped as in the partitions
   const int nparts = (ctx + kPartTokens - 1) / kPartTokens;
   if (nparts <= 1) return;
   const int group = a.group;
@@ -389,15 +393,27 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
       pre[k][p] = (g < group && p < nparts) ? a.part_acc[((head0 + g) * P + p) * D + d] : 0.0f;
   }
   for (int g = w; g < group; g += 4) {
-    const float* ml = a.part_ml + (head0 + g) * P * 2;
+    // each lane's (max, sum) pairs are read once, as float2, and kept for the weights
+    constexpr int kPartsPerLane = kMaxParts / 64;
+    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + (head0 + g) * P;
+    float2 mlv[kPartsPerLane];
     float m = -INFINITY;
-    for (int p = lane; p < nparts; p += 64) m = fmaxf(m, ml[p * 2]);
+#pragma unroll
+    for (int j = 0; j < kPartsPerLane; ++j) {
+      const int p = lane + 64 * j;
+      mlv[j] = p < nparts ? ml[p] : make_float2(-INFINITY, 0.0f);
+      m = fmaxf(m, mlv[j].x);
+    }
     m = fi::wave_max(m);
     float l = 0.0f;
-    for (int p = lane; p < nparts; p += 64) {
-      float wgt = __expf(ml[p * 2] - m);
-      s_w[g][p] = wgt;
-      l += ml[p * 2 + 1] * wgt;
+#pragma unroll
+    for (int j = 0; j < kPartsPerLane; ++j) {
+      const int p = lane + 64 * j;
+      if (p < nparts) {
+        const float wgt = __expf(mlv[j].x - m);
+        s_w[g][p] = wgt;
+        l += mlv[j].y * wgt;
+      }
     }
     l = fi::wave_sum(l);
     if (lane == 0) s_inv[g] = 1.0f / l;

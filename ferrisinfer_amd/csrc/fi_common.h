@@ -15,6 +15,7 @@ enum : uint32_t {
   FI_FAULT_BLOCK_RANGE = 1u << 2,  // attention: block id beyond the pool
   FI_FAULT_SAMPLE_TOPK = 1u << 3,       // sampling: top_k (after clamping to the vocabulary) above 1024
   FI_FAULT_SAMPLE_NONFINITE = 1u << 4,  // sampling: the candidate weights do not sum to a finite, positive total
+  FI_FAULT_CONTEXT_RANGE = 1u << 5,     // decode attention: a context length beyond the partitions max_context_len sized
 };
 
 struct fi_context {

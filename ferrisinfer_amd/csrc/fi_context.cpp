@@ -187,6 +187,7 @@ int32_t fi_ctx_check_faults(fi_context* ctx) {
   if (bits & FI_FAULT_BLOCK_RANGE) msg += " block id beyond the block pool;";
   if (bits & FI_FAULT_SAMPLE_TOPK) msg += " sampling top_k above the device limit of 1024;";
   if (bits & FI_FAULT_SAMPLE_NONFINITE) msg += " failed to build a finite sampling distribution;";
+  if (bits & FI_FAULT_CONTEXT_RANGE) msg += " context length beyond max_context_len;";
   return fi::set_error(FI_ERR_RUNTIME, msg);
 }
 

@@ -139,7 +139,9 @@ int32_t fi_ctx_check_faults(fi_context* ctx);
  * runtime/paged_kv.rs:769-791, kernel/cpu/attention.rs:332-518) and
  * decode_causal_attention_f32 (kernel/cpu/attention.rs:520-686).
  * q/out: f32 [num_seqs, Hq, D]; scale is 1/sqrt(D) in the reference (attention.rs:659).
- * max_context_len must bound every context_lens entry (it sizes the grid). */
+ * max_context_len must bound every context_lens entry (it sizes the grid); an entry beyond
+ * the partitions it sizes is clamped to them on device and reported as Runtime by
+ * fi_ctx_check_faults. */
 int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
                              const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
                              int32_t max_blocks_per_seq, const int32_t* d_context_lens,

@@ -195,6 +195,42 @@ def test_kv_append_out_of_range_slot_reported(gpu_ctx):
     gpu_ctx.check_faults()  # flags were cleared
 
 
+def test_decode_context_beyond_max_context_len_reported(gpu_ctx):
+    """A context_lens entry beyond the partitions that max_context_len sizes is clamped to them
+    on device (the block table covers it, so every read stays in the pool and the partials
+    in their stripe) and reported as Runtime; the other sequences are unaffected."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32, FerrisError
+
+    nb, bs, hkv, hq, d, max_len = 320, 16, 2, 4, 64, 600
+    lens = [max_len, 5000]  # 5000 > 600 rounded up to whole partitions, for any partition size
+    g = torch.Generator().manual_seed(11)
+    kc = torch.randn((nb, hkv, bs, d), generator=g).cuda()
+    vc = torch.randn((nb, hkv, bs, d), generator=g).cuda()
+    q = torch.randn((2, hq, d), generator=g).cuda()
+    max_blocks = (lens[1] + bs - 1) // bs
+    bt = torch.arange(2 * max_blocks, dtype=torch.int32).reshape(2, max_blocks) % nb
+    bt = bt.cuda()
+    out = torch.empty_like(q)
+    gpu_ctx.attn_decode_paged(q, kc, vc, DTYPE_F32, bt, torch.tensor(lens, dtype=torch.int32).cuda(),
+                              max_len, hkv, bs, nb, d ** -0.5, out)
+    torch.cuda.synchronize()
+    with pytest.raises(FerrisError) as e:
+        gpu_ctx.check_faults()
+    assert e.value.kind == "Runtime"
+    assert "context length beyond max_context_len" in str(e.value)
+    gpu_ctx.check_faults()  # flags were cleared
+    assert torch.isfinite(out).all()
+    solo = torch.empty_like(q[:1])
+    gpu_ctx.attn_decode_paged(q[:1].contiguous(), kc, vc, DTYPE_F32, bt[:1].contiguous(),
+                              torch.tensor(lens[:1], dtype=torch.int32).cuda(), max_len, hkv, bs,
+                              nb, d ** -0.5, solo)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    assert torch.equal(out[0], solo[0])
+
+
 def test_kv_copy_blocks(gpu_ctx):
     import torch
 
