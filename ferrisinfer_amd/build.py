@@ -71,16 +71,41 @@ def build_runtime(verbose: bool = False) -> str:
     return RUNTIME_PATH
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
+
+
+def _compile(src: str, verbose: bool) -> str:
+    """One translation unit to an object (its device code embedded) under _build/."""
+    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    cmd = [hipcc(), *flags, "-c", "-o", obj, src]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, cwd=PKG_DIR, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {LIB_NAME} (exit {res.returncode})")
+        raise RuntimeError(f"hipcc failed on {os.path.basename(src)} (exit {res.returncode})")
+    return obj
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compiles every translation unit (in parallel, always from source) and links the
+    kernel library, then the host runtime library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    jobs = jobs or max(1, min(len(srcs), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp, *objs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, cwd=PKG_DIR, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed linking {LIB_NAME} (exit {res.returncode})")
     os.replace(tmp, LIB_PATH)
     build_runtime(verbose)
     return LIB_PATH
