@@ -6,8 +6,18 @@
 // KV pool layout (per layer): K and V are [num_blocks][Hkv][block_size][D], so one
 // (block, kv_head) is a contiguous block_size*D run: a 16-token f32 block of D=128 is 8 KiB
 // read with 16-byte loads.
+#include <mutex>
+
 #include "fi_common.h"
 #include "fi_device.h"
+
+// Split-KV partials of fi_attn_decode_paged_noalloc: a fixed array of this library, one copy
+// per device (each GPU holds it from the load of this code object until the process ends).
+// In host code `scratch` names a host-side stand-in, never the device memory: host code uses
+// only the per-device address that decode_noalloc_attach obtains from hipGetSymbolAddress.
+// Calls that overlap on one GPU share this memory and race.
+#define FI_DECODE_NOALLOC_SCRATCH_BYTES (96u << 20)
+static __device__ __align__(256) unsigned char scratch[FI_DECODE_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -550,6 +560,26 @@ int32_t launch_decode_dtype(fi_context* ctx, int32_t dtype, const DecodeArgs& ar
 
 namespace fi {
 
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+}  // namespace
+
+int32_t decode_noalloc_attach(fi_context* ctx) {
+  FI_REQUIRE(ctx->device >= 0 && ctx->device < kMaxDevices, FI_ERR_UNSUPPORTED,
+             "device ordinal " + std::to_string(ctx->device) + " beyond the library's device table");
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (g_noalloc_ptr[ctx->device] == nullptr) {
+    void* p = nullptr;
+    FI_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    FI_REQUIRE(p != nullptr, FI_ERR_RUNTIME, "hipGetSymbolAddress(scratch) returned a null address");
+    g_noalloc_ptr[ctx->device] = p;
+  }
+  ctx->noalloc_scratch = g_noalloc_ptr[ctx->device];
+  return FI_OK;
+}
+
 // Split-KV decode partials live in the context workspace (grow-only).
 int32_t decode_scratch(fi_context* ctx, int32_t num_seqs, int32_t hq, int32_t parts, int32_t head_dim,
                        float** part_acc, float** part_ml) {
@@ -628,12 +658,18 @@ int32_t fi_kv_copy_blocks(fi_context* ctx, void* d_k_cache, void* d_v_cache, int
   return FI_OK;
 }
 
-int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
-                             const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
-                             int32_t max_blocks_per_seq, const int32_t* d_context_lens,
-                             int32_t num_seqs, int32_t max_context_len, int32_t num_q_heads,
-                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                             int32_t num_blocks, float scale, float* d_out) {
+}  // extern "C"
+
+namespace {
+
+// Shared by both decode entry points: validation, launch shape and launches.  With
+// `noalloc` the partials go to the library's fixed scratch array instead of the context
+// workspace (nothing is allocated).
+int32_t decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache, const void* d_v_cache,
+                     int32_t kv_dtype, const int32_t* d_block_tables, int32_t max_blocks_per_seq,
+                     const int32_t* d_context_lens, int32_t num_seqs, int32_t max_context_len,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int32_t num_blocks, float scale, float* d_out, bool noalloc) {
   FI_TRY(fi::enter(ctx));
   FI_REQUIRE(num_seqs >= 0 && max_context_len >= 0, FI_ERR_INVALID_SHAPE,
              "fi_attn_decode_paged: negative sizes");
@@ -673,7 +709,21 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
   args.num_blocks = num_blocks;
   args.scale = scale;
   if (parts > 1) {
-    FI_TRY(fi::decode_scratch(ctx, num_seqs, num_q_heads, parts, head_dim, &args.part_acc, &args.part_ml));
+    if (noalloc) {
+      const size_t slots = static_cast<size_t>(num_seqs) * num_q_heads * parts;
+      const size_t acc_bytes = (slots * head_dim * sizeof(float) + 255) & ~static_cast<size_t>(255);
+      const size_t need = acc_bytes + slots * 2 * sizeof(float);
+      FI_REQUIRE(need <= FI_DECODE_NOALLOC_SCRATCH_BYTES, FI_ERR_RUNTIME,
+                 "fi_attn_decode_paged_noalloc: this launch needs " + std::to_string(need) +
+                     " bytes of split-KV scratch; the fixed scratch holds " +
+                     std::to_string(FI_DECODE_NOALLOC_SCRATCH_BYTES) + " bytes");
+      FI_REQUIRE(ctx->noalloc_scratch != nullptr, FI_ERR_RUNTIME,
+                 "fi_attn_decode_paged_noalloc: the context has no scratch address");
+      args.part_acc = static_cast<float*>(ctx->noalloc_scratch);
+      args.part_ml = reinterpret_cast<float*>(static_cast<char*>(ctx->noalloc_scratch) + acc_bytes);
+    } else {
+      FI_TRY(fi::decode_scratch(ctx, num_seqs, num_q_heads, parts, head_dim, &args.part_acc, &args.part_ml));
+    }
   }
   const unsigned grid = static_cast<unsigned>(num_seqs) * num_kv_heads * parts;
   switch (head_dim) {
@@ -684,6 +734,32 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
     default:
       return launch_decode_dtype<128>(ctx, kv_dtype, args, grid, wt);
   }
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                             const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
+                             int32_t max_blocks_per_seq, const int32_t* d_context_lens,
+                             int32_t num_seqs, int32_t max_context_len, int32_t num_q_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             int32_t num_blocks, float scale, float* d_out) {
+  return decode_paged(ctx, d_q, d_k_cache, d_v_cache, kv_dtype, d_block_tables, max_blocks_per_seq,
+                      d_context_lens, num_seqs, max_context_len, num_q_heads, num_kv_heads, head_dim,
+                      block_size, num_blocks, scale, d_out, false);
+}
+
+int32_t fi_attn_decode_paged_noalloc(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                                     const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
+                                     int32_t max_blocks_per_seq, const int32_t* d_context_lens,
+                                     int32_t num_seqs, int32_t max_context_len, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int32_t num_blocks, float scale, float* d_out) {
+  return decode_paged(ctx, d_q, d_k_cache, d_v_cache, kv_dtype, d_block_tables, max_blocks_per_seq,
+                      d_context_lens, num_seqs, max_context_len, num_q_heads, num_kv_heads, head_dim,
+                      block_size, num_blocks, scale, d_out, true);
 }
 
 }  // extern "C"

@@ -26,6 +26,7 @@ struct fi_context {
   void* workspace = nullptr;     // grow-only scratch for split-KV partials
   size_t workspace_bytes = 0;
   int compute_units = 0;
+  void* noalloc_scratch = nullptr;  // this device's address of the library's fixed decode scratch array
 };
 
 namespace fi {
@@ -42,6 +43,10 @@ int32_t enter(fi_context* ctx);
 
 // Ensures ctx->workspace holds at least `bytes` (grow-only; never shrinks).
 int32_t ensure_workspace(fi_context* ctx, size_t bytes);
+
+// Looks up (once per device, with ctx's device current) the device address of the fixed
+// split-KV scratch array used by fi_attn_decode_paged_noalloc and stores it in ctx.
+int32_t decode_noalloc_attach(fi_context* ctx);
 
 // Split-KV decode partials for the given launch shape.
 int32_t decode_scratch(fi_context* ctx, int32_t num_seqs, int32_t hq, int32_t parts, int32_t head_dim,

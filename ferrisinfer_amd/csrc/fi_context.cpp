@@ -84,6 +84,13 @@ int32_t fi_ctx_create(int32_t ordinal, fi_context** out) {
     delete ctx;
     return fi::hip_error(err, "hipMalloc(fault flags)");
   }
+  int32_t st = fi::decode_noalloc_attach(ctx);
+  if (st != FI_OK) {
+    (void)hipFree(ctx->d_faults);
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return st;
+  }
   *out = ctx;
   return FI_OK;
 }

@@ -59,6 +59,8 @@ _SIGNATURES = {
     "fi_kv_copy_blocks": [_P, _P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
     "fi_attn_decode_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                              _I32, _F32, _P],
+    "fi_attn_decode_paged_noalloc": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32,
+                                     _I32, _I32, _F32, _P],
     "fi_attn_prefill_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32,
                               _I32, _I32, _F32, _P],
     "fi_rms_norm": [_P, _P, _P, _P, _I32, _I32, _F32],
@@ -227,6 +229,17 @@ class Context:
                                             ptr(context_lens), num_seqs, int(max_context_len),
                                             num_q_heads, num_kv_heads, head_dim, block_size,
                                             num_blocks, float(scale), ptr(out)))
+
+    def attn_decode_paged_noalloc(self, q, k_cache, v_cache, kv_dtype, block_tables, context_lens,
+                                  max_context_len, num_kv_heads, block_size, num_blocks, scale, out):
+        """attn_decode_paged with the partials in the library's fixed scratch (no allocation)."""
+        num_seqs, num_q_heads, head_dim = q.shape
+        check(self.lib.fi_attn_decode_paged_noalloc(self.handle, ptr(q), ptr(k_cache), ptr(v_cache),
+                                                    kv_dtype, ptr(block_tables),
+                                                    int(block_tables.shape[1]), ptr(context_lens),
+                                                    num_seqs, int(max_context_len), num_q_heads,
+                                                    num_kv_heads, head_dim, block_size, num_blocks,
+                                                    float(scale), ptr(out)))
 
     def embedding(self, table, ids, out):
         check(self.lib.fi_embedding(self.handle, ptr(table), int(table.shape[0]),

@@ -149,6 +149,22 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                              int32_t num_blocks, float scale, float* d_out);
 
+/* fi_attn_decode_paged without any allocation: the same kernels, same arguments and bit-identical
+ * outputs, with the split-KV partials in a fixed device array of this library (96 MiB per GPU,
+ * held from the library's first use of the decode kernels on that GPU until the process ends)
+ * instead of the grow-only context workspace.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  A launch whose partials (num_seqs * Hq * ceil(max_context_len /
+ * partition) * (D + 2) * 4 bytes, when it has more than one partition) exceed the array is rejected
+ * as Runtime.  Every call on one GPU shares the array, so calls that overlap on one GPU (several
+ * streams or contexts) race; calls on one stream are ordered. */
+int32_t fi_attn_decode_paged_noalloc(fi_context* ctx, const float* d_q, const void* d_k_cache,
+                                     const void* d_v_cache, int32_t kv_dtype, const int32_t* d_block_tables,
+                                     int32_t max_blocks_per_seq, const int32_t* d_context_lens,
+                                     int32_t num_seqs, int32_t max_context_len, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int32_t num_blocks, float scale, float* d_out);
+
 /* Varlen causal prefill attention over the paged pool (MFMA).  Sequence b contributes
  * qlen_b = cu_seqlens[b+1] - cu_seqlens[b] query rows of q/out [T, Hq, D] at positions
  * [context_lens[b] - qlen_b, context_lens[b]); each attends keys [0, position] read through
