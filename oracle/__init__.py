@@ -6,8 +6,11 @@ file:line it follows.  Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``
 ``cpu_baseline`` leg may import this module, and only as the checker or the timed CPU
 baseline.  The product path (ferrisinfer_amd) never imports it.
 
-Parity pinning of every oracle function is listed in tests/test_oracle_golden.py (reference
-known-answer vectors) and tests/test_oracle_invariants.py (closed forms / brute force).
+Parity pinning: tests/test_oracle_golden.py (the reference's known-answer vectors),
+tests/test_oracle_reference_units.py (the reference's own unit tests of the scheduler, prefix
+index, prefix block manager, sequence state, session and KV cache, run against this
+restatement) and tests/test_oracle_invariants.py (closed forms and f64 brute force: RoPE
+angles, norms and pairing, attention, softmax, RMSNorm, SwiGLU, the greedy head).
 """
 from __future__ import annotations
 
@@ -598,3 +601,369 @@ class Scheduler:
         _check(lib().orc_scheduler_block_ref_count(self.h, owner, layer, block, C.byref(out)),
                True)
         return int(out.value)
+
+
+# ----------------------------------------------------------------- runtime units, one at a time
+# (oracle_units_capi.cpp): the prefix index, prefix block manager, sequence state and KV cache
+# on their own, so the reference's unit tests run against the restatement directly.
+_UNITS_READY = False
+
+FINISH_REASONS = {-1: None, 0: "StopToken", 1: "MaxNewTokens", 2: "SessionLimit", 3: "SequenceLength",
+                  4: "Cancelled"}
+PHASES = {0: "Prefill", 1: "Decode", 2: "Finished"}
+BATCH_KINDS = {0: "Prefill", 1: "Decode"}
+
+
+def _units():
+    global _UNITS_READY
+    L = lib()
+    if _UNITS_READY:
+        return L
+    U32 = C.c_uint32
+    P = C.POINTER
+    sigs = {
+        "orc_units_last_error": ([], C.c_char_p),
+        "orc_prefix_index_create": ([I64], VP),
+        "orc_prefix_index_destroy": ([VP], None),
+        "orc_prefix_index_upsert": ([VP, C.c_uint64, U32P, I64, I64, I64], C.c_int32),
+        "orc_prefix_index_best_match": ([VP, C.c_uint64, U32P, I64, P(C.c_int32), P(C.c_uint64), P(I64)],
+                                        C.c_int32),
+        "orc_block_manager_create": ([], VP),
+        "orc_block_manager_destroy": ([VP], None),
+        "orc_block_manager_update_owned": ([VP, C.c_uint64, C.c_int32, I64, I64, I64, I64P, I64P, I64P, I64,
+                                            P(I64)], C.c_int32),
+        "orc_block_manager_update_shared": ([VP, C.c_uint64, C.c_int32, C.c_uint64, I64, I64, I64, I64P, I64P,
+                                             I64P, I64, P(I64)], C.c_int32),
+        "orc_block_manager_remove": ([VP, C.c_uint64, I64P, I64, P(I64)], C.c_int32),
+        "orc_block_manager_ref_count": ([VP, C.c_uint64, I64, I64], I64),
+        "orc_block_manager_tracked": ([VP], I64),
+        "orc_block_manager_prefixes": ([VP, C.c_uint64, P(C.c_int32), P(C.c_uint64)], C.c_int32),
+        "orc_sequence_create": ([C.c_uint64, C.c_uint64, U32P, I64, I64, I64, I64], VP),
+        "orc_sequence_destroy": ([VP], None),
+        "orc_sequence_record_prefill": ([VP, I64], None),
+        "orc_sequence_record_generated": ([VP, U32], None),
+        "orc_sequence_finish": ([VP, C.c_int32], None),
+        "orc_sequence_query": ([VP, I64P], None),
+        "orc_sequence_generated": ([VP, U32P, I64], I64),
+        "orc_sequence_next_chunk": ([VP, I64, U32P, I64], I64),
+        "orc_kvcache_create": ([I64] * 5, VP),
+        "orc_kvcache_destroy": ([VP], None),
+        "orc_kvcache_reserve_slot": ([VP, P(I64)], C.c_int32),
+        "orc_kvcache_advance": ([VP, I64], C.c_int32),
+        "orc_kvcache_write": ([VP, I64, I64, F32P, F32P], C.c_int32),
+        "orc_kvcache_write_uncommitted": ([VP, I64, I64, F32P, F32P], C.c_int32),
+        "orc_kvcache_write_sequence_uncommitted": ([VP, I64, I64, I64, F32P, F32P], C.c_int32),
+        "orc_kvcache_read_prefix": ([VP, I64, I64, F32P, F32P], C.c_int32),
+        "orc_kvcache_counts": ([VP, I64P], None),
+        "orc_kvcache_reset": ([VP], None),
+        "orc_kvcache_prefix_handle": ([VP, I64, P(C.c_int32), I64P, I64P, I64, I64P, I64], C.c_int32),
+        "orc_kvcache_copy_prefix_from": ([VP, VP, I64], C.c_int32),
+        "orc_session_history": ([VP, U32P, I64, P(I64)], C.c_int32),
+        "orc_session_kv_counts": ([VP, I64P], None),
+        "orc_session_prefix_handle": ([VP, I64, P(C.c_int32), I64P, I64P, I64, I64P, I64], C.c_int32),
+        "orc_session_generate": ([VP, U32P, I64, I64, I64, U32P, F32P, I64, P(I64), P(C.c_int32)], C.c_int32),
+        "orc_scheduler_plan": ([VP, P(C.c_int32), P(C.c_int32), np.ctypeslib.ndpointer(np.uint64), I64, P(I64)],
+                               C.c_int32),
+        "orc_scheduler_sequence": ([VP, C.c_uint64, I64P], C.c_int32),
+        "orc_scheduler_resident_sessions": ([VP], I64),
+        "orc_scheduler_shared_prefix": ([VP, C.c_uint64, P(C.c_int32), P(C.c_uint64)], C.c_int32),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _UNITS_READY = True
+    return L
+
+
+def _ucheck(status: int):
+    if status != 0:
+        raise OracleError(status, (_units().orc_units_last_error() or b"").decode())
+
+
+def _ids(tokens) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+
+
+def _flatten_handle(handle: dict):
+    """handle = {token_count, page_size, layers: [[(logical, block_id, start, count), ...], ...]}"""
+    layers = handle["layers"]
+    counts = np.array([len(l) for l in layers] or [0], np.int64)
+    rows = [e for l in layers for e in l]
+    entries = np.array(rows or [(0, 0, 0, 0)], np.int64).reshape(-1, 4)
+    return handle["token_count"], handle["page_size"], len(layers), counts, np.ascontiguousarray(entries)
+
+
+def _read_handle(fn, *args):
+    has = C.c_int32()
+    header = np.zeros(3, np.int64)
+    counts = np.zeros(256, np.int64)
+    entries = np.zeros((1 << 14, 4), np.int64)
+    _ucheck(fn(*args, C.byref(has), header, counts, counts.size, entries, entries.shape[0]))
+    if not has.value:
+        return None
+    layers, k = [], 0
+    for l in range(int(header[2])):
+        n = int(counts[l])
+        layers.append([tuple(int(x) for x in entries[k + i]) for i in range(n)])
+        k += n
+    return {"token_count": int(header[0]), "page_size": int(header[1]), "layers": layers}
+
+
+def _released(buf, n):
+    return [tuple(int(x) for x in buf[i]) for i in range(n)]
+
+
+class PrefixIndex:
+    """runtime/prefix_index.rs:24-113."""
+
+    def __init__(self, min_prefix_share_tokens: int):
+        self.h = _units().orc_prefix_index_create(min_prefix_share_tokens)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _units().orc_prefix_index_destroy(self.h)
+            self.h = None
+
+    def upsert(self, sequence_id, prompt_tokens, cached_prompt_tokens, session_position):
+        t = _ids(prompt_tokens)
+        _ucheck(_units().orc_prefix_index_upsert(self.h, sequence_id, t, t.size, cached_prompt_tokens,
+                                                 session_position))
+
+    def best_match(self, target_sequence_id, target_prompt_tokens):
+        """(sequence_id, shared_prefix_tokens) or None."""
+        t = _ids(target_prompt_tokens)
+        found, seq, shared = C.c_int32(), C.c_uint64(), I64()
+        _ucheck(_units().orc_prefix_index_best_match(self.h, target_sequence_id, t, t.size, C.byref(found),
+                                                     C.byref(seq), C.byref(shared)))
+        return (int(seq.value), int(shared.value)) if found.value else None
+
+
+class PrefixBlockManager:
+    """runtime/block_manager.rs:58-172; released blocks are (owner, layer, block_id)."""
+
+    def __init__(self):
+        self.h = _units().orc_block_manager_create()
+        self._buf = np.zeros((1 << 14, 3), np.int64)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _units().orc_block_manager_destroy(self.h)
+            self.h = None
+
+    def update_owned_prefix(self, sequence_id, handle):
+        n = I64()
+        if handle is None:
+            z = np.zeros(1, np.int64)
+            _ucheck(_units().orc_block_manager_update_owned(self.h, sequence_id, 0, 0, 0, 0, z,
+                                                            np.zeros((1, 4), np.int64), self._buf,
+                                                            self._buf.shape[0], C.byref(n)))
+        else:
+            tc, ps, nl, counts, entries = _flatten_handle(handle)
+            _ucheck(_units().orc_block_manager_update_owned(self.h, sequence_id, 1, tc, ps, nl, counts, entries,
+                                                            self._buf, self._buf.shape[0], C.byref(n)))
+        return _released(self._buf, n.value)
+
+    def update_shared_prefix(self, sequence_id, assignment):
+        """assignment = None or (source_sequence_id, handle)."""
+        n = I64()
+        if assignment is None:
+            _ucheck(_units().orc_block_manager_update_shared(self.h, sequence_id, 0, 0, 0, 0, 0,
+                                                             np.zeros(1, np.int64), np.zeros((1, 4), np.int64),
+                                                             self._buf, self._buf.shape[0], C.byref(n)))
+        else:
+            source, handle = assignment
+            tc, ps, nl, counts, entries = _flatten_handle(handle)
+            _ucheck(_units().orc_block_manager_update_shared(self.h, sequence_id, 1, source, tc, ps, nl, counts,
+                                                             entries, self._buf, self._buf.shape[0], C.byref(n)))
+        return _released(self._buf, n.value)
+
+    def remove_sequence(self, sequence_id):
+        n = I64()
+        _ucheck(_units().orc_block_manager_remove(self.h, sequence_id, self._buf, self._buf.shape[0], C.byref(n)))
+        return _released(self._buf, n.value)
+
+    def block_ref_count(self, owner, layer, block_id):
+        return int(_units().orc_block_manager_ref_count(self.h, owner, layer, block_id))
+
+    def tracked_block_count(self):
+        return int(_units().orc_block_manager_tracked(self.h))
+
+    def prefixes(self, sequence_id):
+        """(has owned prefix, shared prefix source or None)."""
+        flags, source = C.c_int32(), C.c_uint64()
+        _ucheck(_units().orc_block_manager_prefixes(self.h, sequence_id, C.byref(flags), C.byref(source)))
+        return bool(flags.value & 1), (int(source.value) if flags.value & 2 else None)
+
+
+class SequenceState:
+    """runtime/sequence.rs:43-205 (new / with_generation_budget)."""
+
+    _FIELDS = ("request_id", "sequence_id", "prompt_len", "generated_len", "cached_tokens",
+               "cached_prompt_tokens", "pending_prompt_tokens", "requested_max_new_tokens", "max_new_tokens",
+               "stop_token_id", "phase", "finish_reason", "is_finished", "generation_budget_reached",
+               "generation_budget_finish_reason", "total_tokens")
+
+    def __init__(self, request_id, sequence_id, prompt_tokens, max_new_tokens, stop_token_id=None,
+                 generation_budget=None):
+        t = _ids(prompt_tokens)
+        budget = max_new_tokens if generation_budget is None else generation_budget
+        self.h = _units().orc_sequence_create(request_id, sequence_id, t, t.size, max_new_tokens, budget,
+                                              -1 if stop_token_id is None else stop_token_id)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _units().orc_sequence_destroy(self.h)
+            self.h = None
+
+    def state(self) -> dict:
+        f = np.zeros(16, np.int64)
+        _units().orc_sequence_query(self.h, f)
+        d = dict(zip(self._FIELDS, (int(x) for x in f)))
+        d["stop_token_id"] = None if d["stop_token_id"] < 0 else d["stop_token_id"]
+        d["phase"] = PHASES[d["phase"]]
+        d["finish_reason"] = FINISH_REASONS[d["finish_reason"]]
+        d["generation_budget_finish_reason"] = FINISH_REASONS[d["generation_budget_finish_reason"]]
+        d["is_finished"] = bool(d["is_finished"])
+        d["generation_budget_reached"] = bool(d["generation_budget_reached"])
+        return d
+
+    def generated_tokens(self):
+        out = np.zeros(1 << 12, np.uint32)
+        n = _units().orc_sequence_generated(self.h, out, out.size)
+        return [int(x) for x in out[:n]]
+
+    def next_prefill_chunk(self, max_chunk_tokens):
+        out = np.zeros(max(max_chunk_tokens, 1), np.uint32)
+        n = _units().orc_sequence_next_chunk(self.h, max_chunk_tokens, out, out.size)
+        return [int(x) for x in out[:n]]
+
+    def record_prefill(self, appended):
+        _units().orc_sequence_record_prefill(self.h, appended)
+
+    def record_generated_token(self, token):
+        _units().orc_sequence_record_generated(self.h, token)
+
+    def finish(self, reason: str):
+        code = {v: k for k, v in FINISH_REASONS.items()}[reason]
+        _units().orc_sequence_finish(self.h, code)
+
+
+class KvCache:
+    """runtime/kv_cache.rs:359-597: contiguous (page_size 0) or paged storage."""
+
+    def __init__(self, layers, kv_heads, head_dim, max_seq, page_size=0):
+        self.h = _units().orc_kvcache_create(layers, kv_heads, head_dim, max_seq, page_size)
+        if not self.h:
+            raise OracleError(6, (_units().orc_units_last_error() or b"").decode())
+        self.kv_heads, self.head_dim = kv_heads, head_dim
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _units().orc_kvcache_destroy(self.h)
+            self.h = None
+
+    def counts(self) -> dict:
+        c = np.zeros(5, np.int64)
+        _units().orc_kvcache_counts(self.h, c)
+        return dict(used_tokens=int(c[0]), remaining_tokens=int(c[1]), paged=bool(c[2]), layers=int(c[3]),
+                    layer_elements=int(c[4]))
+
+    def reserve_slot(self):
+        pos = I64()
+        _ucheck(_units().orc_kvcache_reserve_slot(self.h, C.byref(pos)))
+        return int(pos.value)
+
+    def advance(self, n):
+        _ucheck(_units().orc_kvcache_advance(self.h, n))
+
+    def reset(self):
+        _units().orc_kvcache_reset(self.h)
+
+    def write(self, layer, position, key, value):
+        _ucheck(_units().orc_kvcache_write(self.h, layer, position, f32(key).reshape(-1), f32(value).reshape(-1)))
+
+    def write_uncommitted(self, layer, position, key, value):
+        _ucheck(_units().orc_kvcache_write_uncommitted(self.h, layer, position, f32(key).reshape(-1),
+                                                       f32(value).reshape(-1)))
+
+    def write_sequence_uncommitted(self, layer, start, keys, values):
+        k, v = f32(keys), f32(values)
+        n = k.size // (self.kv_heads * self.head_dim)
+        _ucheck(_units().orc_kvcache_write_sequence_uncommitted(self.h, layer, start, n, k.reshape(-1),
+                                                                v.reshape(-1)))
+
+    def read_prefix(self, layer, length):
+        k = np.zeros((length, self.kv_heads, self.head_dim), np.float32)
+        v = np.zeros_like(k)
+        _ucheck(_units().orc_kvcache_read_prefix(self.h, layer, length, k.reshape(-1), v.reshape(-1)))
+        return k, v
+
+    def prefix_handle(self, token_count):
+        return _read_handle(_units().orc_kvcache_prefix_handle, self.h, token_count)
+
+    def copy_prefix_from(self, source: "KvCache", token_count):
+        _ucheck(_units().orc_kvcache_copy_prefix_from(self.h, source.h, token_count))
+
+
+def session_token_history(session: Session):
+    out = np.zeros(1 << 16, np.uint32)
+    n = I64()
+    _ucheck(_units().orc_session_history(session.h, out, out.size, C.byref(n)))
+    return [int(x) for x in out[: n.value]]
+
+
+def session_kv_used_tokens(session: Session) -> int:
+    c = np.zeros(2, np.int64)
+    _units().orc_session_kv_counts(session.h, c)
+    return int(c[0])
+
+
+def session_kv_is_paged(session: Session) -> bool:
+    c = np.zeros(2, np.int64)
+    _units().orc_session_kv_counts(session.h, c)
+    return bool(c[1])
+
+
+def session_prefix_handle(session: Session, token_count: int):
+    return _read_handle(_units().orc_session_prefix_handle, session.h, token_count)
+
+
+def session_generate_from_tokens(session: Session, prompt, max_new_tokens, stop_token_id=None):
+    """Session::generate_reference_from_tokens (session.rs:276-331): ([(token, prob)], finish)."""
+    t = _ids(prompt)
+    cap = max(int(max_new_tokens), 1)
+    toks = np.zeros(cap, np.uint32)
+    probs = np.zeros(cap, np.float32)
+    n, finish = I64(), C.c_int32()
+    _ucheck(_units().orc_session_generate(session.h, t, t.size, max_new_tokens,
+                                          -1 if stop_token_id is None else stop_token_id, toks, probs, cap,
+                                          C.byref(n), C.byref(finish)))
+    return [(int(toks[i]), float(probs[i])) for i in range(n.value)], FINISH_REASONS[finish.value]
+
+
+def scheduler_plan_next_tick(sched: Scheduler):
+    """ReferenceScheduler::plan_next_tick: None or (batch kind, [sequence ids])."""
+    has, kind, n = C.c_int32(), C.c_int32(), I64()
+    ids = np.zeros(4096, np.uint64)
+    _ucheck(_units().orc_scheduler_plan(sched.h, C.byref(has), C.byref(kind), ids, ids.size, C.byref(n)))
+    if not has.value:
+        return None
+    return BATCH_KINDS[kind.value], [int(x) for x in ids[: n.value]]
+
+
+def scheduler_sequence_state(sched: Scheduler, seq: int) -> dict:
+    out = np.zeros(5, np.int64)
+    _ucheck(_units().orc_scheduler_sequence(sched.h, seq, out))
+    return dict(phase=PHASES[int(out[0])], finish_reason=FINISH_REASONS[int(out[1])], cached_tokens=int(out[2]),
+                generated_len=int(out[3]), has_session=bool(out[4]))
+
+
+def scheduler_resident_session_count(sched: Scheduler) -> int:
+    return int(_units().orc_scheduler_resident_sessions(sched.h))
+
+
+def scheduler_shared_prefix_source(sched: Scheduler, seq: int):
+    has, source = C.c_int32(), C.c_uint64()
+    _ucheck(_units().orc_scheduler_shared_prefix(sched.h, seq, C.byref(has), C.byref(source)))
+    return int(source.value) if has.value else None

@@ -324,6 +324,24 @@ void KvCache::advance(size_t tokens) {
   used_tokens_ = next;
 }
 
+size_t KvCache::reserve_slot() {
+  size_t position = used_tokens_;
+  advance(1);
+  return position;
+}
+
+void KvCache::write(size_t layer, size_t position, const float* key, const float* value) {
+  if (position >= used_tokens_) {
+    fail(ErrorKind::InvalidShape, "KV cache position " + std::to_string(position) +
+                                      " has not been reserved yet; committed tokens " + std::to_string(used_tokens_));
+  }
+  if (paged_) {
+    paged_->write_slot(layer, position, key, value);
+  } else {
+    contiguous_->write_slot(layer, position, key, value);
+  }
+}
+
 void KvCache::write_uncommitted(size_t layer, size_t position, const float* key,
                                 const float* value) {
   if (position > used_tokens_) {
@@ -721,6 +739,29 @@ TokenSample Session::step_reference() {
   return s;
 }
 
+std::vector<TokenSample> Session::generate_from_tokens(const std::vector<uint32_t>& prompt, size_t max_new_tokens,
+                                                       std::optional<uint32_t> stop_token, FinishReason* finish) {
+  reset();
+  prefill_tokens(prompt);
+  const size_t budget = std::min(max_new_tokens, config_.max_generated_tokens);
+  FinishReason reason = budget < max_new_tokens ? FinishReason::SessionLimit : FinishReason::MaxNewTokens;
+  std::vector<TokenSample> out;
+  for (size_t i = 0; i < budget; ++i) {
+    if (position_ >= config_.max_sequence_length) {
+      reason = FinishReason::SequenceLength;
+      break;
+    }
+    TokenSample s = step_reference();
+    out.push_back(s);
+    if (stop_token && *stop_token == s.token_id) {
+      reason = FinishReason::StopToken;
+      break;
+    }
+  }
+  *finish = reason;
+  return out;
+}
+
 void Session::process_token(uint32_t token) {
   if (position_ >= config_.max_sequence_length) fail(ErrorKind::Runtime, "cannot process tokens beyond max sequence length");
   if (position_ != kv_.used_tokens()) fail(ErrorKind::Runtime, "session position and KV cache usage diverged");
@@ -912,6 +953,12 @@ const Session* ReferenceScheduler::session(uint64_t seq) const {
     if (e.state.sequence_id == seq) return e.session.get();
   }
   return nullptr;
+}
+
+size_t ReferenceScheduler::resident_session_count() const {
+  size_t n = 0;
+  for (const auto& e : sequences_) n += e.session ? 1 : 0;
+  return n;
 }
 
 bool ReferenceScheduler::has_pending() const {

@@ -122,6 +122,10 @@ class KvCache {
   size_t remaining_tokens() const;
   void reset();
   void advance(size_t tokens);
+  // kv_cache.rs:419-423: the next position, committed at once.
+  size_t reserve_slot();
+  // kv_cache.rs:441-451: a write at a committed position only (ensure_position_committed).
+  void write(size_t layer, size_t position, const float* key, const float* value);
   void write_uncommitted(size_t layer, size_t position, const float* key, const float* value);
   void write_sequence_uncommitted(size_t layer, size_t start, size_t seq_len, const float* key,
                                   const float* value);
@@ -178,6 +182,8 @@ struct TokenSample {
   float probability;
 };
 
+enum class FinishReason : int32_t;
+
 // ---- runtime/reference.rs model drivers ----
 // Full-sequence logits [T, V] (reference.rs:517-524).
 std::vector<float> decoder_model_forward(const Model& m, const std::vector<uint32_t>& ids);
@@ -226,6 +232,11 @@ class Session {
   void reset();
   void prefill_tokens(const std::vector<uint32_t>& ids);
   TokenSample step_reference();
+  // session.rs:262-331 generate_reference_from_tokens: reset, prefill the prompt, then step up
+  // to min(max_new_tokens, max_generated_tokens) times, stopping at the stop token or at the
+  // sequence length.  Returns the generated samples and the finish reason.
+  std::vector<TokenSample> generate_from_tokens(const std::vector<uint32_t>& prompt, size_t max_new_tokens,
+                                                std::optional<uint32_t> stop_token, FinishReason* finish);
   // Logits of the last processed position, recomputed by the logits path (parity aid).
   std::vector<float> last_hidden() const { return last_hidden_; }
 
@@ -272,6 +283,13 @@ struct SequenceState {
   size_t next_prefill_chunk_len(size_t max_chunk) const {
     return std::min(pending_prompt_tokens(), max_chunk);
   }
+  // sequence.rs:135-139
+  std::vector<uint32_t> next_prefill_chunk(size_t max_chunk) const {
+    size_t start = cached_prompt_tokens();
+    return std::vector<uint32_t>(prompt.begin() + start, prompt.begin() + start + next_prefill_chunk_len(max_chunk));
+  }
+  bool is_finished() const { return phase == SequencePhase::Finished; }
+  size_t total_tokens() const { return prompt.size() + generated.size(); }
   bool generation_budget_reached() const { return generated.size() >= max_new_tokens; }
   FinishReason generation_budget_finish_reason() const {
     return requested_max_new_tokens > max_new_tokens ? FinishReason::SessionLimit
@@ -388,6 +406,8 @@ class ReferenceScheduler {
   std::optional<SchedulerTick> plan_next_tick() const;
   std::optional<SchedulerReport> execute_next_tick();
   bool has_pending() const;
+  // scheduler.rs:184-189: sequences still holding a session.
+  size_t resident_session_count() const;
   const SequenceState* sequence_state(uint64_t seq) const;
   const Session* session(uint64_t seq) const;
   const PrefixBlockManager& block_manager() const { return block_manager_; }

@@ -5,7 +5,7 @@
 #include <memory>
 #include <string>
 
-#include "oracle_runtime.h"
+#include "oracle_handles.h"
 
 using namespace orc;
 
@@ -105,9 +105,6 @@ int32_t orc_paged_kv_import_prefix(void* dst, const void* src, int64_t tokens) {
 }
 
 // ---------------------------------------------------------------- model
-struct OrcModel {
-  std::shared_ptr<Model> model;
-};
 
 void* orc_model_create(int64_t hidden, int64_t intermediate, int64_t layers, int64_t heads,
                        int64_t kv_heads, int64_t vocab, int64_t max_pos, float eps, float theta,
@@ -146,9 +143,6 @@ int32_t orc_model_forward_logits(void* m, const uint32_t* ids, int64_t n, float*
 }
 
 // ---------------------------------------------------------------- session
-struct OrcSession {
-  std::unique_ptr<Session> session;
-};
 void* orc_session_create(void* m, int64_t max_seq, int64_t max_gen, int64_t page_size) {
   OrcSession* s = nullptr;
   guard([&] {
@@ -214,12 +208,6 @@ int32_t orc_session_read_prefix(void* s, int64_t layer, int64_t len, float* k, f
 }
 
 // ---------------------------------------------------------------- scheduler
-struct OrcScheduler {
-  std::unique_ptr<ReferenceScheduler> sched;
-  std::optional<SchedulerReport> last;
-  std::unique_ptr<GlobalPagePacker> packer;
-  PackedTick packed;
-};
 void* orc_scheduler_create(void* m, int64_t max_seq, int64_t max_gen, int64_t page_size,
                            int64_t max_batch, int64_t max_chunk, int64_t max_batch_tokens,
                            int64_t max_consecutive_prefill, int64_t min_share) {

@@ -32,7 +32,7 @@ PACK_KEYS = ("positions", "slot_mapping", "cu_seqlens", "context_lens", "block_t
              "copy_src", "copy_dst", "copy_count", "sequence_ids")
 
 
-def drive(sched, requests, packs=None):
+def drive(sched, requests, packs=None, after_tick=None):
     ids = [sched.submit(p, max_new_tokens=n) for p, n in requests]
     ticks = []
     while True:
@@ -42,8 +42,47 @@ def drive(sched, requests, packs=None):
         ticks.append(t)
         if packs is not None:
             packs.append(sched.packed() if hasattr(sched, "packed") else sched.last_batch())
+        if after_tick is not None:
+            after_tick(ids)
         assert len(ticks) < 10000
     return ids, ticks
+
+
+def oracle_pages_are_logical(ref, requests):
+    """After-tick hook for the oracle scheduler: every live sequence's own paged storage holds
+    logical block i in page i (a fresh or imported per-sequence storage hands pages out of its
+    LIFO list [n-1 .. 0] in logical order, runtime/paged_kv.rs:329-389, 469-527, 794-796), so the
+    block ids of the oracle's released lists are logical block indices."""
+    def check(ids):
+        for seq, (prompt, _) in zip(ids, requests):
+            tokens = min(orc_cached_tokens(ref, seq), len(prompt))
+            if tokens == 0:
+                continue
+            pages = ref.session_blocks(seq, 0, tokens)
+            if pages is not None:
+                assert pages == list(range(len(pages))), (seq, pages)
+    return check
+
+
+def orc_cached_tokens(ref, seq):
+    from oracle import scheduler_sequence_state
+
+    return scheduler_sequence_state(ref, seq)["cached_tokens"]
+
+
+def gpu_released_as_logical(gticks, gpacks, block_size=16):
+    """The GPU runtime's released (owner, layer, pool block id) entries mapped to (owner, layer,
+    logical block index) through the owner's block table as packed up to that tick."""
+    tables, out = {}, []
+    for (_, updates), pack in zip(gticks, gpacks):
+        for i, seq in enumerate(pack["sequence_ids"]):
+            n = (int(pack["context_lens"][i]) + block_size - 1) // block_size
+            tables[int(seq)] = [int(b) for b in pack["block_tables"][i][:n]]
+        tick = []
+        for u in updates:
+            tick.append([(o, l, tables[o].index(b)) for o, l, b in u["released"]])
+        out.append(tick)
+    return out
 
 
 def near_tie(model, history, vocab):
@@ -54,7 +93,7 @@ def near_tie(model, history, vocab):
 
 def compare(model, ref, gpu, requests):
     rpacks, gpacks = [], []
-    rid, rticks = drive(ref, requests, rpacks)
+    rid, rticks = drive(ref, requests, rpacks, after_tick=oracle_pages_are_logical(ref, requests))
     gid, gticks = drive(gpu, requests, gpacks)
     assert rid == gid
     assert len(rticks) == len(gticks)
@@ -62,13 +101,15 @@ def compare(model, ref, gpu, requests):
         assert a["kind"] == b["kind"], i
         for key in PACK_KEYS:
             assert np.array_equal(a[key], b[key]), (i, key, a[key], b[key])
-    for (rk, ru), (gk, gu) in zip(rticks, gticks):
+    g_released = gpu_released_as_logical(gticks, gpacks)
+    for t, ((rk, ru), (gk, gu)) in enumerate(zip(rticks, gticks)):
         assert rk == gk
         assert [u["sequence_id"] for u in ru] == [u["sequence_id"] for u in gu]
-        for a, b in zip(ru, gu):
+        for j, (a, b) in enumerate(zip(ru, gu)):
             for key in ("batch_kind", "reused", "appended", "phase", "finish_reason"):
                 assert a[key] == b[key], (key, a, b)
-            assert len(a["released"]) == len(b["released"])
+            # released prefix blocks: same owners, layers, logical blocks and order
+            assert a["released"] == g_released[t][j], (t, a["released"], g_released[t][j])
             assert (a["token"] is None) == (b["token"] is None)
     ties = 0
     for seq, (prompt, _) in zip(rid, requests):
