@@ -98,6 +98,23 @@ def test_decode_c2_full_size(orc, gpu_ctx, kv_dtype):
     assert err <= (F32_TOL if kv_dtype == "f32" else BF16_TOL), err
 
 
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_decode_c5_context_range(orc, gpu_ctx, kv_dtype):
+    """BASELINE config C5's decode attention range: contexts up to 8192 (8 to 16 partitions of
+    512 tokens through the split-KV merge), Hq 32 / Hkv 8 / D 128, 10 sequences."""
+    import torch
+
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    print(f"decode C5 context range dtype={kv_dtype}", flush=True)
+    wl = paged_decode_c2(seed=7, num_seqs=10, min_len=4000, max_len=8192, num_blocks=5200)
+    assert wl.max_context_len > 7680  # the longest sequence spans 16 partitions
+    got = run_decode(gpu_ctx, wl, kv_dtype, torch)
+    ref = oracle_decode(orc, wl, kv_dtype)
+    err = normwise_error(got, ref)
+    assert err <= F32_TOL, err  # bf16: the oracle attends the same widened values
+
+
 def test_decode_batch_invariance(gpu_ctx):
     """A sequence's output does not depend on the batch around it (bit-identical)."""
     import torch

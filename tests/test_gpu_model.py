@@ -319,3 +319,23 @@ def test_c4_qwen2_shape_matches_reference(orc):
             if x != y:
                 assert near_tie(model, list(r["prompt"]) + a[:i], None), (seq, i, x, y)
                 break
+
+
+def test_c4_qwen2_shape_reaches_decode_batch_64(orc):
+    """BASELINE config C4's model (Qwen2-0.5B shape, 24 layers, tied, q/k/v biases) at the
+    headline decode batch: 64 requests of 32-token prompts and 8 new tokens under max_batch 64,
+    so the decode ticks carry all 64 sequences.  Ticks, reports, released blocks and every
+    tick's packing must equal the oracle's; greedy tokens too, except at a reported near tie."""
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, random_weights
+
+    print("C4 shape at decode batch 64", flush=True)
+    cfg = QWEN2_05B_C4
+    weights = random_weights(cfg, seed=0, qkv_bias=True)
+    rng = np.random.default_rng(64)
+    requests = [(rng.integers(0, cfg["vocab"], 32).astype(np.uint32), 8) for _ in range(64)]
+    model, ref, gpu = build_pair(orc, cfg, weights, dict(max_batch=64, max_seq=64), num_blocks=512)
+    del weights
+    ticks, ties = compare(model, ref, gpu, requests)
+    assert sum(1 for kind, us in ticks if kind == 1 and len(us) == 64) >= 7
+    print(f"C4 batch 64: {len(ticks)} ticks, near ties {ties}", flush=True)
+    assert gpu.pool_free_count() == 512

@@ -140,3 +140,96 @@ def test_prefill_one_token_matches_decode(gpu_ctx):
                                wl.block_size, wl.num_blocks, wl.scale, out_p)
     torch.cuda.synchronize()
     assert normwise_error(out_p.cpu().numpy(), out_d.cpu().numpy()) <= 1e-5
+
+
+def brute_force_f64(q, k, v, start):
+    """f64 causal attention of the rows of q at positions start + t over keys [0, start + t]
+    (the closed form the oracle is pinned to in tests/test_oracle_invariants.py)."""
+    t, hq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    out = np.zeros((t, hq, d), np.float64)
+    n = start + t
+    mask = np.arange(n)[None, :] > (start + np.arange(t))[:, None]
+    for kv in range(hkv):
+        qg = q[:, kv * g:(kv + 1) * g].astype(np.float64).transpose(1, 0, 2)  # [g, t, d]
+        s = qg @ k[:n, kv].astype(np.float64).T / np.sqrt(d)                   # [g, t, n]
+        s[:, mask] = -np.inf
+        s -= s.max(axis=2, keepdims=True)
+        w = np.exp(s)
+        w /= w.sum(axis=2, keepdims=True)
+        out[:, kv * g:(kv + 1) * g] = (w @ v[:n, kv].astype(np.float64)).transpose(1, 0, 2)
+    return out
+
+
+def test_prefill_c5_chunk_after_cached_prefix(orc, gpu_ctx):
+    """BASELINE config C5's prefill chunk: 2048 new tokens after a 2048-token cached prefix
+    (Hq 32 / Hkv 8 / D 128), batched with a ragged 37-token chunk after 1500 cached tokens, on
+    f32 and bf16 pools through fi_attn_prefill_paged and fi_attn_prefill_paged_bf16.  Every row
+    is compared with the f64 closed form (1e-4 f32, 2e-2 bf16 storage) and the first and last 16
+    rows of the long chunk with the oracle's cached-prefixed attention."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+
+    print("prefill C5 chunk 2048 after 2048", flush=True)
+    rng = np.random.default_rng(55)
+    hq, hkv, d, bs = 32, 8, 128, 16
+    ctx_lens = np.array([4096, 1537], np.int32)
+    qlens = np.array([2048, 37], np.int32)
+    nblk = (ctx_lens + bs - 1) // bs
+    num_blocks = 512
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    tables = np.zeros((2, nblk.max()), np.int32)
+    tables[0, :nblk[0]] = perm[:nblk[0]]
+    tables[1, :nblk[1]] = perm[nblk[0]:nblk[0] + nblk[1]]
+    k_seq = [rng.standard_normal((L, hkv, d), dtype=np.float32) for L in ctx_lens]
+    v_seq = [rng.standard_normal((L, hkv, d), dtype=np.float32) for L in ctx_lens]
+    q = rng.standard_normal((int(qlens.sum()), hq, d), dtype=np.float32)
+    cu = np.array([0, qlens[0], qlens.sum()], np.int32)
+    scale = float(1.0 / np.sqrt(np.float32(d)))
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    for kv_dtype in ("f32", "bf16"):
+        pool_k = np.zeros((num_blocks, hkv, bs, d), np.float32)
+        pool_v = np.zeros_like(pool_k)
+        ks, vs = [], []
+        for b in range(2):
+            kb, vb = k_seq[b], v_seq[b]
+            if kv_dtype == "bf16":
+                kb = orc.bf16_to_f32(orc.f32_to_bf16(kb))
+                vb = orc.bf16_to_f32(orc.f32_to_bf16(vb))
+            ks.append(kb)
+            vs.append(vb)
+            for p in range(int(ctx_lens[b])):
+                pool_k[tables[b, p // bs], :, p % bs] = kb[p]
+                pool_v[tables[b, p // bs], :, p % bs] = vb[p]
+        if kv_dtype == "f32":
+            kp, vp, dt = dev(pool_k), dev(pool_v), DTYPE_F32
+        else:
+            kp = dev(orc.f32_to_bf16(pool_k).view(np.int16))
+            vp = dev(orc.f32_to_bf16(pool_v).view(np.int16))
+            dt = DTYPE_BF16
+        refs = [brute_force_f64(q[cu[b]:cu[b + 1]], ks[b], vs[b], int(ctx_lens[b] - qlens[b]))
+                for b in range(2)]
+        ref = np.concatenate(refs)
+        qd, out = dev(q), torch.empty((q.shape[0], hq, d), device="cuda")
+        gpu_ctx.attn_prefill_paged(qd, kp, vp, dt, dev(tables), dev(cu), dev(ctx_lens),
+                                   int(qlens.max()), hkv, bs, num_blocks, scale, out)
+        torch.cuda.synchronize()
+        gpu_ctx.check_faults()
+        got = out.cpu().numpy()
+        assert normwise_error(got, ref) <= 1e-4, (kv_dtype, normwise_error(got, ref))
+        start = int(ctx_lens[0] - qlens[0])
+        for r0 in (0, int(qlens[0]) - 16):
+            o = orc.cached_prefixed_causal_attention(q[r0:r0 + 16], ks[0][:start + r0], vs[0][:start + r0],
+                                                     start + r0, ks[0][start + r0:start + r0 + 16],
+                                                     vs[0][start + r0:start + r0 + 16])
+            assert normwise_error(got[r0:r0 + 16], o) <= 1e-4
+        if kv_dtype == "bf16":
+            gpu_ctx.attn_prefill_paged_bf16(qd, kp, vp, dev(tables), dev(cu), dev(ctx_lens),
+                                            int(qlens.max()), hkv, bs, num_blocks, scale, out)
+            torch.cuda.synchronize()
+            gpu_ctx.check_faults()
+            got16 = out.cpu().numpy()
+            assert normwise_error(got16, ref) <= 2e-2
+            assert normwise_error(got16, got) <= 5e-3
