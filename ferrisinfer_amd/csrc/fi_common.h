@@ -27,6 +27,15 @@ struct fi_context {
   size_t workspace_bytes = 0;
   int compute_units = 0;
   void* noalloc_scratch = nullptr;  // this device's address of the library's fixed decode scratch array
+  uint64_t workspace_generation = 0;  // bumped whenever the workspace is reallocated
+  bool capturing = false;             // the stream is being captured into a graph
+};
+
+// A captured and instantiated launch sequence of one context's stream.
+struct fi_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int device = 0;
 };
 
 namespace fi {

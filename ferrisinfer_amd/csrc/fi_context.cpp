@@ -31,6 +31,11 @@ int32_t enter(fi_context* ctx) {
 
 int32_t ensure_workspace(fi_context* ctx, size_t bytes) {
   if (bytes <= ctx->workspace_bytes) return FI_OK;
+  // A graph being captured would keep the old address; growing is refused instead (the caller
+  // runs the launch once outside capture first, which sizes the workspace).
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME,
+             "the context workspace would grow during graph capture (needs " + std::to_string(bytes) +
+                 " bytes, holds " + std::to_string(ctx->workspace_bytes) + ")");
   if (ctx->workspace != nullptr) {
     // The old workspace may still be read by queued kernels.
     FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
@@ -41,6 +46,7 @@ int32_t ensure_workspace(fi_context* ctx, size_t bytes) {
   size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
   FI_TRY_HIP(hipMalloc(&ctx->workspace, rounded));
   ctx->workspace_bytes = rounded;
+  ctx->workspace_generation += 1;
   return FI_OK;
 }
 
@@ -98,6 +104,11 @@ int32_t fi_ctx_create(int32_t ordinal, fi_context** out) {
 int32_t fi_ctx_destroy(fi_context* ctx) {
   if (ctx == nullptr) return FI_OK;
   FI_TRY(fi::enter(ctx));
+  if (ctx->capturing) {  // a capture left open: end and discard it
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+    ctx->capturing = false;
+  }
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->workspace) (void)hipFree(ctx->workspace);
   if (ctx->d_faults) (void)hipFree(ctx->d_faults);
@@ -108,12 +119,14 @@ int32_t fi_ctx_destroy(fi_context* ctx) {
 
 int32_t fi_ctx_sync(fi_context* ctx) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_ctx_sync: the stream is being captured into a graph");
   FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
   return FI_OK;
 }
 
 int32_t fi_ctx_set_stream(fi_context* ctx, void* stream) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_ctx_set_stream: the stream is being captured");
   ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
   return FI_OK;
 }
@@ -140,6 +153,7 @@ int32_t fi_device_info(fi_context* ctx, char* name, size_t name_len, char* arch,
 
 int32_t fi_buf_alloc(fi_context* ctx, size_t bytes, void** d_out) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_buf_alloc: the stream is being captured into a graph");
   FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_buf_alloc: null output pointer");
   FI_REQUIRE(bytes > 0, FI_ERR_INVALID_SHAPE, "device buffers must be larger than zero bytes");
   FI_TRY_HIP(hipMalloc(d_out, bytes));
@@ -148,6 +162,7 @@ int32_t fi_buf_alloc(fi_context* ctx, size_t bytes, void** d_out) {
 
 int32_t fi_buf_free(fi_context* ctx, void* d_ptr) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_buf_free: the stream is being captured into a graph");
   if (d_ptr == nullptr) return FI_OK;
   FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
   FI_TRY_HIP(hipFree(d_ptr));
@@ -157,6 +172,7 @@ int32_t fi_buf_free(fi_context* ctx, void* d_ptr) {
 int32_t fi_buf_upload(fi_context* ctx, void* d_dst, size_t dst_bytes, const void* src,
                       size_t src_bytes) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_buf_upload: the stream is being captured into a graph");
   FI_REQUIRE(dst_bytes == src_bytes, FI_ERR_INVALID_SHAPE,
              "upload requires matching lengths; buffer has " + std::to_string(dst_bytes) +
                  " bytes but host slice has " + std::to_string(src_bytes) + " bytes");
@@ -169,6 +185,7 @@ int32_t fi_buf_upload(fi_context* ctx, void* d_dst, size_t dst_bytes, const void
 int32_t fi_buf_download(fi_context* ctx, void* dst, size_t dst_bytes, const void* d_src,
                         size_t src_bytes) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_buf_download: the stream is being captured into a graph");
   FI_REQUIRE(dst_bytes == src_bytes, FI_ERR_INVALID_SHAPE,
              "download requires matching lengths; host slice has " + std::to_string(dst_bytes) +
                  " bytes but buffer has " + std::to_string(src_bytes) + " bytes");
@@ -178,8 +195,73 @@ int32_t fi_buf_download(fi_context* ctx, void* dst, size_t dst_bytes, const void
   return FI_OK;
 }
 
+int32_t fi_ctx_workspace_generation(fi_context* ctx, uint64_t* generation) {
+  FI_REQUIRE(ctx != nullptr && generation != nullptr, FI_ERR_INVALID_CONFIG,
+             "fi_ctx_workspace_generation: null argument");
+  *generation = ctx->workspace_generation;
+  return FI_OK;
+}
+
+int32_t fi_graph_begin(fi_context* ctx) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_graph_begin: a capture is already open");
+  FI_REQUIRE(ctx->stream != nullptr, FI_ERR_UNSUPPORTED, "fi_graph_begin: the null stream cannot be captured");
+  FI_TRY_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  ctx->capturing = true;
+  return FI_OK;
+}
+
+int32_t fi_graph_end(fi_context* ctx, fi_graph** out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(ctx->capturing, FI_ERR_RUNTIME, "fi_graph_end: no capture is open");
+  ctx->capturing = false;
+  hipGraph_t g = nullptr;
+  hipError_t err = hipStreamEndCapture(ctx->stream, &g);
+  if (err != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return fi::hip_error(err, "hipStreamEndCapture");
+  }
+  if (out == nullptr) {  // discard
+    (void)hipGraphDestroy(g);
+    return FI_OK;
+  }
+  hipGraphExec_t exec = nullptr;
+  err = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (err != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return fi::hip_error(err, "hipGraphInstantiate");
+  }
+  auto* graph = new fi_graph();
+  graph->graph = g;
+  graph->exec = exec;
+  graph->device = ctx->device;
+  *out = graph;
+  return FI_OK;
+}
+
+int32_t fi_graph_launch(fi_context* ctx, fi_graph* graph) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(graph != nullptr && graph->device == ctx->device, FI_ERR_INVALID_CONFIG,
+             "fi_graph_launch: graph of another device or null");
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_graph_launch: the stream is being captured");
+  FI_TRY_HIP(hipGraphLaunch(graph->exec, ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_graph_destroy(fi_graph* graph) {
+  if (graph == nullptr) return FI_OK;
+  FI_TRY_HIP(hipSetDevice(graph->device));
+  hipError_t e1 = hipGraphExecDestroy(graph->exec);
+  hipError_t e2 = hipGraphDestroy(graph->graph);
+  delete graph;
+  if (e1 != hipSuccess) return fi::hip_error(e1, "hipGraphExecDestroy");
+  if (e2 != hipSuccess) return fi::hip_error(e2, "hipGraphDestroy");
+  return FI_OK;
+}
+
 int32_t fi_ctx_check_faults(fi_context* ctx) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_ctx_check_faults: the stream is being captured into a graph");
   uint32_t words[4] = {0, 0, 0, 0};
   FI_TRY_HIP(hipMemcpyAsync(words, ctx->d_faults, sizeof(words), hipMemcpyDeviceToHost, ctx->stream));
   FI_TRY_HIP(hipStreamSynchronize(ctx->stream));

@@ -177,6 +177,7 @@ int32_t fi_add_rms_norm(fi_context* ctx, const float* d_a, const float* d_residu
 int32_t fi_rope_table(fi_context* ctx, int32_t max_positions, int32_t head_dim, int32_t rotary_dims,
                       float theta, float* d_cos, float* d_sin) {
   FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_rope_table: the stream is being captured into a graph");
   FI_REQUIRE(max_positions > 0 && head_dim > 0, FI_ERR_INVALID_SHAPE,
              "fi_rope_table: positions and head_dim must be positive");
   FI_REQUIRE(rotary_dims >= 0 && rotary_dims <= head_dim && rotary_dims % 2 == 0, FI_ERR_INVALID_SHAPE,

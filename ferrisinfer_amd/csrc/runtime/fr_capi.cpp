@@ -17,6 +17,7 @@ struct Runtime {
   std::unique_ptr<fr::Scheduler> scheduler;
   fr::SessionConfig session;
   fr::SchedulerConfig sched;
+  bool graph_decode = false;
   std::optional<fr::TickReport> last;
   ~Runtime() {
     scheduler.reset();
@@ -25,7 +26,7 @@ struct Runtime {
     if (ctx) fi_ctx_destroy(ctx);
   }
   fr::Scheduler& scheduler_ready() {
-    if (!scheduler) scheduler = std::make_unique<fr::Scheduler>(model.get(), pool.get(), session, sched);
+    if (!scheduler) scheduler = std::make_unique<fr::Scheduler>(model.get(), pool.get(), session, sched, graph_decode);
     return *scheduler;
   }
 };
@@ -83,7 +84,12 @@ int32_t fr_create(int32_t ordinal, const fr_model_config* mc, const fr_runtime_c
     r->sched.max_prefill_batch_tokens = rc->max_prefill_batch_tokens;
     r->sched.max_consecutive_prefill_ticks = rc->max_consecutive_prefill_ticks;
     r->sched.min_prefix_share_tokens = rc->min_prefix_share_tokens;
-    r->model = std::make_unique<fr::DeviceModel>(r->ctx, c, static_cast<int32_t>(rc->max_sequence_length));
+    if (rc->weight_dtype != FI_DTYPE_F32 && rc->weight_dtype != FI_DTYPE_BF16) {
+      fr::fail(fr::ErrorKind::InvalidType, "projection weight dtype must be f32 or bf16");
+    }
+    r->graph_decode = rc->graph_decode != 0;
+    r->model = std::make_unique<fr::DeviceModel>(r->ctx, c, static_cast<int32_t>(rc->max_sequence_length),
+                                                 rc->weight_dtype);
     r->pool = std::make_unique<fr::BlockPool>(r->ctx, c.num_layers, rc->num_blocks, rc->block_size,
                                               c.num_key_value_heads, c.head_dim(), rc->kv_dtype);
     *out = r.release();
@@ -253,6 +259,13 @@ int32_t fr_sequence_blocks(void* h, uint64_t seq, int32_t* out, int64_t capacity
 
 int32_t fr_pool_free_count(void* h, int64_t* out) {
   return guard([&] { *out = static_cast<int64_t>(rt(h)->pool->free_count()); });
+}
+
+int32_t fr_graph_counters(void* h, uint64_t* out) {
+  return guard([&] {
+    const auto c = rt(h)->scheduler_ready().executor().graph_counters();
+    for (size_t i = 0; i < c.size(); ++i) out[i] = c[i];
+  });
 }
 
 int32_t fr_last_tick_profile(void* h, double* out) {

@@ -68,9 +68,13 @@ void ModelConfig::validate() const {
   if (rotary_dims > head_dim()) fail(ErrorKind::InvalidConfig, "rope.rotary_dims cannot exceed attention head dimension");
 }
 
-DeviceModel::DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions)
-    : ctx_(ctx), config_(config), layers_(config.num_layers), rope_positions_(rope_positions) {
+DeviceModel::DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions, int32_t weight_dtype)
+    : ctx_(ctx), config_(config), layers_(config.num_layers), rope_positions_(rope_positions),
+      weight_dtype_(weight_dtype) {
   config.validate();
+  if (weight_dtype != FI_DTYPE_F32 && weight_dtype != FI_DTYPE_BF16) {
+    fail(ErrorKind::InvalidType, "projection weight dtype must be f32 or bf16");
+  }
   const int pairs = config.rotary_dims / 2;
   if (pairs > 0) {
     rope_cos_.reserve(ctx, static_cast<size_t>(rope_positions) * pairs * sizeof(float));
@@ -169,23 +173,47 @@ void DeviceModel::finalize() {
     check(fi_weight_packed_floats(k, n, pw, &out));
     return out;
   };
+  auto bf16_bytes = [](int32_t k, int32_t n, int32_t pair) {
+    size_t out = 0;
+    check(fi_weight_packed_bf16_elems(k, n, pair, &out));
+    return out * sizeof(uint16_t);
+  };
   packed_.resize(c.num_layers);
   for (int32_t l = 0; l < c.num_layers; ++l) {
     Layer& w = layers_[l];
     Packed& p = packed_[l];
-    p.qkv.reserve(ctx_, floats(h, h + 2 * kvw, kQkvPack) * sizeof(float));
-    const float* srcs[3] = {w.wq.f32(), w.wk.f32(), w.wv.f32()};
     const int32_t ns[3] = {h, kvw, kvw};
-    check(fi_weight_pack_columns(ctx_, srcs, ns, 3, h, kQkvPack, p.qkv.f32()));
-    p.wo.reserve(ctx_, floats(h, h, kWoPack) * sizeof(float));
-    check(fi_weight_pack(ctx_, w.wo.f32(), 0, h, h, kWoPack, p.wo.f32()));
-    p.w13.reserve(ctx_, floats(h, 2 * f, 2) * sizeof(float));
-    check(fi_weight_pack_pair(ctx_, w.w1.f32(), w.w3.f32(), h, f, p.w13.f32()));
-    p.w2.reserve(ctx_, floats(f, h, kW2Pack) * sizeof(float));
-    check(fi_weight_pack(ctx_, w.w2.f32(), 0, f, h, kW2Pack, p.w2.f32()));
+    if (weight_dtype_ == FI_DTYPE_BF16) {
+      const void* srcs[3] = {w.wq.get(), w.wk.get(), w.wv.get()};
+      p.qkv.reserve(ctx_, bf16_bytes(h, h + 2 * kvw, 0));
+      check(fi_weight_pack_bf16_columns(ctx_, srcs, ns, 3, FI_DTYPE_F32, h, static_cast<uint16_t*>(p.qkv.get())));
+      p.wo.reserve(ctx_, bf16_bytes(h, h, 0));
+      check(fi_weight_pack_bf16(ctx_, w.wo.get(), FI_DTYPE_F32, 0, h, h, static_cast<uint16_t*>(p.wo.get())));
+      p.w13.reserve(ctx_, bf16_bytes(h, f, 1));
+      check(fi_weight_pack_bf16_pair(ctx_, w.w1.get(), w.w3.get(), FI_DTYPE_F32, h, f,
+                                     static_cast<uint16_t*>(p.w13.get())));
+      p.w2.reserve(ctx_, bf16_bytes(f, h, 0));
+      check(fi_weight_pack_bf16(ctx_, w.w2.get(), FI_DTYPE_F32, 0, f, h, static_cast<uint16_t*>(p.w2.get())));
+    } else {
+      const float* srcs[3] = {w.wq.f32(), w.wk.f32(), w.wv.f32()};
+      p.qkv.reserve(ctx_, floats(h, h + 2 * kvw, kQkvPack) * sizeof(float));
+      check(fi_weight_pack_columns(ctx_, srcs, ns, 3, h, kQkvPack, p.qkv.f32()));
+      p.wo.reserve(ctx_, floats(h, h, kWoPack) * sizeof(float));
+      check(fi_weight_pack(ctx_, w.wo.f32(), 0, h, h, kWoPack, p.wo.f32()));
+      p.w13.reserve(ctx_, floats(h, 2 * f, 2) * sizeof(float));
+      check(fi_weight_pack_pair(ctx_, w.w1.f32(), w.w3.f32(), h, f, p.w13.f32()));
+      p.w2.reserve(ctx_, floats(f, h, kW2Pack) * sizeof(float));
+      check(fi_weight_pack(ctx_, w.w2.f32(), 0, f, h, kW2Pack, p.w2.f32()));
+    }
   }
-  lm_packed_.reserve(ctx_, floats(h, c.vocab_size, kLmPack) * sizeof(float));
-  check(fi_weight_pack(ctx_, output_weight(), 1, h, c.vocab_size, kLmPack, lm_packed_.f32()));
+  if (weight_dtype_ == FI_DTYPE_BF16) {
+    lm_packed_.reserve(ctx_, bf16_bytes(h, c.vocab_size, 0));
+    check(fi_weight_pack_bf16(ctx_, output_weight(), FI_DTYPE_F32, 1, h, c.vocab_size,
+                              static_cast<uint16_t*>(lm_packed_.get())));
+  } else {
+    lm_packed_.reserve(ctx_, floats(h, c.vocab_size, kLmPack) * sizeof(float));
+    check(fi_weight_pack(ctx_, output_weight(), 1, h, c.vocab_size, kLmPack, lm_packed_.f32()));
+  }
   check(fi_ctx_sync(ctx_));
   for (Layer& w : layers_) {
     w.wq = DeviceBuffer();
@@ -236,8 +264,23 @@ void BlockPool::decref(int32_t block) {
 }
 
 // ----------------------------------------------------------------------------- forward
-ForwardExecutor::ForwardExecutor(const DeviceModel* model, BlockPool* pool)
-    : model_(model), pool_(pool), ctx_(model->ctx()) {}
+ForwardExecutor::ForwardExecutor(const DeviceModel* model, BlockPool* pool, bool graph_decode)
+    : model_(model), pool_(pool), ctx_(model->ctx()), graph_decode_(graph_decode) {}
+
+ForwardExecutor::~ForwardExecutor() { drop_graphs(); }
+
+void ForwardExecutor::drop_graphs() {
+  if (!graphs_.empty()) graph_drops_ += graphs_.size();
+  for (auto& kv : graphs_) (void)fi_graph_destroy(kv.second);
+  graphs_.clear();
+  seen_.clear();
+}
+
+void ForwardExecutor::grow(DeviceBuffer& b, size_t bytes) {
+  const void* before = b.get();
+  b.reserve(ctx_, bytes);
+  if (b.get() != before) buffers_moved_ += 1;
+}
 
 void ForwardExecutor::copy_only(const PackedBatch& b) {
   // A tick whose sequences only shared a prefix still owes the copy-on-write of a partially
@@ -247,7 +290,7 @@ void ForwardExecutor::copy_only(const PackedBatch& b) {
   std::vector<int32_t> host(b.copy_src);
   host.insert(host.end(), b.copy_dst.begin(), b.copy_dst.end());
   host.insert(host.end(), b.copy_count.begin(), b.copy_count.end());
-  meta_.reserve(ctx_, host.size() * 4);
+  grow(meta_, host.size() * 4);
   check(fi_buf_upload(ctx_, meta_.get(), host.size() * 4, host.data(), host.size() * 4));
   const int32_t* d = static_cast<const int32_t*>(meta_.get());
   const ModelConfig& c = model_->config();
@@ -265,15 +308,32 @@ void ForwardExecutor::reserve(size_t tokens, size_t seqs) {
   cap_seqs_ = std::max(seqs, cap_seqs_);
   const ModelConfig& c = model_->config();
   const size_t t = cap_tokens_, h = c.hidden_size, f = c.intermediate_size;
-  hidden_.reserve(ctx_, t * h * 4);
-  normed_.reserve(ctx_, t * h * 4);
-  q_.reserve(ctx_, t * h * 4);
-  attn_.reserve(ctx_, t * h * 4);
-  h1_.reserve(ctx_, t * h * 4);
-  act_.reserve(ctx_, t * f * 4);
-  last_norm_.reserve(ctx_, cap_seqs_ * h * 4);
-  tok_.reserve(ctx_, cap_seqs_ * 4);
-  prob_.reserve(ctx_, cap_seqs_ * 4);
+  grow(hidden_, t * h * 4);
+  grow(normed_, t * h * 4);
+  grow(q_, t * h * 4);
+  grow(attn_, t * h * 4);
+  grow(h1_, t * h * 4);
+  grow(act_, t * f * 4);
+  grow(last_norm_, cap_seqs_ * h * 4);
+  grow(tok_, cap_seqs_ * 4);
+  grow(prob_, cap_seqs_ * 4);
+}
+
+void ForwardExecutor::splits(int32_t m, int32_t k, int32_t n, int32_t pack_width, int32_t* out) const {
+  if (model_->weight_dtype() == FI_DTYPE_BF16) {
+    check(fi_gemm_bf16_splits(ctx_, m, k, n, out));
+  } else {
+    check(fi_gemm_packed_splits(ctx_, m, k, n, pack_width, out));
+  }
+}
+
+void ForwardExecutor::projection(const float* a, int32_t lda, const DeviceBuffer& w, int32_t k, int32_t n,
+                                 int32_t pack_width, int32_t m, int32_t splits, float* out) const {
+  if (model_->weight_dtype() == FI_DTYPE_BF16) {
+    check(fi_gemm_bf16(ctx_, a, lda, static_cast<const uint16_t*>(w.get()), k, n, m, splits, out));
+  } else {
+    check(fi_gemm_packed(ctx_, a, lda, w.f32(), k, n, pack_width, m, splits, out));
+  }
 }
 
 uint64_t sampler_state_new(uint64_t seed) { return seed == 0 ? 0x9e3779b97f4a7c15ULL : seed; }
@@ -283,6 +343,95 @@ uint64_t sampler_state_next(uint64_t x) {
   x ^= x << 25;
   x ^= x >> 27;
   return x;
+}
+
+// The launch sequence of one tick (runtime/reference.rs:372-423 / 664-710: embed, L blocks,
+// final norm, head).  Block order as reference.rs:163-370: rmsnorm -> q,k,v (+bias) -> rope ->
+// attention (the chunk's own K/V appended first, so they are read from the pool) -> wo (+bias)
+// -> +x -> rmsnorm -> w1, w3 (+bias) -> silu(w3) * w1 -> w2 (+bias) -> +h1.  Each rmsnorm runs
+// fused with the residual add before it; the last one applies the model's final norm.  Nothing
+// here allocates, copies to or from the host or waits, so the sequence can be captured.
+void ForwardExecutor::enqueue(const Plan& p) {
+  const ModelConfig& c = model_->config();
+  const int32_t T = p.T, B = p.B;
+  const int32_t H = c.hidden_size, F = c.intermediate_size, hq = c.num_attention_heads;
+  const int32_t hkv = c.num_key_value_heads, D = c.head_dim(), W = H + 2 * hkv * D;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // attention.rs:659
+  const bool bf16 = model_->weight_dtype() == FI_DTYPE_BF16;
+  float* hidden = hidden_.f32();
+  float* normed = normed_.f32();
+  float* q = q_.f32();
+  float* attn = attn_.f32();
+  float* h1 = h1_.f32();
+  float* act = act_.f32();
+  float* part = parts_.f32();
+
+  check(fi_embedding(ctx_, model_->tok_embeddings(), c.vocab_size, H, p.ids, T, hidden));
+  check(fi_rms_norm(ctx_, hidden, model_->layer(0).attention_norm.f32(), normed, T, H, c.rms_norm_eps));
+  for (int32_t l = 0; l < c.num_layers; ++l) {
+    const DeviceModel::Layer& w = model_->layer(l);
+    const DeviceModel::Packed& pk = model_->packed(l);
+    projection(normed, H, pk.qkv, H, W, DeviceModel::kQkvPack, T, p.s_qkv, part);
+    check(fi_qkv_rope_append(ctx_, part, p.s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), p.pos,
+                             model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(), p.slot,
+                             pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(), pool_->block_size(), T,
+                             hq, hkv, D, q));
+    if (p.n_copy > 0) {
+      check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.cs, p.cd, p.cc, p.n_copy,
+                              pool_->num_blocks(), pool_->block_size(), hkv, D));
+    }
+    if (p.kind == BatchKind::Decode) {
+      check(fi_attn_decode_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.ctx, B,
+                                 p.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
+                                 attn));
+    } else {
+      check(fi_attn_prefill_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.cu,
+                                  p.ctx, B, p.max_query_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(),
+                                  scale, attn));
+    }
+    projection(attn, H, pk.wo, H, H, DeviceModel::kWoPack, T, p.s_o, part);
+    check(fi_splitk_residual_rms_norm(ctx_, part, p.s_o, w.wo_bias.f32(), hidden, h1, w.ffn_norm.f32(), normed, T, H,
+                                      c.rms_norm_eps));
+    if (bf16) {
+      check(fi_gemm_bf16_swiglu(ctx_, normed, H, static_cast<const uint16_t*>(pk.w13.get()), H, F, T,
+                                w.w1_bias.f32(), w.w3_bias.f32(), act));
+    } else {
+      check(fi_gemm_packed_swiglu(ctx_, normed, H, pk.w13.f32(), H, F, T, w.w1_bias.f32(), w.w3_bias.f32(), act));
+    }
+    projection(act, F, pk.w2, F, H, DeviceModel::kW2Pack, T, p.s_w2, part);
+    const float* next_norm = l + 1 < c.num_layers ? model_->layer(l + 1).attention_norm.f32() : model_->norm();
+    check(fi_splitk_residual_rms_norm(ctx_, part, p.s_w2, w.w2_bias.f32(), h1, hidden, next_norm, normed, T, H,
+                                      c.rms_norm_eps));
+  }
+  // the final norm ran over every row; each sequence's last row feeds the head
+  check(fi_embedding(ctx_, normed, T, H, p.last, B, last_norm_.f32()));
+  const void* lm = model_->lm_head_packed();
+  if (p.greedy) {
+    // fused greedy head (matmul_rhs_transposed_argmax_f32, matmul.rs:190-274), as the
+    // reference session's greedy path (session.rs:349-356, 393-398)
+    if (bf16) {
+      check(fi_lm_head_argmax_bf16(ctx_, last_norm_.f32(), H, static_cast<const uint16_t*>(lm), B, H, c.vocab_size,
+                                   static_cast<int32_t*>(tok_.get()), prob_.f32()));
+    } else {
+      check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), B, H, c.vocab_size,
+                                     static_cast<int32_t*>(tok_.get()), prob_.f32()));
+    }
+  } else {
+    // last-row logits (matmul_rhs_transposed, one K split) and sample_last_token per row
+    // (session.rs:357-373, 399-406) with each sequence's sampler state; the states and the
+    // per-row configuration were uploaded to samp_ before this sequence
+    if (bf16) {
+      check(fi_gemm_bf16(ctx_, last_norm_.f32(), H, static_cast<const uint16_t*>(lm), H, c.vocab_size, B, 1,
+                         logits_.f32()));
+    } else {
+      check(fi_gemm_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), H, c.vocab_size,
+                           DeviceModel::kLmPack, B, 1, logits_.f32()));
+    }
+    uint8_t* d = static_cast<uint8_t*>(samp_.get());
+    check(fi_sample_tokens(ctx_, logits_.f32(), c.vocab_size, B, c.vocab_size, reinterpret_cast<const float*>(d + B * 8),
+                           reinterpret_cast<const int32_t*>(d + B * 12), reinterpret_cast<const float*>(d + B * 16),
+                           reinterpret_cast<uint64_t*>(d), static_cast<int32_t*>(tok_.get()), prob_.f32()));
+  }
 }
 
 std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const SamplerConfig& sampler,
@@ -298,20 +447,48 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   }
   if (!model_->finalized()) fail(ErrorKind::Runtime, "model weights are not packed (DeviceModel::finalize)");
   reserve(T, B);
-  const int32_t H = c.hidden_size, F = c.intermediate_size, hq = c.num_attention_heads;
-  const int32_t hkv = c.num_key_value_heads, D = c.head_dim(), kvw = hkv * D, W = H + 2 * kvw;
-  const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // attention.rs:659
+  const int32_t H = c.hidden_size, F = c.intermediate_size, W = H + 2 * c.num_key_value_heads * c.head_dim();
+  const bool greedy = sampler.is_greedy();
+  const bool use_graph = graph_decode_ && b.kind == BatchKind::Decode;
 
+  Plan p{};
+  p.kind = b.kind;
+  p.T = T;
+  p.B = B;
+  p.max_query_len = b.max_query_len;
+  p.n_copy = static_cast<int32_t>(b.copy_src.size());
+  p.greedy = greedy;
+  p.max_blocks = b.max_blocks;
+  p.max_context_len = b.max_context_len;
   // split-K counts of the three partial-output projections; one partials buffer serves all
-  int32_t s_qkv = 1, s_o = 1, s_w2 = 1;
-  check(fi_gemm_packed_splits(ctx_, T, H, W, DeviceModel::kQkvPack, &s_qkv));
-  check(fi_gemm_packed_splits(ctx_, T, H, H, DeviceModel::kWoPack, &s_o));
-  check(fi_gemm_packed_splits(ctx_, T, F, H, DeviceModel::kW2Pack, &s_w2));
-  const size_t parts = std::max({static_cast<size_t>(s_qkv) * T * W, static_cast<size_t>(s_o) * T * H,
-                                 static_cast<size_t>(s_w2) * T * H});
+  splits(T, H, W, DeviceModel::kQkvPack, &p.s_qkv);
+  splits(T, H, H, DeviceModel::kWoPack, &p.s_o);
+  splits(T, F, H, DeviceModel::kW2Pack, &p.s_w2);
+  const size_t parts = std::max({static_cast<size_t>(p.s_qkv) * T * W, static_cast<size_t>(p.s_o) * T * H,
+                                 static_cast<size_t>(p.s_w2) * T * H});
   if (parts > cap_parts_) {
-    parts_.reserve(ctx_, parts * 4);
+    grow(parts_, parts * 4);
     cap_parts_ = parts;
+  }
+
+  // The block table as uploaded: the packer's [B, max_blocks], or, for a replayable decode tick,
+  // padded to the width of max_context_len rounded up to kGraphContextBucket tokens.
+  const int32_t bs = pool_->block_size();
+  std::vector<int32_t> padded;
+  const std::vector<int32_t>* tables = &b.block_tables;
+  if (use_graph) {
+    const int64_t bucket = ((static_cast<int64_t>(b.max_context_len) + kGraphContextBucket - 1) / kGraphContextBucket) *
+                           kGraphContextBucket;
+    p.max_context_len = static_cast<int32_t>(std::max<int64_t>(bucket, kGraphContextBucket));
+    p.max_blocks = (p.max_context_len + bs - 1) / bs;
+    if (p.max_blocks < b.max_blocks) fail(ErrorKind::Runtime, "graph block-table width below the packed width");
+    padded.assign(static_cast<size_t>(B) * p.max_blocks, 0);
+    for (int32_t i = 0; i < B; ++i) {
+      std::copy(b.block_tables.begin() + static_cast<size_t>(i) * b.max_blocks,
+                b.block_tables.begin() + static_cast<size_t>(i + 1) * b.max_blocks,
+                padded.begin() + static_cast<size_t>(i) * p.max_blocks);
+    }
+    tables = &padded;
   }
 
   // One upload of all integer metadata (8-byte aligned sections).
@@ -327,88 +504,31 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   const size_t o_slot = section(b.slot_mapping.data(), b.slot_mapping.size() * 8);
   const size_t o_cu = section(b.cu_seqlens.data(), b.cu_seqlens.size() * 4);
   const size_t o_ctx = section(b.context_lens.data(), b.context_lens.size() * 4);
-  const size_t o_bt = section(b.block_tables.data(), b.block_tables.size() * 4);
+  const size_t o_bt = section(tables->data(), tables->size() * 4);
   const size_t o_last = section(b.last_rows.data(), b.last_rows.size() * 4);
   const size_t o_cs = section(b.copy_src.data(), b.copy_src.size() * 4);
   const size_t o_cd = section(b.copy_dst.data(), b.copy_dst.size() * 4);
   const size_t o_cc = section(b.copy_count.data(), b.copy_count.size() * 4);
-  meta_.reserve(ctx_, host.size());
+  grow(meta_, host.size());
   check(fi_buf_upload(ctx_, meta_.get(), host.size(), host.data(), host.size()));
   auto at = [&](size_t off) { return static_cast<uint8_t*>(meta_.get()) + off; };
-  const int32_t* d_ids = reinterpret_cast<const int32_t*>(at(o_ids));
-  const int32_t* d_pos = reinterpret_cast<const int32_t*>(at(o_pos));
-  const int64_t* d_slot = reinterpret_cast<const int64_t*>(at(o_slot));
-  const int32_t* d_cu = reinterpret_cast<const int32_t*>(at(o_cu));
-  const int32_t* d_ctx = reinterpret_cast<const int32_t*>(at(o_ctx));
-  const int32_t* d_bt = reinterpret_cast<const int32_t*>(at(o_bt));
-  const int32_t* d_last = reinterpret_cast<const int32_t*>(at(o_last));
-  const int32_t n_copy = static_cast<int32_t>(b.copy_src.size());
+  p.ids = reinterpret_cast<const int32_t*>(at(o_ids));
+  p.pos = reinterpret_cast<const int32_t*>(at(o_pos));
+  p.slot = reinterpret_cast<const int64_t*>(at(o_slot));
+  p.cu = reinterpret_cast<const int32_t*>(at(o_cu));
+  p.ctx = reinterpret_cast<const int32_t*>(at(o_ctx));
+  p.bt = reinterpret_cast<const int32_t*>(at(o_bt));
+  p.last = reinterpret_cast<const int32_t*>(at(o_last));
+  p.cs = reinterpret_cast<const int32_t*>(at(o_cs));
+  p.cd = reinterpret_cast<const int32_t*>(at(o_cd));
+  p.cc = reinterpret_cast<const int32_t*>(at(o_cc));
 
-  float* hidden = hidden_.f32();
-  float* normed = normed_.f32();
-  float* q = q_.f32();
-  float* attn = attn_.f32();
-  float* h1 = h1_.f32();
-  float* act = act_.f32();
-  float* part = parts_.f32();
-
-  // runtime/reference.rs:372-423 / 664-710: embed, L blocks, final norm, greedy head.  Block
-  // order as reference.rs:163-370: rmsnorm -> q,k,v (+bias) -> rope -> attention (the chunk's
-  // own K/V appended first, so they are read from the pool) -> wo (+bias) -> +x -> rmsnorm ->
-  // w1, w3 (+bias) -> silu(w3) * w1 -> w2 (+bias) -> +h1.  Each rmsnorm runs fused with the
-  // residual add before it; the last one applies the model's final norm.
-  check(fi_embedding(ctx_, model_->tok_embeddings(), c.vocab_size, H, d_ids, T, hidden));
-  check(fi_rms_norm(ctx_, hidden, model_->layer(0).attention_norm.f32(), normed, T, H, c.rms_norm_eps));
-  for (int32_t l = 0; l < c.num_layers; ++l) {
-    const DeviceModel::Layer& w = model_->layer(l);
-    const DeviceModel::Packed& p = model_->packed(l);
-    check(fi_gemm_packed(ctx_, normed, H, p.qkv.f32(), H, W, DeviceModel::kQkvPack, T, s_qkv, part));
-    check(fi_qkv_rope_append(ctx_, part, s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), d_pos,
-                             model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(), d_slot,
-                             pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(), pool_->block_size(), T,
-                             hq, hkv, D, q));
-    if (n_copy > 0) {
-      check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(),
-                              reinterpret_cast<const int32_t*>(at(o_cs)), reinterpret_cast<const int32_t*>(at(o_cd)),
-                              reinterpret_cast<const int32_t*>(at(o_cc)), n_copy, pool_->num_blocks(),
-                              pool_->block_size(), hkv, D));
-    }
-    if (b.kind == BatchKind::Decode) {
-      check(fi_attn_decode_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), d_bt, b.max_blocks, d_ctx, B,
-                                 b.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
-                                 attn));
-    } else {
-      check(fi_attn_prefill_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), d_bt, b.max_blocks, d_cu,
-                                  d_ctx, B, b.max_query_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(),
-                                  scale, attn));
-    }
-    check(fi_gemm_packed(ctx_, attn, H, p.wo.f32(), H, H, DeviceModel::kWoPack, T, s_o, part));
-    check(fi_splitk_residual_rms_norm(ctx_, part, s_o, w.wo_bias.f32(), hidden, h1, w.ffn_norm.f32(), normed, T, H,
-                                      c.rms_norm_eps));
-    check(fi_gemm_packed_swiglu(ctx_, normed, H, p.w13.f32(), H, F, T, w.w1_bias.f32(), w.w3_bias.f32(), act));
-    check(fi_gemm_packed(ctx_, act, F, p.w2.f32(), F, H, DeviceModel::kW2Pack, T, s_w2, part));
-    const float* next_norm = l + 1 < c.num_layers ? model_->layer(l + 1).attention_norm.f32() : model_->norm();
-    check(fi_splitk_residual_rms_norm(ctx_, part, s_w2, w.w2_bias.f32(), h1, hidden, next_norm, normed, T, H,
-                                      c.rms_norm_eps));
-  }
-  // the final norm ran over every row; each sequence's last row feeds the head
-  check(fi_embedding(ctx_, normed, T, H, d_last, B, last_norm_.f32()));
-  const bool greedy = sampler.is_greedy();
-  if (greedy) {
-    // fused greedy head (matmul_rhs_transposed_argmax_f32, matmul.rs:190-274), as the
-    // reference session's greedy path (session.rs:349-356, 393-398)
-    check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, model_->lm_head_packed(), B, H, c.vocab_size,
-                                   static_cast<int32_t*>(tok_.get()), prob_.f32()));
-  } else {
-    // last-row logits (matmul_rhs_transposed, one K split) and sample_last_token per row
-    // (session.rs:357-373, 399-406) with each sequence's sampler state
+  if (!greedy) {
+    // one upload: states [B] u64, temperature [B] f32, top_k [B] i32, top_p [B] f32
     if (states == nullptr || states->size() != static_cast<size_t>(B)) {
       fail(ErrorKind::InvalidShape, "sampled batch requires one sampler state per sequence");
     }
-    logits_.reserve(ctx_, static_cast<size_t>(B) * c.vocab_size * 4);
-    check(fi_gemm_packed(ctx_, last_norm_.f32(), H, model_->lm_head_packed(), H, c.vocab_size, DeviceModel::kLmPack,
-                         B, 1, logits_.f32()));
-    // one upload: states [B] u64, temperature [B] f32, top_k [B] i32, top_p [B] f32
+    grow(logits_, static_cast<size_t>(B) * c.vocab_size * 4);
     std::vector<uint8_t> cfg(static_cast<size_t>(B) * 20);
     std::memcpy(cfg.data(), states->data(), static_cast<size_t>(B) * 8);
     const int32_t k32 = static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(sampler.top_k, 0), INT32_MAX));
@@ -417,13 +537,44 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
       std::memcpy(cfg.data() + B * 12 + i * 4, &k32, 4);
       std::memcpy(cfg.data() + B * 16 + i * 4, &sampler.top_p, 4);
     }
-    samp_.reserve(ctx_, cfg.size());
+    grow(samp_, cfg.size());
     check(fi_buf_upload(ctx_, samp_.get(), cfg.size(), cfg.data(), cfg.size()));
-    uint8_t* d = static_cast<uint8_t*>(samp_.get());
-    check(fi_sample_tokens(ctx_, logits_.f32(), c.vocab_size, B, c.vocab_size, reinterpret_cast<const float*>(d + B * 8),
-                           reinterpret_cast<const int32_t*>(d + B * 12), reinterpret_cast<const float*>(d + B * 16),
-                           reinterpret_cast<uint64_t*>(d), static_cast<int32_t*>(tok_.get()), prob_.f32()));
   }
+
+  if (use_graph) {
+    uint64_t ws = 0;
+    check(fi_ctx_workspace_generation(ctx_, &ws));
+    if (ws != graphs_workspace_ || buffers_moved_ != graphs_buffers_) {
+      drop_graphs();
+      graphs_workspace_ = ws;
+      graphs_buffers_ = buffers_moved_;
+    }
+    const std::array<int32_t, 4> key{B, p.max_blocks, p.max_context_len, greedy ? 1 : 0};
+    auto it = graphs_.find(key);
+    if (it != graphs_.end()) {
+      check(fi_graph_launch(ctx_, it->second));
+      graph_replays_ += 1;
+    } else if (seen_[key]++ == 0) {
+      enqueue(p);  // first occurrence: eager, sizing the context workspace for this shape
+    } else {
+      check(fi_graph_begin(ctx_));
+      fi_graph* g = nullptr;
+      try {
+        enqueue(p);
+      } catch (...) {
+        (void)fi_graph_end(ctx_, nullptr);
+        throw;
+      }
+      check(fi_graph_end(ctx_, &g));
+      graphs_[key] = g;
+      graph_captures_ += 1;
+      check(fi_graph_launch(ctx_, g));
+      graph_replays_ += 1;
+    }
+  } else {
+    enqueue(p);
+  }
+
   const auto t_enqueued = std::chrono::steady_clock::now();
   std::vector<int32_t> tok(B);
   std::vector<float> prob(B);

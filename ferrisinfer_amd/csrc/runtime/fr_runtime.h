@@ -83,14 +83,17 @@ class DeviceModel {
     DeviceBuffer attention_norm, wq, wq_bias, wk, wk_bias, wv, wv_bias, wo, wo_bias;
     DeviceBuffer ffn_norm, w1, w1_bias, w2, w2_bias, w3, w3_bias;
   };
-  // Projections re-laid out for fi_gemm_packed (include/ferrisinfer_kernel.h): q|k|v as one
-  // column-concatenated matrix, wo, w1/w3 as a SwiGLU pair, w2; pack widths below.
+  // Projections re-laid out once for the projection GEMMs (include/ferrisinfer_kernel.h): q|k|v
+  // as one column-concatenated matrix, wo, w1/w3 as a SwiGLU pair, w2.  f32 weights are packed
+  // for fi_gemm_packed (pack widths below); bf16 weights (rounded to nearest even from the f32
+  // tensors, exact for bf16 checkpoints) for fi_gemm_bf16.
   struct Packed {
     DeviceBuffer qkv, wo, w13, w2;
   };
   static constexpr int32_t kQkvPack = 1, kWoPack = 1, kW2Pack = 4, kLmPack = 2;
 
-  DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions);
+  // weight_dtype: FI_DTYPE_F32 or FI_DTYPE_BF16, the storage of the packed projections and head.
+  DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions, int32_t weight_dtype = FI_DTYPE_F32);
   void set_weight(const std::string& name, const float* host, size_t count);
   // The device buffer of weight `name` sized for `count` floats (contents undefined until
   // written); InvalidShape when count is not the tensor's size, MissingWeight for an unknown
@@ -102,7 +105,8 @@ class DeviceModel {
   void finalize();
   bool finalized() const { return finalized_; }
   const Packed& packed(int i) const { return packed_.at(i); }
-  const float* lm_head_packed() const { return lm_packed_.f32(); }
+  const void* lm_head_packed() const { return lm_packed_.get(); }
+  int32_t weight_dtype() const { return weight_dtype_; }
   const ModelConfig& config() const { return config_; }
   const Layer& layer(int i) const { return layers_.at(i); }
   const float* tok_embeddings() const { return tok_embeddings_.f32(); }
@@ -122,6 +126,7 @@ class DeviceModel {
   std::vector<Packed> packed_;
   DeviceBuffer tok_embeddings_, norm_, output_, rope_cos_, rope_sin_, lm_packed_;
   int32_t rope_positions_;
+  int32_t weight_dtype_;
   bool finalized_ = false;
 };
 
@@ -322,9 +327,24 @@ struct PackedBatch {
 };
 
 // Runs the decoder over packed batches (one launch sequence per tick).
+//
+// Decode ticks can be replayed from HIP graphs (BackendCapabilities.graph_capture,
+// kernel/backend.rs:3-10; docs/performance-roadmap.md:321-326).  A decode tick's launch sequence
+// is fixed by (batch size, block-table stride, max_context_len, sampler kind) once every device
+// buffer it touches stays put; the batch metadata is re-uploaded into the same buffer before each
+// replay.  With graphs on, a decode tick rounds max_context_len up to a multiple of
+// kGraphContextBucket tokens and pads the block table to that width: the extra partitions of the
+// decode kernel find no keys and exit, and each sequence's reduction order depends only on its own
+// context length, so replays give the eager path's bits.  A shape is captured the second time it
+// occurs (the first, eager run sizes the context workspace); graphs are dropped whenever a buffer
+// they recorded moves (an executor buffer grows, or the context workspace's generation changes).
 class ForwardExecutor {
  public:
-  ForwardExecutor(const DeviceModel* model, BlockPool* pool);
+  static constexpr int32_t kGraphContextBucket = 1024;
+  ForwardExecutor(const DeviceModel* model, BlockPool* pool, bool graph_decode = false);
+  ~ForwardExecutor();
+  ForwardExecutor(const ForwardExecutor&) = delete;
+  ForwardExecutor& operator=(const ForwardExecutor&) = delete;
   // Returns one sample per batch sequence from its last row: the fused argmax head for a
   // greedy sampler, else the row's logits through the device sampler with states[i]
   // (advanced in place by one draw per sequence).
@@ -332,22 +352,46 @@ class ForwardExecutor {
   // Host seconds of the last run: enqueueing every launch, then waiting for the samples.
   double last_enqueue_seconds() const { return enqueue_s_; }
   double last_wait_seconds() const { return wait_s_; }
+  // Decode ticks replayed from a graph, graphs captured, graphs dropped (since creation).
+  std::array<uint64_t, 3> graph_counters() const { return {graph_replays_, graph_captures_, graph_drops_}; }
 
  private:
+  // Every scalar and device pointer of one tick's launch sequence.
+  struct Plan {
+    BatchKind kind;
+    int32_t T, B, max_blocks, max_context_len, max_query_len, n_copy;
+    int32_t s_qkv, s_o, s_w2;
+    const int32_t *ids, *pos, *cu, *ctx, *bt, *last, *cs, *cd, *cc;
+    const int64_t* slot;
+    bool greedy;
+  };
   void reserve(size_t tokens, size_t seqs);
+  void grow(DeviceBuffer& b, size_t bytes);  // reserve, noting a moved buffer
   void copy_only(const PackedBatch& batch);
+  void splits(int32_t m, int32_t k, int32_t n, int32_t pack_width, int32_t* out) const;
+  void projection(const float* a, int32_t lda, const DeviceBuffer& w, int32_t k, int32_t n, int32_t pack_width,
+                  int32_t m, int32_t splits, float* out) const;
+  void enqueue(const Plan& p);
+  void drop_graphs();
   const DeviceModel* model_;
   BlockPool* pool_;
   fi_context* ctx_;
   DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, tok_, prob_, logits_, samp_;
   size_t cap_tokens_ = 0, cap_seqs_ = 0, cap_parts_ = 0;
   double enqueue_s_ = 0.0, wait_s_ = 0.0;
+  bool graph_decode_;
+  uint64_t buffers_moved_ = 0;             // bumped whenever an executor buffer is reallocated
+  uint64_t graphs_buffers_ = 0, graphs_workspace_ = 0;  // generations the cached graphs recorded
+  std::map<std::array<int32_t, 4>, fi_graph*> graphs_;  // (B, stride, max_context_len, greedy)
+  std::map<std::array<int32_t, 4>, int32_t> seen_;       // eager runs per shape since the last drop
+  uint64_t graph_replays_ = 0, graph_captures_ = 0, graph_drops_ = 0;
 };
 
 // runtime/scheduler.rs:109-648 over the batched executor.
 class Scheduler {
  public:
-  Scheduler(DeviceModel* model, BlockPool* pool, const SessionConfig& session, const SchedulerConfig& config);
+  Scheduler(DeviceModel* model, BlockPool* pool, const SessionConfig& session, const SchedulerConfig& config,
+            bool graph_decode = false);
   uint64_t submit(const std::vector<uint32_t>& prompt, size_t max_new_tokens, std::optional<uint32_t> stop_token);
   std::optional<std::pair<BatchKind, std::vector<uint64_t>>> plan_next_tick() const;
   std::optional<TickReport> execute_next_tick();
@@ -359,6 +403,7 @@ class Scheduler {
   std::array<double, 4> last_tick_profile() const { return tick_profile_; }
   const PrefixBlockManager& block_manager() const { return block_manager_; }
   const BlockPool& pool() const { return *pool_; }
+  const ForwardExecutor& executor() const { return executor_; }
 
  private:
   size_t index_of(uint64_t id) const;

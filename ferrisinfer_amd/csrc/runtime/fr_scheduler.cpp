@@ -144,8 +144,9 @@ std::optional<std::pair<uint64_t, size_t>> PrefixIndex::best_match(uint64_t targ
 }
 
 // ----------------------------------------------------------------------------- scheduler
-Scheduler::Scheduler(DeviceModel* model, BlockPool* pool, const SessionConfig& session, const SchedulerConfig& config)
-    : model_(model), pool_(pool), executor_(model, pool), session_(session), config_(config),
+Scheduler::Scheduler(DeviceModel* model, BlockPool* pool, const SessionConfig& session, const SchedulerConfig& config,
+                     bool graph_decode)
+    : model_(model), pool_(pool), executor_(model, pool, graph_decode), session_(session), config_(config),
       prefix_index_(config.min_prefix_share_tokens) {
   if (config.max_batch_size == 0) fail(ErrorKind::InvalidConfig, "scheduler max_batch_size must be greater than zero");
   if (config.max_prefill_chunk_tokens == 0) {

@@ -31,7 +31,8 @@ class RuntimeConfig(C.Structure):
                 ("min_prefix_share_tokens", C.c_int64), ("num_blocks", C.c_int32),
                 ("block_size", C.c_int32), ("kv_dtype", C.c_int32),
                 ("temperature", C.c_float), ("top_k", C.c_int64), ("top_p", C.c_float),
-                ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
+                ("repetition_penalty", C.c_float), ("seed", C.c_uint64),
+                ("weight_dtype", C.c_int32), ("graph_decode", C.c_int32)]
 
 
 _P = C.c_void_p
@@ -60,6 +61,7 @@ def load() -> C.CDLL:
             "fr_generated": [_P, C.c_uint64, _P, _I64, C.POINTER(_I64)],
             "fr_sequence_blocks": [_P, C.c_uint64, _P, _I64, C.POINTER(_I64)],
             "fr_pool_free_count": [_P, C.POINTER(_I64)],
+            "fr_graph_counters": [_P, _P],
             "fr_last_batch_sizes": [_P, _P],
             "fr_last_batch": [_P] + [_P] * 10,
             "fr_last_tick_profile": [_P, _P],
@@ -139,9 +141,10 @@ class Runtime:
                  eps=1e-6, theta=10000.0, rotary_dims=None, tie=False, max_seq=4096,
                  max_gen=512, max_batch=16, max_chunk=256, max_batch_tokens=1024,
                  max_consecutive_prefill=2, min_share=64, num_blocks=4096, block_size=16,
-                 kv_dtype="f32", ordinal=0, sampler=None):
+                 kv_dtype="f32", ordinal=0, sampler=None, weight_dtype="f32", graph_decode=False):
         """sampler: None (greedy) or (temperature, top_k, top_p, seed), the SamplerConfig of
-        every session (runtime/sampler.rs:3-43)."""
+        every session (runtime/sampler.rs:3-43).  weight_dtype "f32" or "bf16": storage of the
+        packed projections and head.  graph_decode: replay decode ticks from HIP graphs."""
         L = load()
         temperature, top_k, top_p, seed = (0.0, 1, 1.0, 0) if sampler is None else sampler
         head_dim = hidden // heads
@@ -150,7 +153,9 @@ class Runtime:
         rc = RuntimeConfig(max_seq, max_gen, max_batch, max_chunk, max_batch_tokens,
                            max_consecutive_prefill, min_share, num_blocks, block_size,
                            DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16,
-                           temperature, top_k, top_p, 1.0, seed)
+                           temperature, top_k, top_p, 1.0, seed,
+                           DTYPE_F32 if weight_dtype == "f32" else DTYPE_BF16,
+                           1 if graph_decode else 0)
         h = _P()
         _check(L.fr_create(ordinal, C.byref(mc), C.byref(rc), C.byref(h)))
         self.h = h
@@ -166,6 +171,12 @@ class Runtime:
             self.close()
         except Exception:
             pass
+
+    def graph_counters(self) -> dict:
+        """Decode ticks replayed from graphs, graphs captured, graphs dropped."""
+        out = np.zeros(3, np.uint64)
+        _check(load().fr_graph_counters(self.h, _addr(out)))
+        return dict(replays=int(out[0]), captures=int(out[1]), drops=int(out[2]))
 
     def set_weight(self, name, array):
         a = np.ascontiguousarray(np.asarray(array, dtype=np.float32)).reshape(-1)

@@ -87,6 +87,28 @@ void* fi_ctx_stream(fi_context* ctx);
 int32_t fi_device_info(fi_context* ctx, char* name, size_t name_len, char* arch, size_t arch_len,
                        uint64_t* hbm_bytes, int32_t* compute_units);
 
+/* ---------------------------------------------------------------- graph capture
+ * BackendCapabilities.graph_capture (kernel/backend.rs:3-10) and the roadmap's graph capture of
+ * the decode step (docs/performance-roadmap.md:321-326; the reference backend captures nothing).
+ * fi_graph_begin starts capturing the context's stream (which must not be the null stream);
+ * every op enqueued on the context until fi_graph_end is recorded instead of run.  fi_graph_end
+ * instantiates the recording (out = NULL discards it); fi_graph_launch replays it on the
+ * context's stream with the device pointers and scalar arguments it was recorded with (device
+ * memory contents, e.g. re-uploaded batch metadata, may change between replays).  While a capture
+ * is open, calls that allocate, copy to or from the host or wait (fi_buf_*, fi_ctx_sync,
+ * fi_ctx_check_faults) return Runtime, and an op that would grow the context workspace returns
+ * Runtime instead; run such a launch once outside capture first. */
+typedef struct fi_graph fi_graph;
+int32_t fi_graph_begin(fi_context* ctx);
+int32_t fi_graph_end(fi_context* ctx, fi_graph** out);
+int32_t fi_graph_launch(fi_context* ctx, fi_graph* graph);
+int32_t fi_graph_destroy(fi_graph* graph);
+
+/* Counts reallocations of the context workspace (ops that split K or the decode partials of
+ * fi_attn_decode_paged live there).  A graph recorded at generation g reads the workspace of
+ * generation g: replay it only while the generation is unchanged. */
+int32_t fi_ctx_workspace_generation(fi_context* ctx, uint64_t* generation);
+
 /* ---------------------------------------------------------------- memory */
 
 /* Device allocation; rejects 0 bytes like validate_buffer_len (kernel/gpu/nvidia.rs:910-919). */

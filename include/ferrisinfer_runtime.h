@@ -54,6 +54,13 @@ typedef struct fr_runtime_config {
   float top_p;
   float repetition_penalty; /* carried, unused by the sampler (as in the reference) */
   uint64_t seed;
+  /* Storage of the packed projection weights and head: FI_DTYPE_F32 (fi_gemm_packed) or
+   * FI_DTYPE_BF16 (fi_gemm_bf16: weights rounded to nearest even at packing, exact for bf16
+   * checkpoints, which the reference widens at load, io/safetensors.rs:540-542). */
+  int32_t weight_dtype;
+  /* Non-zero: decode ticks replay HIP graphs of their launch sequence (fi_graph_*), captured
+   * per (batch size, context bucket, sampler kind); results are the eager path's. */
+  int32_t graph_decode;
 } fr_runtime_config;
 
 const char* fr_last_error(void);
@@ -112,6 +119,8 @@ int32_t fr_generated(void* runtime, uint64_t sequence_id, uint32_t* out, int64_t
 int32_t fr_sequence_blocks(void* runtime, uint64_t sequence_id, int32_t* out, int64_t capacity,
                            int64_t* n_out);
 int32_t fr_pool_free_count(void* runtime, int64_t* out);
+/* Decode ticks replayed from graphs, graphs captured, graphs dropped (buffers moved). */
+int32_t fr_graph_counters(void* runtime, uint64_t* out3);
 /* The last packed batch: sizes = [T, B, max_blocks, copies, kind, max_query_len,
  * max_context_len]; then its arrays (token ids, positions, slot mapping, cu_seqlens, context
  * lengths, block tables [B, max_blocks], copy-on-write src/dst/count, sequence ids). */

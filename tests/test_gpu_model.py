@@ -339,3 +339,65 @@ def test_c4_qwen2_shape_reaches_decode_batch_64(orc):
     assert sum(1 for kind, us in ticks if kind == 1 and len(us) == 64) >= 7
     print(f"C4 batch 64: {len(ticks)} ticks, near ties {ties}", flush=True)
     assert gpu.pool_free_count() == 512
+
+
+def bf16_rounded(orc, weights):
+    """The weights a bf16 checkpoint holds: every matrix rounded to bf16 (nearest even) and
+    widened back, which is what the reference's loader hands its f32 kernels
+    (io/safetensors.rs:540-542); vectors (norms, biases) stay f32."""
+    return {k: (orc.bf16_to_f32(orc.f32_to_bf16(v)) if np.ndim(v) == 2 else v) for k, v in weights.items()}
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_bf16_weight_runtime_tracks_reference(orc, kv_dtype):
+    """The runtime serving bf16-stored projection weights and head (weight_dtype "bf16",
+    fi_gemm_bf16 / fi_gemm_bf16_swiglu / fi_lm_head_argmax_bf16), over an f32 or bf16 KV pool,
+    against the oracle scheduler on the same bf16-valued weights in f32.  Ticks, reports and
+    every tick's packing are exact; greedy tokens equal the reference's except where its top-2
+    logit gap is within the bf16 activation rounding (2e-2 relative), after which that sequence
+    is not compared further.  The graph-replayed runtime on the same weights equals the eager
+    one bit for bit."""
+    from test_gpu_graph import assert_same_run, make_runtime
+
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1, c1_requests, random_weights
+
+    print(f"bf16 weights runtime kv={kv_dtype}", flush=True)
+    cfg = dict(TINY_LLAMA_C1, layers=2)
+    weights = bf16_rounded(orc, random_weights(cfg, seed=21))
+    model = orc.Model(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
+                      cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
+                      tie=cfg["tie"])
+    model.set_weights(weights)
+    ref = orc.Scheduler(model, page_size=16)
+    ref.attach_packer(4096, 16)
+    gpu = make_runtime(cfg, weights, False, {}, weight_dtype="bf16", kv_dtype=kv_dtype)
+    requests = c1_requests(5)
+    rpacks, gpacks = [], []
+    rid, rticks = drive(ref, requests, rpacks)
+    gid, gticks = drive(gpu, requests, gpacks)
+    assert rid == gid and len(rticks) == len(gticks)
+    for i, (a, b) in enumerate(zip(rpacks, gpacks)):
+        for key in PACK_KEYS:
+            assert np.array_equal(a[key], b[key]), (i, key)
+    for (rk, ru), (gk, gu) in zip(rticks, gticks):
+        assert rk == gk
+        for a, b in zip(ru, gu):
+            for key in ("sequence_id", "reused", "appended", "phase", "finish_reason"):
+                assert a[key] == b[key], (key, a, b)
+    matched = 0
+    for seq, (prompt, _) in zip(rid, requests):
+        r, g = ref.generated(seq), gpu.generated(seq)
+        assert len(r) == len(g)
+        for i, (a, b) in enumerate(zip(r, g)):
+            if a != b:
+                logits = model.forward_logits(np.asarray(list(prompt) + r[:i], np.uint32))[-1]
+                top = np.sort(logits)[-2:]
+                assert float(top[1] - top[0]) <= 2e-2 * max(1.0, abs(float(top[1]))), (seq, i, a, b)
+                break
+            matched += 1
+    print(f"bf16 weights: {matched} tokens matched before any near tie", flush=True)
+    assert matched >= len(requests) * 8
+    assert gpu.pool_free_count() == 4096
+    eager = make_runtime(cfg, weights, False, {}, weight_dtype="bf16", kv_dtype=kv_dtype)
+    graph = make_runtime(cfg, weights, True, {}, weight_dtype="bf16", kv_dtype=kv_dtype)
+    assert_same_run(eager, graph, requests)
