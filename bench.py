@@ -378,13 +378,66 @@ def hf_load(seed):
             "load_gbs": round(nbytes / t_load / 1e9, 2), "first_submit_pack_s": round(t_pack, 3)}
 
 
-def c4_continuous(seed, n_requests, sampler=None):
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def c4_model_bytes_flops(cfg, weight_bytes):
+    """Per decode token: the projection and head weights every tick streams (bytes at the given
+    storage width) and their multiply-adds (2 FLOPs per weight per token)."""
+    h, f, v = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
+    kvw = cfg["kv_heads"] * (h // cfg["heads"])
+    per_layer = h * (h + 2 * kvw) + h * h + 2 * h * f + f * h
+    params = cfg["layers"] * per_layer + v * h
+    return params * weight_bytes, 2 * params
+
+
+def c4_roofline(cfg, ticks, weight_bytes, peak_tfs):
+    """Roofline of the decode ticks at batch 64: algorithmic bytes = the weights once per tick +
+    every sequence's K/V (ctx tokens x layers x 2 x Hkv x D x 4 bytes, f32 pool) + the new K/V rows;
+    FLOPs = 2 x params x 64 + attention 4 x Hq x D x ctx per layer.  The bound is whichever of
+    HBM (8 TB/s) and the MFMA peak of the weight dtype needs more time."""
+    full = [t for t in ticks if t["kind"] == 1 and t["batch"] == 64 and "ctx_sum" in t]
+    if not full:
+        return None
+    d = cfg["hidden"] // cfg["heads"]
+    wbytes, wflops_per_tok = c4_model_bytes_flops(cfg, weight_bytes)
+    kv_per_tok = cfg["layers"] * 2 * cfg["kv_heads"] * d * 4
+    secs = sum(t["seconds"] for t in full)
+    byt = sum(wbytes + t["ctx_sum"] * kv_per_tok for t in full)
+    flops = sum(64 * wflops_per_tok + cfg["layers"] * 4 * cfg["heads"] * d * t["ctx_sum"] for t in full)
+    t_hbm = byt / (HBM_PEAK_GBS * 1e9)
+    t_mfma = flops / (peak_tfs * 1e12)
+    bound = "hbm" if t_hbm >= t_mfma else "mfma"
+    return {
+        "bound": bound,
+        "ticks": len(full),
+        "bytes_per_tick": int(byt / len(full)),
+        "flops_per_tick": int(flops / len(full)),
+        "achieved_gbs": round(byt / secs / 1e9, 1),
+        "achieved_tflops": round(flops / secs / 1e12, 2),
+        "roofline_ms_per_tick": round(max(t_hbm, t_mfma) / len(full) * 1e3, 4),
+        "ms_per_tick": round(secs / len(full) * 1e3, 4),
+        "frac": round(max(t_hbm, t_mfma) / secs, 4),
+        "peaks": {"hbm_gbs": HBM_PEAK_GBS, "mfma_tflops": peak_tfs},
+    }
+
+
+def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"):
     """C4: the Qwen2-0.5B-shaped model (f32, tied, q/k/v biases, random N(0, 0.02) weights)
     served by the GPU runtime under continuous batching (max batch 64, block 16, the
     reference scheduler's other defaults), Poisson arrivals at 8 req/s on 50 ms virtual
     ticks.  Decode tok/s = generated tokens / summed decode-tick wall time, the reference's
     continuous-batching definition (cli/main.rs:1502-1512, 1619-1622).  sampler: None for
-    greedy sessions, or (temperature, top_k, top_p, seed) for sampled ones."""
+    greedy sessions, or (temperature, top_k, top_p, seed) for sampled ones; graph: decode ticks
+    replayed from HIP graphs; weight_dtype: storage of the packed projections and head."""
     import numpy as np
 
     from ferrisinfer_amd.runtime import Runtime
@@ -394,7 +447,8 @@ def c4_continuous(seed, n_requests, sampler=None):
     weights = random_weights(cfg, seed=seed, qkv_bias=True)
     rt = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
                  cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"], tie=True, max_seq=4096,
-                 max_gen=512, max_batch=64, num_blocks=16384, block_size=16, sampler=sampler)
+                 max_gen=512, max_batch=64, num_blocks=16384, block_size=16, sampler=sampler,
+                 graph_decode=graph, weight_dtype=weight_dtype)
     rt.set_weights(weights)
     del weights
     # warm-up: one short request through prefill and decode (module load, first launches)
@@ -414,7 +468,8 @@ def c4_continuous(seed, n_requests, sampler=None):
                     "ticks, prompts lognormal(median 512, sigma 0.5) clipped [1,2048], outputs "
                     "U[64,256], " + ("greedy" if sampler is None else
                                      "sampled (temperature, top_k, top_p, seed) = " + str(sampler))
-                    + ", max batch 64, block 16, f32 weights+KV",
+                    + f", max batch 64, block 16, {weight_dtype} weights, f32 KV, decode ticks "
+                    + ("replayed from HIP graphs" if graph else "enqueued eagerly"),
         "decode_tok_s": round(rep["decode_tok_s"], 1),
         "decode_tok_s_at_batch_64": round(64 * len(full) / full_s, 1) if full_s > 0 else None,
         "ms_per_decode_tick_at_batch_64": round(full_s / len(full) * 1e3, 3) if full else None,
@@ -426,7 +481,11 @@ def c4_continuous(seed, n_requests, sampler=None):
         "decode_ticks_at_batch_64": len(full),
         "decode_tick_host_ms": split,
         "wall_s": round(wall, 3),
+        "roofline_at_batch_64": c4_roofline(cfg, rep["ticks"], 4 if weight_dtype == "f32" else 2,
+                                            FP32_PEAK_TFS if weight_dtype == "f32" else BF16_PEAK_TFS),
     }
+    if graph:
+        out["graph_counters"] = rt.graph_counters()
     rt.close()
     return out
 
@@ -552,7 +611,9 @@ def c5_step(seed, steps):
 
 def c4_cpu_baseline(seed, threads):
     """The oracle's restatement of the reference (per-sequence sessions, its thread fan-out)
-    on a declared C4 subset: the first 4 requests, prompts cut to 64 tokens, 8 new tokens."""
+    on a fixed 64-sequence decode window: the first 64 C4 requests with prompts cut to 16 tokens
+    (one prefill tick) and 2 new tokens each, so both decode ticks run at batch 64 like the GPU
+    figure it sits next to; tok/s by the reference's definition (generated / decode-tick time)."""
     import oracle
     from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, random_weights, run_continuous
 
@@ -563,19 +624,22 @@ def c4_cpu_baseline(seed, threads):
                          cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
                          tie=True)
     model.set_weights(random_weights(cfg, seed=seed, qkv_bias=True))
-    reqs = c4_requests(seed=seed)[:4]
+    reqs = c4_requests(seed=seed)[:64]
     for r in reqs:
-        r["prompt"] = r["prompt"][:64]
-        r["max_new_tokens"] = 8
-    rep = run_continuous(oracle.Scheduler(model, max_batch=64), reqs)
+        r["prompt"] = r["prompt"][:16]
+        r["max_new_tokens"] = 2
+        r["arrival_tick"] = 0
+    rep = run_continuous(oracle.Scheduler(model, max_batch=64, max_seq=64), reqs)
     return {
         "value": round(rep["decode_tok_s"], 3),
         "unit": "decode tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": "C4 model, first 4 C4 requests with prompts cut to 64 tokens, 8 new tokens "
-                  f"each ({rep['generated_tokens']} decode tokens over {rep['decode_ticks']} "
-                  f"ticks); host {os.cpu_count()} cpus",
+        "sample": "C4 model, fixed 64-sequence decode window: the first 64 C4 requests with prompts "
+                  f"cut to 16 tokens, 2 decode ticks at batch 64 ({rep['generated_tokens']} decode "
+                  f"tokens over {rep['decode_ticks']} ticks); host {os.cpu_count()} cpus, "
+                  f"{cpu_model()}",
+        "avg_decode_batch": round(rep["avg_decode_batch"], 2),
         "prefill_tok_s": round(rep["prefill_tok_s"], 2),
     }
 
@@ -662,8 +726,11 @@ def main():
         "vs_baseline": None,
         "dtype": "f32" if args.kv_dtype == "f32" else "f32 compute, bf16 KV",
         "data": "synthetic (seeded numpy PCG64, N(0,1) Q/K/V)",
+        "value_is": "C2 paged-attention op rate: 64 query tokens per fi_attn_decode_paged launch "
+                    "(one layer's decode attention over the batch) / wall time per launch; the model-"
+                    "level decode rate is c4_decode_tok_s_at_batch_64",
         "config": {
-            "workload": "C2 paged decode attention: 64 ragged seqs, L~U[128,2048] "
+            "workload": "C2 paged decode attention (one layer's op): 64 ragged seqs, L~U[128,2048] "
                         f"(sum L={int(wl.context_lens.sum())}), Hq=32, Hkv=8, D=128, block 16, "
                         f"8192-block pool, {args.kv_dtype} KV",
             "global_batch": wl.num_seqs,
@@ -682,7 +749,7 @@ def main():
             "algorithmic_bytes_per_launch": alg_bytes,
             "avg_launch_us": round(kernel_ms * 1e3, 3),
         },
-        "device": info,
+        "device": dict(info, host_cpu=cpu_model(), host_cpus=os.cpu_count()),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_reps)
@@ -693,14 +760,20 @@ def main():
     ctx.close()
     if not args.no_c4:
         print("bench: C4 continuous batching on the GPU runtime", file=sys.stderr, flush=True)
-        result["c4"] = c4_continuous(args.seed, args.c4_requests)
+        keys = ("workload", "decode_tok_s", "decode_tok_s_at_batch_64", "ms_per_decode_tick_at_batch_64",
+                "prefill_tok_s", "generated_tokens", "decode_tick_host_ms", "roofline_at_batch_64")
+        result["c4"] = c4_continuous(args.seed, args.c4_requests, graph=True)
+        # the same requests with every decode tick enqueued launch by launch
+        eager = c4_continuous(args.seed, args.c4_requests, graph=False)
+        result["c4"]["eager"] = {k: eager[k] for k in keys}
         # the same requests under the reference's chat_default sampler (sampler.rs:30-37):
         # logits head + device sampling in every tick
-        sampled = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42))
-        result["c4"]["sampled_chat_default"] = {
-            k: sampled[k] for k in ("workload", "decode_tok_s", "decode_tok_s_at_batch_64",
-                                    "ms_per_decode_tick_at_batch_64", "prefill_tok_s",
-                                    "generated_tokens", "decode_tick_host_ms")}
+        sampled = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42), graph=True)
+        result["c4"]["sampled_chat_default"] = {k: sampled[k] for k in keys}
+        # bf16-stored projections and head (the storage of the real Qwen2.5-0.5B checkpoints)
+        b16 = c4_continuous(args.seed, args.c4_requests, graph=True, weight_dtype="bf16")
+        result["c4"]["bf16_weights"] = {k: b16[k] for k in keys}
+        result["c4_decode_tok_s_at_batch_64"] = result["c4"]["decode_tok_s_at_batch_64"]
         if not args.no_cpu_baseline:
             print("bench: C4 CPU baseline (oracle, declared subset)", file=sys.stderr, flush=True)
             result["c4"]["cpu_baseline"] = c4_cpu_baseline(args.seed, min(16, os.cpu_count() or 1))

@@ -16,6 +16,8 @@ enum : uint32_t {
   FI_FAULT_SAMPLE_TOPK = 1u << 3,       // sampling: top_k (after clamping to the vocabulary) above 1024
   FI_FAULT_SAMPLE_NONFINITE = 1u << 4,  // sampling: the candidate weights do not sum to a finite, positive total
   FI_FAULT_CONTEXT_RANGE = 1u << 5,     // decode attention: a context length beyond the partitions max_context_len sized
+  FI_FAULT_QUERY_RANGE = 1u << 6,       // prefill attention: a query length beyond the tiles max_query_len sized
+  FI_FAULT_POSITION_RANGE = 1u << 7,    // RoPE: a position outside the cos/sin table
 };
 
 struct fi_context {

@@ -277,6 +277,8 @@ int32_t fi_ctx_check_faults(fi_context* ctx) {
   if (bits & FI_FAULT_SAMPLE_TOPK) msg += " sampling top_k above the device limit of 1024;";
   if (bits & FI_FAULT_SAMPLE_NONFINITE) msg += " failed to build a finite sampling distribution;";
   if (bits & FI_FAULT_CONTEXT_RANGE) msg += " context length beyond max_context_len;";
+  if (bits & FI_FAULT_QUERY_RANGE) msg += " query length beyond max_query_len (its rows past the tiles were not computed);";
+  if (bits & FI_FAULT_POSITION_RANGE) msg += " position outside the RoPE table;";
   return fi::set_error(FI_ERR_RUNTIME, msg);
 }
 

@@ -591,6 +591,20 @@ __device__ __forceinline__ void put_kv(KVT* cache, size_t idx, float x) {
   }
 }
 
+// Four consecutive pool elements from one 16-byte (f32) or 8-byte (bf16) store; idx is a
+// multiple of 4 (the pool's rows are D elements, D a multiple of 4).
+template <typename KVT>
+__device__ __forceinline__ void put_kv4(KVT* cache, size_t idx, const float4& x) {
+  if constexpr (sizeof(KVT) == 4) {
+    *reinterpret_cast<float4*>(cache + idx) = x;
+  } else {
+    uint2 w;
+    w.x = fi::f32_to_bf16_bits(x.x) | (fi::f32_to_bf16_bits(x.y) << 16);
+    w.y = fi::f32_to_bf16_bits(x.z) | (fi::f32_to_bf16_bits(x.w) << 16);
+    *reinterpret_cast<uint2*>(cache + idx) = w;
+  }
+}
+
 template <typename KVT>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float* __restrict__ parts, int splits, const float* __restrict__ bias_q, const float* __restrict__ bias_k,
@@ -636,7 +650,7 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
 #pragma clang fp contract(off)
       int pos = positions[t];
       if (pos < 0 || pos >= max_positions) {
-        if (idx == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+        if (idx == 0) atomicOr(faults, FI_FAULT_POSITION_RANGE);
         pos = 0;
       }
       const float lo = value(col0 + r), hi = value(col0 + r + half);
@@ -695,11 +709,7 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
     if (head < hq) {
       *reinterpret_cast<float4*>(q_out + (size_t)t * qw + head * d + i) = x;
     } else if (write_kv) {
-      const size_t base = (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i;
-      put_kv(k_cache, base, x.x);
-      put_kv(k_cache, base + 1, x.y);
-      put_kv(k_cache, base + 2, x.z);
-      put_kv(k_cache, base + 3, x.w);
+      put_kv4(k_cache, (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i, x);
     }
   };
   if (idx < rot_items) {
@@ -709,7 +719,7 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
 #pragma clang fp contract(off)
       int pos = positions[t];
       if (pos < 0 || pos >= max_positions) {
-        if (idx == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+        if (idx == 0) atomicOr(faults, FI_FAULT_POSITION_RANGE);
         pos = 0;
       }
       const float4 lo = value4(col0 + r), hi = value4(col0 + r + half);
@@ -727,11 +737,7 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
     const int v = 4 * (idx - rot_items);
     const int h = v / d, i = v - h * d;
     const float4 x = value4(qw + kw + v);
-    const size_t base = (((size_t)blk * hkv + h) * block_size + off) * d + i;
-    put_kv(v_cache, base, x.x);
-    put_kv(v_cache, base + 1, x.y);
-    put_kv(v_cache, base + 2, x.z);
-    put_kv(v_cache, base + 3, x.w);
+    put_kv4(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i, x);
   }
 }
 

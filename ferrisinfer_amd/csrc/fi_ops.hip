@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kRowThreads) void rope_kernel(float* __restrict__ q
   const int t = blockIdx.x;
   const int pos = positions[t];
   if (pos < 0 || pos >= max_positions) {
-    if (threadIdx.x == 0) atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+    if (threadIdx.x == 0) atomicOr(faults, FI_FAULT_POSITION_RANGE);
     return;
   }
   const float* ct = cos_t + (size_t)pos * pairs;

@@ -57,12 +57,16 @@ struct PrefillArgs {
 // which no result depends on; tiles past a sequence's end sort last).
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int* __restrict__ cu, const int* __restrict__ ctxl,
                                                             int num_seqs, int ntiles, int qt_rows, int kb,
-                                                            int* __restrict__ order) {
+                                                            int* __restrict__ order, uint32_t* __restrict__ faults) {
   __shared__ int hist[1024];
   __shared__ int part[1024];
   const int tid = threadIdx.x;
   const int total = num_seqs * ntiles;
   hist[tid] = 0;
+  // a query length beyond the tiles that max_query_len sized: its tail rows get no workgroup
+  for (int s = tid; s < num_seqs; s += 1024) {
+    if (cu[s + 1] - cu[s] > ntiles * qt_rows) atomicOr(faults, FI_FAULT_QUERY_RANGE);
+  }
   __syncthreads();
   auto bucket = [&](int t) {  // 0 = past the sequence's end, else chunks + 1 (capped)
     const int seq = t / ntiles, qt = t - (t / ntiles) * ntiles;
@@ -349,7 +353,7 @@ int32_t plan_tiles(fi_context* ctx, PrefillArgs& args, int qt, int kb, const cha
   FI_TRY(fi::ensure_workspace(ctx, (size_t)pairs * sizeof(int)));
   int* order = static_cast<int*>(ctx->workspace);
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, ctx->stream, args.cu_seqlens, args.context_lens,
-                     args.num_seqs, ntiles, qt, kb, order);
+                     args.num_seqs, ntiles, qt, kb, order, ctx->d_faults);
   FI_CHECK_LAUNCH("prefill_plan_kernel");
   args.order = order;
   *grid = dim3(static_cast<unsigned>(pairs * args.hkv));

@@ -268,6 +268,10 @@ class Runtime:
         return dict(schedule=float(out[0]), enqueue=float(out[1]), wait=float(out[2]),
                     total=float(out[3]))
 
+    def last_batch_context_sum(self) -> int:
+        """Sum of the context lengths of the last tick's packed batch (its KV tokens read)."""
+        return int(self.last_batch()["context_lens"].sum())
+
     def last_batch(self) -> dict:
         L = load()
         sizes = np.zeros(7, np.int64)

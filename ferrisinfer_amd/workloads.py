@@ -291,6 +291,8 @@ def run_continuous(sched, requests: list, max_ticks: int | None = None) -> dict:
                           seconds=sched.last_tick_seconds))
         if hasattr(sched, "last_tick_profile"):
             ticks[-1]["profile"] = sched.last_tick_profile()
+        if hasattr(sched, "last_batch_context_sum"):
+            ticks[-1]["ctx_sum"] = sched.last_batch_context_sum()
         tick_index += 1
     dec = [t for t in ticks if t["kind"] == 1]
     pre = [t for t in ticks if t["kind"] == 0]

@@ -193,8 +193,10 @@ int32_t fi_attn_decode_paged_noalloc(fi_context* ctx, const float* d_q, const vo
  * block_tables (the chunk's own K/V rows must already be appended).  Replaces
  * causal_self_attention_f32 / cached_prefixed_causal_attention_f32 with the paged prefix
  * gather (kernel/cpu/attention.rs:222-518, runtime/reference.rs:425-465,
- * runtime/paged_kv.rs:769-791).  max_query_len must bound every qlen_b (it sizes the grid);
- * q, out and the pools must be 16-byte aligned (InvalidLayout otherwise). */
+ * runtime/paged_kv.rs:769-791).  max_query_len must bound every qlen_b (it sizes the grid); a
+ * longer qlen_b is reported as Runtime by fi_ctx_check_faults and its rows past the tiles that
+ * max_query_len sized are left unwritten.  q, out and the pools must be 16-byte aligned
+ * (InvalidLayout otherwise). */
 int32_t fi_attn_prefill_paged(fi_context* ctx, const float* d_q, const void* d_k_cache,
                               const void* d_v_cache, int32_t kv_dtype,
                               const int32_t* d_block_tables, int32_t max_blocks_per_seq,
@@ -244,7 +246,9 @@ int32_t fi_rope_table(fi_context* ctx, int32_t max_positions, int32_t head_dim,
 
 /* Rotates q [T, Hq, D] and k [T, Hkv, D] in place at per-token positions (NeoX half
  * split, products rounded before the add).  Replaces rope_f32 with position_offset
- * (kernel/cpu/attention.rs:165-220) for a ragged batch; bit-identical to the reference. */
+ * (kernel/cpu/attention.rs:165-220) for a ragged batch; bit-identical to the reference.  A
+ * position outside [0, max_positions) leaves its token unrotated and is reported as Runtime by
+ * fi_ctx_check_faults (as in fi_qkv_rope_append). */
 int32_t fi_rope(fi_context* ctx, float* d_q, float* d_k, const int32_t* d_positions,
                 const float* d_cos, const float* d_sin, int32_t num_tokens, int32_t num_q_heads,
                 int32_t num_kv_heads, int32_t head_dim, int32_t rotary_dims,

@@ -122,3 +122,27 @@ def test_silu_mul_and_add(orc, gpu_ctx):
     ref = orc.mul(up, orc.silu(gate))
     assert normwise_error(out.cpu().numpy(), ref) <= 1e-6
     assert np.array_equal(s.cpu().numpy(), orc.add(up, gate))
+
+
+def test_rope_position_outside_table_reported(gpu_ctx):
+    """A position beyond the RoPE table leaves its token unrotated and is reported as Runtime
+    with the position message (not the token-id message)."""
+    import torch
+
+    from ferrisinfer_amd import FerrisError
+
+    d, rot, npos = 32, 32, 16
+    cos_t = torch.empty((npos, rot // 2), device="cuda")
+    sin_t = torch.empty_like(cos_t)
+    gpu_ctx.rope_table(npos, d, rot, 10000.0, cos_t, sin_t)
+    q = torch.ones((2, 2, d), device="cuda")
+    k = torch.ones((2, 1, d), device="cuda")
+    pos = torch.tensor([3, npos + 5], dtype=torch.int32, device="cuda")
+    gpu_ctx.rope(q, k, pos, cos_t, sin_t, rot, npos)
+    torch.cuda.synchronize()
+    with pytest.raises(FerrisError) as e:
+        gpu_ctx.check_faults()
+    assert "position outside the RoPE table" in str(e.value)
+    assert "vocabulary" not in str(e.value)
+    assert torch.equal(q[1], torch.ones_like(q[1]))
+    gpu_ctx.check_faults()

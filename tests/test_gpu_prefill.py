@@ -233,3 +233,35 @@ def test_prefill_c5_chunk_after_cached_prefix(orc, gpu_ctx):
             got16 = out.cpu().numpy()
             assert normwise_error(got16, ref) <= 2e-2
             assert normwise_error(got16, got) <= 5e-3
+
+
+def test_prefill_query_beyond_max_query_len_reported(gpu_ctx):
+    """A cu_seqlens entry longer than max_query_len: the tiles max_query_len sized are computed,
+    the sequence's rows past them are not, and the host gets Runtime with its own message; the
+    other sequence is unaffected."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32, FerrisError
+
+    nb, bs, hkv, hq, d = 64, 16, 2, 4, 64
+    g = torch.Generator().manual_seed(3)
+    kc = torch.randn((nb, hkv, bs, d), generator=g).cuda()
+    vc = torch.randn((nb, hkv, bs, d), generator=g).cuda()
+    qlens = [20, 300]  # the second exceeds max_query_len = 20 by more than any tile size
+    q = torch.randn((sum(qlens), hq, d), generator=g).cuda()
+    cu = torch.tensor([0, 20, 320], dtype=torch.int32).cuda()
+    ctxl = torch.tensor([20, 300], dtype=torch.int32).cuda()
+    bt = torch.arange(2 * 20, dtype=torch.int32).reshape(2, 20).cuda()
+    out = torch.zeros_like(q)
+    gpu_ctx.attn_prefill_paged(q, kc, vc, DTYPE_F32, bt, cu, ctxl, 20, hkv, bs, nb, d ** -0.5, out)
+    torch.cuda.synchronize()
+    with pytest.raises(FerrisError) as e:
+        gpu_ctx.check_faults()
+    assert e.value.kind == "Runtime" and "max_query_len" in str(e.value)
+    gpu_ctx.check_faults()  # flags were cleared
+    solo = torch.zeros_like(q[:20])
+    gpu_ctx.attn_prefill_paged(q[:20].contiguous(), kc, vc, DTYPE_F32, bt[:1].contiguous(), cu[:2].contiguous(),
+                               ctxl[:1].contiguous(), 20, hkv, bs, nb, d ** -0.5, solo)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    assert torch.equal(out[:20], solo)
