@@ -48,6 +48,9 @@ def parse_args():
     p.add_argument("--no-c4", action="store_true",
                    help="skip the C4 (Qwen2-0.5B-shaped) continuous-batching measurement")
     p.add_argument("--c4-requests", type=int, default=128)
+    p.add_argument("--c4-variants", default="graph,eager,sampled,bf16",
+                   help="C4 runs to make (comma list of graph, eager, sampled, bf16); the first "
+                        "listed of graph / eager fills the top-level c4 figures")
     p.add_argument("--no-c5", action="store_true",
                    help="skip the C5 (Llama-3-8B-shaped, bf16 weights and KV) decode-step measurement")
     p.add_argument("--c5-steps", type=int, default=5)
@@ -762,17 +765,22 @@ def main():
         print("bench: C4 continuous batching on the GPU runtime", file=sys.stderr, flush=True)
         keys = ("workload", "decode_tok_s", "decode_tok_s_at_batch_64", "ms_per_decode_tick_at_batch_64",
                 "prefill_tok_s", "generated_tokens", "decode_tick_host_ms", "roofline_at_batch_64")
-        result["c4"] = c4_continuous(args.seed, args.c4_requests, graph=True)
-        # the same requests with every decode tick enqueued launch by launch
-        eager = c4_continuous(args.seed, args.c4_requests, graph=False)
-        result["c4"]["eager"] = {k: eager[k] for k in keys}
-        # the same requests under the reference's chat_default sampler (sampler.rs:30-37):
-        # logits head + device sampling in every tick
-        sampled = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42), graph=True)
-        result["c4"]["sampled_chat_default"] = {k: sampled[k] for k in keys}
-        # bf16-stored projections and head (the storage of the real Qwen2.5-0.5B checkpoints)
-        b16 = c4_continuous(args.seed, args.c4_requests, graph=True, weight_dtype="bf16")
-        result["c4"]["bf16_weights"] = {k: b16[k] for k in keys}
+        variants = [v for v in args.c4_variants.split(",") if v]
+        main_graph = "graph" in variants or "eager" not in variants
+        result["c4"] = c4_continuous(args.seed, args.c4_requests, graph=main_graph)
+        if main_graph and "eager" in variants:
+            # the same requests with every decode tick enqueued launch by launch
+            eager = c4_continuous(args.seed, args.c4_requests, graph=False)
+            result["c4"]["eager"] = {k: eager[k] for k in keys}
+        if "sampled" in variants:
+            # the same requests under the reference's chat_default sampler (sampler.rs:30-37):
+            # logits head + device sampling in every tick
+            sampled = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42), graph=main_graph)
+            result["c4"]["sampled_chat_default"] = {k: sampled[k] for k in keys}
+        if "bf16" in variants:
+            # bf16-stored projections and head (the storage of the real Qwen2.5-0.5B checkpoints)
+            b16 = c4_continuous(args.seed, args.c4_requests, graph=main_graph, weight_dtype="bf16")
+            result["c4"]["bf16_weights"] = {k: b16[k] for k in keys}
         result["c4_decode_tok_s_at_batch_64"] = result["c4"]["decode_tok_s_at_batch_64"]
         if not args.no_cpu_baseline:
             print("bench: C4 CPU baseline (oracle, declared subset)", file=sys.stderr, flush=True)

@@ -605,6 +605,15 @@ __device__ __forceinline__ void put_kv4(KVT* cache, size_t idx, const float4& x)
   }
 }
 
+// The split-K sum of one column of the fused q|k|v partials (splits added in order) plus its
+// bias, if any.
+__device__ __forceinline__ float qkv_value(const float* __restrict__ p0, size_t plane, int splits,
+                                           const float* __restrict__ bias, int bias_col, int col) {
+  float x = p0[col];
+  for (int z = 1; z < splits; ++z) x = x + p0[(size_t)z * plane + col];
+  return bias ? x + bias[bias_col] : x;
+}
+
 template <typename KVT>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float* __restrict__ parts, int splits, const float* __restrict__ bias_q, const float* __restrict__ bias_k,
@@ -625,27 +634,20 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   const int width = qw + 2 * kw;
   const size_t plane = (size_t)tokens * width;
   const float* p0 = parts + (size_t)t * width;
-  auto value = [&](int col) {
-    const float x = sum_splits(p0 + col, plane, splits);
-    const float* b = col < qw ? bias_q : (col < qw + kw ? bias_k : bias_v);
-    const int bc = col < qw ? col : (col < qw + kw ? col - qw : col - qw - kw);
-    return b ? x + b[bc] : x;
-  };
   const int64_t slot = slots[t];
   const bool write_kv = slot >= 0 && slot < pool_slots;
   if (idx == 0 && slot >= pool_slots) atomicOr(faults, FI_FAULT_SLOT_RANGE);
   const int64_t blk = write_kv ? slot / block_size : 0;
   const int off = write_kv ? static_cast<int>(slot % block_size) : 0;
-  auto store = [&](int head, int i, float x) {  // head < hq: q; else k head (head - hq)
-    if (head < hq) {
-      q_out[(size_t)t * qw + head * d + i] = x;
-    } else if (write_kv) {
-      put_kv(k_cache, (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i, x);
-    }
-  };
   if (idx < rot_items) {
     const int head = idx / per_head, r = idx - head * per_head;
-    const int col0 = head < hq ? head * d : qw + (head - hq) * d;
+    const bool is_q = head < hq;
+    if (!is_q && !write_kv) return;
+    const int col0 = is_q ? head * d : qw + (head - hq) * d;
+    const float* bias = is_q ? bias_q : bias_k;
+    const int bcol0 = is_q ? head * d : (head - hq) * d;
+    float* qdst = q_out + (size_t)t * qw + (is_q ? head * d : 0);
+    const size_t kbase = (((size_t)blk * hkv + (is_q ? 0 : head - hq)) * block_size + off) * d;
     if (r < half) {
 #pragma clang fp contract(off)
       int pos = positions[t];
@@ -653,25 +655,51 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
         if (idx == 0) atomicOr(faults, FI_FAULT_POSITION_RANGE);
         pos = 0;
       }
-      const float lo = value(col0 + r), hi = value(col0 + r + half);
+      const float lo = qkv_value(p0, plane, splits, bias, bcol0 + r, col0 + r);
+      const float hi = qkv_value(p0, plane, splits, bias, bcol0 + r + half, col0 + r + half);
       const float c = cos_t[(size_t)pos * half + r], sn = sin_t[(size_t)pos * half + r];
-      store(head, r, lo * c - hi * sn);  // each product rounded before the add, as Rust does
-      store(head, r + half, hi * c + lo * sn);
+      const float y0 = lo * c - hi * sn;  // each product rounded before the add, as Rust does
+      const float y1 = hi * c + lo * sn;
+      if (is_q) {
+        qdst[r] = y0;
+        qdst[r + half] = y1;
+      } else {
+        put_kv(k_cache, kbase + r, y0);
+        put_kv(k_cache, kbase + r + half, y1);
+      }
     } else {
       const int i = 2 * half + (r - half);
-      store(head, i, value(col0 + i));
+      const float y = qkv_value(p0, plane, splits, bias, bcol0 + i, col0 + i);
+      if (is_q) {
+        qdst[i] = y;
+      } else {
+        put_kv(k_cache, kbase + i, y);
+      }
     }
   } else if (write_kv) {
     const int v = idx - rot_items;
     const int h = v / d, i = v - h * d;
-    put_kv(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i, value(qw + kw + v));
+    put_kv(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i,
+           qkv_value(p0, plane, splits, bias_v, v, qw + kw + v));
   }
+}
+
+// The split-K sum of one float4 of the fused q|k|v partials (splits added in order) plus its
+// bias, if any: column col of the [T, Hq*D + 2*Hkv*D] row at p0.
+__device__ __forceinline__ float4 qkv_value4(const float* __restrict__ p0, size_t plane, int splits,
+                                             const float* __restrict__ bias, int bias_col, int col) {
+  const float* p = p0 + col;
+  float4 x = *reinterpret_cast<const float4*>(p);
+  for (int z = 1; z < splits; ++z) x = add(x, *reinterpret_cast<const float4*>(p + (size_t)z * plane));
+  if (bias) x = add(x, *reinterpret_cast<const float4*>(bias + bias_col));
+  return x;
 }
 
 // Four consecutive columns per thread: the same per-element arithmetic as
 // qkv_rope_append_kernel (splits summed in order, bias added, RoPE with each product rounded
 // before the add) on 16-byte loads and stores.  Needs rotary_dims / 2, the pass-through width
 // and D to be multiples of 4 and 16-byte aligned operands (checked by the entry point).
+// Written without closures so that nothing lives in scratch memory.
 template <typename KVT>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
     const float* __restrict__ parts, int splits, const float* __restrict__ bias_q, const float* __restrict__ bias_k,
@@ -690,31 +718,23 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
   if (t >= tokens) return;
   const int idx = gid - t * items;
   const int width = qw + 2 * kw;
-  const size_t plane4 = (size_t)tokens * width / 4;
+  const size_t plane = (size_t)tokens * width;
   const float* p0 = parts + (size_t)t * width;
-  auto value4 = [&](int col) {
-    const float4 x = sum_splits(reinterpret_cast<const float4*>(p0 + col), plane4, splits);
-    const float* b = col < qw ? bias_q : (col < qw + kw ? bias_k : bias_v);
-    const int bc = col < qw ? col : (col < qw + kw ? col - qw : col - qw - kw);
-    if (!b) return x;
-    const float4 bv = *reinterpret_cast<const float4*>(b + bc);
-    return make_float4(x.x + bv.x, x.y + bv.y, x.z + bv.z, x.w + bv.w);
-  };
   const int64_t slot = slots[t];
   const bool write_kv = slot >= 0 && slot < pool_slots;
   if (idx == 0 && slot >= pool_slots) atomicOr(faults, FI_FAULT_SLOT_RANGE);
   const int64_t blk = write_kv ? slot / block_size : 0;
   const int off = write_kv ? static_cast<int>(slot % block_size) : 0;
-  auto store4 = [&](int head, int i, const float4& x) {  // head < hq: q; else k head (head - hq)
-    if (head < hq) {
-      *reinterpret_cast<float4*>(q_out + (size_t)t * qw + head * d + i) = x;
-    } else if (write_kv) {
-      put_kv4(k_cache, (((size_t)blk * hkv + (head - hq)) * block_size + off) * d + i, x);
-    }
-  };
   if (idx < rot_items) {
     const int head = idx / quads_per_head, r = 4 * (idx - head * quads_per_head);
-    const int col0 = head < hq ? head * d : qw + (head - hq) * d;
+    const bool is_q = head < hq;
+    const int col0 = is_q ? head * d : qw + (head - hq) * d;
+    const float* bias = is_q ? bias_q : bias_k;
+    const int bcol0 = is_q ? head * d : (head - hq) * d;
+    // destination of this head's row: q_out, or the K pool row of the token's slot
+    float* qdst = q_out + (size_t)t * qw + (is_q ? head * d : 0);
+    const size_t kbase = (((size_t)blk * hkv + (is_q ? 0 : head - hq)) * block_size + off) * d;
+    if (!is_q && !write_kv) return;
     if (r < half) {
 #pragma clang fp contract(off)
       int pos = positions[t];
@@ -722,21 +742,34 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
         if (idx == 0) atomicOr(faults, FI_FAULT_POSITION_RANGE);
         pos = 0;
       }
-      const float4 lo = value4(col0 + r), hi = value4(col0 + r + half);
+      const float4 lo = qkv_value4(p0, plane, splits, bias, bcol0 + r, col0 + r);
+      const float4 hi = qkv_value4(p0, plane, splits, bias, bcol0 + r + half, col0 + r + half);
       const float4 c = *reinterpret_cast<const float4*>(cos_t + (size_t)pos * half + r);
       const float4 sn = *reinterpret_cast<const float4*>(sin_t + (size_t)pos * half + r);
-      store4(head, r, make_float4(lo.x * c.x - hi.x * sn.x, lo.y * c.y - hi.y * sn.y, lo.z * c.z - hi.z * sn.z,
-                                  lo.w * c.w - hi.w * sn.w));
-      store4(head, r + half, make_float4(hi.x * c.x + lo.x * sn.x, hi.y * c.y + lo.y * sn.y,
-                                         hi.z * c.z + lo.z * sn.z, hi.w * c.w + lo.w * sn.w));
+      const float4 y0 = make_float4(lo.x * c.x - hi.x * sn.x, lo.y * c.y - hi.y * sn.y, lo.z * c.z - hi.z * sn.z,
+                                    lo.w * c.w - hi.w * sn.w);
+      const float4 y1 = make_float4(hi.x * c.x + lo.x * sn.x, hi.y * c.y + lo.y * sn.y, hi.z * c.z + lo.z * sn.z,
+                                    hi.w * c.w + lo.w * sn.w);
+      if (is_q) {
+        *reinterpret_cast<float4*>(qdst + r) = y0;
+        *reinterpret_cast<float4*>(qdst + r + half) = y1;
+      } else {
+        put_kv4(k_cache, kbase + r, y0);
+        put_kv4(k_cache, kbase + r + half, y1);
+      }
     } else {
       const int i = 2 * half + (r - half);
-      store4(head, i, value4(col0 + i));
+      const float4 y = qkv_value4(p0, plane, splits, bias, bcol0 + i, col0 + i);
+      if (is_q) {
+        *reinterpret_cast<float4*>(qdst + i) = y;
+      } else {
+        put_kv4(k_cache, kbase + i, y);
+      }
     }
   } else if (write_kv) {
     const int v = 4 * (idx - rot_items);
     const int h = v / d, i = v - h * d;
-    const float4 x = value4(qw + kw + v);
+    const float4 x = qkv_value4(p0, plane, splits, bias_v, v, qw + kw + v);
     put_kv4(v_cache, (((size_t)blk * hkv + h) * block_size + off) * d + i, x);
   }
 }
