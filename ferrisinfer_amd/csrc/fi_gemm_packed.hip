@@ -23,6 +23,7 @@
 // consumer kernels in split order.  Every summation order is fixed by the shape, so results
 // are deterministic and independent of the batch composition of other rows.
 #include <algorithm>
+#include <type_traits>
 
 #include "fi_common.h"
 #include "fi_device.h"
@@ -380,6 +381,162 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_lds_kernel(PGemmArgs g) {
     }
     if (more) store_a_chunk((c + 1) & 1);
     __syncthreads();
+  }
+  if (slab_id < g.slabs) store_tile<MT, PW, EPI>(g, acc, m0, slab, z, lane);
+}
+
+// ---------------------------------------------------------------------------------------
+// Three-term bf16 kernel.  Each f32 operand is split exactly into three bf16 terms,
+// x = hi + mid + lo (hi = x rounded to nearest even, mid the same of the exact remainder, lo the
+// rest, which has at most 8 significant bits), and a product is the sum of the six terms above
+// 2^-24 relative (hi*hi, hi*mid, mid*hi, hi*lo, lo*hi, mid*mid; the dropped three are below 2^-23
+// together, the size of one f32 rounding) on v_mfma_f32_16x16x32_bf16 with f32 accumulation.
+// Six bf16 MFMAs of 32 k take 96 cycles against 256 for the same k on
+// v_mfma_f32_16x16x4_f32, so the projections keep f32 accuracy at 2.7x the f32 MFMA rate.
+//
+// The weights keep the packed f32 layout above: a 32-k MFMA step takes the two 16-k steps
+// 2s and 2s+1, and lane (i, g) = (lane % 16, lane / 16) feeds k slots 0-3 from step 2s
+// (k = 32s + 4g + e) and 4-7 from step 2s+1 (k = 32s + 16 + 4g + e) for both operands, so the
+// sum runs over the same k set in a permuted slot order.  The four waves of a workgroup own
+// four consecutive slabs and share the activation block: chunks of KC 32-k steps of A are
+// loaded once per workgroup, split into their three bf16 terms and stored in LDS in fragment
+// order (one 16-byte read per lane per term); each wave streams its slab through a register
+// ring of B loads DEPTH steps ahead and splits them on use.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void split3(const f32x8& x, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+  hi = __builtin_convertvector(x, bf16x8);
+  const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
+  mid = __builtin_convertvector(r1, bf16x8);
+  const f32x8 r2 = r1 - __builtin_convertvector(mid, f32x8);
+  lo = __builtin_convertvector(r2, bf16x8);
+}
+
+__device__ __forceinline__ v4f mfma_s3(const bf16x8& ah, const bf16x8& am, const bf16x8& al, const bf16x8& bh,
+                                       const bf16x8& bm, const bf16x8& bl, v4f acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bm, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bm, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+template <int MT, int PW, int EPI, bool KTAIL>
+__global__ __launch_bounds__(kThreads, 2) void gemm_s3_kernel(PGemmArgs g) {
+  using BV = typename PVec<PW>::T;
+  constexpr int KC = 2;                 // 32-k steps per staged A chunk
+  constexpr int R = 2 * KC;             // B ring slots span two chunks: slot of step j of chunk c = (c % 2) KC + j
+  constexpr int DEPTH = R - 1;          // B steps in flight ahead of the MFMAs
+  constexpr int FRAGS = KC * MT * 64;   // A fragments (8 k of one row) per chunk
+  constexpr int F_PER_T = (FRAGS + kThreads - 1) / kThreads;
+  __shared__ bf16x8 s_a[2][3][FRAGS];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int slab_id = blockIdx.x * kWaves + w;
+  const int slab = min(slab_id, g.slabs - 1);  // a short last group still loads valid data
+  const int m0 = blockIdx.y * 16 * MT, z = blockIdx.z;
+  const int q0 = z * g.q_per_split;
+  const int q1 = min(g.q_total, q0 + g.q_per_split);
+  const int nsteps = (q1 - q0 + 1) / 2;  // 32-k steps; an odd last 16-k step is zero-padded
+  const int nchunks = (nsteps + KC - 1) / KC;
+
+  // fragment f = (j * MT + mt) * 64 + ln: row m0 + 16mt + ln % 16, k slots of 32-k step j of the
+  // chunk for lane group ln / 16
+  float4 areg[F_PER_T][2];
+  auto load_a_chunk = [&](int c) {
+#pragma unroll
+    for (int r = 0; r < F_PER_T; ++r) {
+      const int f = tid + r * kThreads;
+      const int j = f / (MT * 64), mt = (f / 64) % MT, ln = f % 64;
+      const int row = min(m0 + 16 * mt + (ln & 15), g.m - 1);
+      const float* arow = g.a + (size_t)row * g.lda + 4 * (ln >> 4);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int q = q0 + 2 * (c * KC + j) + h;
+        const float4 x = load_a<KTAIL>(arow, 16 * min(q, q1 - 1), g.k - 4 * (ln >> 4));
+        const bool ok = q < q1 && f < FRAGS;
+        areg[r][h] = ok ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  auto store_a_chunk = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < F_PER_T; ++r) {
+      const int f = tid + r * kThreads;
+      if (FRAGS % kThreads == 0 || f < FRAGS) {
+        const f32x8 x = {areg[r][0].x, areg[r][0].y, areg[r][0].z, areg[r][0].w,
+                         areg[r][1].x, areg[r][1].y, areg[r][1].z, areg[r][1].w};
+        bf16x8 hi, mid, lo;
+        split3(x, hi, mid, lo);
+        s_a[buf][0][f] = hi;
+        s_a[buf][1][f] = mid;
+        s_a[buf][2][f] = lo;
+      }
+    }
+  };
+
+  const BV* bbase = reinterpret_cast<const BV*>(g.bp) + (size_t)slab * g.q_total * 4 * 64 + lane;
+  BV rb[R][2][4];
+  auto issue_b = [&](int s, int slot) {  // 32-k step s of the split: 16-k steps q0 + 2s, q0 + 2s + 1
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q = min(q0 + 2 * s + h, q1 - 1);  // clamped refetches hit the cache (and A is zero there)
+      const BV* bq = bbase + (size_t)q * 4 * 64;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rb[slot][h][e] = bq[e * 64];
+    }
+  };
+
+  v4f acc[MT][PW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int p = 0; p < PW; ++p) acc[mt][p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // one chunk: cs is the chunk's ring half (compile time)
+  auto chunk = [&](int c, auto cs_tag) {
+    constexpr int cs = decltype(cs_tag)::value;
+    const bool more = c + 1 < nchunks;  // workgroup-uniform
+    if (more) load_a_chunk(c + 1);
+    const bf16x8* sa = s_a[c & 1][0];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int s = c * KC + j;
+      issue_b(s + DEPTH, (cs * KC + j + DEPTH) % R);
+      sched_fence();
+      if (s < nsteps) {
+#pragma unroll
+        for (int p = 0; p < PW; ++p) {
+          const int slot = cs * KC + j;
+          const f32x8 x = {PVec<PW>::get(rb[slot][0][0], p), PVec<PW>::get(rb[slot][0][1], p),
+                           PVec<PW>::get(rb[slot][0][2], p), PVec<PW>::get(rb[slot][0][3], p),
+                           PVec<PW>::get(rb[slot][1][0], p), PVec<PW>::get(rb[slot][1][1], p),
+                           PVec<PW>::get(rb[slot][1][2], p), PVec<PW>::get(rb[slot][1][3], p)};
+          bf16x8 bh, bm, bl;
+          split3(x, bh, bm, bl);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int f = (j * MT + mt) * 64 + lane;
+            acc[mt][p] = mfma_s3(sa[f], sa[FRAGS + f], sa[2 * FRAGS + f], bh, bm, bl, acc[mt][p]);
+          }
+        }
+      }
+      sched_fence();
+    }
+    if (more) store_a_chunk((c + 1) & 1);
+    __syncthreads();
+  };
+
+  load_a_chunk(0);
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue_b(d, d);
+  store_a_chunk(0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; c += 2) {
+    chunk(c, std::integral_constant<int, 0>{});
+    if (c + 1 < nchunks) chunk(c + 1, std::integral_constant<int, 1>{});
   }
   if (slab_id < g.slabs) store_tile<MT, PW, EPI>(g, acc, m0, slab, z, lane);
 }
@@ -826,7 +983,13 @@ void launch_one(fi_context* ctx, const PGemmArgs& g, const Plan& p, unsigned spl
   if constexpr (PW <= 2) {
     if (p.shared) {
       dim3 grid(static_cast<unsigned>((g.slabs + kWaves - 1) / kWaves), p.mblocks, splits);
-      hipLaunchKernelGGL((gemm_lds_kernel<MT, PW, EPI, KTAIL>), grid, dim3(kThreads), 0, ctx->stream, g);
+      // The three-term kernel wins on two-column slabs with full 64-row tiles (w1|w3 at M 1024:
+      // 180 -> 132 us; the 64-row greedy head: 209 -> 184 us); on one-column slabs and short tiles
+      // its per-step splitting costs as much as it saves.
+      if constexpr (PW == 2 && MT == 4)
+        hipLaunchKernelGGL((gemm_s3_kernel<MT, PW, EPI, KTAIL>), grid, dim3(kThreads), 0, ctx->stream, g);
+      else
+        hipLaunchKernelGGL((gemm_lds_kernel<MT, PW, EPI, KTAIL>), grid, dim3(kThreads), 0, ctx->stream, g);
       return;
     }
   }
