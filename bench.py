@@ -64,7 +64,83 @@ def parse_args():
     p.add_argument("--pmc-copy-reference", action="store_true",
                    help="only run a plain 512 MiB device copy (5 launches): the known-size "
                         "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    p.add_argument("--paged-read-ceiling", action="store_true",
+                   help="only time read-only kernels over the C2 f32 pools in three decompositions "
+                        "(per-kv-head chunks, whole blocks, linear) at several partition sizes, "
+                        "next to the decode op itself: the HBM rate the access pattern allows")
     return p.parse_args()
+
+
+def paged_read_ceiling(seed):
+    """Pure-read rates of C2's bytes (every context token's K and V row of every kv head) in the
+    decode kernel's decomposition and two others, from libferrisinfer_probe.so, against the
+    decode op on the same pools.  One JSON line per configuration."""
+    import ctypes
+
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32, Context
+    from ferrisinfer_amd.build import PROBE_PATH
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    lib = ctypes.CDLL(PROBE_PATH)
+    lib.fp_paged_read.restype = ctypes.c_int32
+    lib.fp_paged_read.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int32] * 5 + [
+        ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    wl = paged_decode_c2(seed=seed)
+    kp = torch.from_numpy(wl.k_pool).cuda()
+    vp = torch.from_numpy(wl.v_pool).cuda()
+    bt = torch.from_numpy(wl.block_tables).cuda()
+    cl = torch.from_numpy(wl.context_lens).cuda()
+    sink = torch.zeros(1024, device="cuda")
+    stream = torch.cuda.current_stream()
+    total = int(wl.context_lens.sum())
+    kv_bytes = total * wl.num_kv_heads * wl.head_dim * 4 * 2
+
+    def timed(fn, reps=50):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    def probe(mode, part):
+        def fn():
+            rc = lib.fp_paged_read(kp.data_ptr(), vp.data_ptr(), bt.data_ptr(), cl.data_ptr(),
+                                   wl.num_seqs, wl.num_kv_heads, wl.block_tables.shape[1],
+                                   wl.num_blocks, wl.max_context_len, total, mode, part,
+                                   sink.data_ptr(), stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"fp_paged_read(mode {mode}, part {part}) failed")
+        return fn
+
+    names = {0: "head_chunks", 1: "whole_blocks", 2: "linear"}
+    print(json.dumps({"workload": f"C2 f32 pools, {wl.num_seqs} seqs, sum L {total}, "
+                      f"Hkv {wl.num_kv_heads}, D {wl.head_dim}", "bytes_read": kv_bytes}), flush=True)
+    for mode in (0, 1, 2):
+        for part in (64, 128, 256, 512, 1024):
+            us = timed(probe(mode, part))
+            print(json.dumps({"layout": names[mode], "partition_tokens": part, "us": round(us, 2),
+                              "GB_s": round(kv_bytes / us / 1e3, 1),
+                              "frac_of_8TBs": round(kv_bytes / us / 8e6, 4)}), flush=True)
+    ctx = Context(0)
+    q = torch.from_numpy(wl.q).cuda()
+    out = torch.empty_like(q)
+
+    def op():
+        ctx.attn_decode_paged(q, kp, vp, DTYPE_F32, bt, cl, wl.max_context_len, wl.num_kv_heads,
+                              wl.block_size, wl.num_blocks, wl.scale, out)
+
+    us = timed(op)
+    alg = wl.algorithmic_bytes(4)
+    print(json.dumps({"layout": "fi_attn_decode_paged (partition + merge)", "us": round(us, 2),
+                      "GB_s": round(alg / us / 1e3, 1), "frac_of_8TBs": round(alg / us / 8e6, 4)}),
+          flush=True)
 
 
 def pmc_copy_reference():
@@ -654,6 +730,9 @@ def main():
         return
     if args.gemm_shapes:
         gemm_shapes(args.seed)
+        return
+    if args.paged_read_ceiling:
+        paged_read_ceiling(args.seed)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
