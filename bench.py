@@ -626,10 +626,12 @@ def c5_step(seed, steps):
     nd = batch.num_decode
     lw = dec.layers[0]
     normed, q, attn, act = dec.normed[:t], dec.q[:t], dec.attn[:t], dec.act[:t]
+    # the projections' inputs as the step hands them over (bf16 bits)
+    xin, ain = dec.normed16[:t], dec.attn16[:t]
     ops = {}
     s_qkv = ctx.gemm_bf16_splits(t, h, dec.nqkv)
     parts = dec._parts(t, dec.nqkv, s_qkv)
-    ops["qkv_gemm"] = (timed(lambda: ctx.gemm_bf16(normed, lw["qkv"], h, dec.nqkv, s_qkv, parts), 10),
+    ops["qkv_gemm"] = (timed(lambda: ctx.gemm_bf16(xin, lw["qkv"], h, dec.nqkv, s_qkv, parts), 10),
                        2.0 * t * h * dec.nqkv, "mfma")
     ops["qkv_rope_append"] = (timed(lambda: ctx.qkv_rope_append(
         parts, s_qkv, None, batch.positions, dec.cos, dec.sin, d, dec.max_pos, batch.slot_mapping,
@@ -644,11 +646,12 @@ def c5_step(seed, steps):
         q[nd:], dec.k_pools[0], dec.v_pools[0], batch.pf_block_tables, batch.pf_cu_seqlens,
         batch.pf_context_lens, batch.pf_max_query, hkv, bs, num_blocks, scale, attn[nd:]), 10),
         pf_flops, "mfma")
+    ops["attn_out_to_bf16"] = (timed(lambda: ctx.convert_f32_to_bf16(attn, ain), 10), t * h * 6, "hbm")
     s_o = ctx.gemm_bf16_splits(t, h, h)
     parts = dec._parts(t, h, s_o)
-    ops["wo_gemm"] = (timed(lambda: ctx.gemm_bf16(attn.view(t, h), lw["wo"], h, h, s_o, parts), 10),
+    ops["wo_gemm"] = (timed(lambda: ctx.gemm_bf16(ain, lw["wo"], h, h, s_o, parts), 10),
                       2.0 * t * h * h, "mfma")
-    ops["w13_swiglu_gemm"] = (timed(lambda: ctx.gemm_bf16_swiglu(normed, lw["w13"], h, f, act), 10),
+    ops["w13_swiglu_gemm"] = (timed(lambda: ctx.gemm_bf16_swiglu(xin, lw["w13"], h, f, act), 10),
                               4.0 * t * h * f, "mfma")
     s_w2 = ctx.gemm_bf16_splits(t, f, h)
     parts = dec._parts(t, h, s_w2)

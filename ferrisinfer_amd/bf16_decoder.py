@@ -21,6 +21,13 @@ The reference loads bf16 weights by exact widening (io/safetensors.rs:540-542) a
 math; the projections here multiply bf16-rounded activations by the bf16 weights with f32
 accumulation; the prefill chunk's attention multiplies bf16-rounded queries and probabilities
 by the bf16 K/V; the rest (norms, RoPE, decode attention, softmax, SwiGLU) stays f32.
+
+With `bf16_activations` (the default) the projections' inputs are handed over as bf16 bits,
+rounded to nearest even where they are produced: the residual norms write them directly
+(fi_splitk_residual_rms_norm_bf16), the SwiGLU epilogue stores them, and the attention output
+and the first norm are narrowed by fi_convert_f32_to_bf16.  The GEMMs round f32 activations
+the same way, so the step's results are bit-identical either way; bf16 inputs halve the bytes
+the projections stage per K step.
 """
 from __future__ import annotations
 
@@ -54,10 +61,11 @@ class Bf16Decoder:
     `max_tokens` rows."""
 
     def __init__(self, ctx, cfg: dict, num_blocks: int, block_size: int, max_tokens: int,
-                 max_last_rows: int):
+                 max_last_rows: int, bf16_activations: bool = True):
         import torch
 
         self.ctx, self.cfg = ctx, cfg
+        self.bf16_activations = bool(bf16_activations)
         self.h, self.f, self.v = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
         self.hq, self.hkv = cfg["heads"], cfg["kv_heads"]
         self.d = self.h // self.hq
@@ -75,7 +83,12 @@ class Bf16Decoder:
         self.normed = torch.empty(t, self.h, device=dev)
         self.q = torch.empty(t, self.hq, self.d, device=dev)
         self.attn = torch.empty(t, self.hq, self.d, device=dev)
-        self.act = torch.empty(t, self.f, device=dev)
+        if self.bf16_activations:  # bf16 bits (int16) of the projections' inputs
+            self.normed16 = torch.empty(t, self.h, dtype=torch.int16, device=dev)
+            self.attn16 = torch.empty(t, self.h, dtype=torch.int16, device=dev)
+            self.act = torch.empty(t, self.f, dtype=torch.int16, device=dev)
+        else:
+            self.act = torch.empty(t, self.f, device=dev)
         self.max_tokens = t
         self.last = torch.empty(max_last_rows, self.h, device=dev)
         self.tok = torch.empty(max_last_rows, dtype=torch.int32, device=dev)
@@ -127,13 +140,19 @@ class Bf16Decoder:
         res.copy_(x)
         normed, q, attn, act = self.normed[:t], self.q[:t], self.attn[:t], self.act[:t]
         c.rms_norm(res, self.layers[0]["attention_norm"], normed, eps)
+        b16 = self.bf16_activations
+        # the projections' inputs: bf16 bits of the normed rows and the attention output
+        xin = self.normed16[:t] if b16 else normed
+        ain = self.attn16[:t] if b16 else attn.view(t, h)
+        if b16:
+            c.convert_f32_to_bf16(normed, xin)
         s_qkv = c.gemm_bf16_splits(t, h, self.nqkv)
         s_o = c.gemm_bf16_splits(t, h, h)
         s_w2 = c.gemm_bf16_splits(t, f, h)
         for li in range(nl):
             w = self.layers[li]
             parts = self._parts(t, self.nqkv, s_qkv)
-            c.gemm_bf16(normed, w["qkv"], h, self.nqkv, s_qkv, parts)
+            c.gemm_bf16(xin, w["qkv"], h, self.nqkv, s_qkv, parts)
             c.qkv_rope_append(parts, s_qkv, None, b.positions, self.cos, self.sin, self.d, self.max_pos,
                               b.slot_mapping, self.k_pools[li], self.v_pools[li], DTYPE_BF16,
                               self.num_blocks, self.block_size, self.hq, self.hkv, self.d, q)
@@ -145,14 +164,17 @@ class Bf16Decoder:
                 c.attn_prefill_paged_bf16(q[nd:], self.k_pools[li], self.v_pools[li], b.pf_block_tables,
                                           b.pf_cu_seqlens, b.pf_context_lens, b.pf_max_query, self.hkv,
                                           self.block_size, self.num_blocks, scale, attn[nd:])
+            if b16:
+                c.convert_f32_to_bf16(attn, ain)
             parts = self._parts(t, h, s_o)
-            c.gemm_bf16(attn.view(t, h), w["wo"], h, h, s_o, parts)
-            c.splitk_residual_rms_norm(parts, s_o, None, res, other, w["ffn_norm"], normed, eps)
-            c.gemm_bf16_swiglu(normed, w["w13"], h, f, act)
+            c.gemm_bf16(ain, w["wo"], h, h, s_o, parts)
+            c.splitk_residual_rms_norm(parts, s_o, None, res, other, w["ffn_norm"], xin, eps)
+            c.gemm_bf16_swiglu(xin, w["w13"], h, f, act)
             parts = self._parts(t, h, s_w2)
             c.gemm_bf16(act, w["w2"], f, h, s_w2, parts)
             nxt = self.layers[li + 1]["attention_norm"] if li + 1 < nl else self.final_norm
-            c.splitk_residual_rms_norm(parts, s_w2, None, other, res, nxt, normed, eps)
+            # the final norm stays f32: its last rows feed the head
+            c.splitk_residual_rms_norm(parts, s_w2, None, other, res, nxt, xin if li + 1 < nl else normed, eps)
         if not head:
             return res
         r = int(b.last_rows.numel())

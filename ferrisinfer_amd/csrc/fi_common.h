@@ -70,7 +70,7 @@ int32_t argmax_merge(fi_context* ctx, const float* amax, int32_t n_tiles, int32_
 // out[M, N] = (sum_z up + bias_up) * silu(sum_z gate + bias_gate) over split partials
 // [splits, M, 2N] holding (up c, gate c) at columns (2c, 2c + 1).
 int32_t splitk_swiglu(fi_context* ctx, const float* parts, int32_t splits, const float* bias_up,
-                      const float* bias_gate, int32_t m, int32_t n, float* out);
+                      const float* bias_gate, int32_t m, int32_t n, void* out, bool out_bf16);
 
 }  // namespace fi
 

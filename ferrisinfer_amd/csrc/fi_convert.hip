@@ -79,9 +79,44 @@ void launch_widen(fi_context* ctx, const void* src, int64_t rows, int64_t cols, 
   }
 }
 
+// dst[i] = bf16 bits of src[i], rounded to nearest even (NaN stays NaN): four elements per
+// thread and step where both pointers allow 16- and 8-byte accesses, one otherwise.
+__global__ void narrow_bf16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst, int64_t n, int vec) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (vec) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = first; i < n4; i += stride) {
+      const float4 x = reinterpret_cast<const float4*>(src)[i];
+      const uint32_t b0 = fi::f32_to_bf16_bits(x.x), b1 = fi::f32_to_bf16_bits(x.y);
+      const uint32_t b2 = fi::f32_to_bf16_bits(x.z), b3 = fi::f32_to_bf16_bits(x.w);
+      reinterpret_cast<uint2*>(dst)[i] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+    }
+    for (int64_t i = 4 * n4 + first; i < n; i += stride) dst[i] = static_cast<uint16_t>(fi::f32_to_bf16_bits(src[i]));
+  } else {
+    for (int64_t i = first; i < n; i += stride) dst[i] = static_cast<uint16_t>(fi::f32_to_bf16_bits(src[i]));
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+int32_t fi_convert_f32_to_bf16(fi_context* ctx, const float* d_src, int64_t n, uint16_t* d_dst) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(n >= 0, FI_ERR_INVALID_SHAPE, "fi_convert_f32_to_bf16: negative length");
+  if (n == 0) return FI_OK;
+  FI_REQUIRE(d_src != nullptr && d_dst != nullptr, FI_ERR_INVALID_CONFIG, "fi_convert_f32_to_bf16: null pointer");
+  const uintptr_t s = reinterpret_cast<uintptr_t>(d_src), d = reinterpret_cast<uintptr_t>(d_dst);
+  FI_REQUIRE(d + 2 * static_cast<uintptr_t>(n) <= s || s + 4 * static_cast<uintptr_t>(n) <= d, FI_ERR_INVALID_CONFIG,
+             "fi_convert_f32_to_bf16: source and destination must not overlap");
+  const int vec = s % 16 == 0 && d % 8 == 0;
+  const int64_t blocks = std::min<int64_t>((n / (vec ? 4 : 1) + 255) / 256 + 1, 8192);
+  hipLaunchKernelGGL(narrow_bf16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, ctx->stream, d_src, d_dst,
+                     n, vec);
+  FI_CHECK_LAUNCH("narrow_bf16_kernel");
+  return FI_OK;
+}
 
 int32_t fi_convert_to_f32(fi_context* ctx, const void* d_src, int32_t src_dtype, int64_t rows, int64_t cols,
                           int32_t transpose, float* d_dst) {

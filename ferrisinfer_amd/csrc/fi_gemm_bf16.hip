@@ -14,8 +14,11 @@
 // load is 16 contiguous bytes per lane and one group's K step is 16 KiB contiguous.
 //
 // Kernel: a workgroup of 4 waves computes a (16 MT) x (64 NT) tile over one split's K range.
-// The activation block (16 MT rows x 32 k, f32) is staged per K step through double-buffered
-// LDS, rounded to bf16 on the way in; each wave owns NT slabs and streams their fragments from
+// The activation block (16 MT rows x 32 k) is staged per K step through double-buffered LDS:
+// f32 activations are rounded to bf16 (nearest even) on the way in, bf16 activations (rounded
+// the same way by their producer) are copied, so both give the same products; bf16 halves the
+// bytes the vector memory path carries per step, which at these tile sizes is as busy as the
+// MFMAs; each wave owns NT slabs and streams their fragments from
 // HBM through a register ring kDepth steps deep, and reads the A fragments of its MT row tiles
 // from LDS.  Two workgroups share a CU, so one's barrier wait overlaps the other's MFMAs.  Workgroups are ordered so each XCD takes a contiguous range of (row block
 // fastest, then column group, then split): the row blocks that share a column group's weights
@@ -38,12 +41,13 @@ constexpr int kStepK = 32;        // K per MFMA step
 constexpr int kGroupSlabs = 16;   // slabs per packed column group
 constexpr int kDepth = 2;         // B ring depth (K steps in flight per wave)
 constexpr int kOccupancy = 2;     // workgroups per CU the register budget allows
-constexpr int kLdsRow = kStepK + 8;  // bf16 per staged A row (80 bytes: conflict-free fragment reads)
+// bf16 per staged A row: a stage of S K steps plus 8 (80 or 144 bytes: conflict-free fragment reads)
+constexpr int lds_row(int steps) { return steps * kStepK + 8; }
 
 enum { kEpiPartial = 0, kEpiPairPartial = 1, kEpiSwiglu = 2, kEpiArgmax = 3 };
 
 struct BGemmArgs {
-  const float* a;            // [M, K] f32, row stride lda
+  const void* a;             // [M, K] f32 or bf16 bits, row stride lda (elements)
   const uint16_t* bp;        // packed bf16 weight
   float* out;
   const float* bias0;        // SwiGLU: up bias
@@ -57,6 +61,7 @@ struct BGemmArgs {
   int splits;
   int total;                 // groups * mblocks * splits
   int tiles;                 // greedy head: 64 NT / 4-column wave tiles holding data
+  int out_bf16;              // SwiGLU: store bf16 bits (nearest even) instead of f32
 };
 
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -101,7 +106,11 @@ __device__ __forceinline__ void store_tile(const BGemmArgs& g, v4f (&acc)[MT][NT
           const float up = g.bias0 ? acc[mt][nt][v] + b0 : acc[mt][nt][v];
           float gate = g.bias1 ? acc[mt][nt + 1][v] + b1 : acc[mt][nt + 1][v];
           gate = gate * (1.0f / (1.0f + __expf(-gate)));
-          g.out[(size_t)row * g.n + c] = up * gate;
+          if (g.out_bf16)
+            reinterpret_cast<uint16_t*>(g.out)[(size_t)row * g.n + c] =
+                static_cast<uint16_t>(fi::f32_to_bf16_bits(up * gate));
+          else
+            g.out[(size_t)row * g.n + c] = up * gate;
         }
     }
   } else {
@@ -152,13 +161,20 @@ __device__ __forceinline__ void store_tile(const BGemmArgs& g, v4f (&acc)[MT][NT
   }
 }
 
-template <int MT, int NT, int EPI, bool KTAIL>
+template <int MT, int NT, int EPI, bool KTAIL, bool A16>
 __global__ __launch_bounds__(kThreads, kOccupancy) void gemm_bf16_kernel(BGemmArgs g) {
   constexpr int ROWS = 16 * MT;
-  constexpr int A_QUADS = ROWS * (kStepK / 4);           // float4 per staged A step
+  // A stage: f32 activations one K step (32 k = 128 bytes of a row), bf16 activations two K
+  // steps (64 k = again 128 contiguous bytes of a row per stage, and half the barriers)
+  constexpr int KS = A16 ? 2 : 1;
+  constexpr int A_VEC = A16 ? 8 : 4;                     // elements per 16-byte A load
+  constexpr int A_ROWQ = KS * kStepK / A_VEC;            // loads per row and stage
+  constexpr int A_QUADS = ROWS * A_ROWQ;                 // 16-byte loads per stage
   constexpr int A_PER = (A_QUADS + kThreads - 1) / kThreads;
-  static_assert(A_QUADS % kThreads == 0 || A_QUADS < kThreads, "A step must split over the threads");
-  __shared__ __align__(16) uint16_t As[2][ROWS][kLdsRow];
+  constexpr int LDS_ROW = lds_row(KS);
+  static_assert(A_QUADS % kThreads == 0 || A_QUADS < kThreads, "A stage must split over the threads");
+  static_assert(!A16 || kDepth == 2, "bf16 stages hold the ring's two K steps");
+  __shared__ __align__(16) uint16_t As[2][ROWS][LDS_ROW];
 
   // tile of this workgroup: the grid is padded to a multiple of 8; hardware workgroup L runs on
   // XCD L % 8 and takes logical tile (L % 8) * (grid / 8) + L / 8
@@ -186,23 +202,49 @@ __global__ __launch_bounds__(kThreads, kOccupancy) void gemm_bf16_kernel(BGemmAr
     for (int nt = 0; nt < NT; ++nt) slot[nt] = *b_ptr(q, nt);
   };
 
-  // ---- A staging: quad i = tid + r * kThreads -> row i / 8, k quad i % 8 ----
-  float4 areg[A_PER];
-  auto load_a = [&](int step) {
-    const int kq = (q0 + min(step, nq - 1)) * kStepK;
+  // ---- A staging: load i = tid + r * kThreads -> row i / A_ROWQ, k group i % A_ROWQ ----
+  const int nst = (nq + KS - 1) / KS;  // stages of the split
+  uint4 areg[A_PER];  // f32: one float4; bf16: eight bf16
+  auto load_a = [&](int stage) {
+    const int kq = (q0 + KS * min(stage, nst - 1)) * kStepK;
 #pragma unroll
     for (int r = 0; r < A_PER; ++r) {
       const int i = tid + r * kThreads;
-      const int row = min(m0 + i / 8, g.m - 1);
-      const int kk = kq + 4 * (i % 8);
-      if constexpr (KTAIL) {
-        // rows hold at least K rounded up to 4 floats (lda); elements past K read as zero
-        const int kc = min(kk, ((g.k + 3) & ~3) - 4);
-        const float4 x = *reinterpret_cast<const float4*>(g.a + (size_t)row * g.lda + kc);
-        areg[r] = make_float4(kk < g.k ? x.x : 0.f, kk + 1 < g.k ? x.y : 0.f, kk + 2 < g.k ? x.z : 0.f,
-                              kk + 3 < g.k ? x.w : 0.f);
+      const int row = min(m0 + i / A_ROWQ, g.m - 1);
+      const int kk = kq + A_VEC * (i % A_ROWQ);
+      if constexpr (A16) {
+        const uint16_t* a16 = static_cast<const uint16_t*>(g.a) + (size_t)row * g.lda;
+        // the stage's second K step may lie past K (an odd last step): its groups are masked
+        // like a K tail; rows hold at least K rounded up to 8 (lda)
+        if (!KTAIL && kk + A_VEC <= g.k) {
+          areg[r] = *reinterpret_cast<const uint4*>(a16 + kk);
+        } else {
+          // elements past K read as zero
+          const int kc = min(kk, ((g.k + 7) & ~7) - 8);
+          const uint4 x = *reinterpret_cast<const uint4*>(a16 + kc);
+          const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+          uint32_t yw[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {  // kc < kk: the whole group lies past K
+            const uint32_t lo = kc == kk && kk + 2 * e < g.k ? (xw[e] & 0xffffu) : 0u;
+            const uint32_t hi = kc == kk && kk + 2 * e + 1 < g.k ? (xw[e] & 0xffff0000u) : 0u;
+            yw[e] = lo | hi;
+          }
+          areg[r] = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+        }
       } else {
-        areg[r] = *reinterpret_cast<const float4*>(g.a + (size_t)row * g.lda + kk);
+        const float* a32 = static_cast<const float*>(g.a) + (size_t)row * g.lda;
+        float4 v;
+        if constexpr (KTAIL) {
+          // rows hold at least K rounded up to 4 floats (lda); elements past K read as zero
+          const int kc = min(kk, ((g.k + 3) & ~3) - 4);
+          const float4 x = *reinterpret_cast<const float4*>(a32 + kc);
+          v = make_float4(kk < g.k ? x.x : 0.f, kk + 1 < g.k ? x.y : 0.f, kk + 2 < g.k ? x.z : 0.f,
+                          kk + 3 < g.k ? x.w : 0.f);
+        } else {
+          v = *reinterpret_cast<const float4*>(a32 + kk);
+        }
+        areg[r] = __builtin_bit_cast(uint4, v);
       }
     }
   };
@@ -211,9 +253,14 @@ __global__ __launch_bounds__(kThreads, kOccupancy) void gemm_bf16_kernel(BGemmAr
     for (int r = 0; r < A_PER; ++r) {
       const int i = tid + r * kThreads;
       if (A_QUADS >= kThreads || i < A_QUADS) {
-        const f32x4 v = {areg[r].x, areg[r].y, areg[r].z, areg[r].w};
-        const bf16x4 h = __builtin_convertvector(v, bf16x4);
-        *reinterpret_cast<bf16x4*>(&As[buf][i / 8][4 * (i % 8)]) = h;
+        if constexpr (A16) {
+          *reinterpret_cast<uint4*>(&As[buf][i / A_ROWQ][A_VEC * (i % A_ROWQ)]) = areg[r];
+        } else {
+          const float4 x = __builtin_bit_cast(float4, areg[r]);
+          const f32x4 v = {x.x, x.y, x.z, x.w};
+          const bf16x4 h = __builtin_convertvector(v, bf16x4);
+          *reinterpret_cast<bf16x4*>(&As[buf][i / A_ROWQ][A_VEC * (i % A_ROWQ)]) = h;
+        }
       }
     }
   };
@@ -233,21 +280,45 @@ __global__ __launch_bounds__(kThreads, kOccupancy) void gemm_bf16_kernel(BGemmAr
   sched_fence();
 
   const int li = lane & 15, lk = lane >> 4;
-  // one K step with ring slot u (compile-time): MFMAs from LDS buffer step & 1 and the slot,
-  // refill the slot DEPTH steps ahead, stage step + 1's activations, prefetch step + 2's
-  auto k_step = [&](int step, uint4 (&slot)[NT]) {
-    const int buf = step & 1;
+  auto mfmas = [&](int buf, int col, const uint4 (&slot)[NT]) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const bf16x8 af = *reinterpret_cast<const bf16x8*>(&As[buf][16 * mt + li][8 * lk]);
+      const bf16x8 af = *reinterpret_cast<const bf16x8*>(&As[buf][16 * mt + li][col + 8 * lk]);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
         acc[mt][nt] =
             __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8, slot[nt]), acc[mt][nt], 0, 0, 0);
     }
-    issue_b(step + kDepth, slot);
+  };
+  if constexpr (A16) {
+    // stage st = K steps 2st (ring slot 0) and 2st + 1 (slot 1; absent past the split's end):
+    // MFMAs from LDS buffer st & 1, stage st + 1's activations, prefetch st + 2's, then the
+    // two slots' weight steps two steps ahead (after the activation loads, as below)
+    for (int st = 0; st < nst; ++st) {
+      const int buf = st & 1;
+      mfmas(buf, 0, ring[0]);
+      if (2 * st + 1 < nq) mfmas(buf, kStepK, ring[1]);  // workgroup-uniform
+      store_a(buf ^ 1);
+      load_a(st + 2);
+      issue_b(2 * st + 2, ring[0]);
+      issue_b(2 * st + 3, ring[1]);
+      __syncthreads();
+      sched_fence();
+    }
+    store_tile<MT, NT, EPI>(g, acc, m0, slab0, z, lane);
+    return;
+  }
+  // one K step with ring slot u (compile-time): MFMAs from LDS buffer step & 1 and the slot,
+  // stage step + 1's activations, prefetch step + 2's, then refill the slot kDepth steps ahead.
+  // Loads complete in issue order, so the weight loads go out after the activation loads: the
+  // wait for step + 2's activations (next step's LDS store) leaves them in flight, and a weight
+  // step is waited for only by the MFMAs that use it, kDepth steps after its issue.
+  auto k_step = [&](int step, uint4 (&slot)[NT]) {
+    const int buf = step & 1;
+    mfmas(buf, 0, slot);
     store_a(buf ^ 1);
     load_a(step + 2);
+    issue_b(step + kDepth, slot);
     __syncthreads();
     sched_fence();
   };
@@ -258,8 +329,9 @@ __global__ __launch_bounds__(kThreads, kOccupancy) void gemm_bf16_kernel(BGemmAr
   }
   // remainder (workgroup-uniform): slot u of the ring holds step full + u
   const int rem = nq - full;
-  static_assert(kDepth == 2, "one remainder step for a ring of 2");
-  if (rem > 0) k_step(full, ring[0]);
+#pragma unroll
+  for (int u = 0; u + 1 < kDepth; ++u)
+    if (u < rem) k_step(full + u, ring[u]);
   store_tile<MT, NT, EPI>(g, acc, m0, slab0, z, lane);
 }
 
@@ -287,18 +359,26 @@ int split_count(fi_context* ctx, int m, int k, int slabs) {
   return (q + per - 1) / per;  // every split non-empty
 }
 
-template <int MT, int EPI>
+template <int MT, int EPI, bool A16>
 void launch_mt(fi_context* ctx, const BGemmArgs& g) {
   const dim3 grid(static_cast<unsigned>((g.total + 7) / 8 * 8));
   if (g.k % kStepK == 0) {
-    hipLaunchKernelGGL((gemm_bf16_kernel<MT, kNt, EPI, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+    hipLaunchKernelGGL((gemm_bf16_kernel<MT, kNt, EPI, false, A16>), grid, dim3(kThreads), 0, ctx->stream, g);
   } else {
-    hipLaunchKernelGGL((gemm_bf16_kernel<MT, kNt, EPI, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+    hipLaunchKernelGGL((gemm_bf16_kernel<MT, kNt, EPI, true, A16>), grid, dim3(kThreads), 0, ctx->stream, g);
   }
 }
 
+template <int MT, int EPI>
+void launch_mt(fi_context* ctx, const BGemmArgs& g, bool a16) {
+  if (a16)
+    launch_mt<MT, EPI, true>(ctx, g);
+  else
+    launch_mt<MT, EPI, false>(ctx, g);
+}
+
 template <int EPI>
-int32_t launch_bgemm(fi_context* ctx, BGemmArgs g, int splits) {
+int32_t launch_bgemm(fi_context* ctx, BGemmArgs g, int splits, bool a16) {
   const int mt = mt_for(g.m);
   g.mblocks = (g.m + 16 * mt - 1) / (16 * mt);
   g.groups = (g.slabs + kWaves * kNt - 1) / (kWaves * kNt);
@@ -306,16 +386,16 @@ int32_t launch_bgemm(fi_context* ctx, BGemmArgs g, int splits) {
   g.total = g.groups * g.mblocks * splits;
   switch (mt) {
     case 8:
-      launch_mt<8, EPI>(ctx, g);
+      launch_mt<8, EPI>(ctx, g, a16);
       break;
     case 4:
-      launch_mt<4, EPI>(ctx, g);
+      launch_mt<4, EPI>(ctx, g, a16);
       break;
     case 2:
-      launch_mt<2, EPI>(ctx, g);
+      launch_mt<2, EPI>(ctx, g, a16);
       break;
     default:
-      launch_mt<1, EPI>(ctx, g);
+      launch_mt<1, EPI>(ctx, g, a16);
       break;
   }
   FI_CHECK_LAUNCH("gemm_bf16_kernel");
@@ -397,12 +477,16 @@ int32_t launch_pack(fi_context* ctx, const PackSourcesBf16& s, int32_t src_dtype
   return FI_OK;
 }
 
-int32_t check_common(fi_context* ctx, const float* a, int32_t lda, const uint16_t* bp, int32_t m, int32_t k,
-                     int32_t n) {
+int32_t check_common(fi_context* ctx, const void* a, int32_t a_dtype, int32_t lda, const uint16_t* bp, int32_t m,
+                     int32_t k, int32_t n) {
   FI_TRY(fi::enter(ctx));
   FI_REQUIRE(m >= 0 && k > 0 && n > 0, FI_ERR_INVALID_SHAPE, "bf16 GEMM: bad shape");
-  FI_REQUIRE(lda % 4 == 0 && lda >= (k + 3) / 4 * 4, FI_ERR_INVALID_SHAPE,
-             "bf16 GEMM: lda must be a multiple of 4 and at least K rounded up to 4");
+  FI_REQUIRE(a_dtype == FI_DTYPE_F32 || a_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
+             "bf16 GEMM: the activation dtype must be f32 or bf16");
+  const int vec = a_dtype == FI_DTYPE_BF16 ? 8 : 4;  // elements per 16-byte load
+  FI_REQUIRE(lda % vec == 0 && lda >= (k + vec - 1) / vec * vec, FI_ERR_INVALID_SHAPE,
+             a_dtype == FI_DTYPE_BF16 ? "bf16 GEMM: lda must be a multiple of 8 and at least K rounded up to 8 (bf16 A)"
+                                      : "bf16 GEMM: lda must be a multiple of 4 and at least K rounded up to 4");
   FI_REQUIRE(m == 0 || (a && bp), FI_ERR_INVALID_CONFIG, "bf16 GEMM: null pointer");
   FI_REQUIRE(m == 0 || (reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(bp) % 16 == 0),
              FI_ERR_INVALID_CONFIG, "bf16 GEMM: A and the packed weight must be 16-byte aligned");
@@ -470,9 +554,9 @@ int32_t fi_gemm_bf16_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, in
   return FI_OK;
 }
 
-int32_t fi_gemm_bf16(fi_context* ctx, const float* d_a, int32_t lda, const uint16_t* d_bp, int32_t k, int32_t n,
-                     int32_t m, int32_t splits, float* d_out) {
-  FI_TRY(check_common(ctx, d_a, lda, d_bp, m, k, n));
+int32_t fi_gemm_bf16(fi_context* ctx, const void* d_a, int32_t a_dtype, int32_t lda, const uint16_t* d_bp, int32_t k,
+                     int32_t n, int32_t m, int32_t splits, float* d_out) {
+  FI_TRY(check_common(ctx, d_a, a_dtype, lda, d_bp, m, k, n));
   FI_REQUIRE(splits >= 1 && splits <= q_steps(k), FI_ERR_INVALID_CONFIG, "fi_gemm_bf16: splits out of range");
   if (m == 0) return FI_OK;
   FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_bf16: null output");
@@ -490,14 +574,18 @@ int32_t fi_gemm_bf16(fi_context* ctx, const float* d_a, int32_t lda, const uint1
   const int used = (g.q_total + g.q_per_split - 1) / g.q_per_split;
   FI_REQUIRE(used == splits, FI_ERR_INVALID_CONFIG,
              "fi_gemm_bf16: splits must divide the K steps into non-empty ranges (use fi_gemm_bf16_splits)");
-  return launch_bgemm<kEpiPartial>(ctx, g, splits);
+  return launch_bgemm<kEpiPartial>(ctx, g, splits, a_dtype == FI_DTYPE_BF16);
 }
 
-int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const float* d_a, int32_t lda, const uint16_t* d_bp_pair, int32_t k,
-                            int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate, float* d_out) {
-  FI_TRY(check_common(ctx, d_a, lda, d_bp_pair, m, k, n));
+int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const void* d_a, int32_t a_dtype, int32_t lda, const uint16_t* d_bp_pair,
+                            int32_t k, int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate,
+                            void* d_out, int32_t out_dtype) {
+  FI_TRY(check_common(ctx, d_a, a_dtype, lda, d_bp_pair, m, k, n));
+  FI_REQUIRE(out_dtype == FI_DTYPE_F32 || out_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
+             "fi_gemm_bf16_swiglu: the output dtype must be f32 or bf16");
   if (m == 0) return FI_OK;
   FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_bf16_swiglu: null output");
+  const bool a16 = a_dtype == FI_DTYPE_BF16;
   BGemmArgs g{};
   g.a = d_a;
   g.bp = d_bp_pair;
@@ -511,21 +599,23 @@ int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const float* d_a, int32_t lda, cons
   g.slabs = data_slabs(n, true);
   const int splits = split_count(ctx, m, k, g.slabs);
   if (splits == 1) {  // the epilogue applies SwiGLU directly
-    g.out = d_out;
+    g.out = static_cast<float*>(d_out);
+    g.out_bf16 = out_dtype == FI_DTYPE_BF16;
     g.q_per_split = g.q_total;
-    return launch_bgemm<kEpiSwiglu>(ctx, g, 1);
+    return launch_bgemm<kEpiSwiglu>(ctx, g, 1, a16);
   }
   // (up, gate) partial pairs per split, then the split sum + SwiGLU
   FI_TRY(fi::ensure_workspace(ctx, (size_t)splits * m * 2 * n * sizeof(float)));
   g.out = static_cast<float*>(ctx->workspace);
   g.q_per_split = (g.q_total + splits - 1) / splits;
-  FI_TRY(launch_bgemm<kEpiPairPartial>(ctx, g, splits));
-  return fi::splitk_swiglu(ctx, g.out, splits, d_bias_up, d_bias_gate, m, n, d_out);
+  FI_TRY(launch_bgemm<kEpiPairPartial>(ctx, g, splits, a16));
+  return fi::splitk_swiglu(ctx, g.out, splits, d_bias_up, d_bias_gate, m, n, d_out, out_dtype == FI_DTYPE_BF16);
 }
 
-int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const float* d_hidden, int32_t lda, const uint16_t* d_bp, int32_t m,
-                               int32_t hidden, int32_t vocab, int32_t* d_token, float* d_prob) {
-  FI_TRY(check_common(ctx, d_hidden, lda, d_bp, m, hidden, vocab));
+int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const void* d_hidden, int32_t a_dtype, int32_t lda,
+                               const uint16_t* d_bp, int32_t m, int32_t hidden, int32_t vocab, int32_t* d_token,
+                               float* d_prob) {
+  FI_TRY(check_common(ctx, d_hidden, a_dtype, lda, d_bp, m, hidden, vocab));
   if (m == 0) return FI_OK;
   FI_REQUIRE(d_token && d_prob, FI_ERR_INVALID_CONFIG, "fi_lm_head_argmax_bf16: null output");
   BGemmArgs g{};
@@ -541,7 +631,7 @@ int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const float* d_hidden, int32_t l
   g.tiles = (g.slabs + kNt - 1) / kNt;
   FI_TRY(fi::ensure_workspace(ctx, (size_t)m * g.tiles * 3 * sizeof(float)));
   g.out = static_cast<float*>(ctx->workspace);
-  FI_TRY(launch_bgemm<kEpiArgmax>(ctx, g, 1));
+  FI_TRY(launch_bgemm<kEpiArgmax>(ctx, g, 1, a_dtype == FI_DTYPE_BF16));
   return fi::argmax_merge(ctx, g.out, g.tiles, m, d_token, d_prob);
 }
 

@@ -543,8 +543,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_s3_kernel(PGemmArgs g) {
 
 // Pair-pack partials [splits, M, 2N] (up, gate interleaved per column) -> out[M, N] =
 // (sum up + b1) * silu(sum gate + b3), sums in split order (elementwise.rs:118-207).
+// bf16 output (out_bf16): the products rounded to nearest even.
 __global__ void splitk_swiglu_kernel(const float* __restrict__ parts, int splits, const float* __restrict__ b_up,
-                                     const float* __restrict__ b_gate, int m, int n, float* __restrict__ out) {
+                                     const float* __restrict__ b_gate, int m, int n, void* __restrict__ out,
+                                     int out_bf16) {
   const size_t total = (size_t)m * n;
   const size_t plane2 = total;  // float2 elements per split plane
   const float2* p2 = reinterpret_cast<const float2*>(parts);
@@ -565,7 +567,10 @@ __global__ void splitk_swiglu_kernel(const float* __restrict__ parts, int splits
     const float up = b_up ? x.x + b_up[c] : x.x;
     float gate = b_gate ? x.y + b_gate[c] : x.y;
     gate = gate * (1.0f / (1.0f + __expf(-gate)));
-    out[i] = up * gate;
+    if (out_bf16)
+      static_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(fi::f32_to_bf16_bits(up * gate));
+    else
+      static_cast<float*>(out)[i] = up * gate;
   }
 }
 
@@ -663,9 +668,10 @@ __device__ __forceinline__ T sum_splits(const T* __restrict__ p, size_t plane, i
 // rms_norm(h) * w (reduction.rs:3-73: ms = sum(x^2)/H, inv = 1/sqrt(ms + eps), (x*inv)*w).
 // Four columns per thread when hidden is a multiple of 4.
 constexpr int kRowThreads = 256;
+template <bool OUT16>
 __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
     const float* __restrict__ parts, int splits, const float* __restrict__ bias, const float* __restrict__ residual,
-    float* __restrict__ sum_out, const float* __restrict__ weight, float* __restrict__ out, int rows, int hidden,
+    float* __restrict__ sum_out, const float* __restrict__ weight, void* __restrict__ out_v, int rows, int hidden,
     float eps) {
   __shared__ float s_red[kRowThreads / 64];
   const int row = blockIdx.x;
@@ -714,10 +720,19 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
 #pragma unroll
   for (int i = 0; i < kRowThreads / 64; ++i) total += s_red[i];
   const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+  // OUT16: the normalised row is stored as bf16 bits, each value rounded to nearest even
+  float* out = static_cast<float*>(out_v);
+  uint16_t* out16 = static_cast<uint16_t*>(out_v);
   auto norm_quad = [&](int c, const float4& x) {
     const float4 wv = reinterpret_cast<const float4*>(weight)[c];
-    reinterpret_cast<float4*>(out + base)[c] =
-        make_float4((x.x * inv) * wv.x, (x.y * inv) * wv.y, (x.z * inv) * wv.z, (x.w * inv) * wv.w);
+    const float4 y = make_float4((x.x * inv) * wv.x, (x.y * inv) * wv.y, (x.z * inv) * wv.z, (x.w * inv) * wv.w);
+    if constexpr (OUT16) {
+      const uint32_t b0 = fi::f32_to_bf16_bits(y.x), b1 = fi::f32_to_bf16_bits(y.y);
+      const uint32_t b2 = fi::f32_to_bf16_bits(y.z), b3 = fi::f32_to_bf16_bits(y.w);
+      reinterpret_cast<uint2*>(out16 + base)[c] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+    } else {
+      reinterpret_cast<float4*>(out + base)[c] = y;
+    }
   };
   if (held) {
 #pragma unroll
@@ -728,7 +743,13 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
   } else if (vec) {
     for (int c = threadIdx.x; c < h4; c += kRowThreads) norm_quad(c, reinterpret_cast<const float4*>(sum_out + base)[c]);
   } else {
-    for (int c = threadIdx.x; c < hidden; c += kRowThreads) out[base + c] = (sum_out[base + c] * inv) * weight[c];
+    for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
+      const float y = (sum_out[base + c] * inv) * weight[c];
+      if constexpr (OUT16)
+        out16[base + c] = static_cast<uint16_t>(fi::f32_to_bf16_bits(y));
+      else
+        out[base + c] = y;
+    }
   }
 }
 
@@ -1041,11 +1062,11 @@ int32_t check_common(fi_context* ctx, const float* a, int32_t lda, const float* 
 namespace fi {
 
 int32_t splitk_swiglu(fi_context* ctx, const float* parts, int32_t splits, const float* bias_up,
-                      const float* bias_gate, int32_t m, int32_t n, float* out) {
+                      const float* bias_gate, int32_t m, int32_t n, void* out, bool out_bf16) {
   const size_t total = (size_t)m * n;
   const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 4096));
   hipLaunchKernelGGL(splitk_swiglu_kernel, dim3(blocks), dim3(256), 0, ctx->stream, parts, splits, bias_up, bias_gate,
-                     m, n, out);
+                     m, n, out, out_bf16 ? 1 : 0);
   FI_CHECK_LAUNCH("splitk_swiglu_kernel");
   return FI_OK;
 }
@@ -1171,7 +1192,7 @@ int32_t fi_gemm_packed_swiglu(fi_context* ctx, const float* d_a, int32_t lda, co
   g.n = 2 * n;
   g.q_per_split = (g.q_total + splits - 1) / splits;
   FI_TRY((launch_pgemm<2, kEpiPartial>(ctx, g, splits)));
-  return fi::splitk_swiglu(ctx, g.out, splits, d_bias_up, d_bias_gate, m, n, d_out);
+  return fi::splitk_swiglu(ctx, g.out, splits, d_bias_up, d_bias_gate, m, n, d_out, false);
 }
 
 int32_t fi_lm_head_argmax_packed(fi_context* ctx, const float* d_hidden, int32_t lda, const float* d_bp, int32_t m,
@@ -1203,8 +1224,25 @@ int32_t fi_splitk_residual_rms_norm(fi_context* ctx, const float* d_parts, int32
   if (rows == 0) return FI_OK;
   FI_REQUIRE(d_parts && d_residual && d_sum && d_weight && d_out, FI_ERR_INVALID_CONFIG,
              "fi_splitk_residual_rms_norm: null pointer");
-  hipLaunchKernelGGL(splitk_residual_rms_norm_kernel, dim3(rows), dim3(kRowThreads), 0, ctx->stream, d_parts, splits,
-                     d_bias, d_residual, d_sum, d_weight, d_out, rows, hidden, eps);
+  hipLaunchKernelGGL(splitk_residual_rms_norm_kernel<false>, dim3(rows), dim3(kRowThreads), 0, ctx->stream, d_parts,
+                     splits, d_bias, d_residual, d_sum, d_weight, d_out, rows, hidden, eps);
+  FI_CHECK_LAUNCH("splitk_residual_rms_norm_kernel");
+  return FI_OK;
+}
+
+int32_t fi_splitk_residual_rms_norm_bf16(fi_context* ctx, const float* d_parts, int32_t splits, const float* d_bias,
+                                         const float* d_residual, float* d_sum, const float* d_weight,
+                                         uint16_t* d_out, int32_t rows, int32_t hidden, float eps) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(rows >= 0 && hidden > 0 && splits >= 1, FI_ERR_INVALID_SHAPE,
+             "fi_splitk_residual_rms_norm_bf16: bad shape");
+  if (rows == 0) return FI_OK;
+  FI_REQUIRE(d_parts && d_residual && d_sum && d_weight && d_out, FI_ERR_INVALID_CONFIG,
+             "fi_splitk_residual_rms_norm_bf16: null pointer");
+  FI_REQUIRE(hidden % 4 != 0 || reinterpret_cast<uintptr_t>(d_out) % 8 == 0, FI_ERR_INVALID_LAYOUT,
+             "fi_splitk_residual_rms_norm_bf16: the output must be 8-byte aligned");
+  hipLaunchKernelGGL(splitk_residual_rms_norm_kernel<true>, dim3(rows), dim3(kRowThreads), 0, ctx->stream, d_parts,
+                     splits, d_bias, d_residual, d_sum, d_weight, d_out, rows, hidden, eps);
   FI_CHECK_LAUNCH("splitk_residual_rms_norm_kernel");
   return FI_OK;
 }

@@ -330,7 +330,7 @@ void ForwardExecutor::splits(int32_t m, int32_t k, int32_t n, int32_t pack_width
 void ForwardExecutor::projection(const float* a, int32_t lda, const DeviceBuffer& w, int32_t k, int32_t n,
                                  int32_t pack_width, int32_t m, int32_t splits, float* out) const {
   if (model_->weight_dtype() == FI_DTYPE_BF16) {
-    check(fi_gemm_bf16(ctx_, a, lda, static_cast<const uint16_t*>(w.get()), k, n, m, splits, out));
+    check(fi_gemm_bf16(ctx_, a, FI_DTYPE_F32, lda, static_cast<const uint16_t*>(w.get()), k, n, m, splits, out));
   } else {
     check(fi_gemm_packed(ctx_, a, lda, w.f32(), k, n, pack_width, m, splits, out));
   }
@@ -393,8 +393,8 @@ void ForwardExecutor::enqueue(const Plan& p) {
     check(fi_splitk_residual_rms_norm(ctx_, part, p.s_o, w.wo_bias.f32(), hidden, h1, w.ffn_norm.f32(), normed, T, H,
                                       c.rms_norm_eps));
     if (bf16) {
-      check(fi_gemm_bf16_swiglu(ctx_, normed, H, static_cast<const uint16_t*>(pk.w13.get()), H, F, T,
-                                w.w1_bias.f32(), w.w3_bias.f32(), act));
+      check(fi_gemm_bf16_swiglu(ctx_, normed, FI_DTYPE_F32, H, static_cast<const uint16_t*>(pk.w13.get()), H, F, T,
+                                w.w1_bias.f32(), w.w3_bias.f32(), act, FI_DTYPE_F32));
     } else {
       check(fi_gemm_packed_swiglu(ctx_, normed, H, pk.w13.f32(), H, F, T, w.w1_bias.f32(), w.w3_bias.f32(), act));
     }
@@ -410,8 +410,8 @@ void ForwardExecutor::enqueue(const Plan& p) {
     // fused greedy head (matmul_rhs_transposed_argmax_f32, matmul.rs:190-274), as the
     // reference session's greedy path (session.rs:349-356, 393-398)
     if (bf16) {
-      check(fi_lm_head_argmax_bf16(ctx_, last_norm_.f32(), H, static_cast<const uint16_t*>(lm), B, H, c.vocab_size,
-                                   static_cast<int32_t*>(tok_.get()), prob_.f32()));
+      check(fi_lm_head_argmax_bf16(ctx_, last_norm_.f32(), FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), B, H,
+                                   c.vocab_size, static_cast<int32_t*>(tok_.get()), prob_.f32()));
     } else {
       check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), B, H, c.vocab_size,
                                      static_cast<int32_t*>(tok_.get()), prob_.f32()));
@@ -421,8 +421,8 @@ void ForwardExecutor::enqueue(const Plan& p) {
     // (session.rs:357-373, 399-406) with each sequence's sampler state; the states and the
     // per-row configuration were uploaded to samp_ before this sequence
     if (bf16) {
-      check(fi_gemm_bf16(ctx_, last_norm_.f32(), H, static_cast<const uint16_t*>(lm), H, c.vocab_size, B, 1,
-                         logits_.f32()));
+      check(fi_gemm_bf16(ctx_, last_norm_.f32(), FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), H, c.vocab_size,
+                         B, 1, logits_.f32()));
     } else {
       check(fi_gemm_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), H, c.vocab_size,
                            DeviceModel::kLmPack, B, 1, logits_.f32()));

@@ -90,9 +90,11 @@ _SIGNATURES = {
     "fi_weight_pack_bf16_columns": [_P, C.POINTER(_P), C.POINTER(_I32), _I32, _I32, _I32, _P],
     "fi_weight_pack_bf16_pair": [_P, _P, _P, _I32, _I32, _I32, _P],
     "fi_gemm_bf16_splits": [_P, _I32, _I32, _I32, C.POINTER(_I32)],
-    "fi_gemm_bf16": [_P, _P, _I32, _P, _I32, _I32, _I32, _I32, _P],
-    "fi_gemm_bf16_swiglu": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P],
-    "fi_lm_head_argmax_bf16": [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P],
+    "fi_gemm_bf16": [_P, _P, _I32, _I32, _P, _I32, _I32, _I32, _I32, _P],
+    "fi_gemm_bf16_swiglu": [_P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _I32],
+    "fi_lm_head_argmax_bf16": [_P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P],
+    "fi_splitk_residual_rms_norm_bf16": [_P, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32, _F32],
+    "fi_convert_f32_to_bf16": [_P, _P, C.c_int64, _P],
     "fi_sample_tokens": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
@@ -357,10 +359,19 @@ class Context:
                                                 ptr(token_out), ptr(prob_out)))
 
     def splitk_residual_rms_norm(self, parts, splits, bias, residual, sum_out, weight, out, eps):
+        """out = rms_norm(sum) * weight with sum = split sum (+ bias) + residual stored to sum_out;
+        a 2-byte `out` (bf16 or int16) receives the normalised row as bf16 bits."""
         rows, hidden = residual.shape
-        check(self.lib.fi_splitk_residual_rms_norm(self.handle, ptr(parts), int(splits), ptr(bias),
-                                                   ptr(residual), ptr(sum_out), ptr(weight),
-                                                   ptr(out), int(rows), int(hidden), float(eps)))
+        fn = (self.lib.fi_splitk_residual_rms_norm_bf16 if self._act_dtype(out) == DTYPE_BF16
+              else self.lib.fi_splitk_residual_rms_norm)
+        check(fn(self.handle, ptr(parts), int(splits), ptr(bias), ptr(residual), ptr(sum_out), ptr(weight),
+                 ptr(out), int(rows), int(hidden), float(eps)))
+
+    def convert_f32_to_bf16(self, src, out):
+        """out (bf16 or int16, same element count) = src (f32) rounded to nearest even."""
+        if src.numel() != out.numel():
+            raise FerrisError(3, "convert_f32_to_bf16: element counts differ")
+        check(self.lib.fi_convert_f32_to_bf16(self.handle, ptr(src), int(src.numel()), ptr(out)))
 
     def weight_pack_columns(self, srcs, k, pack_width):
         """Packs the column concatenation of up to three device weights [K, n_i]."""
@@ -428,22 +439,34 @@ class Context:
         check(self.lib.fi_gemm_bf16_splits(self.handle, int(m), int(k), int(n), C.byref(out)))
         return int(out.value)
 
+    @staticmethod
+    def _act_dtype(t):
+        """Activation dtype of a tensor: f32, or bf16 bits in any 2-byte dtype."""
+        import torch
+
+        if t.dtype == torch.float32:
+            return DTYPE_F32
+        if t.element_size() == 2 and t.dtype != torch.float16:
+            return DTYPE_BF16
+        raise FerrisError(5, f"activation dtype {t.dtype} is neither f32 nor bf16")
+
     def gemm_bf16(self, a, bp, k, n, splits, out):
-        """out [splits, M, N] = split-K partial products of a [M, K] (f32) and the packed bf16
-        weight."""
-        check(self.lib.fi_gemm_bf16(self.handle, ptr(a), int(a.stride(0)), ptr(bp), int(k), int(n),
-                                    int(a.shape[0]), int(splits), ptr(out)))
+        """out [splits, M, N] = split-K partial products of a [M, K] (f32, or bf16 bits) and the
+        packed bf16 weight."""
+        check(self.lib.fi_gemm_bf16(self.handle, ptr(a), self._act_dtype(a), int(a.stride(0)), ptr(bp),
+                                    int(k), int(n), int(a.shape[0]), int(splits), ptr(out)))
 
     def gemm_bf16_swiglu(self, a, bp_pair, k, n, out, bias_up=None, bias_gate=None):
-        check(self.lib.fi_gemm_bf16_swiglu(self.handle, ptr(a), int(a.stride(0)), ptr(bp_pair),
-                                           int(k), int(n), int(a.shape[0]), ptr(bias_up),
-                                           ptr(bias_gate), ptr(out)))
+        """out [M, N] (f32, or bf16 bits when out is a 2-byte tensor) = SwiGLU of the pair."""
+        check(self.lib.fi_gemm_bf16_swiglu(self.handle, ptr(a), self._act_dtype(a), int(a.stride(0)),
+                                           ptr(bp_pair), int(k), int(n), int(a.shape[0]), ptr(bias_up),
+                                           ptr(bias_gate), ptr(out), self._act_dtype(out)))
 
     def lm_head_argmax_bf16(self, hidden, bp, vocab, token_out, prob_out):
         m, h = hidden.shape
-        check(self.lib.fi_lm_head_argmax_bf16(self.handle, ptr(hidden), int(hidden.stride(0)),
-                                              ptr(bp), int(m), int(h), int(vocab), ptr(token_out),
-                                              ptr(prob_out)))
+        check(self.lib.fi_lm_head_argmax_bf16(self.handle, ptr(hidden), self._act_dtype(hidden),
+                                              int(hidden.stride(0)), ptr(bp), int(m), int(h), int(vocab),
+                                              ptr(token_out), ptr(prob_out)))
 
     def sample_tokens(self, logits, temperature, top_k, top_p, rng_state, token_out, prob_out):
         """One token per row of logits [rows, vocab] (f32, row stride logits.stride(0)) under the

@@ -362,7 +362,11 @@ int32_t fi_qkv_rope_append(fi_context* ctx, const float* d_parts, int32_t splits
  * The reference loads bf16 weights by exact widening (io/safetensors.rs:540-542) and runs the
  * f32 kernels; this path keeps the weights bf16 in HBM, packed for v_mfma_f32_16x16x32_bf16,
  * rounds the f32 activations to bf16 (nearest even) and accumulates in f32.  The outputs use
- * the formats of the f32 packed path above, so the same consumers sum the split partials. */
+ * the formats of the f32 packed path above, so the same consumers sum the split partials.
+ * Activations (a_dtype) may also be given as bf16 bits already rounded to nearest even (by
+ * fi_convert_f32_to_bf16, fi_splitk_residual_rms_norm_bf16 or a bf16 SwiGLU output): the
+ * products are then bit-identical to the f32 call, and the kernels read half the activation
+ * bytes. */
 
 /* bf16 elements of the packed form of a [K, N] weight (pair != 0: the up/gate pair of two
  * [K, N] weights). */
@@ -387,22 +391,40 @@ int32_t fi_weight_pack_bf16_pair(fi_context* ctx, const void* d_up, const void* 
 int32_t fi_gemm_bf16_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, int32_t* splits);
 
 /* d_out[z] = A * W over split z's K range (as fi_gemm_packed): matmul_f32 / linear_f32_with_bias
- * (kernel/cpu/matmul.rs:46-118, 424-499) with bf16 operands and f32 accumulation.  A [M, K] f32
- * with row stride lda (a multiple of 4, at least K rounded up to 4; 16-byte aligned rows). */
-int32_t fi_gemm_bf16(fi_context* ctx, const float* d_a, int32_t lda, const uint16_t* d_bp, int32_t k, int32_t n,
-                     int32_t m, int32_t splits, float* d_out);
+ * (kernel/cpu/matmul.rs:46-118, 424-499) with bf16 operands and f32 accumulation.  A [M, K] of
+ * a_dtype (FI_DTYPE_F32 or FI_DTYPE_BF16) with row stride lda in elements (f32: a multiple of 4,
+ * at least K rounded up to 4; bf16: a multiple of 8, at least K rounded up to 8; 16-byte
+ * aligned rows). */
+int32_t fi_gemm_bf16(fi_context* ctx, const void* d_a, int32_t a_dtype, int32_t lda, const uint16_t* d_bp, int32_t k,
+                     int32_t n, int32_t m, int32_t splits, float* d_out);
 
 /* out[M, N] = (A W1 + b1) * silu(A W3 + b3) over the pair-packed bf16 weight (the decoder
  * block's up/gate projections and SwiGLU, runtime/reference.rs:346-360,
- * kernel/cpu/elementwise.rs:118-207).  Uses the context workspace when K is split. */
-int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const float* d_a, int32_t lda, const uint16_t* d_bp_pair, int32_t k,
-                            int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate, float* d_out);
+ * kernel/cpu/elementwise.rs:118-207).  A as for fi_gemm_bf16; out_dtype FI_DTYPE_F32 or
+ * FI_DTYPE_BF16 (the f32 result rounded to nearest even, the input of a bf16-activation
+ * fi_gemm_bf16).  Uses the context workspace when K is split. */
+int32_t fi_gemm_bf16_swiglu(fi_context* ctx, const void* d_a, int32_t a_dtype, int32_t lda, const uint16_t* d_bp_pair,
+                            int32_t k, int32_t n, int32_t m, const float* d_bias_up, const float* d_bias_gate,
+                            void* d_out, int32_t out_dtype);
 
 /* Greedy head over a bf16 weight packed from its [vocab, hidden] layout
  * (matmul_rhs_transposed_argmax_f32, kernel/cpu/matmul.rs:190-274): first maximal index and
  * 1 / sum(exp(logit - max)) per row.  Uses the context workspace. */
-int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const float* d_hidden, int32_t lda, const uint16_t* d_bp, int32_t m,
-                               int32_t hidden, int32_t vocab, int32_t* d_token, float* d_prob);
+int32_t fi_lm_head_argmax_bf16(fi_context* ctx, const void* d_hidden, int32_t a_dtype, int32_t lda,
+                               const uint16_t* d_bp, int32_t m, int32_t hidden, int32_t vocab, int32_t* d_token,
+                               float* d_prob);
+
+/* fi_splitk_residual_rms_norm with the normalised output stored as bf16 bits, each value the
+ * f32 result rounded to nearest even (the sum stays f32): the producer of bf16 activations for
+ * fi_gemm_bf16 / fi_gemm_bf16_swiglu.  d_out 8-byte aligned when hidden is a multiple of 4. */
+int32_t fi_splitk_residual_rms_norm_bf16(fi_context* ctx, const float* d_parts, int32_t splits, const float* d_bias,
+                                         const float* d_residual, float* d_sum, const float* d_weight,
+                                         uint16_t* d_out, int32_t rows, int32_t hidden, float eps);
+
+/* d_dst[i] = bf16 bits of d_src[i] rounded to nearest even (NaN stays NaN), n elements; the
+ * narrowing of f32 activations for the bf16 projections.  Source and destination must not
+ * overlap. */
+int32_t fi_convert_f32_to_bf16(fi_context* ctx, const float* d_src, int64_t n, uint16_t* d_dst);
 
 /* ---------------------------------------------------------------- sampling */
 

@@ -144,3 +144,60 @@ def test_bf16_decoder_layer_matches_reference(orc):
             continue  # near tie at bf16 resolution
         ridx, _ = orc.matmul_rhs_transposed_argmax(fin_r[i:i + 1], headf)
         assert int(tok[i]) == ridx, i
+
+
+def test_bf16_decoder_activation_handover_bit_identical():
+    """Two C5-shaped layers over the same mixed step with the projections' inputs handed over as
+    bf16 bits (the default) and as f32: the GEMMs round f32 inputs to bf16 by the same rule, so
+    the final hidden rows, the appended K/V pools, tokens and probabilities agree bit for bit."""
+    import torch
+
+    from ferrisinfer_amd import Context
+    from ferrisinfer_amd.bf16_decoder import LLAMA3_8B_C5, Bf16Decoder, build_step_batch
+
+    import oracle
+
+    cfg = dict(LLAMA3_8B_C5, layers=2, vocab=4096)
+    h, f, v, hq, hkv = cfg["hidden"], cfg["intermediate"], cfg["vocab"], cfg["heads"], cfg["kv_heads"]
+    d = h // hq
+    bs = 16
+    rng = np.random.default_rng(11)
+    decode_ctx = [300, 5, 1030]
+    prefill = [(64, 200)]
+    lens = decode_ctx + [p + n for p, n in prefill]
+    num_blocks = sum((n + bs - 1) // bs for n in lens) + 2
+    t = len(decode_ctx) + sum(n for _, n in prefill)
+    print(f"bf16 decoder handover: decode {decode_ctx}, prefill {prefill}", flush=True)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+
+    def wbits(*shape):
+        return dev(oracle.f32_to_bf16((rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02))).view(np.int16))
+
+    layers = [[wbits(h, h), wbits(h, hkv * d), wbits(h, hkv * d), wbits(h, h), wbits(h, f), wbits(f, h), wbits(h, f),
+               dev((1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32)),
+               dev((1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32))] for _ in range(2)]
+    final_norm = dev((1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32))
+    head = wbits(v, h)
+    pools = dev(oracle.f32_to_bf16(rng.standard_normal((4, num_blocks, hkv, bs, d), dtype=np.float32)).view(np.int16))
+    x = dev((rng.standard_normal((t, h), dtype=np.float32) * np.float32(0.5)).astype(np.float32))
+    ctx = Context(0)
+    runs = []
+    for b16 in (True, False):
+        dec = Bf16Decoder(ctx, cfg, num_blocks, bs, max_tokens=t, max_last_rows=len(lens), bf16_activations=b16)
+        for lw in layers:
+            dec.set_layer(*lw)
+        dec.set_head(final_norm, head)
+        for i in range(2):
+            dec.k_pools[i].copy_(pools[2 * i])
+            dec.v_pools[i].copy_(pools[2 * i + 1])
+        batch, _ = build_step_batch(decode_ctx, prefill, bs, num_blocks, seed=4)
+        hid = dec.step(x, batch, head=False).clone()
+        tok, prob = dec.step(x, batch)
+        runs.append((hid, tok.clone(), prob.clone(), [p.clone() for p in dec.k_pools + dec.v_pools]))
+        del dec
+    ctx.check_faults()
+    ctx.close()
+    (h16, t16, p16, k16), (h32, t32, p32, k32) = runs
+    assert torch.equal(h16, h32)
+    assert torch.equal(t16, t32) and torch.equal(p16, p32)
+    assert all(torch.equal(a, b) for a, b in zip(k16, k32))

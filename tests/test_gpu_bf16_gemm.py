@@ -182,3 +182,101 @@ def test_bf16_lm_head_reference_vector_and_ties(gpu_ctx):
     gpu_ctx.lm_head_argmax_bf16(dev(np.array([[1, 0, 0, 0]], np.float32)), bp, v, tok, prob)
     torch.cuda.synchronize()
     assert int(tok[0]) == 5
+
+
+def padded16(bits):
+    """Device copy of [M, K] bf16 bits (uint16) with rows padded to a multiple of 8 elements (NaN
+    bits in the padding: the kernel must not read past K)."""
+    import torch
+
+    m, k = bits.shape
+    lda = (k + 7) // 8 * 8
+    d = torch.full((m, lda), 0x7fc0, dtype=torch.int16, device="cuda")
+    d[:, :k] = dev(bits.view(np.int16))
+    return d[:, :k]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bf16_gemm_bf16_activations_bit_identical(orc, gpu_ctx, shape):
+    """A handed over as bf16 bits (RNE of the f32 activations) gives exactly the f32 call's
+    partials: the kernel rounds f32 activations with the same rule."""
+    import torch
+
+    m, k, n = shape
+    print(f"bf16-activation gemm shape={shape}", flush=True)
+    rng = np.random.default_rng(5 * m + k + n)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    wb = bf16_weights(rng, (k, n))
+    bp = gpu_ctx.weight_pack_bf16(dev(wb.view(np.int16)), k, n)
+    splits = gpu_ctx.gemm_bf16_splits(m, k, n)
+    ref = torch.full((splits, m, n), float("nan"), device="cuda")
+    got = torch.full((splits, m, n), float("nan"), device="cuda")
+    gpu_ctx.gemm_bf16(padded(a), bp, k, n, splits, ref)
+    gpu_ctx.gemm_bf16(padded16(orc.f32_to_bf16(a)), bp, k, n, splits, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), shape
+
+
+@pytest.mark.parametrize("m,k,f", [(300, 256, 688), (2304, 4096, 1024), (64, 896, 4864), (3, 100, 40)])
+def test_bf16_swiglu_bf16_in_out(orc, gpu_ctx, m, k, f):
+    """bf16 activations in: the same f32 output as the f32 call; bf16 output: exactly the RNE
+    of the f32 output (direct epilogue and the split-sum path alike)."""
+    import torch
+
+    print(f"bf16 swiglu bf16 in/out m={m} k={k} f={f}", flush=True)
+    rng = np.random.default_rng(m * 7 + k + f)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    w1b, w3b = bf16_weights(rng, (k, f)), bf16_weights(rng, (k, f))
+    bp = gpu_ctx.weight_pack_bf16_pair(dev(w1b.view(np.int16)), dev(w3b.view(np.int16)), k, f)
+    b1 = dev(rng.standard_normal(f, dtype=np.float32) * 0.1)
+    out32 = torch.full((m, f), float("nan"), device="cuda")
+    gpu_ctx.gemm_bf16_swiglu(padded(a), bp, k, f, out32, b1, None)
+    a16 = padded16(orc.f32_to_bf16(a))
+    out32b = torch.full((m, f), float("nan"), device="cuda")
+    gpu_ctx.gemm_bf16_swiglu(a16, bp, k, f, out32b, b1, None)
+    out16 = torch.full((m, f), 0x7fc0, dtype=torch.int16, device="cuda")
+    gpu_ctx.gemm_bf16_swiglu(a16, bp, k, f, out16, b1, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out32b, out32)
+    want = orc.f32_to_bf16(out32.cpu().numpy())
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), want)
+
+
+def test_bf16_head_bf16_activations(orc, gpu_ctx):
+    """The greedy head over bf16 activations: the f32 call's tokens and probabilities exactly."""
+    import torch
+
+    rng = np.random.default_rng(21)
+    m, h, v = 33, 200, 1000
+    hid = rng.standard_normal((m, h), dtype=np.float32)
+    bp = gpu_ctx.weight_pack_bf16(dev(bf16_weights(rng, (v, h)).view(np.int16)), h, v, src_layout=1)
+    tok = [torch.empty(m, dtype=torch.int32, device="cuda") for _ in range(2)]
+    prob = [torch.empty(m, device="cuda") for _ in range(2)]
+    gpu_ctx.lm_head_argmax_bf16(padded(hid), bp, v, tok[0], prob[0])
+    gpu_ctx.lm_head_argmax_bf16(padded16(orc.f32_to_bf16(hid)), bp, v, tok[1], prob[1])
+    torch.cuda.synchronize()
+    assert torch.equal(tok[0], tok[1]) and torch.equal(prob[0], prob[1])
+
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (4096 * 37 + 3, 0), (1000, 1), (1 << 20, 0)])
+def test_convert_f32_to_bf16(orc, gpu_ctx, n, offset):
+    """fi_convert_f32_to_bf16 against the oracle's nearest-even narrowing, with ties, the
+    largest finite values, infinities, NaN, denormals and signed zeros; an offset start
+    exercises the unaligned path."""
+    import torch
+
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n + offset, dtype=np.float32) * np.float32(100)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3.4028235e38, -3.4028235e38, 1e-40, -1e-41,
+                        1.00390625, 1.01171875, -1.00390625], np.float32)  # ties: 1 + 2^-8, 1 + 3 * 2^-8
+    x[offset:offset + min(n, special.size)] = special[:min(n, special.size)]
+    src = dev(x)[offset:]
+    out = torch.full((n + 1,), 0x1234, dtype=torch.int16, device="cuda")
+    gpu_ctx.convert_f32_to_bf16(src, out[:n])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    want = orc.f32_to_bf16(x[offset:])
+    nan = np.isnan(x[offset:])
+    assert np.array_equal(got[:n][~nan], want[~nan])
+    assert np.all((got[:n][nan] & 0x7f80) == 0x7f80) and np.all((got[:n][nan] & 0x7f) != 0)
+    assert got[n] == 0x1234  # nothing written past n

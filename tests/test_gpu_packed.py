@@ -171,7 +171,8 @@ def test_packed_lm_head_reference_vector_and_ties(gpu_ctx):
     assert int(tok[0]) == 5
 
 
-@pytest.mark.parametrize("rows,hidden,splits,bias", [(64, 896, 4, True), (3, 256, 1, False), (17, 4096, 3, True)])
+@pytest.mark.parametrize("rows,hidden,splits,bias", [(64, 896, 4, True), (3, 256, 1, False), (17, 4096, 3, True),
+                                                     (5, 30, 2, True)])  # last: the scalar (hidden % 4) path
 def test_splitk_residual_rms_norm(orc, gpu_ctx, rows, hidden, splits, bias):
     import torch
 
@@ -191,6 +192,14 @@ def test_splitk_residual_rms_norm(orc, gpu_ctx, rows, hidden, splits, bias):
     h = h + res
     assert np.array_equal(s.cpu().numpy(), h)  # same additions in the same order
     assert normwise_error(out.cpu().numpy(), orc.rms_norm(h, w, 1e-6)) <= 1e-5
+    # bf16 output: the same sum, and exactly the nearest-even rounding of the f32 output
+    s16 = torch.empty((rows, hidden), device="cuda")
+    out16 = torch.empty((rows, hidden), dtype=torch.int16, device="cuda")
+    gpu_ctx.splitk_residual_rms_norm(dev(parts), splits, dev(b) if bias else None, dev(res), s16,
+                                     dev(w), out16, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(s16, s)
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), orc.f32_to_bf16(out.cpu().numpy()))
 
 
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
