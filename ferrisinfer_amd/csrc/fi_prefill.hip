@@ -437,8 +437,10 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
   constexpr int PER_T = KB * RV / kThreads;
   static_assert(KB * RV % kThreads == 0 && kThreads % KB == 0, "chunk must split over the workgroup");
   constexpr int KP = D + 8;              // padded LDS rows (conflict-free fragment reads)
-  __shared__ __align__(16) uint16_t Ks[KB][KP];
-  __shared__ __align__(16) uint16_t Vs[KB][KP];  // row-major like K; read through transpose loads
+  // double-buffered: chunk c + 1 is staged into the other buffer while chunk c is consumed,
+  // so one barrier per chunk orders both the reuse and the new contents
+  __shared__ __align__(16) uint16_t Ks[2][KB][KP];
+  __shared__ __align__(16) uint16_t Vs[2][KB][KP];  // row-major like K; read through transpose loads
 
   const uint16_t* __restrict__ k_cache = static_cast<const uint16_t*>(a.k_cache);
   const uint16_t* __restrict__ v_cache = static_cast<const uint16_t*>(a.v_cache);
@@ -522,22 +524,23 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
       vr[r] = valid ? vx : make_uint4(0u, 0u, 0u, 0u);
     }
   };
-  auto stage = [&]() {
+  auto stage = [&](int buf) {
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int dv = w + 4 * r;
-      *reinterpret_cast<uint4*>(&Ks[lane][8 * dv]) = kr[r];
-      *reinterpret_cast<uint4*>(&Vs[lane][8 * dv]) = vr[r];
+      *reinterpret_cast<uint4*>(&Ks[buf][lane][8 * dv]) = kr[r];
+      *reinterpret_cast<uint4*>(&Vs[buf][lane][8 * dv]) = vr[r];
     }
   };
 
   lookup(0);
   fetch(0);
   lookup(1);
-  stage();
+  stage(0);
   __syncthreads();
   for (int c = 0; c < nchunks; ++c) {
     const int k0 = c * KB;
+    const int buf = c & 1;
     fetch(c + 1);
     lookup(c + 2);
     __builtin_amdgcn_sched_barrier(0);
@@ -550,7 +553,7 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
       for (int g = 0; g < RG; ++g) s_acc[g][jt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < DS; ++t) {
-        const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[16 * jt + li][32 * t + 8 * lk]);
+        const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[buf][16 * jt + li][32 * t + 8 * lk]);
 #pragma unroll
         for (int g = 0; g < RG; ++g)
           s_acc[g][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qf[g][t], s_acc[g][jt], 0, 0, 0);
@@ -588,8 +591,12 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
           ls += pexp;
         }
       l_part[g] = l_part[g] * alpha + ls;
+      // alpha is exactly 1 where the row maximum did not grow: skip the rescale when that
+      // holds for every lane of the wave (same results, fewer VALU operations)
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[g][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) o[g][dt] *= alpha;
+      }
     }
 
     // ---- O^T += V^T P^T over the chunk's 32-key steps ----
@@ -610,18 +617,17 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
       const int vrow = 32 * u + 4 * lk + (li >> 2), vcol = 4 * (li & 3);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const v4s lo = lds_read_tr16(&Vs[vrow][16 * dt + vcol]);
-        const v4s hi = lds_read_tr16(&Vs[vrow + 16][16 * dt + vcol]);
+        const v4s lo = lds_read_tr16(&Vs[buf][vrow][16 * dt + vcol]);
+        const v4s hi = lds_read_tr16(&Vs[buf][vrow + 16][16 * dt + vcol]);
         const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int g = 0; g < RG; ++g) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], o[g][dt], 0, 0, 0);
       }
     }
-    __syncthreads();  // every wave is done with this chunk's K/V
-    if (c + 1 < nchunks) {
-      stage();
-      __syncthreads();
-    }
+    // the other buffer was last read in chunk c - 1, which every wave finished before the
+    // previous barrier; this barrier publishes chunk c + 1 and retires chunk c's buffer
+    if (c + 1 < nchunks) stage(buf ^ 1);  // workgroup-uniform
+    __syncthreads();
   }
 
   if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
