@@ -56,10 +56,11 @@ struct PrefillArgs {
 // attend, largest first (counting sort over 1024 buckets; order within a bucket arbitrary,
 // which no result depends on; tiles past a sequence's end sort last).
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int* __restrict__ cu, const int* __restrict__ ctxl,
-                                                            int num_seqs, int ntiles, int qt_rows, int kb,
+                                                            int num_seqs, int ntiles, int qt_rows, int kb, int fold,
                                                             int* __restrict__ order, uint32_t* __restrict__ faults) {
   __shared__ int hist[1024];
   __shared__ int part[1024];
+  __shared__ int s_live;
   const int tid = threadIdx.x;
   const int total = num_seqs * ntiles;
   hist[tid] = 0;
@@ -78,6 +79,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int* __restric
   };
   for (int t = tid; t < total; t += 1024) atomicAdd(&hist[1023 - bucket(t)], 1);
   __syncthreads();
+  if (tid == 0) s_live = total - hist[1023];  // tiles with rows (bucket 0 sorts last)
   const int v = hist[tid];  // exclusive scan of the bucket counts (Hillis-Steele)
   part[tid] = v;
   __syncthreads();
@@ -89,7 +91,15 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int* __restric
   }
   hist[tid] = part[tid] - v;
   __syncthreads();
-  for (int t = tid; t < total; t += 1024) order[atomicAdd(&hist[1023 - bucket(t)], 1)] = t;
+  // fold (a launch that fits the device in one round, two workgroups per CU): sorted position
+  // p of the n live tiles goes to rank p in the first half and to rank half + (n - 1 - p) in
+  // the second, so ranks r and r + half, which the dispatcher places on the same CU, pair a
+  // long tile with a short one
+  const int n = s_live, half = (n + 1) / 2;
+  for (int t = tid; t < total; t += 1024) {
+    const int p = atomicAdd(&hist[1023 - bucket(t)], 1);
+    order[fold && p < n && p >= half ? half + (n - 1 - p) : p] = t;
+  }
 }
 
 // Four consecutive K/V elements of one row as raw registers, widened when staged.
@@ -346,14 +356,21 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
 
 // Sorts the tiles largest first into the context workspace (one small launch before the
 // attention kernel) and sizes the grid: one workgroup per (tile, kv head).
+#ifndef FI_PREFILL_FOLD
+#define FI_PREFILL_FOLD 1
+#endif
+
 int32_t plan_tiles(fi_context* ctx, PrefillArgs& args, int qt, int kb, const char* name, dim3* grid) {
   const int ntiles = (args.max_query_len + qt - 1) / qt;
   const long pairs = (long)ntiles * args.num_seqs;
   FI_REQUIRE(pairs * args.hkv <= 0x7fffffffL, FI_ERR_INVALID_SHAPE, std::string(name) + ": grid too large");
   FI_TRY(fi::ensure_workspace(ctx, (size_t)pairs * sizeof(int)));
   int* order = static_cast<int*>(ctx->workspace);
+  // one round of workgroups (two per CU): pair long and short tiles on each CU
+  const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  const int fold = FI_PREFILL_FOLD && pairs * args.hkv <= 2 * cus;
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, ctx->stream, args.cu_seqlens, args.context_lens,
-                     args.num_seqs, ntiles, qt, kb, order, ctx->d_faults);
+                     args.num_seqs, ntiles, qt, kb, fold, order, ctx->d_faults);
   FI_CHECK_LAUNCH("prefill_plan_kernel");
   args.order = order;
   *grid = dim3(static_cast<unsigned>(pairs * args.hkv));
@@ -500,31 +517,46 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
   uint4 kr[PER_T], vr[PER_T];
   int id_next = 0, off_next = 0;
   bool bad_block = false;
+  bool part_next = false, valid_next = true;  // the fetched chunk: partial (uniform), this lane's key valid
+  // blocks that divide the chunk (the common case): the lane's block within the chunk and its
+  // offset are constants, so the lookup needs no division
+  const bool aligned = KB % a.block_size == 0;  // workgroup-uniform
+  const int lane_blk = aligned ? lane / a.block_size : 0;
+  const int lane_off = aligned ? lane - lane_blk * a.block_size : 0;
+  const int chunk_blks = aligned ? KB / a.block_size : 0;
   auto lookup = [&](int c) {
     c = min(c, nchunks - 1);
     const int kpc = max(min(c * KB + lane, kend - 1), 0);
-    const int lb = kpc / a.block_size;
+    const bool exact = aligned && c * KB + lane < kend;  // the unclamped key: lb, off are constants
+    const int lb = exact ? c * chunk_blks + lane_blk : kpc / a.block_size;
     const bool in_table = lb < a.max_blocks;
     const int id = a.block_tables[(size_t)seq * a.max_blocks + (in_table ? lb : 0)];
     id_next = in_table ? id : -1;
-    off_next = kpc - lb * a.block_size;
+    off_next = exact ? lane_off : kpc - lb * a.block_size;
   };
   auto fetch = [&](int c) {
     c = min(c, nchunks - 1);
-    const bool valid = c * KB + lane < kend;
+    part_next = (c + 1) * KB > kend;  // workgroup-uniform: the chunk has padding keys
+    valid_next = c * KB + lane < kend;
     const bool bad = id_next < 0 || id_next >= a.num_blocks;
     bad_block |= bad;
     const size_t row = ((size_t)(bad ? 0 : id_next) * a.hkv + kvh) * a.block_size + off_next;
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int dv = w + 4 * r;
-      const uint4 kx = *reinterpret_cast<const uint4*>(k_cache + row * D + 8 * dv);
-      const uint4 vx = *reinterpret_cast<const uint4*>(v_cache + row * D + 8 * dv);
-      kr[r] = valid ? kx : make_uint4(0u, 0u, 0u, 0u);
-      vr[r] = valid ? vx : make_uint4(0u, 0u, 0u, 0u);
+      kr[r] = *reinterpret_cast<const uint4*>(k_cache + row * D + 8 * dv);
+      vr[r] = *reinterpret_cast<const uint4*>(v_cache + row * D + 8 * dv);
     }
   };
+  // padding keys of a partial chunk are stored as zero (their clamped loads hold a valid row)
   auto stage = [&](int buf) {
+    if (part_next && !valid_next) {
+#pragma unroll
+      for (int r = 0; r < PER_T; ++r) {
+        kr[r] = make_uint4(0u, 0u, 0u, 0u);
+        vr[r] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int dv = w + 4 * r;
@@ -563,12 +595,14 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
     const bool full = k0 + KB - 1 <= start + q0;  // workgroup-uniform
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
+      // raw scores: the maximum is taken before scaling (c2 > 0 and rounding are monotone, so
+      // max(s) * c2 is the maximum of the scaled scores) and each exponent is one fma
       float mx = -INFINITY;
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          float x = s_acc[g][jt][v] * c2;
+          float x = s_acc[g][jt][v];
           if (!full) {
             const int kp = k0 + 16 * jt + 4 * lk + v;
             x = (kp <= qpos[g] && kp < ctx) ? x : -INFINITY;
@@ -578,7 +612,7 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
         }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_row[g], mx);  // finite: key 0 of chunk 0 is visible to every row
+      const float m_new = fmaxf(m_row[g], mx * c2);  // finite: key 0 of chunk 0 is visible to every row
       const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
       m_row[g] = m_new;
       float ls = 0.0f;
@@ -586,7 +620,7 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
       for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float pexp = __builtin_amdgcn_exp2f(s_acc[g][jt][v] - m_new);
+          const float pexp = __builtin_amdgcn_exp2f(fmaf(s_acc[g][jt][v], c2, -m_new));
           s_acc[g][jt][v] = pexp;
           ls += pexp;
         }
