@@ -23,6 +23,8 @@
 // top-p prefix, the retained total, the xorshift64* draw and the threshold walk, sequentially
 // in f32 in list order.  The exponential is the device expf; the reference's is the host
 // libm's, so a weight may differ in its last bit.
+#include <algorithm>
+
 #include "fi_common.h"
 #include "fi_device.h"
 
@@ -410,266 +412,303 @@ __device__ __forceinline__ void merge_softmax(float& m, float& sum, float om, fl
   m = nm;
 }
 
+// ---- shared phases of the two launches ----
+// Each phase takes the kernel's LDS object by reference and is force-inlined: compiled as a
+// separate function (a call from the kernel), the fast path's results were wrong.
+
+constexpr int kMaxSegs = kWaves;  // row segments: segment j's candidates fill wave buffer j of the finish
+
+// One segment's greedy partial: last maximal key / index, (running maximum, sum of 2^(x - max))
+// in log2 units, and whether a NaN or +inf was seen.
+struct GreedyPart {
+  int key;
+  int idx;
+  float m;
+  float sum;
+  int bad;
+  int pad[3];
+};
+
+// What the scan leaves per (row, segment): its candidate count and flags (bit 0 NaN, bit 1 a
+// buffer overflowed), or the greedy partial.
+struct ScanMeta {
+  int count;
+  int flags;
+  int pad[2];
+  GreedyPart g;
+};
+
+__device__ __forceinline__ bool greedy_row(float T, int K, float P) {  // SamplerConfig::is_greedy (sampler.rs:40-42)
+  return T <= 0.0f || K == 1 || P <= 0.0f;
+}
+
+// Greedy pass over wave steps [s0, s1) (logit indices below lim), whole workgroup: the last
+// maximal key by total_cmp (later equal maxima win: indices ascend per lane) and the sum of
+// exp(l - max) against a running maximum raised once per 16 logits (base-2 exponentials of
+// log2e-scaled logits); a NaN or +inf marks the row bad.  tid 0 returns the workgroup's part.
 template <int VEC>
-__global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restrict__ logits, int ld, int vocab,
-                                                          const float* __restrict__ temperature,
-                                                          const int32_t* __restrict__ top_k,
-                                                          const float* __restrict__ top_p, uint64_t* __restrict__ rng,
-                                                          int32_t* __restrict__ token, float* __restrict__ prob,
-                                                          uint32_t* __restrict__ faults) {
-  __shared__ SampleShared sh;
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const float* row = logits + (size_t)r * ld;
-  const float T = temperature[r];
-  const int K = top_k[r];
-  const float P = top_p[r];
-  const int nsteps = (vocab + kStep - 1) / kStep;
-
-  if (T <= 0.0f || K == 1 || P <= 0.0f) {  // SamplerConfig::is_greedy (sampler.rs:40-42)
-    // Last maximal index by total_cmp (Iterator::max_by) and 1 / sum exp(l - max) in one pass,
-    // the sum over finite logits against a running maximum raised once per 16 logits (base-2
-    // exponentials of log2e-scaled logits: within 1e-6 of the exact sum, where the reference's
-    // own sequential f32 sum is within (vocab - 1) * 2^-24); a NaN, a +inf or a row of -inf
-    // makes the reference's sum NaN.
-    int bk = kIntMin, bi = -1;
-    float m = -INFINITY, sum = 0.0f;
-    bool bad = false;
-    stream_steps<VEC>(row, vocab, w, kWaves, nsteps, lane, [&](const float (&v)[kPerLane], int s) {
-      const int valid = vocab - s * kStep;
-      float xs[kPerLane];
-      float smax = -INFINITY;
+__device__ __forceinline__ GreedyPart greedy_pass(const float* row, int vocab, int s0, int s1, int lim, int w, int lane, int tid,
+                                  SampleShared& sh) {
+  int bk = kIntMin, bi = -1;
+  float m = -INFINITY, sum = 0.0f;
+  bool bad = false;
+  stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, [&](const float (&v)[kPerLane], int s) {
+    const int valid = lim - s * kStep;
+    float xs[kPerLane];
+    float smax = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < kPerLane; ++e) {
-        const int off = step_index<VEC>(0, lane, e);
-        const bool in = off < valid;
-        const float x = v[e];
-        const int key = total_key(x);
-        const bool take = in && key >= bk;  // indices ascend per lane: a later equal maximum wins
-        bk = take ? key : bk;
-        bi = take ? s * kStep + off : bi;
-        bad = bad || (in && !(x < INFINITY));
-        xs[e] = (in && x > -INFINITY && x < INFINITY) ? x * kLog2e : -INFINITY;
-        smax = fmaxf(smax, xs[e]);
-      }
-      // m and xs in log2 units: sum of 2^(xs - m) = sum of exp(x - max)
-      const float nm = fmaxf(m, smax);
-      sum = (nm > m) ? sum * __builtin_amdgcn_exp2f(m - nm) : sum;  // m = -inf: sum is 0
-      m = nm;
-      const float base = m > -INFINITY ? m : 0.0f;
+    for (int e = 0; e < kPerLane; ++e) {
+      const int off = step_index<VEC>(0, lane, e);
+      const bool in = off < valid;
+      const float x = v[e];
+      const int key = total_key(x);
+      const bool take = in && key >= bk;
+      bk = take ? key : bk;
+      bi = take ? s * kStep + off : bi;
+      bad = bad || (in && !(x < INFINITY));
+      xs[e] = (in && x > -INFINITY && x < INFINITY) ? x * kLog2e : -INFINITY;
+      smax = fmaxf(smax, xs[e]);
+    }
+    const float nm = fmaxf(m, smax);
+    sum = (nm > m) ? sum * __builtin_amdgcn_exp2f(m - nm) : sum;  // m = -inf: sum is 0
+    m = nm;
+    const float base = m > -INFINITY ? m : 0.0f;
 #pragma unroll
-      for (int e = 0; e < kPerLane; ++e) sum += __builtin_amdgcn_exp2f(xs[e] - base);
-    });
+    for (int e = 0; e < kPerLane; ++e) sum += __builtin_amdgcn_exp2f(xs[e] - base);
+  });
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const int ok = __shfl_xor(bk, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ok > bk || (ok == bk && oi > bi)) {
-        bk = ok;
-        bi = oi;
-      }
-      merge_softmax(m, sum, __shfl_xor(m, off, 64), __shfl_xor(sum, off, 64));
+  for (int off = 32; off > 0; off >>= 1) {
+    const int ok = __shfl_xor(bk, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (ok > bk || (ok == bk && oi > bi)) {
+      bk = ok;
+      bi = oi;
     }
-    bad = __ballot(bad) != 0;
-    if (lane == 0) {
-      sh.red_i[w][0] = bk;
-      sh.red_i[w][1] = bi;
-      sh.red_i[w][2] = bad;
-      sh.red_f[w][0] = m;
-      sh.red_f[w][1] = sum;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int i = 1; i < kWaves; ++i) {
-        if (sh.red_i[i][0] > bk || (sh.red_i[i][0] == bk && sh.red_i[i][1] > bi)) {
-          bk = sh.red_i[i][0];
-          bi = sh.red_i[i][1];
-        }
-        merge_softmax(m, sum, sh.red_f[i][0], sh.red_f[i][1]);
-        bad = bad || sh.red_i[i][2];
-      }
-      token[r] = bi;
-      prob[r] = (bad || !(sum > 0.0f)) ? __int_as_float(0x7fc00000) : 1.0f / sum;
-    }
-    return;
+    merge_softmax(m, sum, __shfl_xor(m, off, 64), __shfl_xor(sum, off, 64));
   }
-
-  const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
-  if (k > kMaxTopK) {
-    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
-    return;
-  }
-  if (tid < kWaves) sh.bound[tid] = kIntMin;
-  if (tid == 0) {
-    sh.flags = 0;
-    sh.m = 0;
+  bad = __ballot(bad) != 0;
+  if (lane == 0) {
+    sh.red_i[w][0] = bk;
+    sh.red_i[w][1] = bi;
+    sh.red_i[w][2] = bad;
+    sh.red_f[w][0] = m;
+    sh.red_f[w][1] = sum;
   }
   __syncthreads();
+  GreedyPart g{bk, bi, m, sum, bad ? 1 : 0, {0, 0, 0}};
+  if (tid == 0) {
+    for (int i = 1; i < kWaves; ++i) {
+      if (sh.red_i[i][0] > g.key || (sh.red_i[i][0] == g.key && sh.red_i[i][1] > g.idx)) {
+        g.key = sh.red_i[i][0];
+        g.idx = sh.red_i[i][1];
+      }
+      merge_softmax(g.m, g.sum, sh.red_f[i][0], sh.red_f[i][1]);
+      g.bad = g.bad || sh.red_i[i][2];
+    }
+  }
+  return g;
+}
 
-  bool sorted = false;  // s_val / s_idx hold the sorted list
+// One pass over wave steps [s0, s1) (logit indices below lim): each wave buffers in its LDS
+// region the logits that can be among the k+1 largest of what the workgroup has seen (whole
+// workgroup).  Leaves sh.count[w] and sets sh.flags bit 0 (NaN) / bit 1 (a region overflowed
+// with equal logits).
+template <int VEC>
+__device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0, int s1, int lim, int k, int w, int lane,
+                            SampleShared& sh) {
+  int* rkey = sh.key[w];
+  int* ridx = sh.idx[w];
+  int bound = kIntMin, cnt = 0;
+  uint32_t nan_bits = 0;  // max of |bits|: above 0x7f800000 when a NaN was seen
+  stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, [&](const float (&v)[kPerLane], int s) {
+    const int valid = lim - s * kStep;  // logits of this step below lim: step_index offsets < valid
+    if (k < 64 && s < s0 + kWaves) {
+      // the wave's first step seeds its bound: the (k+1)-th largest of the 64 lane maxima.
+      // k+1 distinct logits of the step are at or above it, so nothing below it can be among
+      // the k+1 largest (a bitonic network sorts the lane maxima descending across the wave;
+      // empty lanes hold the minimum key).  Later steps raise the bound by compaction.
+      int lmax = kIntMin;
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e)
+        lmax = max(lmax, step_index<VEC>(0, lane, e) < valid ? total_key(v[e]) : kIntMin);
+#pragma unroll
+      for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          const int o = __shfl_xor(lmax, stride, 64);
+          const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
+          lmax = keep_max ? max(lmax, o) : min(lmax, o);
+        }
+      bound = max(bound, __shfl(lmax, k, 64));
+    }
+    int hits = 0;
+#pragma unroll
+    for (int e = 0; e < kPerLane; ++e) {
+      const bool in = step_index<VEC>(0, lane, e) < valid;
+      const uint32_t bits = __float_as_uint(v[e]);
+      nan_bits = max(nan_bits, in ? bits & 0x7fffffffu : 0u);
+      hits += (in && total_key(v[e]) >= bound) ? 1 : 0;
+    }
+    if (__ballot(hits > 0)) {  // rare once the bound has risen: append a group at a time
+#pragma unroll
+      for (int g = 0; g < kPerLane / (kGroup / 64); ++g) {
+#pragma unroll
+        for (int e = g * (kGroup / 64); e < (g + 1) * (kGroup / 64); ++e) {
+          const bool pass = step_index<VEC>(0, lane, e) < valid && total_key(v[e]) >= bound;
+          const uint64_t ball = __ballot(pass);
+          if (pass) {
+            const int pos = cnt + lanes_below(ball);
+            rkey[pos] = total_key(v[e]);
+            ridx[pos] = step_index<VEC>(s, lane, e);
+          }
+          cnt += __popcll(ball);
+        }
+        if (cnt > kRegion - kGroup) {
+          wave_sync();
+          bound = max(bound, wave_select_desc(rkey, cnt, k, sh.hist[w], lane));
+          cnt = wave_compact(rkey, ridx, cnt, bound, lane);
+          if (lane == 0) atomicMax(&sh.bound[w], bound);
+          if (cnt > kRegion - kGroup) {  // equal logits fill the buffer: the row is replayed
+            if (lane == 0) atomicOr(&sh.flags, 2);
+            cnt = 0;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) {
+      bound = max(bound, __hip_atomic_load(&sh.bound[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    }
+  });
+  if (__ballot(nan_bits > 0x7f800000u) && lane == 0) atomicOr(&sh.flags, 1);
+  if (lane == 0) sh.count[w] = cnt;
+  __syncthreads();
+}
+
+// The key of descending rank `rank` over the wave buffers' sh.count[q] entries (radix
+// selection, 8 bits a round; whole workgroup; the buffers hold more than `rank` entries).
+__device__ __forceinline__ int select_desc(SampleShared& sh, int rank, int tid, int w, int lane) {
+  uint32_t prefix = 0, mask = 0;
+  int want = rank;
+  for (int d = 24; d >= 0; d -= 8) {
+    if (tid < 256) sh.hist[0][tid] = 0;
+    __syncthreads();
+    for (int q = 0; q < kWaves; ++q) {
+      for (int i = tid; i < sh.count[q]; i += kThreads) {
+        const uint32_t u = static_cast<uint32_t>(sh.key[q][i]) ^ 0x80000000u;
+        if ((u & mask) == prefix) atomicAdd(&sh.hist[0][(u >> d) & 255u], 1);
+      }
+    }
+    __syncthreads();
+    if (w == 0) {
+      const int digit = pick_digit_desc(sh.hist[0], lane, want);
+      if (lane == 0) {
+        sh.sel[0] = digit;
+        sh.sel[1] = want;
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(sh.sel[0]) << d;
+    mask |= 255u << d;
+    want = sh.sel[1];
+    __syncthreads();
+  }
+  return static_cast<int>(prefix ^ 0x80000000u);
+}
+
+// Fast path after the buffering: the k+1-th largest key over the wave buffers, the candidates
+// at or above it sorted by (key descending, index ascending) into s_val / s_idx.  Returns true
+// when the top k+1 are strictly decreasing (the list is then exactly the top k in value order);
+// false sends the row to the replay.
+__device__ __forceinline__ bool fast_top_k(SampleShared& sh, int k, int tid, int w, int lane) {
+  const int kth = select_desc(sh, k, tid, w, lane);
+  for (int q = 0; q < kWaves; ++q) {
+    for (int i = tid; i < sh.count[q]; i += kThreads) {
+      if (sh.key[q][i] >= kth) {
+        const int pos = atomicAdd(&sh.m, 1);
+        if (pos < kSortMax) {
+          sh.u.fast.key[pos] = sh.key[q][i];
+          sh.u.fast.idx[pos] = sh.idx[q][i];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int m = sh.m;
+  if (m > kSortMax) return false;
+  // ---- ranks 0..k by (key descending, index ascending) ----
+  if (m <= kRankSortMax) {
+    for (int i = tid; i < m; i += kThreads) {
+      const int key = sh.u.fast.key[i], id = sh.u.fast.idx[i];
+      int rank = 0;
+      for (int j = 0; j < m; ++j) rank += before(sh.u.fast.key[j], sh.u.fast.idx[j], key, id);
+      if (rank <= k) {
+        sh.s_val[rank] = key_value(key);
+        sh.s_idx[rank] = id;
+      }
+    }
+  } else {
+    block_bitonic_sort(sh.u.fast.key, sh.u.fast.idx, m, tid);
+    for (int i = tid; i <= k; i += kThreads) {
+      sh.s_val[i] = key_value(sh.u.fast.key[i]);
+      sh.s_idx[i] = sh.u.fast.idx[i];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < k; i += kThreads) {
+    if (!(sh.s_val[i] > sh.s_val[i + 1])) atomicOr(&sh.flags, 4);
+  }
+  __syncthreads();
+  return sh.flags == 0;
+}
+
+// The reference's replacement over the whole row, replayed; then a stable sort by total_cmp
+// into s_val / s_idx (whole workgroup).
+template <int VEC>
+__device__ __forceinline__ void replay_sorted(const float* row, int vocab, int k, int tid, int w, int lane,
+                                              SampleShared& sh) {
   if (k < vocab) {
-    // ---- one pass: buffer the logits that can be among the k+1 largest ----
-    int* rkey = sh.key[w];
-    int* ridx = sh.idx[w];
-    int bound = kIntMin, cnt = 0;
-    uint32_t nan_bits = 0;  // max of |bits|: above 0x7f800000 when a NaN was seen
-    stream_steps<VEC>(row, vocab, w, kWaves, nsteps, lane, [&](const float (&v)[kPerLane], int s) {
-      const int valid = vocab - s * kStep;  // logits of this step below vocab: step_index offsets < valid
-      int hits = 0;
-#pragma unroll
-      for (int e = 0; e < kPerLane; ++e) {
-        const bool in = step_index<VEC>(0, lane, e) < valid;
-        const uint32_t bits = __float_as_uint(v[e]);
-        nan_bits = max(nan_bits, in ? bits & 0x7fffffffu : 0u);
-        hits += (in && total_key(v[e]) >= bound) ? 1 : 0;
-      }
-      if (__ballot(hits > 0)) {  // rare once the bound has risen: append a group at a time
-#pragma unroll
-        for (int g = 0; g < kPerLane / (kGroup / 64); ++g) {
-#pragma unroll
-          for (int e = g * (kGroup / 64); e < (g + 1) * (kGroup / 64); ++e) {
-            const bool pass = step_index<VEC>(0, lane, e) < valid && total_key(v[e]) >= bound;
-            const uint64_t ball = __ballot(pass);
-            if (pass) {
-              const int pos = cnt + lanes_below(ball);
-              rkey[pos] = total_key(v[e]);
-              ridx[pos] = step_index<VEC>(s, lane, e);
-            }
-            cnt += __popcll(ball);
-          }
-          if (cnt > kRegion - kGroup) {
-            wave_sync();
-            bound = max(bound, wave_select_desc(rkey, cnt, k, sh.hist[w], lane));
-            cnt = wave_compact(rkey, ridx, cnt, bound, lane);
-            if (lane == 0) atomicMax(&sh.bound[w], bound);
-            if (cnt > kRegion - kGroup) {  // equal logits fill the buffer: the row is replayed
-              if (lane == 0) atomicOr(&sh.flags, 2);
-              cnt = 0;
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < kWaves; ++q) {
-        bound = max(bound, __hip_atomic_load(&sh.bound[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-      }
-    });
-    if (__ballot(nan_bits > 0x7f800000u) && lane == 0) atomicOr(&sh.flags, 1);
-    if (lane == 0) sh.count[w] = cnt;
-    __syncthreads();
-
-    if (sh.flags == 0) {
-      // ---- the k+1-th largest over all buffers (radix selection, 8 bits a round) ----
-      uint32_t prefix = 0, mask = 0;
-      int want = k;
-      for (int d = 24; d >= 0; d -= 8) {
-        if (tid < 256) sh.hist[0][tid] = 0;
-        __syncthreads();
-        for (int q = 0; q < kWaves; ++q) {
-          for (int i = tid; i < sh.count[q]; i += kThreads) {
-            const uint32_t u = static_cast<uint32_t>(sh.key[q][i]) ^ 0x80000000u;
-            if ((u & mask) == prefix) atomicAdd(&sh.hist[0][(u >> d) & 255u], 1);
-          }
-        }
-        __syncthreads();
-        if (w == 0) {
-          const int digit = pick_digit_desc(sh.hist[0], lane, want);
-          if (lane == 0) {
-            sh.sel[0] = digit;
-            sh.sel[1] = want;
-          }
-        }
-        __syncthreads();
-        prefix |= static_cast<uint32_t>(sh.sel[0]) << d;
-        mask |= 255u << d;
-        want = sh.sel[1];
-        __syncthreads();
-      }
-      const int kth = static_cast<int>(prefix ^ 0x80000000u);
-      // ---- gather the candidates at or above it ----
-      for (int q = 0; q < kWaves; ++q) {
-        for (int i = tid; i < sh.count[q]; i += kThreads) {
-          if (sh.key[q][i] >= kth) {
-            const int pos = atomicAdd(&sh.m, 1);
-            if (pos < kSortMax) {
-              sh.u.fast.key[pos] = sh.key[q][i];
-              sh.u.fast.idx[pos] = sh.idx[q][i];
-            }
-          }
-        }
-      }
-      __syncthreads();
-      const int m = sh.m;
-      if (m <= kSortMax) {
-        // ---- ranks 0..k by (key descending, index ascending) ----
-        if (m <= kRankSortMax) {
-          for (int i = tid; i < m; i += kThreads) {
-            const int key = sh.u.fast.key[i], id = sh.u.fast.idx[i];
-            int rank = 0;
-            for (int j = 0; j < m; ++j) rank += before(sh.u.fast.key[j], sh.u.fast.idx[j], key, id);
-            if (rank <= k) {
-              sh.s_val[rank] = key_value(key);
-              sh.s_idx[rank] = id;
-            }
-          }
-        } else {
-          block_bitonic_sort(sh.u.fast.key, sh.u.fast.idx, m, tid);
-          for (int i = tid; i <= k; i += kThreads) {
-            sh.s_val[i] = key_value(sh.u.fast.key[i]);
-            sh.s_idx[i] = sh.u.fast.idx[i];
-          }
-        }
-        __syncthreads();
-        for (int i = tid; i < k; i += kThreads) {
-          if (!(sh.s_val[i] > sh.s_val[i + 1])) atomicOr(&sh.flags, 4);
-        }
-        __syncthreads();
-        sorted = sh.flags == 0;
-      }
-    }
-  }
-
-  if (!sorted) {
-    // ---- the reference's replacement, replayed; then a stable sort by total_cmp ----
-    if (k < vocab) {
-      if (k <= 64) {
-        replay_top_k<VEC, 1>(row, vocab, k, w, lane, sh);
-      } else if (k <= 256) {
-        replay_top_k<VEC, 4>(row, vocab, k, w, lane, sh);
-      } else {
-        replay_top_k<VEC, 16>(row, vocab, k, w, lane, sh);
-      }
+    if (k <= 64) {
+      replay_top_k<VEC, 1>(row, vocab, k, w, lane, sh);
+    } else if (k <= 256) {
+      replay_top_k<VEC, 4>(row, vocab, k, w, lane, sh);
     } else {
-      for (int p = tid; p < k; p += kThreads) {
-        sh.u.list.val[p] = row[p];
-        sh.u.list.idx[p] = p;
-      }
-      __syncthreads();
+      replay_top_k<VEC, 16>(row, vocab, k, w, lane, sh);
     }
-    if (k <= kRankSortMax) {
-      for (int i = tid; i < k; i += kThreads) {
-        const int key = total_key(sh.u.list.val[i]);
-        int rank = 0;
-        for (int j = 0; j < k; ++j) rank += before(total_key(sh.u.list.val[j]), j, key, i);
-        sh.s_val[rank] = sh.u.list.val[i];
-        sh.s_idx[rank] = sh.u.list.idx[i];
-      }
-    } else {  // (key, list position) pairs in the first wave buffer
-      for (int i = tid; i < k; i += kThreads) {
-        sh.key[0][i] = total_key(sh.u.list.val[i]);
-        sh.idx[0][i] = i;
-      }
-      __syncthreads();
-      block_bitonic_sort(sh.key[0], sh.idx[0], k, tid);
-      for (int i = tid; i < k; i += kThreads) {
-        sh.s_val[i] = sh.u.list.val[sh.idx[0][i]];
-        sh.s_idx[i] = sh.u.list.idx[sh.idx[0][i]];
-      }
+  } else {
+    for (int p = tid; p < k; p += kThreads) {
+      sh.u.list.val[p] = row[p];
+      sh.u.list.idx[p] = p;
     }
     __syncthreads();
   }
+  if (k <= kRankSortMax) {
+    for (int i = tid; i < k; i += kThreads) {
+      const int key = total_key(sh.u.list.val[i]);
+      int rank = 0;
+      for (int j = 0; j < k; ++j) rank += before(total_key(sh.u.list.val[j]), j, key, i);
+      sh.s_val[rank] = sh.u.list.val[i];
+      sh.s_idx[rank] = sh.u.list.idx[i];
+    }
+  } else {  // (key, list position) pairs in the first wave buffer
+    for (int i = tid; i < k; i += kThreads) {
+      sh.key[0][i] = total_key(sh.u.list.val[i]);
+      sh.idx[0][i] = i;
+    }
+    __syncthreads();
+    block_bitonic_sort(sh.key[0], sh.idx[0], k, tid);
+    for (int i = tid; i < k; i += kThreads) {
+      sh.s_val[i] = sh.u.list.val[sh.idx[0][i]];
+      sh.s_idx[i] = sh.u.list.idx[sh.idx[0][i]];
+    }
+  }
+  __syncthreads();
+}
 
-  // ---- weights (parallel), then total, top-p, draw and threshold walk (one lane, in order) ----
+// Weights (parallel), then the total, top-p, draw and threshold walk (one lane, in the
+// reference's sequential f32 order) over the sorted list s_val / s_idx of k candidates.
+__device__ __forceinline__ void weights_and_draw(SampleShared& sh, int k, float T, float P, uint64_t* rng,
+                                                 int32_t* token, float* prob, uint32_t* faults, int r, int tid) {
   const float temp = fmaxf(T, 1.1920929e-7f);  // max(f32::EPSILON); a NaN temperature gives EPSILON
   const float scaled_max = sh.s_val[0] / temp;
   for (int i = tid; i < kMaxTopK; i += kThreads) sh.wts[i] = i < k ? expf((sh.s_val[i] / temp) - scaled_max) : 0.0f;
@@ -748,6 +787,184 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float* __restric
   }
 }
 
+// ---- launch 1: one workgroup per (row segment, row) ----
+// Segment j covers wave steps [j * seg_steps, (j + 1) * seg_steps).  Greedy rows leave their
+// segment's partial; sampled rows with k < vocab and k <= 1024 leave every logit of the segment
+// at or above the segment's k+1-th largest (a superset of the row's top k+1 that lies in the
+// segment) in the workspace, unordered; a flag (NaN, overflow, more than one region of
+// candidates) sends the row to the full replay in the finish.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void sample_scan_kernel(const float* __restrict__ logits, int ld, int vocab,
+                                                               int segs, int seg_steps,
+                                                               const float* __restrict__ temperature,
+                                                               const int32_t* __restrict__ top_k,
+                                                               const float* __restrict__ top_p, ScanMeta* __restrict__ meta,
+                                                               int* __restrict__ cand_key, int* __restrict__ cand_idx) {
+  __shared__ SampleShared sh;
+  const int seg = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float* row = logits + (size_t)r * ld;
+  const int nsteps = (vocab + kStep - 1) / kStep;
+  const int s0 = seg * seg_steps, s1 = min(nsteps, s0 + seg_steps);
+  const int lim = min(vocab, s1 * kStep);
+  ScanMeta* out = meta + (size_t)r * segs + seg;
+  if (greedy_row(temperature[r], top_k[r], top_p[r])) {
+    const GreedyPart g = greedy_pass<VEC>(row, vocab, s0, s1, lim, w, lane, tid, sh);
+    if (tid == 0) out->g = g;
+    return;
+  }
+  const int k = min(max(top_k[r], 1), vocab);
+  if (k > kMaxTopK || k >= vocab) return;  // the finish handles these rows alone
+  if (tid < kWaves) sh.bound[tid] = kIntMin;
+  if (tid == 0) {
+    sh.flags = 0;
+    sh.m = 0;
+  }
+  __syncthreads();
+  buffer_pass<VEC>(row, vocab, s0, s1, lim, k, w, lane, sh);
+  int total = 0;
+  for (int q = 0; q < kWaves; ++q) total += sh.count[q];
+  int* okey = cand_key + ((size_t)r * segs + seg) * kRegion;
+  int* oidx = cand_idx + ((size_t)r * segs + seg) * kRegion;
+  if (sh.flags == 0) {
+    // the segment's k+1-th largest (every buffered logit when the segment holds at most k+1)
+    const int kth = total > k + 1 ? select_desc(sh, k, tid, w, lane) : kIntMin;
+    for (int q = 0; q < kWaves; ++q) {
+      for (int i = tid; i < sh.count[q]; i += kThreads) {
+        if (sh.key[q][i] >= kth) {
+          const int pos = atomicAdd(&sh.m, 1);
+          if (pos < kRegion) {
+            okey[pos] = sh.key[q][i];
+            oidx[pos] = sh.idx[q][i];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    out->count = min(sh.m, kRegion);
+    out->flags = sh.flags | (sh.m > kRegion ? 2 : 0);
+  }
+}
+
+// ---- launch 2: one workgroup per row ----
+// Greedy rows merge their segments' partials in segment order; sampled rows gather the
+// segments' candidates into the wave buffers and take the fast path, or replay the reference's
+// replacement over the whole row; then the weights, top-p, draw and threshold walk.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void sample_finish_kernel(
+    const float* __restrict__ logits, int ld, int vocab, int segs, const float* __restrict__ temperature,
+    const int32_t* __restrict__ top_k, const float* __restrict__ top_p, uint64_t* __restrict__ rng,
+    const ScanMeta* __restrict__ meta, const int* __restrict__ cand_key, const int* __restrict__ cand_idx,
+    int32_t* __restrict__ token, float* __restrict__ prob, uint32_t* __restrict__ faults) {
+  __shared__ SampleShared sh;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float* row = logits + (size_t)r * ld;
+  const float T = temperature[r];
+  const int K = top_k[r];
+  const float P = top_p[r];
+  const ScanMeta* rm = meta + (size_t)r * segs;
+
+  if (greedy_row(T, K, P)) {
+    if (tid == 0) {
+      GreedyPart g = rm[0].g;
+      for (int j = 1; j < segs; ++j) {
+        const GreedyPart o = rm[j].g;
+        if (o.key > g.key || (o.key == g.key && o.idx > g.idx)) {
+          g.key = o.key;
+          g.idx = o.idx;
+        }
+        merge_softmax(g.m, g.sum, o.m, o.sum);
+        g.bad = g.bad || o.bad;
+      }
+      token[r] = g.idx;
+      prob[r] = (g.bad || !(g.sum > 0.0f)) ? __int_as_float(0x7fc00000) : 1.0f / g.sum;
+    }
+    return;
+  }
+
+  const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
+  if (k > kMaxTopK) {
+    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
+    return;
+  }
+  if (tid == 0) {
+    int f = 0;
+    for (int j = 0; j < segs; ++j) f |= rm[j].flags;
+    sh.flags = k < vocab ? f : 0;
+    sh.m = 0;
+  }
+  __syncthreads();
+
+  bool sorted = false;  // s_val / s_idx hold the sorted list
+  if (k < vocab && sh.flags == 0) {
+    for (int q = w; q < kWaves; q += kWaves) {  // wave q copies segment q's candidates
+      const int c = q < segs ? rm[q].count : 0;
+      const int* ck = cand_key + ((size_t)r * segs + q) * kRegion;
+      const int* ci = cand_idx + ((size_t)r * segs + q) * kRegion;
+      for (int i = lane; i < c; i += 64) {
+        sh.key[q][i] = ck[i];
+        sh.idx[q][i] = ci[i];
+      }
+      if (lane == 0) sh.count[q] = c;
+    }
+    __syncthreads();
+    sorted = fast_top_k(sh, k, tid, w, lane);
+  }
+
+  if (!sorted) replay_sorted<VEC>(row, vocab, k, tid, w, lane, sh);
+  weights_and_draw(sh, k, T, P, rng, token, prob, faults, r, tid);
+}
+
+// ---- the single-launch form: one workgroup per row over the whole row ----
+// For launches where a row gets one segment (rows enough to fill the device): the scan's
+// buffering and the finish's fast path run back to back on the wave buffers, with no
+// workspace round trip.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void sample_row_kernel(const float* __restrict__ logits, int ld, int vocab,
+                                                              const float* __restrict__ temperature,
+                                                              const int32_t* __restrict__ top_k,
+                                                              const float* __restrict__ top_p,
+                                                              uint64_t* __restrict__ rng, int32_t* __restrict__ token,
+                                                              float* __restrict__ prob, uint32_t* __restrict__ faults) {
+  __shared__ SampleShared sh;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float* row = logits + (size_t)r * ld;
+  const float T = temperature[r];
+  const int K = top_k[r];
+  const float P = top_p[r];
+  const int nsteps = (vocab + kStep - 1) / kStep;
+  if (greedy_row(T, K, P)) {
+    const GreedyPart g = greedy_pass<VEC>(row, vocab, 0, nsteps, vocab, w, lane, tid, sh);
+    if (tid == 0) {
+      token[r] = g.idx;
+      prob[r] = (g.bad || !(g.sum > 0.0f)) ? __int_as_float(0x7fc00000) : 1.0f / g.sum;
+    }
+    return;
+  }
+  const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
+  if (k > kMaxTopK) {
+    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
+    return;
+  }
+  if (tid < kWaves) sh.bound[tid] = kIntMin;
+  if (tid == 0) {
+    sh.flags = 0;
+    sh.m = 0;
+  }
+  __syncthreads();
+  bool sorted = false;
+  if (k < vocab) {
+    buffer_pass<VEC>(row, vocab, 0, nsteps, vocab, k, w, lane, sh);
+    if (sh.flags == 0) sorted = fast_top_k(sh, k, tid, w, lane);
+  }
+  if (!sorted) replay_sorted<VEC>(row, vocab, k, tid, w, lane, sh);
+  weights_and_draw(sh, k, T, P, rng, token, prob, faults, r, tid);
+}
+
 }  // namespace
 
 extern "C" {
@@ -761,15 +978,49 @@ int32_t fi_sample_tokens(fi_context* ctx, const float* d_logits, int32_t ld, int
   if (rows == 0) return FI_OK;
   FI_REQUIRE(d_logits && d_temperature && d_top_k && d_top_p && d_rng_state && d_token && d_prob,
              FI_ERR_INVALID_CONFIG, "fi_sample_tokens: null pointer");
+  FI_REQUIRE(rows <= 65535, FI_ERR_INVALID_SHAPE, "fi_sample_tokens: at most 65535 rows per call");
+  // rows split only as far as it takes to give every CU a workgroup (one fits a CU): a short
+  // segment buffers nearly all of its logits, so more segments cost more than they spread.
+  // Segments hold at least four wave steps (4096 logits, more than k + 1 for any k the device
+  // takes) and at most one per wave buffer of the finish.
+  const int nsteps = (vocab + kStep - 1) / kStep;
+  const int cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  const int fill = (cus + rows - 1) / rows;
+  const int segs = std::max(1, std::min({kMaxSegs, nsteps / 4, fill}));
+  const int seg_steps = (nsteps + segs - 1) / segs;
   const bool vec4 = vocab % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(d_logits) % 16 == 0;
-  if (vec4) {
-    hipLaunchKernelGGL(sample_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
-                       d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
-  } else {
-    hipLaunchKernelGGL(sample_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
-                       d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+  if (segs == 1) {
+    if (vec4) {
+      hipLaunchKernelGGL(sample_row_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                         d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+    } else {
+      hipLaunchKernelGGL(sample_row_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                         d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+    }
+    FI_CHECK_LAUNCH("sample_row_kernel");
+    return FI_OK;
   }
-  FI_CHECK_LAUNCH("sample_kernel");
+  const size_t meta_bytes = ((size_t)rows * segs * sizeof(ScanMeta) + 255) / 256 * 256;
+  const size_t cand_bytes = (size_t)rows * segs * kRegion * sizeof(int);
+  FI_TRY(fi::ensure_workspace(ctx, meta_bytes + 2 * cand_bytes));
+  ScanMeta* meta = static_cast<ScanMeta*>(ctx->workspace);
+  int* cand_key = reinterpret_cast<int*>(static_cast<char*>(ctx->workspace) + meta_bytes);
+  int* cand_idx = reinterpret_cast<int*>(static_cast<char*>(ctx->workspace) + meta_bytes + cand_bytes);
+  const dim3 scan_grid(static_cast<unsigned>(segs), static_cast<unsigned>(rows));
+  if (vec4) {
+    hipLaunchKernelGGL(sample_scan_kernel<4>, scan_grid, dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
+                       seg_steps, d_temperature, d_top_k, d_top_p, meta, cand_key, cand_idx);
+    hipLaunchKernelGGL(sample_finish_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
+                       d_temperature, d_top_k, d_top_p, d_rng_state, meta, cand_key, cand_idx, d_token, d_prob,
+                       ctx->d_faults);
+  } else {
+    hipLaunchKernelGGL(sample_scan_kernel<1>, scan_grid, dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
+                       seg_steps, d_temperature, d_top_k, d_top_p, meta, cand_key, cand_idx);
+    hipLaunchKernelGGL(sample_finish_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
+                       d_temperature, d_top_k, d_top_p, d_rng_state, meta, cand_key, cand_idx, d_token, d_prob,
+                       ctx->d_faults);
+  }
+  FI_CHECK_LAUNCH("sample_finish_kernel");
   return FI_OK;
 }
 
