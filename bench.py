@@ -396,7 +396,8 @@ def kernel_legs(ctx, seed):
         ms = timed(lambda: ctx.sample_tokens(logits, temp, topk, topp, st, tok, prob), 20)
         b = rows * vocab * 4
         out[f"sample_tokens_{tag}"] = {
-            "kernel": "sample_kernel<4>", "bound": "hbm", "rows": rows, "vocab": vocab,
+            "kernel": ("sample_row_kernel<4>" if rows >= 256 else "sample_scan_kernel<4> + sample_finish_kernel<4>"),
+            "bound": "hbm", "rows": rows, "vocab": vocab,
             "temperature": cfg[0], "top_k": cfg[1], "top_p": cfg[2], "bytes_per_launch": b,
             "avg_launch_us": round(ms * 1e3, 2), "achieved_gbs": round(b / (ms * 1e-3) / 1e9, 1),
             "peak_gbs": HBM_PEAK_GBS, "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
