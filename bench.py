@@ -510,6 +510,19 @@ def c4_roofline(cfg, ticks, weight_bytes, peak_tfs):
     }
 
 
+_C4_WEIGHTS = {}
+
+
+def c4_weights(seed):
+    """The C4 model's seeded weights, generated once per seed for every leg that serves them."""
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, random_weights
+
+    if seed not in _C4_WEIGHTS:
+        _C4_WEIGHTS.clear()
+        _C4_WEIGHTS[seed] = random_weights(QWEN2_05B_C4, seed=seed, qkv_bias=True)
+    return _C4_WEIGHTS[seed]
+
+
 def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"):
     """C4: the Qwen2-0.5B-shaped model (f32, tied, q/k/v biases, random N(0, 0.02) weights)
     served by the GPU runtime under continuous batching (max batch 64, block 16, the
@@ -521,10 +534,10 @@ def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"
     import numpy as np
 
     from ferrisinfer_amd.runtime import Runtime
-    from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, random_weights, run_continuous
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, run_continuous
 
     cfg = QWEN2_05B_C4
-    weights = random_weights(cfg, seed=seed, qkv_bias=True)
+    weights = c4_weights(seed)
     rt = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
                  cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"], tie=True, max_seq=4096,
                  max_gen=512, max_batch=64, num_blocks=16384, block_size=16, sampler=sampler,
@@ -698,7 +711,7 @@ def c4_cpu_baseline(seed, threads):
     (one prefill tick) and 2 new tokens each, so both decode ticks run at batch 64 like the GPU
     figure it sits next to; tok/s by the reference's definition (generated / decode-tick time)."""
     import oracle
-    from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, random_weights, run_continuous
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, c4_requests, run_continuous
 
     oracle.build()
     oracle.set_threads(threads)
@@ -706,7 +719,7 @@ def c4_cpu_baseline(seed, threads):
     model = oracle.Model(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"],
                          cfg["kv_heads"], cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"],
                          tie=True)
-    model.set_weights(random_weights(cfg, seed=seed, qkv_bias=True))
+    model.set_weights(c4_weights(seed))
     reqs = c4_requests(seed=seed)[:64]
     for r in reqs:
         r["prompt"] = r["prompt"][:16]

@@ -1,7 +1,10 @@
 """Seeded synthetic inputs for the BASELINE configurations (host numpy arrays).
 
-All randomness comes from ``numpy.random.default_rng(seed)`` (PCG64), so the GPU path and
-the CPU oracle see bit-identical inputs.  Layouts follow include/ferrisinfer_kernel.h.
+C1-C4 draw from the reference's xorshift64* through ferrisinfer_amd.seeded (uniforms,
+Box-Muller normals, integers, Fisher-Yates permutations, one tag per field), so any host can
+regenerate them; the GPU path and the CPU oracle see bit-identical inputs.  The synthetic
+checkpoints of the import tests keep numpy's PCG64.  Layouts follow
+include/ferrisinfer_kernel.h.
 """
 from __future__ import annotations
 
@@ -11,6 +14,9 @@ import struct
 from dataclasses import dataclass
 
 import numpy as np
+
+from . import seeded
+from .seeded import tag_of
 
 
 @dataclass
@@ -53,29 +59,29 @@ def paged_decode_c2(seed: int = 0, num_seqs: int = 64, min_len: int = 128, max_l
                     num_q_heads: int = 32, num_kv_heads: int = 8, head_dim: int = 128,
                     block_size: int = 16, num_blocks: int = 8192,
                     fill_unused_blocks: bool = False) -> PagedDecodeWorkload:
-    """C2: lengths ~ U[min_len, max_len]; block ids are the first sum(ceil(L/bs)) entries of a
-    seeded permutation of the pool, handed to the sequences in order; Q/K/V ~ N(0, 1);
+    """C2: lengths ~ U[min_len, max_len] (tag "c2.lens"); block ids are the first
+    sum(ceil(L/bs)) entries of a permutation of the pool ("c2.perm"), handed to the sequences in
+    order; Q ("c2.q") and the used blocks' K / V ("c2.k", "c2.v", in block-id order) ~ N(0, 1);
     scale 1/sqrt(D).  Unused pool blocks are zero unless ``fill_unused_blocks``."""
-    rng = np.random.default_rng(seed)
-    lens = rng.integers(min_len, max_len + 1, size=num_seqs).astype(np.int32)
+    lens = seeded.integers(seed, tag_of("c2.lens"), num_seqs, min_len, max_len).astype(np.int32)
     nblk = (lens + block_size - 1) // block_size
     total = int(nblk.sum())
     if total > num_blocks:
         raise ValueError(f"workload needs {total} blocks, pool has {num_blocks}")
-    perm = rng.permutation(num_blocks).astype(np.int32)
+    perm = seeded.permutation(seed, tag_of("c2.perm"), num_blocks)
     max_blocks = int(nblk.max())
     tables = np.zeros((num_seqs, max_blocks), np.int32)
     cursor = 0
     for i, n in enumerate(nblk):
         tables[i, :n] = perm[cursor:cursor + n]
         cursor += n
-    q = rng.standard_normal((num_seqs, num_q_heads, head_dim), dtype=np.float32)
+    q = seeded.normals(seed, tag_of("c2.q"), (num_seqs, num_q_heads, head_dim))
     shape = (num_blocks, num_kv_heads, block_size, head_dim)
     k_pool = np.zeros(shape, np.float32)
     v_pool = np.zeros(shape, np.float32)
-    used = perm[:total] if not fill_unused_blocks else perm
-    k_pool[used] = rng.standard_normal((used.size,) + shape[1:], dtype=np.float32)
-    v_pool[used] = rng.standard_normal((used.size,) + shape[1:], dtype=np.float32)
+    used = np.sort(perm[:total] if not fill_unused_blocks else perm)
+    k_pool[used] = seeded.normals(seed, tag_of("c2.k"), (used.size,) + shape[1:])
+    v_pool[used] = seeded.normals(seed, tag_of("c2.v"), (used.size,) + shape[1:])
     return PagedDecodeWorkload(num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                                num_blocks, lens, tables, q, k_pool, v_pool,
                                float(1.0 / np.sqrt(np.float32(head_dim))))
@@ -141,9 +147,9 @@ def prefill_c3(seed: int = 0, num_seqs: int = 16, min_len: int = 32, max_len: in
     min(shared_prefix, floor((L - 1) / block_size) * block_size) tokens (block aligned and
     never the whole prompt, as runtime/prefix_index.rs:98-109 keeps one token to compute)
     and computes only its suffix.  The source computes all its tokens in the same batch;
-    KV append precedes attention, so members read the source's freshly written blocks."""
-    rng = np.random.default_rng(seed)
-    lens = rng.integers(min_len, max_len + 1, size=num_seqs).astype(np.int32)
+    KV append precedes attention, so members read the source's freshly written blocks.
+    Seeded fields: "c3.lens", "c3.perm", "c3.q", "c3.k", "c3.v"."""
+    lens = seeded.integers(seed, tag_of("c3.lens"), num_seqs, min_len, max_len).astype(np.int32)
     shared = np.zeros(num_seqs, np.int32)
     source = np.full(num_seqs, -1, np.int32)
     for g in range(min(groups, num_seqs // group_size)):
@@ -157,7 +163,7 @@ def prefill_c3(seed: int = 0, num_seqs: int = 16, min_len: int = 32, max_len: in
             source[b] = src if shared[b] > 0 else -1
     nblk = (lens + block_size - 1) // block_size
     own_blocks = nblk - shared // block_size
-    perm = rng.permutation(num_blocks).astype(np.int32)
+    perm = seeded.permutation(seed, tag_of("c3.perm"), num_blocks)
     if int(own_blocks.sum()) > num_blocks:
         raise ValueError("pool too small")
     tables = np.zeros((num_seqs, int(nblk.max())), np.int32)
@@ -178,9 +184,9 @@ def prefill_c3(seed: int = 0, num_seqs: int = 16, min_len: int = 32, max_len: in
         for i in range(int(qlens[b])):
             pos = int(shared[b]) + i
             slots[cu[b] + i] = int(tables[b, pos // block_size]) * block_size + pos % block_size
-    q = rng.standard_normal((T, num_q_heads, head_dim), dtype=np.float32)
-    k = rng.standard_normal((T, num_kv_heads, head_dim), dtype=np.float32)
-    v = rng.standard_normal((T, num_kv_heads, head_dim), dtype=np.float32)
+    q = seeded.normals(seed, tag_of("c3.q"), (T, num_q_heads, head_dim))
+    k = seeded.normals(seed, tag_of("c3.k"), (T, num_kv_heads, head_dim))
+    v = seeded.normals(seed, tag_of("c3.v"), (T, num_kv_heads, head_dim))
     return PrefillWorkload(num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, lens, shared,
                            source, tables, cu, lens.copy(), slots, q, k, v,
                            float(1.0 / np.sqrt(np.float32(head_dim))))
@@ -197,40 +203,40 @@ QWEN2_05B_C4 = dict(hidden=896, intermediate=4864, layers=24, heads=14, kv_heads
 
 def random_weights(cfg: dict, seed: int = 0, qkv_bias: bool = False, std: float = 0.02) -> dict:
     """Weights named as model/decoder.rs:30-52 in the reference's [in, out] layout.  Matrices,
-    embeddings and (optional, Qwen2-style) q/k/v biases ~ N(0, std); RMSNorm weights = 1."""
-    rng = np.random.default_rng(seed)
+    embeddings and (optional, Qwen2-style) q/k/v biases ~ N(0, std), each tensor seeded by its
+    name (tag = CRC-32 of the name); RMSNorm weights = 1."""
     h, f, v = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
     kvw = cfg["kv_heads"] * (h // cfg["heads"])
 
-    def n(*shape):
-        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+    def n(name, *shape):
+        return seeded.normals(seed, tag_of(name), shape, scale=std)
 
-    w = {"tok_embeddings.weight": n(v, h)}
+    w = {"tok_embeddings.weight": n("tok_embeddings.weight", v, h)}
     for layer in range(cfg["layers"]):
         p = f"layers.{layer}."
         w[p + "attention_norm.weight"] = np.ones(h, np.float32)
-        w[p + "attention.wq.weight"] = n(h, h)
-        w[p + "attention.wk.weight"] = n(h, kvw)
-        w[p + "attention.wv.weight"] = n(h, kvw)
+        for name, shape in (("attention.wq.weight", (h, h)), ("attention.wk.weight", (h, kvw)),
+                            ("attention.wv.weight", (h, kvw))):
+            w[p + name] = n(p + name, *shape)
         if qkv_bias:
-            w[p + "attention.wq.bias"] = n(h)
-            w[p + "attention.wk.bias"] = n(kvw)
-            w[p + "attention.wv.bias"] = n(kvw)
-        w[p + "attention.wo.weight"] = n(h, h)
+            for name, width in (("attention.wq.bias", h), ("attention.wk.bias", kvw), ("attention.wv.bias", kvw)):
+                w[p + name] = n(p + name, width)
+        w[p + "attention.wo.weight"] = n(p + "attention.wo.weight", h, h)
         w[p + "ffn_norm.weight"] = np.ones(h, np.float32)
-        w[p + "feed_forward.w1.weight"] = n(h, f)
-        w[p + "feed_forward.w2.weight"] = n(f, h)
-        w[p + "feed_forward.w3.weight"] = n(h, f)
+        for name, shape in (("feed_forward.w1.weight", (h, f)), ("feed_forward.w2.weight", (f, h)),
+                            ("feed_forward.w3.weight", (h, f))):
+            w[p + name] = n(p + name, *shape)
     w["norm.weight"] = np.ones(h, np.float32)
     if not cfg.get("tie", False):
-        w["output.weight"] = n(v, h)
+        w["output.weight"] = n("output.weight", v, h)
     return w
 
 
 def c1_requests(seed: int = 0, vocab: int = 4096):
-    """C1: 4 prompts of 16/24/32/48 ids ~ U[0, vocab), 32 greedy tokens each."""
-    rng = np.random.default_rng(seed + 1)
-    return [(rng.integers(0, vocab, size=n).astype(np.uint32), 32) for n in (16, 24, 32, 48)]
+    """C1: 4 prompts of 16/24/32/48 ids ~ U[0, vocab) (tags "c1.prompt.<i>"), 32 greedy tokens
+    each."""
+    return [(seeded.integers(seed, tag_of(f"c1.prompt.{i}"), n, 0, vocab - 1).astype(np.uint32), 32)
+            for i, n in enumerate((16, 24, 32, 48))]
 
 
 # ----------------------------------------------------------------------------- C4
@@ -245,17 +251,20 @@ def c4_requests(seed: int = 0, n: int = 128, vocab: int = 151936) -> list:
     """C4 workload: ``n`` requests, Poisson arrivals at 8/s mapped to integer ticks of a
     fixed 50 ms virtual duration (the reference's continuous-batching driver admits requests
     by integer arrival tick, cli/main.rs:1721-1741), prompt lengths lognormal (median 512,
-    sigma 0.5) clipped to [1, 2048], ids ~ U[0, vocab), output lengths ~ U[64, 256]."""
-    rng = np.random.default_rng(seed + 4)
-    gaps = rng.exponential(1.0 / C4_ARRIVAL_RATE, size=n)
+    sigma 0.5) clipped to [1, 2048], ids ~ U[0, vocab), output lengths ~ U[64, 256].
+    Seeded fields: gaps -ln(1 - u) / rate ("c4.gaps"), log-lengths from normals ("c4.lens"),
+    outputs ("c4.outs"), the ids of request i ("c4.prompt.<i>"); f64 arithmetic."""
+    u = seeded.uniforms(seed, tag_of("c4.gaps"), n).astype(np.float64)
+    gaps = -np.log(1.0 - u) / C4_ARRIVAL_RATE
     arrival_s = np.cumsum(gaps) - gaps[0]
     ticks = np.floor(arrival_s / C4_VIRTUAL_TICK_S).astype(np.int64)
-    lens = np.exp(np.log(C4_PROMPT_MEDIAN) + C4_PROMPT_SIGMA * rng.standard_normal(n))
+    z = seeded.normals(seed, tag_of("c4.lens"), (n,)).astype(np.float64)
+    lens = np.exp(np.log(C4_PROMPT_MEDIAN) + C4_PROMPT_SIGMA * z)
     lens = np.clip(np.rint(lens), 1, C4_MAX_PROMPT).astype(np.int64)
-    outs = rng.integers(64, 257, size=n)
-    return [dict(prompt=rng.integers(0, vocab, size=int(L)).astype(np.uint32),
+    outs = seeded.integers(seed, tag_of("c4.outs"), n, 64, 256)
+    return [dict(prompt=seeded.integers(seed, tag_of(f"c4.prompt.{i}"), int(L), 0, vocab - 1).astype(np.uint32),
                  max_new_tokens=int(o), arrival_tick=int(t))
-            for L, o, t in zip(lens, outs, ticks)]
+            for i, (L, o, t) in enumerate(zip(lens, outs, ticks))]
 
 
 def run_continuous(sched, requests: list, max_ticks: int | None = None) -> dict:
