@@ -672,7 +672,7 @@ def c5_step(seed, steps):
     ops["w2_gemm"] = (timed(lambda: ctx.gemm_bf16(act, lw["w2"], f, h, s_w2, parts), 10),
                       2.0 * t * f * h, "mfma")
     r = int(batch.last_rows.numel())
-    ops["lm_head_argmax"] = (timed(lambda: ctx.lm_head_argmax_bf16(dec.last[:r], dec.lm_head, v, dec.tok[:r],
+    ops["lm_head_argmax"] = (timed(lambda: ctx.lm_head_argmax_bf16(dec.last16[:r], dec.lm_head, v, dec.tok[:r],
                                                                    dec.prob[:r]), 10), 2.0 * r * h * v, "mfma")
     ctx.check_faults()
     out_ops = {}

@@ -91,6 +91,8 @@ class Bf16Decoder:
             self.act = torch.empty(t, self.f, device=dev)
         self.max_tokens = t
         self.last = torch.empty(max_last_rows, self.h, device=dev)
+        if self.bf16_activations:
+            self.last16 = torch.empty(max_last_rows, self.h, dtype=torch.int16, device=dev)
         self.tok = torch.empty(max_last_rows, dtype=torch.int32, device=dev)
         self.prob = torch.empty(max_last_rows, device=dev)
         self.max_pos = cfg["max_pos"]
@@ -180,6 +182,9 @@ class Bf16Decoder:
         r = int(b.last_rows.numel())
         last = self.last[:r]
         c.embedding(normed, b.last_rows, last)
+        if b16:  # the head's input as bf16 bits (the kernel rounds f32 the same way)
+            c.convert_f32_to_bf16(last, self.last16[:r])
+            last = self.last16[:r]
         c.lm_head_argmax_bf16(last, self.lm_head, self.v, self.tok[:r], self.prob[:r])
         return self.tok[:r], self.prob[:r]
 

@@ -343,14 +343,16 @@ int mt_for(int m) { return m > 64 ? 8 : (m > 32 ? 4 : (m > 16 ? 2 : 1)); }
 
 constexpr int kNt = 4;  // slabs per wave: a workgroup covers 256 columns
 
-// Split count: two workgroups per CU where the tile grid is smaller, every split at least 8 K
+// Split count: three workgroups per CU where the tile grid is smaller, every split at least 8 K
 // steps, and the partials (splits x M x N f32) at most the weight's bytes.
 int split_count(fi_context* ctx, int m, int k, int slabs) {
   const int mblocks = (m + 16 * mt_for(m) - 1) / (16 * mt_for(m));
   const int groups = (slabs + kWaves * kNt - 1) / (kWaves * kNt);
   const int q = q_steps(k);
   const long tiles = (long)mblocks * groups;
-  const long target = (long)kOccupancy * (ctx->compute_units > 0 ? ctx->compute_units : 256);
+  // three workgroups per CU: a CU's two resident tiles are followed by a third, so the last
+  // round is a third of a round (w2 at M 2304: 2 -> 3 splits, 345 -> 314 us with its consumer)
+  const long target = (long)(kOccupancy + 1) * (ctx->compute_units > 0 ? ctx->compute_units : 256);
   long s = std::max(1L, (target + tiles - 1) / tiles);
   s = std::min(s, std::max(1L, static_cast<long>(q / 8)));
   s = std::min(s, std::max(1L, static_cast<long>(k) / (2L * std::max(m, 16))));
