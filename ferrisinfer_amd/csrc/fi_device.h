@@ -40,6 +40,20 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// The value lane ^ 32 (lane ^ 16) holds, from v_permlane32_swap (v_permlane16_swap): a VALU
+// exchange between the wave's halves (16-lane rows) with no LDS round trip.  With both
+// operands x, the swap's second result holds the partner in lanes 0-31 (even rows) and its
+// first result in lanes 32-63 (odd rows).
+__device__ __forceinline__ float lane_xor32(float x, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(lane < 32 ? r[1] : r[0]);
+}
+
+__device__ __forceinline__ float lane_xor16(float x, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(((lane >> 4) & 1) == 0 ? r[1] : r[0]);
+}
+
 // bf16 storage: widening is exact (bits << 16); narrowing rounds to nearest even.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);

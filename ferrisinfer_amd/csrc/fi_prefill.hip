@@ -284,8 +284,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
           s_acc[g][jt][v] = x;
           mx = fmaxf(mx, x);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = fmaxf(mx, fi::lane_xor16(mx, lane));
+      mx = fmaxf(mx, fi::lane_xor32(mx, lane));
       const float m_new = fmaxf(m_row[g], mx);  // finite: key 0 of chunk 0 is visible to every row
       const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
       m_row[g] = m_new;
@@ -334,8 +334,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   // ---- normalise and store: lane holds row li of each group, d = 64 h + 16 lk + 4 v + p ----
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
-    float l_row = l_part[g] + __shfl_xor(l_part[g], 16, 64);
-    l_row += __shfl_xor(l_row, 32, 64);
+    float l_row = l_part[g] + fi::lane_xor16(l_part[g], lane);
+    l_row += fi::lane_xor32(l_row, lane);
     const int hd = row_r[g] / QT, t = row_r[g] % QT;
     if (hd < a.group && q0 + t < qlen) {
       const float inv = 1.0f / l_row;
@@ -610,8 +610,8 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
           s_acc[g][jt][v] = x;
           mx = fmaxf(mx, x);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = fmaxf(mx, fi::lane_xor16(mx, lane));
+      mx = fmaxf(mx, fi::lane_xor32(mx, lane));
       const float m_new = fmaxf(m_row[g], mx * c2);  // finite: key 0 of chunk 0 is visible to every row
       const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
       m_row[g] = m_new;
@@ -669,8 +669,8 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
   // ---- normalise and store: lane holds row li of each group, d = 16 dt + 4 lk + v ----
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
-    float l_row = l_part[g] + __shfl_xor(l_part[g], 16, 64);
-    l_row += __shfl_xor(l_row, 32, 64);
+    float l_row = l_part[g] + fi::lane_xor16(l_part[g], lane);
+    l_row += fi::lane_xor32(l_row, lane);
     const int h = row_r[g] / QT, t = row_r[g] % QT;
     if (h < a.group && q0 + t < qlen) {
       const float inv = 1.0f / l_row;
