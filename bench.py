@@ -64,11 +64,75 @@ def parse_args():
     p.add_argument("--pmc-copy-reference", action="store_true",
                    help="only run a plain 512 MiB device copy (5 launches): the known-size "
                         "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    p.add_argument("--c4-layer-ops", action="store_true",
+                   help="only run one C4 decode-tick layer's ops at batch 64 (Qwen2-0.5B shape: the "
+                        "M = 64 projections, the q|k|v consumer, KV append, residual norm, SwiGLU "
+                        "split sum, greedy head), 10 launches each: the command the C4 counter "
+                        "profiles run under rocprofv3")
     p.add_argument("--paged-read-ceiling", action="store_true",
                    help="only time read-only kernels over the C2 f32 pools in three decompositions "
                         "(per-kv-head chunks, whole blocks, linear) at several partition sizes, "
                         "next to the decode op itself: the HBM rate the access pattern allows")
     return p.parse_args()
+
+
+def c4_layer_ops(seed):
+    """One C4 decode-tick layer's kernels at batch 64 on random inputs, 10 launches each."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32, Context
+
+    ctx = Context(0)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    m, h, f, v, hq, hkv, d = 64, 896, 4864, 151936, 14, 2, 64
+    nb, bs = 4096, 16
+
+    def rn(*shape):
+        return torch.randn(*shape, device="cuda", generator=g)
+
+    x = rn(m, h)
+    nqkv = h + 2 * hkv * d
+    w_qkv = ctx.weight_pack(rn(h, nqkv) * 0.02, h, nqkv, 1)
+    w_o = ctx.weight_pack(rn(h, h) * 0.02, h, h, 1)
+    w_2 = ctx.weight_pack(rn(f, h) * 0.02, f, h, 4)
+    pair = ctx.weight_pack_pair(rn(h, f) * 0.02, rn(h, f) * 0.02, h, f)
+    head = ctx.weight_pack(rn(v, h) * 0.02, h, v, 2, src_layout=1)
+    s_qkv = ctx.gemm_packed_splits(m, h, nqkv, 1)
+    s_o = ctx.gemm_packed_splits(m, h, h, 1)
+    s_w2 = ctx.gemm_packed_splits(m, f, h, 4)
+    p_qkv = torch.empty(s_qkv, m, nqkv, device="cuda")
+    p_o = torch.empty(s_o, m, h, device="cuda")
+    p_w2 = torch.empty(s_w2, m, h, device="cuda")
+    act = torch.empty(m, f, device="cuda")
+    tok = torch.empty(m, dtype=torch.int32, device="cuda")
+    prob = torch.empty(m, device="cuda")
+    kp = torch.zeros(nb, hkv, bs, d, device="cuda")
+    vp = torch.zeros_like(kp)
+    pos = torch.arange(1000, 1000 + m, dtype=torch.int32, device="cuda")
+    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(seed + 1))[:m].to(torch.int64).cuda()
+    cos = torch.empty(4096, d // 2, device="cuda")
+    sin = torch.empty_like(cos)
+    ctx.rope_table(4096, d, d, 1e6, cos, sin)
+    q = torch.empty(m, hq, d, device="cuda")
+    kn, vn = rn(m, hkv, d), rn(m, hkv, d)
+    res = rn(m, h)
+    ssum = torch.empty(m, h, device="cuda")
+    nw = torch.ones(h, device="cuda")
+    nout = torch.empty(m, h, device="cuda")
+    for _ in range(10):
+        ctx.gemm_packed(x, w_qkv, h, nqkv, 1, s_qkv, p_qkv)
+        ctx.qkv_rope_append(p_qkv, s_qkv, None, pos, cos, sin, d, 4096, slots, kp, vp, DTYPE_F32, nb, bs,
+                            hq, hkv, d, q)
+        ctx.kv_append(kn, vn, slots, kp, vp, DTYPE_F32, nb, bs, hkv, d)
+        ctx.gemm_packed(x, w_o, h, h, 1, s_o, p_o)
+        ctx.splitk_residual_rms_norm(p_o, s_o, None, res, ssum, nw, nout, 1e-6)
+        ctx.gemm_packed_swiglu(x, pair, h, f, act)
+        ctx.gemm_packed(act, w_2, f, h, 4, s_w2, p_w2)
+        ctx.lm_head_argmax_packed(x, head, v, tok, prob)
+    torch.cuda.synchronize()
+    ctx.check_faults()
+    print(json.dumps({"c4_layer_ops": "done", "splits": {"qkv": s_qkv, "wo": s_o, "w2": s_w2}}), flush=True)
+    ctx.close()
 
 
 def paged_read_ceiling(seed):
@@ -750,6 +814,9 @@ def main():
         return
     if args.paged_read_ceiling:
         paged_read_ceiling(args.seed)
+        return
+    if args.c4_layer_ops:
+        c4_layer_ops(args.seed)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
