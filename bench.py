@@ -891,7 +891,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if args.kv_dtype == "f32" else "f32 compute, bf16 KV",
-        "data": "synthetic (seeded numpy PCG64, N(0,1) Q/K/V)",
+        "data": "synthetic: N(0,1) Q/K/V from the reference sampler's xorshift64* (splitmix64-seeded "
+                f"streams, Box-Muller), seed {args.seed}",
         "value_is": "C2 paged-attention op rate: 64 query tokens per fi_attn_decode_paged launch "
                     "(one layer's decode attention over the batch) / wall time per launch; the model-"
                     "level decode rate is c4_decode_tok_s_at_batch_64",

@@ -337,16 +337,41 @@ __global__ __launch_bounds__(kThreads, kOccupancy) void gemm_bf16_kernel(BGemmAr
 
 int32_t q_steps(int32_t k) { return (k + kStepK - 1) / kStepK; }
 
-// Row tiles per wave for M rows: 8 (128-row blocks: the accumulators of two workgroups per CU
-// fit the register file) down to 1.
-int mt_for(int m) { return m > 64 ? 8 : (m > 32 ? 4 : (m > 16 ? 2 : 1)); }
-
 constexpr int kNt = 4;  // slabs per wave: a workgroup covers 256 columns
+
+#ifndef FI_BGEMM_FORCE_MT
+#define FI_BGEMM_FORCE_MT 0  // a fixed row tile count above 64 rows (0: chosen per shape)
+#endif
+
+// Row tiles per wave for M rows.  Up to 64 rows: the smallest power of two holding them.
+// Above, 8, 6 or 4 (128-, 96- or 64-row blocks; the accumulators of two workgroups per CU fit
+// the register file at 8), whichever leaves the busiest CU the fewest row tiles of the unsplit
+// grid, ceil(blocks * groups / CUs) * MT, ties going to the larger tile (more MFMAs per weight
+// fragment).  wo at M 2304 (16 column groups): 288 blocks of 128 rows give some CUs two, 384
+// blocks of 96 rows give them two smaller ones.
+int mt_for(fi_context* ctx, int m, int slabs) {
+  if (m <= 64) return m > 32 ? 4 : (m > 16 ? 2 : 1);
+  if (FI_BGEMM_FORCE_MT > 0) return FI_BGEMM_FORCE_MT;
+  const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  const long groups = (slabs + kWaves * kNt - 1) / (kWaves * kNt);
+  int best = 8;
+  long best_cost = -1;
+  for (int mt : {8, 6, 4}) {
+    const long blocks = (m + 16L * mt - 1) / (16L * mt);
+    const long cost = (blocks * groups + cus - 1) / cus * mt;
+    if (best_cost < 0 || cost < best_cost) {
+      best = mt;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
 
 // Split count: three workgroups per CU where the tile grid is smaller, every split at least 8 K
 // steps, and the partials (splits x M x N f32) at most the weight's bytes.
 int split_count(fi_context* ctx, int m, int k, int slabs) {
-  const int mblocks = (m + 16 * mt_for(m) - 1) / (16 * mt_for(m));
+  const int mt = mt_for(ctx, m, slabs);
+  const int mblocks = (m + 16 * mt - 1) / (16 * mt);
   const int groups = (slabs + kWaves * kNt - 1) / (kWaves * kNt);
   const int q = q_steps(k);
   const long tiles = (long)mblocks * groups;
@@ -381,7 +406,7 @@ void launch_mt(fi_context* ctx, const BGemmArgs& g, bool a16) {
 
 template <int EPI>
 int32_t launch_bgemm(fi_context* ctx, BGemmArgs g, int splits, bool a16) {
-  const int mt = mt_for(g.m);
+  const int mt = mt_for(ctx, g.m, g.slabs);
   g.mblocks = (g.m + 16 * mt - 1) / (16 * mt);
   g.groups = (g.slabs + kWaves * kNt - 1) / (kWaves * kNt);
   g.splits = splits;
@@ -389,6 +414,9 @@ int32_t launch_bgemm(fi_context* ctx, BGemmArgs g, int splits, bool a16) {
   switch (mt) {
     case 8:
       launch_mt<8, EPI>(ctx, g, a16);
+      break;
+    case 6:
+      launch_mt<6, EPI>(ctx, g, a16);
       break;
     case 4:
       launch_mt<4, EPI>(ctx, g, a16);

@@ -52,9 +52,12 @@ def padded(a):
     return d[:, :k]
 
 
-SHAPES = [  # (M, K, N): C5 decode / prefill tiles, C1 and C4 shapes, ragged tails
+SHAPES = [  # (M, K, N): C5 decode / prefill tiles, C1 and C4 shapes, ragged tails; the C5 step's
+    # M 2304 runs 128-row blocks over q|k|v's 24 column groups and 96-row blocks over 16 (K cut
+    # short to keep the oracle quick)
     (256, 4096, 1024), (300, 512, 520), (64, 896, 1152), (8, 256, 688), (37, 96, 300),
-    (1, 64, 40), (17, 100, 33), (130, 4096, 256), (5, 2, 3),
+    (1, 64, 40), (17, 100, 33), (130, 4096, 256), (5, 2, 3), (2304, 64, 6144), (2304, 96, 4096),
+    (2300, 100, 4090),
 ]
 
 
