@@ -268,7 +268,19 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         }
     }
     // causal / context mask only where the chunk reaches past the tile's first query position
-    const bool full = k0 + kKeys - 1 <= start + q0;  // workgroup-uniform
+    // (workgroup-uniform; tested once, outside the unrolled score loops; -inf stays -inf when
+    // scaled below)
+    if (k0 + kKeys - 1 > start + q0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kp = k0 + 16 * jt + 4 * lk + v;
+            s_acc[g][jt][v] = (kp <= qpos[g] && kp < ctx) ? s_acc[g][jt][v] : -INFINITY;
+          }
+    }
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
       float mx = -INFINITY;
@@ -276,11 +288,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
       for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          float x = s_acc[g][jt][v] * c2;
-          if (!full) {
-            const int kp = k0 + 16 * jt + 4 * lk + v;
-            x = (kp <= qpos[g] && kp < ctx) ? x : -INFINITY;
-          }
+          const float x = s_acc[g][jt][v] * c2;
           s_acc[g][jt][v] = x;
           mx = fmaxf(mx, x);
         }
@@ -592,7 +600,19 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
       }
     }
     // causal / context mask only where the chunk reaches past the tile's first query position
-    const bool full = k0 + KB - 1 <= start + q0;  // workgroup-uniform
+    // (workgroup-uniform; tested once, outside the unrolled score loops, so that unmasked chunks
+    // run straight-line code)
+    if (k0 + KB - 1 > start + q0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kp = k0 + 16 * jt + 4 * lk + v;
+            s_acc[g][jt][v] = (kp <= qpos[g] && kp < ctx) ? s_acc[g][jt][v] : -INFINITY;
+          }
+    }
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
       // raw scores: the maximum is taken before scaling (c2 > 0 and rounding are monotone, so
@@ -601,15 +621,7 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float x = s_acc[g][jt][v];
-          if (!full) {
-            const int kp = k0 + 16 * jt + 4 * lk + v;
-            x = (kp <= qpos[g] && kp < ctx) ? x : -INFINITY;
-          }
-          s_acc[g][jt][v] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s_acc[g][jt][v]);
       mx = fmaxf(mx, fi::lane_xor16(mx, lane));
       mx = fmaxf(mx, fi::lane_xor32(mx, lane));
       const float m_new = fmaxf(m_row[g], mx * c2);  // finite: key 0 of chunk 0 is visible to every row
