@@ -516,6 +516,7 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
     l_part[g] = 0.0f;
   }
   const float c2 = a.scale * 1.4426950408889634f;  // scores -> log2 units
+  constexpr float kLazy = 8.0f;  // headroom of the exponents' reference point (log2 units)
 
   const int kend = start + min(qlen, q0 + QT);
   const int nchunks = max((kend + KB - 1) / KB, 1);
@@ -624,7 +625,13 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
         for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s_acc[g][jt][v]);
       mx = fmaxf(mx, fi::lane_xor16(mx, lane));
       mx = fmaxf(mx, fi::lane_xor32(mx, lane));
-      const float m_new = fmaxf(m_row[g], mx * c2);  // finite: key 0 of chunk 0 is visible to every row
+      // the reference point of the exponents moves only when the chunk's maximum passes it by
+      // more than kLazy (log2 units): probabilities stay below 2^kLazy, which f32 sums and the
+      // bf16 operand of P V hold with their usual relative precision, and the normalisation by
+      // the row sum (taken against the same point) cancels it.  Chunk 0 always sets it (finite:
+      // key 0 is visible to every row).
+      const float m_chunk = mx * c2;
+      const float m_new = m_chunk > m_row[g] + kLazy ? m_chunk : m_row[g];
       const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
       m_row[g] = m_new;
       float ls = 0.0f;
@@ -637,8 +644,8 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
           ls += pexp;
         }
       l_part[g] = l_part[g] * alpha + ls;
-      // alpha is exactly 1 where the row maximum did not grow: skip the rescale when that
-      // holds for every lane of the wave (same results, fewer VALU operations)
+      // alpha is exactly 1 where the reference point did not move: skip the rescale when that
+      // holds for every lane of the wave (after the first chunks, nearly always)
       if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[g][dt] *= alpha;
