@@ -368,20 +368,40 @@ int mt_for(fi_context* ctx, int m, int slabs) {
 }
 
 // Split count: three workgroups per CU where the tile grid is smaller, every split at least 8 K
-// steps, and the partials (splits x M x N f32) at most the weight's bytes.
+// steps.  Where that asks for partials (splits x M x N f32) beyond the weight's bytes (large M),
+// the split count between the two is the one with the least modelled time: the busiest CU's
+// row-tile K steps, ceil(tiles s / CUs) MT Q / s, at ~67 ns each (16 x 256 x 32 products at the
+// kernel's ~40 % of the bf16 peak per CU), plus each extra partial written and read back at
+// ~6 TB/s (wo at M 2304: 2 splits, 100 -> 83 us with the consumer 23 -> 31 us).
 int split_count(fi_context* ctx, int m, int k, int slabs) {
   const int mt = mt_for(ctx, m, slabs);
   const int mblocks = (m + 16 * mt - 1) / (16 * mt);
   const int groups = (slabs + kWaves * kNt - 1) / (kWaves * kNt);
   const int q = q_steps(k);
   const long tiles = (long)mblocks * groups;
+  const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
   // three workgroups per CU: a CU's two resident tiles are followed by a third, so the last
   // round is a third of a round (w2 at M 2304: 2 -> 3 splits, 345 -> 314 us with its consumer)
-  const long target = (long)(kOccupancy + 1) * (ctx->compute_units > 0 ? ctx->compute_units : 256);
+  const long target = (long)(kOccupancy + 1) * cus;
   long s = std::max(1L, (target + tiles - 1) / tiles);
   s = std::min(s, std::max(1L, static_cast<long>(q / 8)));
-  s = std::min(s, std::max(1L, static_cast<long>(k) / (2L * std::max(m, 16))));
   s = std::min(s, 32L);
+  const long lo = std::min(s, std::max(1L, static_cast<long>(k) / (2L * std::max(m, 16))));
+  if (lo < s) {
+    const double partial_bytes = 8.0 * m * 16.0 * slabs;  // one more partial, written and read
+    double best_ns = 0.0;
+    long best = lo;
+    for (long c = lo; c <= s; ++c) {
+      const long per = (q + c - 1) / c;
+      const double busy = static_cast<double>((tiles * c + cus - 1) / cus) * mt * per;
+      const double ns = 67.0 * busy + static_cast<double>(c - 1) * partial_bytes / 6000.0;  // 6000 B/ns
+      if (c == lo || ns < best_ns) {
+        best = c;
+        best_ns = ns;
+      }
+    }
+    s = best;
+  }
   const int per = (q + static_cast<int>(s) - 1) / static_cast<int>(s);
   return (q + per - 1) / per;  // every split non-empty
 }
