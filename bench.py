@@ -407,7 +407,7 @@ def kernel_legs(ctx, seed):
         "frac": round(flops / (ms_b * 1e-3) / 1e12 / BF16_PEAK_TFS, 4)}
     del kb, vb
     out["c3_kv_append"] = {
-        "kernel": "kv_append_kernel", "bound": "hbm", "tokens": T,
+        "kernel": "kv_append4_kernel", "bound": "hbm", "tokens": T,
         "bytes_per_launch": ab, "avg_launch_us": round(ms_a * 1e3, 2),
         "achieved_gbs": round(ab / (ms_a * 1e-3) / 1e9, 1), "peak_gbs": HBM_PEAK_GBS,
         "frac": round(ab / (ms_a * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}

@@ -476,6 +476,48 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
   }
 }
 
+// Four consecutive elements of one head row per thread over the flat (token, element) range, with
+// 16-byte loads and 16-byte (f32) or 8-byte (bf16) stores: the rows' bytes move in full-width
+// accesses (head dims that are multiples of 4 and 16-byte aligned sources).  Same values as
+// kv_append_kernel.
+template <typename KVT>
+__global__ __launch_bounds__(256) void kv_append4_kernel(const float* __restrict__ key,
+                                                         const float* __restrict__ value,
+                                                         const int64_t* __restrict__ slots,
+                                                         KVT* __restrict__ k_cache,
+                                                         KVT* __restrict__ v_cache, int64_t pool_slots,
+                                                         int block_size, int hkv, int d, int64_t total4,
+                                                         uint32_t* __restrict__ faults) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total4) return;
+  const int row4 = hkv * d / 4;
+  const int64_t t = idx / row4;
+  const int i = static_cast<int>(idx - t * row4) * 4;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  if (slot >= pool_slots) {
+    if (i == 0) atomicOr(faults, FI_FAULT_SLOT_RANGE);
+    return;
+  }
+  const int64_t blk = slot / block_size;
+  const int off = static_cast<int>(slot - blk * block_size);
+  const int h = i / d, e = i - (i / d) * d;
+  const size_t dst = (((size_t)blk * hkv + h) * block_size + off) * d + e;
+  const float4 kf = *reinterpret_cast<const float4*>(key + t * 4 * row4 + i);
+  const float4 vf = *reinterpret_cast<const float4*>(value + t * 4 * row4 + i);
+  if constexpr (sizeof(KVT) == 4) {
+    *reinterpret_cast<float4*>(k_cache + dst) = kf;
+    *reinterpret_cast<float4*>(v_cache + dst) = vf;
+  } else {
+    auto pack = [](float4 x) {
+      return make_uint2(fi::f32_to_bf16_bits(x.x) | (fi::f32_to_bf16_bits(x.y) << 16),
+                        fi::f32_to_bf16_bits(x.z) | (fi::f32_to_bf16_bits(x.w) << 16));
+    };
+    *reinterpret_cast<uint2*>(k_cache + dst) = pack(kf);
+    *reinterpret_cast<uint2*>(v_cache + dst) = pack(vf);
+  }
+}
+
 // One workgroup per (pair, kv_head): copies the first n token rows of a block.
 template <typename KVT>
 __global__ __launch_bounds__(256) void kv_copy_blocks_kernel(KVT* __restrict__ k_cache,
@@ -617,6 +659,22 @@ int32_t fi_kv_append(fi_context* ctx, const float* d_key, const float* d_value,
   FI_REQUIRE(d_key && d_value && d_slot_mapping && d_k_cache && d_v_cache, FI_ERR_INVALID_CONFIG,
              "fi_kv_append: null pointer");
   const int64_t pool_slots = static_cast<int64_t>(num_blocks) * block_size;
+  const bool vec = head_dim % 4 == 0 && reinterpret_cast<uintptr_t>(d_key) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(d_value) % 16 == 0;
+  if (vec) {
+    const int64_t total4 = static_cast<int64_t>(num_tokens) * num_kv_heads * head_dim / 4;
+    const dim3 grid(static_cast<unsigned>((total4 + 255) / 256));
+    if (kv_dtype == FI_DTYPE_F32)
+      hipLaunchKernelGGL(kv_append4_kernel<float>, grid, dim3(256), 0, ctx->stream, d_key, d_value, d_slot_mapping,
+                         static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache), pool_slots, block_size,
+                         num_kv_heads, head_dim, total4, ctx->d_faults);
+    else
+      hipLaunchKernelGGL(kv_append4_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream, d_key, d_value,
+                         d_slot_mapping, static_cast<uint16_t*>(d_k_cache), static_cast<uint16_t*>(d_v_cache),
+                         pool_slots, block_size, num_kv_heads, head_dim, total4, ctx->d_faults);
+    FI_CHECK_LAUNCH("kv_append4_kernel");
+    return FI_OK;
+  }
   if (kv_dtype == FI_DTYPE_F32) {
     hipLaunchKernelGGL(kv_append_kernel<float>, dim3(num_tokens), dim3(256), 0, ctx->stream, d_key, d_value,
                        d_slot_mapping, static_cast<float*>(d_k_cache), static_cast<float*>(d_v_cache),

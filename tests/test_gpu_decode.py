@@ -159,14 +159,17 @@ def test_decode_split_merge_repeatable(gpu_ctx, shape):
 
 
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
-def test_kv_append_scatter_exact(orc, gpu_ctx, kv_dtype):
-    """fi_kv_append writes each token row to block_id*bs+offset, bit-exact (bf16: RNE)."""
+@pytest.mark.parametrize("d,misaligned", [(64, False), (6, False), (64, True)])
+def test_kv_append_scatter_exact(orc, gpu_ctx, kv_dtype, d, misaligned):
+    """fi_kv_append writes each token row to block_id*bs+offset, bit-exact (bf16: RNE): the
+    16-byte path (head dim a multiple of 4, aligned sources) and the element path (head dim 6,
+    or sources one float off 16-byte alignment)."""
     import torch
 
     from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
 
     rng = np.random.default_rng(5)
-    nb, bs, hkv, d, t = 64, 16, 4, 64, 300
+    nb, bs, hkv, t = 64, 16, 4, 300
     slots = rng.permutation(nb * bs)[:t].astype(np.int64)
     slots[::37] = -1  # padding rows are skipped
     key = rng.standard_normal((t, hkv, d), dtype=np.float32)
@@ -174,7 +177,16 @@ def test_kv_append_scatter_exact(orc, gpu_ctx, kv_dtype):
     torch_dt = torch.float32 if kv_dtype == "f32" else torch.int16
     kc = torch.zeros((nb, hkv, bs, d), dtype=torch_dt, device="cuda")
     vc = torch.zeros_like(kc)
-    gpu_ctx.kv_append(_dev(key, torch), _dev(val, torch), _dev(slots, torch), kc, vc,
+
+    def src(x):
+        if not misaligned:
+            return _dev(x, torch)
+        buf = torch.empty(x.size + 1, dtype=torch.float32, device="cuda")
+        view = buf[1:].view(x.shape)
+        view.copy_(torch.from_numpy(x))
+        return view
+
+    gpu_ctx.kv_append(src(key), src(val), _dev(slots, torch), kc, vc,
                       DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16, nb, bs, hkv, d)
     torch.cuda.synchronize()
     gpu_ctx.check_faults()
