@@ -13,14 +13,16 @@
 // which is the B operand of one 16x16x32 MFMA per (slab, step) for lane `lane`: every wave
 // load is 16 contiguous bytes per lane and one group's K step is 16 KiB contiguous.
 //
-// Kernel: a workgroup of 4 waves computes a (16 MT) x (64 NT) tile over one split's K range.
-// The activation block (16 MT rows x 32 k) is staged per K step through double-buffered LDS:
-// f32 activations are rounded to bf16 (nearest even) on the way in, bf16 activations (rounded
-// the same way by their producer) are copied, so both give the same products; bf16 halves the
-// bytes the vector memory path carries per step, which at these tile sizes is as busy as the
-// MFMAs; each wave owns NT slabs and streams their fragments from
-// HBM through a register ring kDepth steps deep, and reads the A fragments of its MT row tiles
-// from LDS.  Two workgroups share a CU, so one's barrier wait overlaps the other's MFMAs.  Workgroups are ordered so each XCD takes a contiguous range of (row block
+// Kernel: a workgroup of 4 waves computes a (16 MT) x (64 NT) tile over one split's K range
+// (MT = 8, 6 or 4 row tiles above 64 rows, chosen per shape so the busiest CU gets the least
+// work).  The activation block (16 MT rows x 32 k, or 64 k for bf16 activations) is staged per
+// step through double-buffered LDS: f32 activations are rounded to bf16 (nearest even) on the
+// way in, bf16 activations (rounded the same way by their producer) are copied, so both give
+// the same products; bf16 halves the bytes the vector memory path carries per step, which at
+// these tile sizes is as busy as the MFMAs.  Each wave owns NT slabs and streams their
+// fragments from HBM through a register ring kDepth steps deep, and reads the A fragments of
+// its MT row tiles from LDS.  Two workgroups share a CU, so one's barrier wait overlaps the
+// other's MFMAs.  Workgroups are ordered so each XCD takes a contiguous range of (row block
 // fastest, then column group, then split): the row blocks that share a column group's weights
 // run together on one L2.
 #include <algorithm>
