@@ -109,6 +109,40 @@ def test_prefill_bf16_mfma_small(orc, gpu_ctx, case):
     assert normwise_error(got, oracle_prefill(orc, wl, "bf16")) <= 2e-2
 
 
+def test_prefill_bf16_mfma_rising_scores(orc, gpu_ctx):
+    """Keys whose norms grow along the sequence (row i scaled by 1 + i / 16), so the row maxima
+    rise chunk after chunk by far more than the kernel's exponent headroom (8 in log2 units):
+    the reference point moves and the accumulators are rescaled on most chunks.  Compared with
+    the f64 closed form on the kernel's own operands (Q rounded to bf16, bf16-stored K/V), which
+    leaves the bf16 rounding of the probabilities and the summation order: 5e-3.  (Against
+    unrounded Q the scores here, up to ~40, move by ~0.08 with Q's rounding.)"""
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    print("prefill bf16 mfma rising scores", flush=True)
+    wl = prefill_c3(seed=7, num_seqs=3, min_len=300, max_len=600, groups=0, group_size=1,
+                    shared_prefix=0, num_q_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
+                    num_blocks=1024)
+    for b in range(len(wl.context_lens)):
+        lo, hi = int(wl.cu_seqlens[b]), int(wl.cu_seqlens[b + 1])
+        wl.k_new[lo:hi] *= (1.0 + np.arange(hi - lo, dtype=np.float32) / 16.0)[:, None, None]
+    got = run_prefill(gpu_ctx, wl, "bf16", bf16_mfma=True)
+    assert np.isfinite(got).all()
+    rb = lambda x: orc.bf16_to_f32(orc.f32_to_bf16(x)).astype(np.float64)  # noqa: E731
+    group = wl.num_q_heads // wl.num_kv_heads
+    ref = np.empty(got.shape, np.float64)
+    for b in range(len(wl.context_lens)):
+        lo, hi = int(wl.cu_seqlens[b]), int(wl.cu_seqlens[b + 1])
+        n = hi - lo
+        q, k, v = rb(wl.q[lo:hi]), rb(wl.k_new[lo:hi]), rb(wl.v_new[lo:hi])
+        causal = np.tril(np.ones((n, n), bool))
+        for h in range(wl.num_q_heads):
+            s = q[:, h] @ k[:, h // group].T * wl.scale
+            s = np.where(causal, s, -np.inf)
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            ref[lo:hi, h] = (p / p.sum(axis=1, keepdims=True)) @ v[:, h // group]
+    assert normwise_error(got, ref) <= 5e-3
+
+
 def test_prefill_bf16_mfma_c3_full_size(orc, gpu_ctx):
     from ferrisinfer_amd.workloads import prefill_c3
 
