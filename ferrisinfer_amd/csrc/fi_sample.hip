@@ -454,6 +454,34 @@ __device__ __forceinline__ GreedyPart greedy_pass(const float* row, int vocab, i
   bool bad = false;
   stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, [&](const float (&v)[kPerLane], int s) {
     const int valid = lim - s * kStep;
+    if (valid <= 0) return;  // a ring slot past the segment (wave-uniform)
+    if (valid >= kStep) {
+      // A whole step.  Its maximum (NaN-propagating, -0 below +0, so for NaN-free steps it is
+      // the maximum by total_cmp) gates the per-logit key comparisons, which then run only
+      // where a lane's best can move.  A step holding a NaN or +inf takes the path below.
+      float top = v[0];
+#pragma unroll
+      for (int e = 1; e < kPerLane; ++e) top = __builtin_elementwise_maximum(top, v[e]);
+      if (!__ballot(!(top < INFINITY))) {
+        if (__ballot(total_key(top) >= bk)) {
+#pragma unroll
+          for (int e = 0; e < kPerLane; ++e) {
+            const int key = total_key(v[e]);
+            const bool take = key >= bk;
+            bk = take ? key : bk;
+            bi = take ? s * kStep + step_index<VEC>(0, lane, e) : bi;
+          }
+        }
+        // the same running maximum and sum as below (x * log2e is monotonic in x)
+        const float nm = fmaxf(m, top * kLog2e);
+        sum = (nm > m) ? sum * __builtin_amdgcn_exp2f(m - nm) : sum;
+        m = nm;
+        const float base = m > -INFINITY ? m : 0.0f;
+#pragma unroll
+        for (int e = 0; e < kPerLane; ++e) sum += __builtin_amdgcn_exp2f(v[e] * kLog2e - base);
+        return;
+      }
+    }
     float xs[kPerLane];
     float smax = -INFINITY;
 #pragma unroll
@@ -522,6 +550,7 @@ __device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0,
   uint32_t nan_bits = 0;  // max of |bits|: above 0x7f800000 when a NaN was seen
   stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, [&](const float (&v)[kPerLane], int s) {
     const int valid = lim - s * kStep;  // logits of this step below lim: step_index offsets < valid
+    if (valid <= 0) return;             // a ring slot past the segment (wave-uniform)
     if (k < 64 && s < s0 + kWaves) {
       // the wave's first step seeds its bound: the (k+1)-th largest of the 64 lane maxima.
       // k+1 distinct logits of the step are at or above it, so nothing below it can be among
@@ -542,12 +571,24 @@ __device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0,
       bound = max(bound, __shfl(lmax, k, 64));
     }
     int hits = 0;
+    if (valid >= kStep) {
+      // a whole step: its NaN-propagating maximum (-0 below +0) decides whether any logit
+      // reaches the bound; a NaN marks the row and sends the step to the appends, which
+      // test every logit
+      float top = v[0];
 #pragma unroll
-    for (int e = 0; e < kPerLane; ++e) {
-      const bool in = step_index<VEC>(0, lane, e) < valid;
-      const uint32_t bits = __float_as_uint(v[e]);
-      nan_bits = max(nan_bits, in ? bits & 0x7fffffffu : 0u);
-      hits += (in && total_key(v[e]) >= bound) ? 1 : 0;
+      for (int e = 1; e < kPerLane; ++e) top = __builtin_elementwise_maximum(top, v[e]);
+      const bool nan = top != top;
+      nan_bits = nan ? 0x7fffffffu : nan_bits;
+      hits = (nan || total_key(top) >= bound) ? 1 : 0;
+    } else {
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) {
+        const bool in = step_index<VEC>(0, lane, e) < valid;
+        const uint32_t bits = __float_as_uint(v[e]);
+        nan_bits = max(nan_bits, in ? bits & 0x7fffffffu : 0u);
+        hits += (in && total_key(v[e]) >= bound) ? 1 : 0;
+      }
     }
     if (__ballot(hits > 0)) {  // rare once the bound has risen: append a group at a time
 #pragma unroll
@@ -621,14 +662,30 @@ __device__ __forceinline__ int select_desc(SampleShared& sh, int rank, int tid, 
 // when the top k+1 are strictly decreasing (the list is then exactly the top k in value order);
 // false sends the row to the replay.
 __device__ __forceinline__ bool fast_top_k(SampleShared& sh, int k, int tid, int w, int lane) {
-  const int kth = select_desc(sh, k, tid, w, lane);
-  for (int q = 0; q < kWaves; ++q) {
-    for (int i = tid; i < sh.count[q]; i += kThreads) {
-      if (sh.key[q][i] >= kth) {
-        const int pos = atomicAdd(&sh.m, 1);
-        if (pos < kSortMax) {
-          sh.u.fast.key[pos] = sh.key[q][i];
-          sh.u.fast.idx[pos] = sh.idx[q][i];
+  int total = 0;
+  for (int q = 0; q < kWaves; ++q) total += sh.count[q];
+  if (total <= kRankSortMax) {
+    // few candidates (every buffer holds more than k of them together): all of them go to the
+    // rank sort, whose order is total, so no selection round is needed
+    int base = 0;
+    for (int q = 0; q < kWaves; ++q) {
+      for (int i = tid; i < sh.count[q]; i += kThreads) {
+        sh.u.fast.key[base + i] = sh.key[q][i];
+        sh.u.fast.idx[base + i] = sh.idx[q][i];
+      }
+      base += sh.count[q];
+    }
+    if (tid == 0) sh.m = total;
+  } else {
+    const int kth = select_desc(sh, k, tid, w, lane);
+    for (int q = 0; q < kWaves; ++q) {
+      for (int i = tid; i < sh.count[q]; i += kThreads) {
+        if (sh.key[q][i] >= kth) {
+          const int pos = atomicAdd(&sh.m, 1);
+          if (pos < kSortMax) {
+            sh.u.fast.key[pos] = sh.key[q][i];
+            sh.u.fast.idx[pos] = sh.idx[q][i];
+          }
         }
       }
     }
