@@ -92,14 +92,15 @@ def c4_layer_ops(seed):
 
     x = rn(m, h)
     nqkv = h + 2 * hkv * d
-    w_qkv = ctx.weight_pack(rn(h, nqkv) * 0.02, h, nqkv, 1)
-    w_o = ctx.weight_pack(rn(h, h) * 0.02, h, h, 1)
-    w_2 = ctx.weight_pack(rn(f, h) * 0.02, f, h, 4)
+    pw = 32  # the runtime's pack width for q|k|v, wo and w2
+    w_qkv = ctx.weight_pack(rn(h, nqkv) * 0.02, h, nqkv, pw)
+    w_o = ctx.weight_pack(rn(h, h) * 0.02, h, h, pw)
+    w_2 = ctx.weight_pack(rn(f, h) * 0.02, f, h, pw)
     pair = ctx.weight_pack_pair(rn(h, f) * 0.02, rn(h, f) * 0.02, h, f)
     head = ctx.weight_pack(rn(v, h) * 0.02, h, v, 2, src_layout=1)
-    s_qkv = ctx.gemm_packed_splits(m, h, nqkv, 1)
-    s_o = ctx.gemm_packed_splits(m, h, h, 1)
-    s_w2 = ctx.gemm_packed_splits(m, f, h, 4)
+    s_qkv = ctx.gemm_packed_splits(m, h, nqkv, pw)
+    s_o = ctx.gemm_packed_splits(m, h, h, pw)
+    s_w2 = ctx.gemm_packed_splits(m, f, h, pw)
     p_qkv = torch.empty(s_qkv, m, nqkv, device="cuda")
     p_o = torch.empty(s_o, m, h, device="cuda")
     p_w2 = torch.empty(s_w2, m, h, device="cuda")
@@ -120,14 +121,14 @@ def c4_layer_ops(seed):
     nw = torch.ones(h, device="cuda")
     nout = torch.empty(m, h, device="cuda")
     for _ in range(10):
-        ctx.gemm_packed(x, w_qkv, h, nqkv, 1, s_qkv, p_qkv)
+        ctx.gemm_packed(x, w_qkv, h, nqkv, pw, s_qkv, p_qkv)
         ctx.qkv_rope_append(p_qkv, s_qkv, None, pos, cos, sin, d, 4096, slots, kp, vp, DTYPE_F32, nb, bs,
                             hq, hkv, d, q)
         ctx.kv_append(kn, vn, slots, kp, vp, DTYPE_F32, nb, bs, hkv, d)
-        ctx.gemm_packed(x, w_o, h, h, 1, s_o, p_o)
+        ctx.gemm_packed(x, w_o, h, h, pw, s_o, p_o)
         ctx.splitk_residual_rms_norm(p_o, s_o, None, res, ssum, nw, nout, 1e-6)
         ctx.gemm_packed_swiglu(x, pair, h, f, act)
-        ctx.gemm_packed(act, w_2, f, h, 4, s_w2, p_w2)
+        ctx.gemm_packed(act, w_2, f, h, pw, s_w2, p_w2)
         ctx.lm_head_argmax_packed(x, head, v, tok, prob)
     torch.cuda.synchronize()
     ctx.check_faults()
@@ -240,7 +241,7 @@ def gemm_shapes(seed):
             c = torch.empty(m, n, device="cuda")
             row = {"shape": name, "m": m, "k": k, "n": n,
                    "fi_gemm_us": round(ms(lambda: ctx.gemm(a, w, c)) * 1e3, 2)}
-            for pw in (1, 2, 4):
+            for pw in (1, 2, 4, 32):
                 bp = ctx.weight_pack(w, k, n, pw)
                 s = ctx.gemm_packed_splits(m, k, n, pw)
                 out = torch.empty(s, m, n, device="cuda")
@@ -414,11 +415,11 @@ def kernel_legs(ctx, seed):
     del kp, vp, k_new, v_new, slots, q, o
 
     # the projections as the runtime runs them: packed weights, pack widths of
-    # DeviceModel (q|k|v 1, wo 1, w1/w3 SwiGLU pair, w2 4, lm_head 4), C4 shapes
+    # DeviceModel (q|k|v, wo and w2 32, w1/w3 SwiGLU pair, lm_head 2), C4 shapes
     g = torch.Generator(device="cuda").manual_seed(seed)
     for m in (64, 1024):
         tag = "decode" if m == 64 else "prefill"
-        for name, k, n, pw in (("qkv", 896, 1152, 1), ("wo", 896, 896, 1), ("w2", 4864, 896, 4)):
+        for name, k, n, pw in (("qkv", 896, 1152, 32), ("wo", 896, 896, 32), ("w2", 4864, 896, 32)):
             a = torch.randn(m, k, device="cuda", generator=g)
             w = torch.randn(k, n, device="cuda", generator=g) * 0.02
             bp = ctx.weight_pack(w, k, n, pw)

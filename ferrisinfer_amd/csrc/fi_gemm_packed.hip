@@ -36,6 +36,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kPackW32 = 32;  // pack width selecting the 32-column layout of gemm_w32_kernel
 
 template <int PW>
 struct PVec;
@@ -541,6 +542,130 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_s3_kernel(PGemmArgs g) {
   if (slab_id < g.slabs) store_tile<MT, PW, EPI>(g, acc, m0, slab, z, lane);
 }
 
+// ---- pack width 32: the three-piece bf16 product on 32 x 32 MFMA tiles ----
+//
+// Packed layout (pack width 32): slabs of 32 output columns; in each 16-k step q, lane l of a
+// wave holds column 32 slab + l % 32 at the eight consecutive k 16q + 8(l / 32) .. +7:
+//   packed[((slab * Q + q) * 64 + l) * 8 + e] = B[16q + 8(l / 32) + e][32 slab + l % 32]
+// (zero outside [0, K) x [0, N)), which is the B operand of v_mfma_f32_32x32x16_bf16 for that
+// step: 32 contiguous bytes a lane.  The activations are read straight from their rows in the
+// same k order (lane l: row l % 32 of a 32-row tile).  Both operands are split into their three
+// bf16 pieces on use and the six cross products above 2^-24 relative accumulate in f32, as in
+// gemm_s3_kernel.  A workgroup of 4 waves owns (32 MT) rows x (32 SL) columns and a range of K
+// steps: each wave a contiguous quarter of it, with loads DEPTH steps ahead of the MFMAs and
+// no barrier in the loop; the quarters are summed through LDS in wave order, and workgroups
+// along z split K further (partials [splits, M, N], summed by the consumers in split order).
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void mfma_x32(v16f& acc, const bf16x8 (&a)[3], const bf16x8 (&b)[3]) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ void split3_pair(const float4& x0, const float4& x1, bf16x8 (&p)[3]) {
+  const f32x8 x = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  split3(x, p[0], p[1], p[2]);
+}
+
+template <int MT, int SL, bool KTAIL>
+__global__ __launch_bounds__(kThreads, 2) void gemm_w32_kernel(PGemmArgs g) {
+  constexpr int DEPTH = 2;  // steps in flight ahead of the MFMAs (3 measured slower at decode M)
+  constexpr int R = DEPTH + 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int m0 = blockIdx.y * 32 * MT, z = blockIdx.z;
+  const int q0 = z * g.q_per_split, q1 = min(g.q_total, q0 + g.q_per_split);
+  const int per = (q1 - q0 + kWaves - 1) / kWaves;
+  const int qb = min(q1, q0 + w * per), qe = min(q1, qb + per);
+  const int kh = 8 * (lane >> 5);  // the lane's k offset within a step
+  const float* arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int row = min(m0 + 32 * t + (lane & 31), g.m - 1);  // clamped rows are never stored
+    arow[t] = g.a + (size_t)row * g.lda + kh;
+  }
+  const float4* wb[SL];
+#pragma unroll
+  for (int s = 0; s < SL; ++s) {
+    const int slab = min(static_cast<int>(blockIdx.x) * SL + s, g.slabs - 1);
+    wb[s] = reinterpret_cast<const float4*>(g.bp) + ((size_t)slab * g.q_total * 64 + lane) * 2;
+  }
+  v16f acc[MT][SL];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int s = 0; s < SL; ++s) acc[t][s] = v16f{};
+  if (qb < qe) {  // wave-uniform
+    float4 ra[R][MT][2], rw[R][SL][2];
+    auto issue = [&](int q, int slot) {
+      q = min(q, qe - 1);  // refetches past the wave's range are never multiplied
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        ra[slot][t][0] = load_a<KTAIL>(arow[t], 16 * q, g.k - kh);
+        ra[slot][t][1] = load_a<KTAIL>(arow[t], 16 * q + 4, g.k - kh);
+      }
+#pragma unroll
+      for (int s = 0; s < SL; ++s) {
+        rw[slot][s][0] = wb[s][(size_t)q * 128];
+        rw[slot][s][1] = wb[s][(size_t)q * 128 + 1];
+      }
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(qb + d, d);
+    for (int q = qb; q < qe; q += R) {
+#pragma unroll
+      for (int d = 0; d < R; ++d) {
+        issue(q + d + DEPTH, (d + DEPTH) % R);
+        sched_fence();
+        if (q + d < qe) {
+          bf16x8 pa[MT][3], pw[SL][3];
+#pragma unroll
+          for (int t = 0; t < MT; ++t) split3_pair(ra[d][t][0], ra[d][t][1], pa[t]);
+#pragma unroll
+          for (int s = 0; s < SL; ++s) split3_pair(rw[d][s][0], rw[d][s][1], pw[s]);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int s = 0; s < SL; ++s) mfma_x32(acc[t][s], pa[t], pw[s]);
+        }
+        sched_fence();
+      }
+    }
+  }
+  __shared__ v16f s_part[kWaves - 1][MT * SL][64];
+  if (w > 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int s = 0; s < SL; ++s) s_part[w - 1][t * SL + s][lane] = acc[t][s];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int src = 0; src < kWaves - 1; ++src)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int s = 0; s < SL; ++s) acc[t][s] += s_part[src][t * SL + s][lane];
+  // lane l holds column l % 32 of each 32 x 32 tile, rows 8(j / 4) + 4(l / 32) + j % 4
+  float* out = g.out + (size_t)z * g.m * g.n;
+#pragma unroll
+  for (int s = 0; s < SL; ++s) {
+    const int col = (static_cast<int>(blockIdx.x) * SL + s) * 32 + (lane & 31);
+    if (col >= g.n) continue;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int row = m0 + 32 * t + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        if (row < g.m) out[(size_t)row * g.n + col] = acc[t][s][j];
+      }
+  }
+}
+
 // Pair-pack partials [splits, M, 2N] (up, gate interleaved per column) -> out[M, N] =
 // (sum up + b1) * silu(sum gate + b3), sums in split order (elementwise.rs:118-207).
 // bf16 output (out_bf16): the products rounded to nearest even.
@@ -621,11 +746,43 @@ __global__ void weight_pack_kernel(PackSources s, int pair, int src_layout, int 
   }
 }
 
+// Pack width 32 (the layout of gemm_w32_kernel), one thread per packed float; in column mode
+// the sources are concatenated along N as above.
+__global__ void weight_pack32_kernel(PackSources s, int src_layout, int k, int q_total, size_t total,
+                                     float* __restrict__ dst) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int e = static_cast<int>(i & 7);
+    const int lane = static_cast<int>((i >> 3) & 63);
+    const size_t sq = i >> 9;
+    const int q = static_cast<int>(sq % q_total);
+    const int slab = static_cast<int>(sq / q_total);
+    const int kk = 16 * q + 8 * (lane >> 5) + e;
+    int col = 32 * slab + (lane & 31);
+    int j = 0;
+    while (j + 1 < s.count && col >= s.n[j]) {
+      col -= s.n[j];
+      ++j;
+    }
+    const float* src = s.src[j];
+    const int ncols = s.n[j];
+    float v = 0.0f;
+    if (kk < k && col < ncols) v = src_layout == 0 ? src[(size_t)kk * ncols + col] : src[(size_t)col * k + kk];
+    dst[i] = v;
+  }
+}
+
 int32_t launch_pack(fi_context* ctx, const PackSources& s, int pair, int src_layout, int k, int n, int pw,
                     float* dst) {
   size_t total = 0;
   FI_TRY(fi_weight_packed_floats(k, pair ? 2 * n : n, pw, &total));
   const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 65536));
+  if (pw == kPackW32) {
+    hipLaunchKernelGGL(weight_pack32_kernel, dim3(blocks), dim3(256), 0, ctx->stream, s, src_layout, k, (k + 15) / 16,
+                       total, dst);
+    FI_CHECK_LAUNCH("weight_pack32_kernel");
+    return FI_OK;
+  }
   hipLaunchKernelGGL(weight_pack_kernel, dim3(blocks), dim3(256), 0, ctx->stream, s, pair, src_layout, k, n, pw,
                      (k + 15) / 16, total, dst);
   FI_CHECK_LAUNCH("weight_pack_kernel");
@@ -685,6 +842,7 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
   const int h4 = hidden / 4;
   const bool held = vec && h4 <= kRowQuads * kRowThreads;
   float4 xs[kRowQuads];
+  float4 ws[kRowQuads];  // held rows: the norm weights, loaded with the partials (one memory round trip)
   auto sum_quad = [&](int c) {
     float4 x = sum_splits(reinterpret_cast<const float4*>(parts + base) + c, plane / 4, splits);
     if (bias) x = add(x, reinterpret_cast<const float4*>(bias)[c]);
@@ -697,6 +855,11 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
     return x;
   };
   if (held) {
+#pragma unroll
+    for (int i = 0; i < kRowQuads; ++i) {
+      const int c = threadIdx.x + i * kRowThreads;
+      if (c < h4) ws[i] = reinterpret_cast<const float4*>(weight)[c];
+    }
 #pragma unroll
     for (int i = 0; i < kRowQuads; ++i) {
       const int c = threadIdx.x + i * kRowThreads;
@@ -723,8 +886,7 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
   // OUT16: the normalised row is stored as bf16 bits, each value rounded to nearest even
   float* out = static_cast<float*>(out_v);
   uint16_t* out16 = static_cast<uint16_t*>(out_v);
-  auto norm_quad = [&](int c, const float4& x) {
-    const float4 wv = reinterpret_cast<const float4*>(weight)[c];
+  auto norm_quad = [&](int c, const float4& x, const float4& wv) {
     const float4 y = make_float4((x.x * inv) * wv.x, (x.y * inv) * wv.y, (x.z * inv) * wv.z, (x.w * inv) * wv.w);
     if constexpr (OUT16) {
       const uint32_t b0 = fi::f32_to_bf16_bits(y.x), b1 = fi::f32_to_bf16_bits(y.y);
@@ -738,10 +900,11 @@ __global__ __launch_bounds__(kRowThreads) void splitk_residual_rms_norm_kernel(
 #pragma unroll
     for (int i = 0; i < kRowQuads; ++i) {
       const int c = threadIdx.x + i * kRowThreads;
-      if (c < h4) norm_quad(c, xs[i]);
+      if (c < h4) norm_quad(c, xs[i], ws[i]);
     }
   } else if (vec) {
-    for (int c = threadIdx.x; c < h4; c += kRowThreads) norm_quad(c, reinterpret_cast<const float4*>(sum_out + base)[c]);
+    for (int c = threadIdx.x; c < h4; c += kRowThreads)
+      norm_quad(c, reinterpret_cast<const float4*>(sum_out + base)[c], reinterpret_cast<const float4*>(weight)[c]);
   } else {
     for (int c = threadIdx.x; c < hidden; c += kRowThreads) {
       const float y = (sum_out[base + c] * inv) * weight[c];
@@ -787,8 +950,7 @@ __device__ __forceinline__ void put_kv4(KVT* cache, size_t idx, const float4& x)
 // bias, if any.
 __device__ __forceinline__ float qkv_value(const float* __restrict__ p0, size_t plane, int splits,
                                            const float* __restrict__ bias, int bias_col, int col) {
-  float x = p0[col];
-  for (int z = 1; z < splits; ++z) x = x + p0[(size_t)z * plane + col];
+  const float x = sum_splits(p0 + col, plane, splits);  // split loads batched before the adds
   return bias ? x + bias[bias_col] : x;
 }
 
@@ -866,9 +1028,8 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
 // bias, if any: column col of the [T, Hq*D + 2*Hkv*D] row at p0.
 __device__ __forceinline__ float4 qkv_value4(const float* __restrict__ p0, size_t plane, int splits,
                                              const float* __restrict__ bias, int bias_col, int col) {
-  const float* p = p0 + col;
-  float4 x = *reinterpret_cast<const float4*>(p);
-  for (int z = 1; z < splits; ++z) x = add(x, *reinterpret_cast<const float4*>(p + (size_t)z * plane));
+  // the split loads are issued in batches before their adds (one memory latency per batch)
+  float4 x = sum_splits(reinterpret_cast<const float4*>(p0 + col), plane / 4, splits);
   if (bias) x = add(x, *reinterpret_cast<const float4*>(bias + bias_col));
   return x;
 }
@@ -958,7 +1119,10 @@ int32_t q_steps(int32_t k) { return (k + 15) / 16; }
 // slabs read one staged activation block), 12 % faster than width 4 at 64 rows, equal at one.
 constexpr int kLmHeadPack = 2;
 
-int32_t slabs_of(int32_t n, int32_t pw, bool pair) { return pair ? (n + 15) / 16 : (n + 16 * pw - 1) / (16 * pw); }
+int32_t slabs_of(int32_t n, int32_t pw, bool pair) {
+  const int32_t cols = pair ? 16 : (pw == kPackW32 ? 32 : 16 * pw);
+  return (n + cols - 1) / cols;
+}
 
 // Row-block height for M rows: 16, 32 or 64.
 int mtiles_for(int m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
@@ -997,6 +1161,56 @@ int split_count(fi_context* ctx, int m, int k, int slabs, int pw) {
   s = std::min(s, 16L);
   const int per = (q + static_cast<int>(s) - 1) / static_cast<int>(s);
   return (q + per - 1) / per;  // every split non-empty
+}
+
+// Pack width 32: 32-row tiles (one for M <= 32, else two per workgroup), and two slabs per
+// workgroup once that still gives half the CUs a workgroup (prefill M); at decode M one slab,
+// with K split until the grid is one workgroup per CU, every split at least 8 steps.  Timed on
+// the box at the C4 shapes against the f32-MFMA kernels: M = 64 q|k|v 8.3 -> 6.7 us (7
+// splits), wo 8.3 -> 6.5 us (7), w2 12.2 -> 11.1 us (9); M = 1024 (one split, two slabs) q|k|v
+// 41.8 -> 31.3 us, wo 24.8 -> 19.9 us, w2 83.9 -> 74.0 us.
+struct W32Plan {
+  int mt, sl, mblocks, blocks;
+};
+
+W32Plan w32_plan(fi_context* ctx, int m, int slabs) {
+  W32Plan p{};
+  p.mt = m <= 32 ? 1 : 2;
+  p.mblocks = (m + 32 * p.mt - 1) / (32 * p.mt);
+  const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  p.sl = static_cast<long>((slabs + 1) / 2) * p.mblocks >= cus / 2 ? 2 : 1;
+  p.blocks = ((slabs + p.sl - 1) / p.sl) * p.mblocks;
+  return p;
+}
+
+int w32_split_count(fi_context* ctx, int m, int k, int slabs) {
+  const W32Plan p = w32_plan(ctx, m, slabs);
+  const int q = q_steps(k);
+  const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  long s = std::max(1L, std::min(cus / p.blocks, static_cast<long>(q / 8)));
+  s = std::min(s, 32L);
+  const int per = (q + static_cast<int>(s) - 1) / static_cast<int>(s);
+  return (q + per - 1) / per;  // every split non-empty
+}
+
+template <int MT, int SL>
+void launch_w32_tail(fi_context* ctx, const PGemmArgs& g, dim3 grid) {
+  if (g.k % 16 != 0)
+    hipLaunchKernelGGL((gemm_w32_kernel<MT, SL, true>), grid, dim3(kThreads), 0, ctx->stream, g);
+  else
+    hipLaunchKernelGGL((gemm_w32_kernel<MT, SL, false>), grid, dim3(kThreads), 0, ctx->stream, g);
+}
+
+int32_t launch_w32(fi_context* ctx, const PGemmArgs& g, int splits) {
+  const W32Plan p = w32_plan(ctx, g.m, g.slabs);
+  const dim3 grid(static_cast<unsigned>((g.slabs + p.sl - 1) / p.sl), static_cast<unsigned>(p.mblocks),
+                  static_cast<unsigned>(splits));
+  if (p.mt == 1)
+    p.sl == 1 ? launch_w32_tail<1, 1>(ctx, g, grid) : launch_w32_tail<1, 2>(ctx, g, grid);
+  else
+    p.sl == 1 ? launch_w32_tail<2, 1>(ctx, g, grid) : launch_w32_tail<2, 2>(ctx, g, grid);
+  FI_CHECK_LAUNCH("gemm_w32_kernel");
+  return FI_OK;
 }
 
 template <int MT, int PW, int EPI, bool KTAIL>
@@ -1077,10 +1291,11 @@ extern "C" {
 
 int32_t fi_weight_packed_floats(int32_t k, int32_t n, int32_t pack_width, size_t* floats) {
   FI_REQUIRE(k > 0 && n > 0, FI_ERR_INVALID_SHAPE, "fi_weight_packed_floats: k and n must be positive");
-  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
-             "fi_weight_packed_floats: pack width must be 1, 2 or 4");
+  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4 || pack_width == kPackW32, FI_ERR_INVALID_CONFIG,
+             "fi_weight_packed_floats: pack width must be 1, 2, 4 or 32");
   FI_REQUIRE(floats != nullptr, FI_ERR_INVALID_CONFIG, "fi_weight_packed_floats: null output");
-  *floats = static_cast<size_t>(slabs_of(n, pack_width, false)) * q_steps(k) * 4 * 64 * pack_width;
+  const size_t per_step = pack_width == kPackW32 ? 64 * 8 : 4 * 64 * pack_width;  // floats per slab and 16-k step
+  *floats = static_cast<size_t>(slabs_of(n, pack_width, false)) * q_steps(k) * per_step;
   return FI_OK;
 }
 
@@ -1125,18 +1340,19 @@ int32_t fi_gemm_packed_splits(fi_context* ctx, int32_t m, int32_t k, int32_t n, 
                               int32_t* splits) {
   FI_TRY(fi::enter(ctx));
   FI_REQUIRE(m >= 0 && k > 0 && n > 0, FI_ERR_INVALID_SHAPE, "fi_gemm_packed_splits: bad shape");
-  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
-             "fi_gemm_packed_splits: pack width must be 1, 2 or 4");
+  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4 || pack_width == kPackW32, FI_ERR_INVALID_CONFIG,
+             "fi_gemm_packed_splits: pack width must be 1, 2, 4 or 32");
   FI_REQUIRE(splits != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_packed_splits: null output");
-  *splits = split_count(ctx, m, k, slabs_of(n, pack_width, false), pack_width);
+  const int slabs = slabs_of(n, pack_width, false);
+  *splits = pack_width == kPackW32 ? w32_split_count(ctx, m, k, slabs) : split_count(ctx, m, k, slabs, pack_width);
   return FI_OK;
 }
 
 int32_t fi_gemm_packed(fi_context* ctx, const float* d_a, int32_t lda, const float* d_bp, int32_t k, int32_t n,
                        int32_t pack_width, int32_t m, int32_t splits, float* d_out) {
   FI_TRY(check_common(ctx, d_a, lda, d_bp, m, k, n));
-  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4, FI_ERR_INVALID_CONFIG,
-             "fi_gemm_packed: pack width must be 1, 2 or 4");
+  FI_REQUIRE(pack_width == 1 || pack_width == 2 || pack_width == 4 || pack_width == kPackW32, FI_ERR_INVALID_CONFIG,
+             "fi_gemm_packed: pack width must be 1, 2, 4 or 32");
   FI_REQUIRE(splits >= 1 && splits <= q_steps(k), FI_ERR_INVALID_CONFIG, "fi_gemm_packed: splits out of range");
   if (m == 0) return FI_OK;
   FI_REQUIRE(d_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_gemm_packed: null output");
@@ -1155,6 +1371,8 @@ int32_t fi_gemm_packed(fi_context* ctx, const float* d_a, int32_t lda, const flo
   FI_REQUIRE(used == splits, FI_ERR_INVALID_CONFIG,
              "fi_gemm_packed: splits must divide the K steps into non-empty ranges (use fi_gemm_packed_splits)");
   switch (pack_width) {
+    case kPackW32:
+      return launch_w32(ctx, g, splits);
     case 1:
       return launch_pgemm<1, kEpiPartial>(ctx, g, splits);
     case 2:

@@ -90,7 +90,9 @@ class DeviceModel {
   struct Packed {
     DeviceBuffer qkv, wo, w13, w2;
   };
-  static constexpr int32_t kQkvPack = 1, kWoPack = 1, kW2Pack = 4, kLmPack = 2;
+  // q|k|v, wo and w2 on the 32-column layout (three-piece bf16 products); the SwiGLU pair and
+  // the greedy head keep their two-column packs
+  static constexpr int32_t kQkvPack = 32, kWoPack = 32, kW2Pack = 32, kLmPack = 2;
 
   // weight_dtype: FI_DTYPE_F32 or FI_DTYPE_BF16, the storage of the packed projections and head.
   DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions, int32_t weight_dtype = FI_DTYPE_F32);

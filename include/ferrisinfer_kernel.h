@@ -291,16 +291,20 @@ int32_t fi_lm_head_argmax(fi_context* ctx, const float* d_hidden, const float* d
  * out once at upload, which the architecture assigns to the GPU backend
  * (docs/architecture.md:53, 97).  Packed layout: slabs of 16*pack_width output columns, each
  * holding its K rows (zero-padded to a multiple of 16) in MFMA fragment order, so a wave
- * streams a slab with contiguous 16-byte loads.  fi_gemm_packed writes split-K partials
- * [splits, M, N]; the consumers below sum them in split order (deterministic) and fuse the
- * elementwise ops the reference runs after each projection. */
+ * streams a slab with contiguous 16-byte loads.  Pack width 32 selects a 32-column layout
+ * whose lanes hold eight consecutive k of one column per 16-k step (32 contiguous bytes);
+ * fi_gemm_packed then multiplies in f32 accuracy on bf16 MFMA, both operands split exactly
+ * into three bf16 pieces and the six cross products above 2^-24 relative accumulated in f32.
+ * fi_gemm_packed writes split-K partials [splits, M, N]; the consumers below sum them in split
+ * order (deterministic) and fuse the elementwise ops the reference runs after each
+ * projection. */
 
 /* Floats of the packed form of a [K, N] weight. */
 int32_t fi_weight_packed_floats(int32_t k, int32_t n, int32_t pack_width, size_t* floats);
 
 /* Packs a device weight: src_layout 0 = [K, N] ([in, out], model/decoder.rs:76-104),
  * 1 = [N, K] (the [vocab, hidden] output / tied embedding weight of matmul_rhs_transposed,
- * kernel/cpu/matmul.rs:120-188).  pack_width 1, 2 or 4. */
+ * kernel/cpu/matmul.rs:120-188).  pack_width 1, 2, 4 or 32. */
 int32_t fi_weight_pack(fi_context* ctx, const float* d_src, int32_t src_layout, int32_t k, int32_t n,
                        int32_t pack_width, float* d_dst);
 

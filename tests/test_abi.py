@@ -45,6 +45,23 @@ def test_ctx_create_without_gpu_reports_unsupported():
         raise AssertionError("context creation must fail without a GPU")
 
 
+def test_packed_weight_sizes():
+    """fi_weight_packed_floats (host arithmetic only): slabs of 16 * width columns, 64 * 4 *
+    width floats per slab and 16-k step; width 32 is the 32-column layout, 512 floats per slab
+    and step; other widths are refused."""
+    from ferrisinfer_amd import kernel
+
+    lib = ctypes.CDLL(kernel.library_path())
+    out = ctypes.c_size_t()
+    for k, n, pw, want in [(896, 1152, 1, 72 * 56 * 256), (896, 1152, 4, 18 * 56 * 1024),
+                           (20, 37, 2, 2 * 2 * 512), (896, 1152, 32, 36 * 56 * 512),
+                           (4864, 896, 32, 28 * 304 * 512), (36, 20, 32, 1 * 3 * 512)]:
+        assert lib.fi_weight_packed_floats(k, n, pw, ctypes.byref(out)) == 0
+        assert out.value == want, (k, n, pw)
+    for pw in (0, 3, 8, 16):
+        assert lib.fi_weight_packed_floats(64, 64, pw, ctypes.byref(out)) != 0
+
+
 RUNTIME_HEADER = os.path.join(ROOT, "include", "ferrisinfer_runtime.h")
 
 

@@ -24,6 +24,11 @@ SHAPES = [  # (M, K, N, pack width): C4 decode / prefill shapes, C1 shapes, ragg
     (64, 896, 1152, 1), (64, 896, 896, 1), (64, 4864, 896, 1), (1, 896, 1152, 1),
     (37, 256, 688, 2), (64, 896, 4864, 2), (200, 896, 4864, 4), (1024, 896, 1152, 4),
     (5, 100, 50, 4), (17, 36, 20, 1), (3, 4, 1, 2), (64, 688, 256, 4),
+    # pack width 32 (three-piece bf16 products on 32 x 32 tiles): the runtime's q|k|v, wo and
+    # w2 at decode and prefill M, one- and two-slab workgroups, K and N tails
+    (64, 896, 1152, 32), (64, 896, 896, 32), (64, 4864, 896, 32), (1, 896, 1152, 32),
+    (1024, 896, 1152, 32), (1024, 896, 896, 32), (300, 4864, 896, 32), (33, 256, 688, 32),
+    (5, 100, 50, 32), (17, 36, 20, 32), (3, 4, 1, 32),
 ]
 
 
@@ -67,18 +72,19 @@ def test_packed_column_concatenation(orc, gpu_ctx):
     m, k = 40, 256
     parts = [(rng.standard_normal((k, n), dtype=np.float32) * 0.05).astype(np.float32)
              for n in (256, 64, 64)]
-    for pw in (1, 2, 4):
+    for pw in (1, 2, 4, 32):
         bp = gpu_ctx.weight_pack_columns([dev(p) for p in parts], k, pw)
         ref_bp = gpu_ctx.weight_pack(dev(np.concatenate(parts, axis=1)), k, 384, pw)
         assert torch.equal(bp, ref_bp)
     a = rng.standard_normal((m, k), dtype=np.float32)
-    splits = gpu_ctx.gemm_packed_splits(m, k, 384, 1)
-    out = torch.empty((splits, m, 384), device="cuda")
-    bp = gpu_ctx.weight_pack_columns([dev(p) for p in parts], k, 1)
-    gpu_ctx.gemm_packed(dev(a), bp, k, 384, 1, splits, out)
-    torch.cuda.synchronize()
     ref = orc.linear_with_bias(a, np.concatenate(parts, axis=1), None)
-    assert normwise_error(sum_splits(out.cpu().numpy()), ref) <= 1e-5
+    for pw in (1, 32):
+        splits = gpu_ctx.gemm_packed_splits(m, k, 384, pw)
+        out = torch.empty((splits, m, 384), device="cuda")
+        bp = gpu_ctx.weight_pack_columns([dev(p) for p in parts], k, pw)
+        gpu_ctx.gemm_packed(dev(a), bp, k, 384, pw, splits, out)
+        torch.cuda.synchronize()
+        assert normwise_error(sum_splits(out.cpu().numpy()), ref) <= 1e-5, pw
 
 
 def test_packed_gemm_transposed_source_and_exact_integers(gpu_ctx):
@@ -87,7 +93,9 @@ def test_packed_gemm_transposed_source_and_exact_integers(gpu_ctx):
     import torch
 
     rng = np.random.default_rng(5)
-    for m, k, n, pw in [(64, 64, 64, 4), (5, 20, 37, 2), (130, 96, 80, 1), (3, 1000, 68, 4)]:
+    for m, k, n, pw in [(64, 64, 64, 4), (5, 20, 37, 2), (130, 96, 80, 1), (3, 1000, 68, 4),
+                        (64, 64, 64, 32), (5, 20, 37, 32), (130, 96, 80, 32), (3, 1000, 68, 32),
+                        (1024, 64, 512, 32)]:
         a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
         w = rng.integers(-4, 5, size=(k, n)).astype(np.float32)
         for layout, src in ((0, w), (1, np.ascontiguousarray(w.T))):
