@@ -443,7 +443,7 @@ def kernel_legs(ctx, seed):
         tok = torch.empty(m, dtype=torch.int32, device="cuda")
         prob = torch.empty(m, device="cuda")
         ms = timed(lambda: ctx.lm_head_argmax_packed(hid, bp, v, tok, prob), 20)
-        out[f"lm_head_argmax_c4_m{m}"] = gemm_row(m, h, v, ms, 1, 4)
+        out[f"lm_head_argmax_c4_m{m}"] = gemm_row(m, h, v, ms, 1, 2)
     del w, bp
     # device sampling (sample_last_token per row, one workgroup per row): the logits are
     # read once, so the bound is HBM at rows * vocab * 4 bytes per launch; N(0, 2.5) logits
