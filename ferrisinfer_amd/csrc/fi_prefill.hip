@@ -1,4 +1,7 @@
-// Varlen causal prefill attention over the paged KV pool, on MFMA (v_mfma_f32_16x16x4_f32).
+// Varlen causal prefill attention over the paged KV pool, on MFMA.  f32 pools run
+// prefill_x3_kernel (f32 accuracy from three-piece bf16 products on v_mfma_f32_16x16x32_bf16,
+// at the end of this file); bf16 pools run prefill_kernel (K/V widened exactly, f32 MFMA,
+// v_mfma_f32_16x16x4_f32) or, through fi_attn_prefill_paged_bf16, prefill_bf16_kernel.
 // Replaces causal_self_attention_f32 / prefixed_causal_attention_f32 /
 // cached_prefixed_causal_attention_f32 (crates/ferrisinfer-kernel/src/cpu/attention.rs:222-518,
 // 688-962) plus the paged prefix gather that feeds them (runtime/paged_kv.rs:769-791,
@@ -426,12 +429,6 @@ int32_t launch_prefill(fi_context* ctx, const PrefillArgs& args_in) {
                                        : launch_prefill_rg<D, KVT, 1>(ctx, args, g);
 }
 
-template <int D>
-int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& args) {
-  if (dtype == FI_DTYPE_F32) return launch_prefill<D, float>(ctx, args);
-  return launch_prefill<D, uint16_t>(ctx, args);
-}
-
 // ---- bf16-MFMA variant for a bf16 pool (fi_attn_prefill_paged_bf16) ----
 // Same workgroup shape, tile order and chunk pipeline as prefill_kernel, on
 // v_mfma_f32_16x16x32_bf16: K and V stay bf16 in LDS, row-major (V^T fragments come from
@@ -732,6 +729,350 @@ int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
   const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
   return row_groups(ctx, args, g) == 2 ? launch_prefill_bf16_rg<D, 2>(ctx, args, g)
                                        : launch_prefill_bf16_rg<D, 1>(ctx, args, g);
+}
+
+// ---- f32 pools in f32 accuracy on bf16 MFMA (fi_attn_prefill_paged over an f32 pool) ----
+// The workgroup shape, tile order, transposed products, masking and softmax of
+// prefill_bf16_kernel, with every operand carried in f32 accuracy: K and V are split exactly
+// into three bf16 planes (x = hi + mid + lo: hi = RNE(x), mid = RNE(x - hi), lo the rest) when
+// a 32-key chunk is staged, Q and the probabilities are split on use, and each product is the
+// sum of the six cross products above 2^-24 relative (the three dropped ones are below one f32
+// rounding together), accumulated in f32 on v_mfma_f32_16x16x32_bf16: the f32 result at 2.7x
+// the f32 MFMA rate.  One LDS buffer (52 KB at D = 128, two workgroups per CU); the next chunk
+// is in registers while the current one is multiplied, two barriers per chunk.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split3(const f32x8& x, bf16x8 (&p)[3]) {
+  p[0] = __builtin_convertvector(x, bf16x8);
+  const f32x8 r1 = x - __builtin_convertvector(p[0], f32x8);
+  p[1] = __builtin_convertvector(r1, bf16x8);
+  const f32x8 r2 = r1 - __builtin_convertvector(p[1], f32x8);
+  p[2] = __builtin_convertvector(r2, bf16x8);
+}
+
+// four f32 values -> their three bf16 pieces, each as 8 bytes
+__device__ __forceinline__ void split3_quad(const float4& v, uint2 (&p)[3]) {
+  const f32x4 x = {v.x, v.y, v.z, v.w};
+  const bf16x4 hi = __builtin_convertvector(x, bf16x4);
+  const f32x4 r1 = x - __builtin_convertvector(hi, f32x4);
+  const bf16x4 mid = __builtin_convertvector(r1, bf16x4);
+  const f32x4 r2 = r1 - __builtin_convertvector(mid, f32x4);
+  const bf16x4 lo = __builtin_convertvector(r2, bf16x4);
+  p[0] = __builtin_bit_cast(uint2, hi);
+  p[1] = __builtin_bit_cast(uint2, mid);
+  p[2] = __builtin_bit_cast(uint2, lo);
+}
+
+// acc += A B over three-piece operands: the six cross products above 2^-24, smallest first
+__device__ __forceinline__ v4f mma6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], v4f acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
+template <int D, int G, int RG>
+__global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) {
+  constexpr int QT = kRows * RG / G;    // query tokens per workgroup (RG 16-row groups a wave)
+  constexpr int KB = 32;                 // keys per chunk: one 32-key step of P V
+  constexpr int DS = D / 32;             // 32-wide d steps of Q K^T
+  constexpr int DT = D / 16;             // 16-wide output d tiles of P V
+  constexpr int JT = KB / 16;            // 16-key score tiles per chunk
+  constexpr int DQ = D / 4;              // float4 quads per K/V row
+  constexpr int KR = kThreads / KB;      // quad columns staged per pass (thread: key tid % KB)
+  constexpr int PER_T = DQ / KR;         // quads per thread per K (and V) chunk
+  static_assert(DQ % KR == 0 && PER_T >= 1, "chunk must split over the workgroup");
+  constexpr int KP = D + 8;              // padded LDS rows
+  __shared__ __align__(16) uint16_t Ks[3][KB][KP];  // the three pieces of K, row-major
+  __shared__ __align__(16) uint16_t Vs[3][KB][KP];  // of V, read through transpose loads
+
+  const float* __restrict__ k_cache = static_cast<const float*>(a.k_cache);
+  const float* __restrict__ v_cache = static_cast<const float*>(a.v_cache);
+  const int ntiles = (a.max_query_len + QT - 1) / QT;
+  const int rank = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
+  const int tile = a.order[rank];
+  const int qt = tile % ntiles, seq = tile / ntiles;
+  const int qs = a.cu_seqlens[seq];
+  const int qlen = a.cu_seqlens[seq + 1] - qs;
+  const int q0 = qt * QT;
+  if (q0 >= qlen) return;
+  const int ctx = a.context_lens[seq];
+  const int start = ctx - qlen;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int li = lane & 15, lk = lane >> 4;
+
+  // Q stays f32 (B operand row li of group g, d = 32 t + 8 lk .. +7) and is split on use
+  int row_r[RG], qpos[RG];
+  f32x8 qf[RG][DS];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    row_r[g] = 16 * (w + 4 * g) + li;
+    qpos[g] = start + q0 + row_r[g] % QT;
+    const int ah = row_r[g] / QT, at = row_r[g] % QT;
+    const bool a_ok = ah < a.group && q0 + at < qlen;
+    const float* qp = a.q + ((size_t)(qs + q0 + (a_ok ? at : 0)) * a.hq + kvh * a.group + (a_ok ? ah : 0)) * D;
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+      const float4 lo = *reinterpret_cast<const float4*>(qp + 32 * t + 8 * lk);
+      const float4 hi = *reinterpret_cast<const float4*>(qp + 32 * t + 8 * lk + 4);
+      const f32x8 v = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const f32x8 z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      qf[g][t] = a_ok ? v : z;
+    }
+  }
+  v4f o[RG][DT];  // O^T tile dt of group g: d = 16 dt + 4 lk + v, row li
+  float m_row[RG], l_part[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[g][dt] = v4f{0.f, 0.f, 0.f, 0.f};
+    m_row[g] = -INFINITY;
+    l_part[g] = 0.0f;
+  }
+  const float c2 = a.scale * 1.4426950408889634f;  // scores -> log2 units
+  constexpr float kLazy = 8.0f;  // headroom of the exponents' reference point (log2 units)
+
+  const int kend = start + min(qlen, q0 + QT);
+  const int nchunks = max((kend + KB - 1) / KB, 1);
+
+  // staging: thread owns key tid % KB of the chunk and quad columns tid / KB + KR r; one block
+  // lookup per chunk, looked up a chunk ahead; loads unconditional (clamped key)
+  const int skey = tid % KB, sq0 = tid / KB;
+  float4 kr[PER_T], vr[PER_T];
+  int id_next = 0, off_next = 0;
+  bool bad_block = false;
+  bool part_next = false, valid_next = true;
+  const bool aligned = KB % a.block_size == 0;  // workgroup-uniform
+  const int key_blk = aligned ? skey / a.block_size : 0;
+  const int key_off = aligned ? skey - key_blk * a.block_size : 0;
+  const int chunk_blks = aligned ? KB / a.block_size : 0;
+  auto lookup = [&](int c) {
+    c = min(c, nchunks - 1);
+    const int kpc = max(min(c * KB + skey, kend - 1), 0);
+    const bool exact = aligned && c * KB + skey < kend;
+    const int lb = exact ? c * chunk_blks + key_blk : kpc / a.block_size;
+    const bool in_table = lb < a.max_blocks;
+    const int id = a.block_tables[(size_t)seq * a.max_blocks + (in_table ? lb : 0)];
+    id_next = in_table ? id : -1;
+    off_next = exact ? key_off : kpc - lb * a.block_size;
+  };
+  auto fetch = [&](int c) {
+    c = min(c, nchunks - 1);
+    part_next = (c + 1) * KB > kend;  // workgroup-uniform: the chunk has padding keys
+    valid_next = c * KB + skey < kend;
+    const bool bad = id_next < 0 || id_next >= a.num_blocks;
+    bad_block |= bad;
+    const size_t row = ((size_t)(bad ? 0 : id_next) * a.hkv + kvh) * a.block_size + off_next;
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) {
+      const int dq = sq0 + KR * r;
+      kr[r] = *reinterpret_cast<const float4*>(k_cache + row * D + 4 * dq);
+      vr[r] = *reinterpret_cast<const float4*>(v_cache + row * D + 4 * dq);
+    }
+  };
+  // padding keys of a partial chunk are stored as zero (their clamped loads hold a valid row)
+  auto stage = [&]() {
+    if (part_next && !valid_next) {
+#pragma unroll
+      for (int r = 0; r < PER_T; ++r) kr[r] = vr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) {
+      const int dq = sq0 + KR * r;
+      uint2 pk[3], pv[3];
+      split3_quad(kr[r], pk);
+      split3_quad(vr[r], pv);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        *reinterpret_cast<uint2*>(&Ks[p][skey][4 * dq]) = pk[p];
+        *reinterpret_cast<uint2*>(&Vs[p][skey][4 * dq]) = pv[p];
+      }
+    }
+  };
+
+  lookup(0);
+  fetch(0);
+  lookup(1);
+  stage();
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int k0 = c * KB;
+
+    // ---- S^T = K Q^T: 32 keys x 16 rows per group ----
+    v4f s_acc[RG][JT];
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) s_acc[g][jt] = v4f{0.f, 0.f, 0.f, 0.f};
+    // K fragments one d step ahead of their MFMAs, in two register slots (each step fenced, so
+    // the lookahead and the registers it holds stay bounded)
+    bf16x8 kf[2][JT][3];
+    auto read_k = [&](int t, int slot) {
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          kf[slot][jt][p] = *reinterpret_cast<const bf16x8*>(&Ks[p][16 * jt + li][32 * t + 8 * lk]);
+    };
+    read_k(0, 0);
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+      if (t + 1 < DS) read_k(t + 1, (t + 1) & 1);
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        bf16x8 qp[3];
+        split3(qf[g][t], qp);
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt) s_acc[g][jt] = mma6(kf[t & 1][jt], qp, s_acc[g][jt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the next chunk's rows are fetched here, after the score products (whose K fragments and
+    // Q pieces are the register peak), and land during the softmax and P V
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(c + 1);  // the last chunk re-reads itself: the loads stay unconditional
+    lookup(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    // causal / context mask only where the chunk reaches past the tile's first query position
+    // (workgroup-uniform, tested once outside the unrolled score loops)
+    if (k0 + KB - 1 > start + q0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kp = k0 + 16 * jt + 4 * lk + v;
+            s_acc[g][jt][v] = (kp <= qpos[g] && kp < ctx) ? s_acc[g][jt][v] : -INFINITY;
+          }
+    }
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      // the softmax of prefill_bf16_kernel: maximum of the raw scores, a lazily moved reference
+      // point, one fma per exponent, the rescale skipped where no row's point moved
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s_acc[g][jt][v]);
+      mx = fmaxf(mx, fi::lane_xor16(mx, lane));
+      mx = fmaxf(mx, fi::lane_xor32(mx, lane));
+      const float m_chunk = mx * c2;
+      const float m_new = m_chunk > m_row[g] + kLazy ? m_chunk : m_row[g];
+      const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
+      m_row[g] = m_new;
+      float ls = 0.0f;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float pexp = __builtin_amdgcn_exp2f(fmaf(s_acc[g][jt][v], c2, -m_new));
+          s_acc[g][jt][v] = pexp;
+          ls += pexp;
+        }
+      l_part[g] = l_part[g] * alpha + ls;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[g][dt] *= alpha;
+      }
+    }
+
+    // ---- O^T += V^T P^T over the chunk's 32 keys (MFMA k index 8 lk + e: key 4 lk + e for
+    // e < 4, 16 + 4 lk + e - 4 above, the keys this lane's probabilities belong to) ----
+    bf16x8 pp[RG][3];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const f32x8 pf = {s_acc[g][0][0], s_acc[g][0][1], s_acc[g][0][2], s_acc[g][0][3],
+                        s_acc[g][1][0], s_acc[g][1][1], s_acc[g][1][2], s_acc[g][1][3]};
+      split3(pf, pp[g]);
+    }
+    // ds_read_b64_tr_b16 as in prefill_bf16_kernel: lane (li, lk) points at key 4 lk + li / 4
+    // (+ 16 for the upper half), d 16 dt + 4 (li % 4) .. + 3, and receives V at d = 16 dt + li
+    // for keys 4 lk + e (+ 16)
+    const int vrow = 4 * lk + (li >> 2), vcol = 4 * (li & 3);
+    bf16x8 vf[2][3];  // V^T fragments one d tile ahead, as the K fragments above
+    auto read_v = [&](int dt, int slot) {
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        const v4s lo = lds_read_tr16(&Vs[p][vrow][16 * dt + vcol]);
+        const v4s hi = lds_read_tr16(&Vs[p][vrow + 16][16 * dt + vcol]);
+        vf[slot][p] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    read_v(0, 0);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      if (dt + 1 < DT) read_v(dt + 1, (dt + 1) & 1);
+#pragma unroll
+      for (int g = 0; g < RG; ++g) o[g][dt] = mma6(vf[dt & 1], pp[g], o[g][dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // every wave is done with this chunk's K/V
+    if (c + 1 < nchunks) {  // workgroup-uniform
+      stage();
+      __syncthreads();
+    }
+  }
+
+  if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
+
+  // ---- normalise and store: lane holds row li of each group, d = 16 dt + 4 lk + v ----
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    float l_row = l_part[g] + fi::lane_xor16(l_part[g], lane);
+    l_row += fi::lane_xor32(l_row, lane);
+    const int h = row_r[g] / QT, t = row_r[g] % QT;
+    if (h < a.group && q0 + t < qlen) {
+      const float inv = 1.0f / l_row;
+      float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        *reinterpret_cast<float4*>(op + 16 * dt + 4 * lk) =
+            make_float4(o[g][dt][0] * inv, o[g][dt][1] * inv, o[g][dt][2] * inv, o[g][dt][3] * inv);
+      }
+    }
+  }
+}
+
+template <int D, int RG>
+int32_t launch_prefill_x3_rg(fi_context* ctx, PrefillArgs& args, int g) {
+  const int qt = kRows * RG / g;
+  dim3 grid;
+  FI_TRY(plan_tiles(ctx, args, qt, 32, "fi_attn_prefill_paged", &grid));
+  switch (g) {
+    case 1:
+      hipLaunchKernelGGL((prefill_x3_kernel<D, 1, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    case 2:
+      hipLaunchKernelGGL((prefill_x3_kernel<D, 2, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    case 4:
+      hipLaunchKernelGGL((prefill_x3_kernel<D, 4, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+    default:
+      hipLaunchKernelGGL((prefill_x3_kernel<D, 8, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
+      break;
+  }
+  FI_CHECK_LAUNCH("prefill_x3_kernel");
+  return FI_OK;
+}
+
+template <int D>
+int32_t launch_prefill_x3(fi_context* ctx, const PrefillArgs& args_in) {
+  PrefillArgs args = args_in;
+  const int g = args.group <= 1 ? 1 : (args.group <= 2 ? 2 : (args.group <= 4 ? 4 : 8));
+  return row_groups(ctx, args, g) == 2 ? launch_prefill_x3_rg<D, 2>(ctx, args, g)
+                                       : launch_prefill_x3_rg<D, 1>(ctx, args, g);
+}
+
+// f32 pools: the three-piece bf16 kernel; bf16 pools: K/V widened exactly to f32 on f32 MFMA
+template <int D>
+int32_t launch_prefill_dtype(fi_context* ctx, int32_t dtype, const PrefillArgs& args) {
+  if (dtype == FI_DTYPE_F32) return launch_prefill_x3<D>(ctx, args);
+  return launch_prefill<D, uint16_t>(ctx, args);
 }
 
 // Checks the arguments of a prefill entry point and fills the kernel arguments; *empty when
