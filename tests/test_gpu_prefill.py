@@ -59,6 +59,10 @@ CASES = [
     (6, 30, 300, 2, 3, 128, 14, 2, 64, 16),   # Qwen2-shaped GQA 7
     (4, 100, 400, 1, 4, 96, 32, 8, 128, 8),   # block size 8
     (3, 1, 150, 0, 1, 0, 4, 2, 128, 32),      # GQA 2, block size 32, 1-token prompts
+    # grids large enough for two row groups a wave (the launch picks them when every CU gets
+    # two workgroups): Qwen2-shaped GQA 7 at D 64, C1-shaped heads at D 32
+    (32, 200, 300, 2, 4, 96, 14, 2, 64, 16),
+    (48, 150, 200, 0, 1, 0, 8, 2, 32, 16),
 ]
 
 
