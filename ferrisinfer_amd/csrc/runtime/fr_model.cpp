@@ -315,8 +315,7 @@ void ForwardExecutor::reserve(size_t tokens, size_t seqs) {
   grow(h1_, t * h * 4);
   grow(act_, t * f * 4);
   grow(last_norm_, cap_seqs_ * h * 4);
-  grow(tok_, cap_seqs_ * 4);
-  grow(prob_, cap_seqs_ * 4);
+  grow(out_, cap_seqs_ * 8);
 }
 
 void ForwardExecutor::splits(int32_t m, int32_t k, int32_t n, int32_t pack_width, int32_t* out) const {
@@ -406,15 +405,17 @@ void ForwardExecutor::enqueue(const Plan& p) {
   // the final norm ran over every row; each sequence's last row feeds the head
   check(fi_embedding(ctx_, normed, T, H, p.last, B, last_norm_.f32()));
   const void* lm = model_->lm_head_packed();
+  int32_t* tok = static_cast<int32_t*>(out_.get());
+  float* prob = out_.f32() + B;
   if (p.greedy) {
     // fused greedy head (matmul_rhs_transposed_argmax_f32, matmul.rs:190-274), as the
     // reference session's greedy path (session.rs:349-356, 393-398)
     if (bf16) {
       check(fi_lm_head_argmax_bf16(ctx_, last_norm_.f32(), FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), B, H,
-                                   c.vocab_size, static_cast<int32_t*>(tok_.get()), prob_.f32()));
+                                   c.vocab_size, tok, prob));
     } else {
       check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), B, H, c.vocab_size,
-                                     static_cast<int32_t*>(tok_.get()), prob_.f32()));
+                                     tok, prob));
     }
   } else {
     // last-row logits (matmul_rhs_transposed, one K split) and sample_last_token per row
@@ -430,7 +431,7 @@ void ForwardExecutor::enqueue(const Plan& p) {
     uint8_t* d = static_cast<uint8_t*>(samp_.get());
     check(fi_sample_tokens(ctx_, logits_.f32(), c.vocab_size, B, c.vocab_size, reinterpret_cast<const float*>(d + B * 8),
                            reinterpret_cast<const int32_t*>(d + B * 12), reinterpret_cast<const float*>(d + B * 16),
-                           reinterpret_cast<uint64_t*>(d), static_cast<int32_t*>(tok_.get()), prob_.f32()));
+                           reinterpret_cast<uint64_t*>(d), tok, prob));
   }
 }
 
@@ -576,16 +577,18 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   }
 
   const auto t_enqueued = std::chrono::steady_clock::now();
-  std::vector<int32_t> tok(B);
-  std::vector<float> prob(B);
-  check(fi_buf_download(ctx_, tok.data(), B * 4, tok_.get(), B * 4));
-  check(fi_buf_download(ctx_, prob.data(), B * 4, prob_.get(), B * 4));
+  std::vector<int32_t> tok(static_cast<size_t>(B) * 2);  // B ids, then B probabilities
+  check(fi_buf_download(ctx_, tok.data(), B * 8, out_.get(), B * 8));
   if (!greedy) check(fi_buf_download(ctx_, states->data(), B * 8, samp_.get(), B * 8));
   check(fi_ctx_check_faults(ctx_));
   enqueue_s_ = std::chrono::duration<double>(t_enqueued - t_start).count();
   wait_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_enqueued).count();
   std::vector<TokenSample> out(B);
-  for (int32_t i = 0; i < B; ++i) out[i] = TokenSample{static_cast<uint32_t>(tok[i]), prob[i]};
+  for (int32_t i = 0; i < B; ++i) {
+    float prob;
+    std::memcpy(&prob, &tok[B + i], 4);
+    out[i] = TokenSample{static_cast<uint32_t>(tok[i]), prob};
+  }
   return out;
 }
 

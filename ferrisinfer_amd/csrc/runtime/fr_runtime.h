@@ -378,7 +378,9 @@ class ForwardExecutor {
   const DeviceModel* model_;
   BlockPool* pool_;
   fi_context* ctx_;
-  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, tok_, prob_, logits_, samp_;
+  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, logits_, samp_;
+  // one tick's samples: B token ids, then B probabilities (one download)
+  DeviceBuffer out_;
   size_t cap_tokens_ = 0, cap_seqs_ = 0, cap_parts_ = 0;
   double enqueue_s_ = 0.0, wait_s_ = 0.0;
   bool graph_decode_;
