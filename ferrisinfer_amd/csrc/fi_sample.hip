@@ -93,22 +93,25 @@ __device__ __forceinline__ void load_step(const float* row, int vocab, int s, in
 // Runs f(logits, s) over wave steps first, first + stride, ... with a ring of four step
 // buffers: three steps of loads are in flight while one is processed.  Every call is made
 // unconditionally (steps at or past nsteps hold no real logit; f masks them by index) so that
-// no load is sunk into a branch next to its use.
+// no load is sunk into a branch next to its use.  Those steps load step nsteps - 1 again, which
+// the range has just read, instead of the logits past the range (another segment's, which
+// would be read from memory twice).
 template <int VEC, typename F>
 __device__ __forceinline__ void stream_steps(const float* row, int vocab, int first, int stride, int nsteps, int lane,
                                              F&& f) {
+  const int last = max(nsteps - 1, 0);
   float b0[kPerLane], b1[kPerLane], b2[kPerLane], b3[kPerLane];
-  load_step<VEC>(row, vocab, first, lane, b0);
-  load_step<VEC>(row, vocab, first + stride, lane, b1);
-  load_step<VEC>(row, vocab, first + 2 * stride, lane, b2);
+  load_step<VEC>(row, vocab, min(first, last), lane, b0);
+  load_step<VEC>(row, vocab, min(first + stride, last), lane, b1);
+  load_step<VEC>(row, vocab, min(first + 2 * stride, last), lane, b2);
   for (int s = first; s < nsteps; s += 4 * stride) {
-    load_step<VEC>(row, vocab, s + 3 * stride, lane, b3);
+    load_step<VEC>(row, vocab, min(s + 3 * stride, last), lane, b3);
     f(b0, s);
-    load_step<VEC>(row, vocab, s + 4 * stride, lane, b0);
+    load_step<VEC>(row, vocab, min(s + 4 * stride, last), lane, b0);
     f(b1, s + stride);
-    load_step<VEC>(row, vocab, s + 5 * stride, lane, b1);
+    load_step<VEC>(row, vocab, min(s + 5 * stride, last), lane, b1);
     f(b2, s + 2 * stride);
-    load_step<VEC>(row, vocab, s + 6 * stride, lane, b2);
+    load_step<VEC>(row, vocab, min(s + 6 * stride, last), lane, b2);
     f(b3, s + 3 * stride);
   }
 }
@@ -554,21 +557,21 @@ __device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0,
     if (k < 64 && s < s0 + kWaves) {
       // the wave's first step seeds its bound: the (k+1)-th largest of the 64 lane maxima.
       // k+1 distinct logits of the step are at or above it, so nothing below it can be among
-      // the k+1 largest (a bitonic network sorts the lane maxima descending across the wave;
-      // empty lanes hold the minimum key).  Later steps raise the bound by compaction.
+      // the k+1 largest (empty lanes hold the minimum key).  It is the largest t with at least
+      // k+1 lane maxima at or above t, built bit by bit from the top over order-preserving
+      // unsigned keys, one ballot a bit.  Later steps raise the bound by compaction.
       int lmax = kIntMin;
 #pragma unroll
       for (int e = 0; e < kPerLane; ++e)
         lmax = max(lmax, step_index<VEC>(0, lane, e) < valid ? total_key(v[e]) : kIntMin);
+      const uint32_t u = static_cast<uint32_t>(lmax) ^ 0x80000000u;
+      uint32_t t = 0;
 #pragma unroll
-      for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          const int o = __shfl_xor(lmax, stride, 64);
-          const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
-          lmax = keep_max ? max(lmax, o) : min(lmax, o);
-        }
-      bound = max(bound, __shfl(lmax, k, 64));
+      for (int b = 31; b >= 0; --b) {
+        const uint32_t c = t | (1u << b);
+        t = __popcll(__ballot(u >= c)) > k ? c : t;
+      }
+      bound = max(bound, static_cast<int>(t ^ 0x80000000u));
     }
     int hits = 0;
     if (valid >= kStep) {
