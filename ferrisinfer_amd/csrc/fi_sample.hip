@@ -572,6 +572,9 @@ __device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0,
         t = __popcll(__ballot(u >= c)) > k ? c : t;
       }
       bound = max(bound, static_cast<int>(t ^ 0x80000000u));
+      // published at once, so the other waves filter their later steps against it too (the
+      // wave buffers the k+1 logits that make it valid in this step)
+      if (lane == 0) atomicMax(&sh.bound[w], bound);
     }
     int hits = 0;
     if (valid >= kStep) {
