@@ -635,15 +635,54 @@ __device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0,
 // The key of descending rank `rank` over the wave buffers' sh.count[q] entries (radix
 // selection, 8 bits a round; whole workgroup; the buffers hold more than `rank` entries).
 __device__ __forceinline__ int select_desc(SampleShared& sh, int rank, int tid, int w, int lane) {
+  // Up to kOwn candidates a thread (flattened over the wave buffers) are read into registers
+  // once, so each round's histogram is a few compares and increments instead of a loop whose
+  // bounds and keys are LDS reads; larger sets read the buffers every round.
+  constexpr int kOwn = 4;
+  int cnt[kWaves];
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < kWaves; ++q) {
+    cnt[q] = sh.count[q];
+    total += cnt[q];
+  }
+  const bool held = total <= kOwn * kThreads;  // workgroup-uniform
+  uint32_t own[kOwn];
+#pragma unroll
+  for (int j = 0; j < kOwn; ++j) {
+    own[j] = 0;
+    int rem = held && tid + j * kThreads < total ? tid + j * kThreads : -1;
+    int qsel = -1, isel = 0;
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) {
+      if (rem >= 0 && qsel < 0) {
+        if (rem < cnt[q]) {
+          qsel = q;
+          isel = rem;
+        } else {
+          rem -= cnt[q];
+        }
+      }
+    }
+    // candidate tid + j * kThreads (held when below total) as an order-preserving unsigned key
+    if (qsel >= 0) own[j] = static_cast<uint32_t>(sh.key[qsel][isel]) ^ 0x80000000u;
+  }
   uint32_t prefix = 0, mask = 0;
   int want = rank;
   for (int d = 24; d >= 0; d -= 8) {
     if (tid < 256) sh.hist[0][tid] = 0;
     __syncthreads();
-    for (int q = 0; q < kWaves; ++q) {
-      for (int i = tid; i < sh.count[q]; i += kThreads) {
-        const uint32_t u = static_cast<uint32_t>(sh.key[q][i]) ^ 0x80000000u;
-        if ((u & mask) == prefix) atomicAdd(&sh.hist[0][(u >> d) & 255u], 1);
+    if (held) {
+#pragma unroll
+      for (int j = 0; j < kOwn; ++j) {
+        if (tid + j * kThreads < total && (own[j] & mask) == prefix) atomicAdd(&sh.hist[0][(own[j] >> d) & 255u], 1);
+      }
+    } else {
+      for (int q = 0; q < kWaves; ++q) {
+        for (int i = tid; i < cnt[q]; i += kThreads) {
+          const uint32_t u = static_cast<uint32_t>(sh.key[q][i]) ^ 0x80000000u;
+          if ((u & mask) == prefix) atomicAdd(&sh.hist[0][(u >> d) & 255u], 1);
+        }
       }
     }
     __syncthreads();
