@@ -132,12 +132,17 @@ __device__ __forceinline__ int pick_digit_desc(const int* hist, int lane, int& w
     c[q] = hist[255 - (4 * lane + q)];  // lanes ascending = digits descending
     tot += c[q];
   }
+  // inclusive prefix sum over the wave in DPP moves (no LDS round trips): row_shr 1, 2, 4, 8
+  // scan each row of 16 lanes (lanes shifted in from outside the row add 0), row_bcast:15
+  // adds the last lane of rows 0 and 2 to rows 1 and 3, row_bcast:31 the last lane of row 1
+  // to rows 2 and 3
   int incl = tot;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += t;
-  }
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);
   const int excl = incl - tot;
   const bool here = excl <= want && want < incl;
   int digit = 0, below = 0, acc = excl;
