@@ -997,6 +997,19 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
     if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
     return;
   }
+  // Wave q copies segment q's candidates (segs <= kWaves).  Its count and first 64 entries are
+  // loaded here, beside tid 0's flag loads, so a segment of at most 64 candidates costs no
+  // further memory round trip (the entries past the count are never used).
+  int c = 0, key0 = 0, idx0 = 0;
+  const int* ck = nullptr;
+  const int* ci = nullptr;
+  if (w < segs) {
+    ck = cand_key + ((size_t)r * segs + w) * kRegion;
+    ci = cand_idx + ((size_t)r * segs + w) * kRegion;
+    c = rm[w].count;
+    key0 = ck[lane];
+    idx0 = ci[lane];
+  }
   if (tid == 0) {
     int f = 0;
     for (int j = 0; j < segs; ++j) f |= rm[j].flags;
@@ -1007,16 +1020,17 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
 
   bool sorted = false;  // s_val / s_idx hold the sorted list
   if (k < vocab && sh.flags == 0) {
-    for (int q = w; q < kWaves; q += kWaves) {  // wave q copies segment q's candidates
-      const int c = q < segs ? rm[q].count : 0;
-      const int* ck = cand_key + ((size_t)r * segs + q) * kRegion;
-      const int* ci = cand_idx + ((size_t)r * segs + q) * kRegion;
-      for (int i = lane; i < c; i += 64) {
-        sh.key[q][i] = ck[i];
-        sh.idx[q][i] = ci[i];
+    if (w < segs) {
+      if (lane < c) {
+        sh.key[w][lane] = key0;
+        sh.idx[w][lane] = idx0;
       }
-      if (lane == 0) sh.count[q] = c;
+      for (int i = lane + 64; i < c; i += 64) {
+        sh.key[w][i] = ck[i];
+        sh.idx[w][i] = ci[i];
+      }
     }
+    if (lane == 0) sh.count[w] = c;
     __syncthreads();
     sorted = fast_top_k(sh, k, tid, w, lane);
   }
