@@ -91,19 +91,35 @@ __device__ __forceinline__ void load_step(const float* row, int vocab, int s, in
 }
 
 // Runs f(logits, s) over wave steps first, first + stride, ... with a ring of four step
-// buffers: three steps of loads are in flight while one is processed.  Every call is made
+// buffers (the first three primed by prime_steps with the same range): three steps of loads
+// are in flight while one is processed.  Every call is made
 // unconditionally (steps at or past nsteps hold no real logit; f masks them by index) so that
 // no load is sunk into a branch next to its use.  Those steps load step nsteps - 1 again, which
 // the range has just read, instead of the logits past the range (another segment's, which
 // would be read from memory twice).
+// The ring's first three steps, loaded by prime_steps before the row's configuration is read
+// (the loads do not depend on it), so the configuration's round trip overlaps them.
+struct StepRing {
+  float b0[kPerLane], b1[kPerLane], b2[kPerLane];
+};
+
+template <int VEC>
+__device__ __forceinline__ void prime_steps(const float* row, int vocab, int first, int stride, int nsteps, int lane,
+                                            StepRing& ring) {
+  const int last = max(nsteps - 1, 0);
+  load_step<VEC>(row, vocab, min(first, last), lane, ring.b0);
+  load_step<VEC>(row, vocab, min(first + stride, last), lane, ring.b1);
+  load_step<VEC>(row, vocab, min(first + 2 * stride, last), lane, ring.b2);
+}
+
 template <int VEC, typename F>
 __device__ __forceinline__ void stream_steps(const float* row, int vocab, int first, int stride, int nsteps, int lane,
-                                             F&& f) {
+                                             StepRing& ring, F&& f) {
   const int last = max(nsteps - 1, 0);
-  float b0[kPerLane], b1[kPerLane], b2[kPerLane], b3[kPerLane];
-  load_step<VEC>(row, vocab, min(first, last), lane, b0);
-  load_step<VEC>(row, vocab, min(first + stride, last), lane, b1);
-  load_step<VEC>(row, vocab, min(first + 2 * stride, last), lane, b2);
+  float(&b0)[kPerLane] = ring.b0;
+  float(&b1)[kPerLane] = ring.b1;
+  float(&b2)[kPerLane] = ring.b2;
+  float b3[kPerLane];
   for (int s = first; s < nsteps; s += 4 * stride) {
     load_step<VEC>(row, vocab, min(s + 3 * stride, last), lane, b3);
     f(b0, s);
@@ -456,11 +472,11 @@ __device__ __forceinline__ bool greedy_row(float T, int K, float P) {  // Sample
 // log2e-scaled logits); a NaN or +inf marks the row bad.  tid 0 returns the workgroup's part.
 template <int VEC>
 __device__ __forceinline__ GreedyPart greedy_pass(const float* row, int vocab, int s0, int s1, int lim, int w, int lane, int tid,
-                                  SampleShared& sh) {
+                                  SampleShared& sh, StepRing& ring) {
   int bk = kIntMin, bi = -1;
   float m = -INFINITY, sum = 0.0f;
   bool bad = false;
-  stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, [&](const float (&v)[kPerLane], int s) {
+  stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, ring, [&](const float (&v)[kPerLane], int s) {
     const int valid = lim - s * kStep;
     if (valid <= 0) return;  // a ring slot past the segment (wave-uniform)
     if (valid >= kStep) {
@@ -551,12 +567,12 @@ __device__ __forceinline__ GreedyPart greedy_pass(const float* row, int vocab, i
 // with equal logits).
 template <int VEC>
 __device__ __forceinline__ void buffer_pass(const float* row, int vocab, int s0, int s1, int lim, int k, int w, int lane,
-                            SampleShared& sh) {
+                            SampleShared& sh, StepRing& ring) {
   int* rkey = sh.key[w];
   int* ridx = sh.idx[w];
   int bound = kIntMin, cnt = 0;
   uint32_t nan_bits = 0;  // max of |bits|: above 0x7f800000 when a NaN was seen
-  stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, [&](const float (&v)[kPerLane], int s) {
+  stream_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, ring, [&](const float (&v)[kPerLane], int s) {
     const int valid = lim - s * kStep;  // logits of this step below lim: step_index offsets < valid
     if (valid <= 0) return;             // a ring slot past the segment (wave-uniform)
     if (k < 64 && s < s0 + kWaves) {
@@ -915,8 +931,10 @@ __global__ __launch_bounds__(kThreads) void sample_scan_kernel(const float* __re
   const int s0 = seg * seg_steps, s1 = min(nsteps, s0 + seg_steps);
   const int lim = min(vocab, s1 * kStep);
   ScanMeta* out = meta + (size_t)r * segs + seg;
+  StepRing ring;
+  prime_steps<VEC>(row, vocab, s0 + w, kWaves, s1, lane, ring);
   if (greedy_row(temperature[r], top_k[r], top_p[r])) {
-    const GreedyPart g = greedy_pass<VEC>(row, vocab, s0, s1, lim, w, lane, tid, sh);
+    const GreedyPart g = greedy_pass<VEC>(row, vocab, s0, s1, lim, w, lane, tid, sh, ring);
     if (tid == 0) out->g = g;
     return;
   }
@@ -928,7 +946,7 @@ __global__ __launch_bounds__(kThreads) void sample_scan_kernel(const float* __re
     sh.m = 0;
   }
   __syncthreads();
-  buffer_pass<VEC>(row, vocab, s0, s1, lim, k, w, lane, sh);
+  buffer_pass<VEC>(row, vocab, s0, s1, lim, k, w, lane, sh, ring);
   int total = 0;
   for (int q = 0; q < kWaves; ++q) total += sh.count[q];
   int* okey = cand_key + ((size_t)r * segs + seg) * kRegion;
@@ -1058,8 +1076,10 @@ __global__ __launch_bounds__(kThreads) void sample_row_kernel(const float* __res
   const int K = top_k[r];
   const float P = top_p[r];
   const int nsteps = (vocab + kStep - 1) / kStep;
+  StepRing ring;
+  prime_steps<VEC>(row, vocab, w, kWaves, nsteps, lane, ring);
   if (greedy_row(T, K, P)) {
-    const GreedyPart g = greedy_pass<VEC>(row, vocab, 0, nsteps, vocab, w, lane, tid, sh);
+    const GreedyPart g = greedy_pass<VEC>(row, vocab, 0, nsteps, vocab, w, lane, tid, sh, ring);
     if (tid == 0) {
       token[r] = g.idx;
       prob[r] = (g.bad || !(g.sum > 0.0f)) ? __int_as_float(0x7fc00000) : 1.0f / g.sum;
@@ -1079,7 +1099,7 @@ __global__ __launch_bounds__(kThreads) void sample_row_kernel(const float* __res
   __syncthreads();
   bool sorted = false;
   if (k < vocab) {
-    buffer_pass<VEC>(row, vocab, 0, nsteps, vocab, k, w, lane, sh);
+    buffer_pass<VEC>(row, vocab, 0, nsteps, vocab, k, w, lane, sh, ring);
     if (sh.flags == 0) sorted = fast_top_k(sh, k, tid, w, lane);
   }
   if (!sorted) replay_sorted<VEC>(row, vocab, k, tid, w, lane, sh);
