@@ -994,9 +994,16 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
 
   if (greedy_row(T, K, P)) {
     if (tid == 0) {
-      GreedyPart g = rm[0].g;
-      for (int j = 1; j < segs; ++j) {
-        const GreedyPart o = rm[j].g;
+      // every segment's part loaded at once (indices clamped, so the loads need no branch),
+      // then merged in segment order
+      GreedyPart parts[kMaxSegs];
+#pragma unroll
+      for (int j = 0; j < kMaxSegs; ++j) parts[j] = rm[min(j, segs - 1)].g;
+      GreedyPart g = parts[0];
+#pragma unroll
+      for (int j = 1; j < kMaxSegs; ++j) {
+        if (j >= segs) break;
+        const GreedyPart o = parts[j];
         if (o.key > g.key || (o.key == g.key && o.idx > g.idx)) {
           g.key = o.key;
           g.idx = o.idx;
@@ -1030,7 +1037,8 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
   }
   if (tid == 0) {
     int f = 0;
-    for (int j = 0; j < segs; ++j) f |= rm[j].flags;
+#pragma unroll
+    for (int j = 0; j < kMaxSegs; ++j) f |= rm[min(j, segs - 1)].flags;  // clamped: loads issued together
     sh.flags = k < vocab ? f : 0;
     sh.m = 0;
   }
