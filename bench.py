@@ -32,6 +32,9 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
 FP32_PEAK_TFS = 157.3  # MI355X dense fp32 (vector and MFMA), AMD public spec
 BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, AMD public spec
+# 5.81 TB/s: read-only kernels over C2's f32 pools at their best decomposition (per-kv-head
+# 8 KiB runs, partitions of <= 128 tokens), measured on MI355X
+C2_F32_READ_CEILING_FRAC = 0.727
 METRIC = "decode tokens/sec @ ragged batch 64; paged-attn achieved HBM GB/s (% peak)"
 
 
@@ -69,10 +72,6 @@ def parse_args():
                         "M = 64 projections, the q|k|v consumer, KV append, residual norm, SwiGLU "
                         "split sum, greedy head), 10 launches each: the command the C4 counter "
                         "profiles run under rocprofv3")
-    p.add_argument("--paged-read-ceiling", action="store_true",
-                   help="only time read-only kernels over the C2 f32 pools in three decompositions "
-                        "(per-kv-head chunks, whole blocks, linear) at several partition sizes, "
-                        "next to the decode op itself: the HBM rate the access pattern allows")
     return p.parse_args()
 
 
@@ -134,78 +133,6 @@ def c4_layer_ops(seed):
     ctx.check_faults()
     print(json.dumps({"c4_layer_ops": "done", "splits": {"qkv": s_qkv, "wo": s_o, "w2": s_w2}}), flush=True)
     ctx.close()
-
-
-def paged_read_ceiling(seed):
-    """Pure-read rates of C2's bytes (every context token's K and V row of every kv head) in the
-    decode kernel's decomposition and two others, from libferrisinfer_probe.so, against the
-    decode op on the same pools.  One JSON line per configuration."""
-    import ctypes
-
-    import torch
-
-    from ferrisinfer_amd import DTYPE_F32, Context
-    from ferrisinfer_amd.build import PROBE_PATH
-    from ferrisinfer_amd.workloads import paged_decode_c2
-
-    lib = ctypes.CDLL(PROBE_PATH)
-    lib.fp_paged_read.restype = ctypes.c_int32
-    lib.fp_paged_read.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int32] * 5 + [
-        ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
-    wl = paged_decode_c2(seed=seed)
-    kp = torch.from_numpy(wl.k_pool).cuda()
-    vp = torch.from_numpy(wl.v_pool).cuda()
-    bt = torch.from_numpy(wl.block_tables).cuda()
-    cl = torch.from_numpy(wl.context_lens).cuda()
-    sink = torch.zeros(1024, device="cuda")
-    stream = torch.cuda.current_stream()
-    total = int(wl.context_lens.sum())
-    kv_bytes = total * wl.num_kv_heads * wl.head_dim * 4 * 2
-
-    def timed(fn, reps=50):
-        for _ in range(5):
-            fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps * 1e3
-
-    def probe(mode, part):
-        def fn():
-            rc = lib.fp_paged_read(kp.data_ptr(), vp.data_ptr(), bt.data_ptr(), cl.data_ptr(),
-                                   wl.num_seqs, wl.num_kv_heads, wl.block_tables.shape[1],
-                                   wl.num_blocks, wl.max_context_len, total, mode, part,
-                                   sink.data_ptr(), stream.cuda_stream)
-            if rc != 0:
-                raise RuntimeError(f"fp_paged_read(mode {mode}, part {part}) failed")
-        return fn
-
-    names = {0: "head_chunks", 1: "whole_blocks", 2: "linear"}
-    print(json.dumps({"workload": f"C2 f32 pools, {wl.num_seqs} seqs, sum L {total}, "
-                      f"Hkv {wl.num_kv_heads}, D {wl.head_dim}", "bytes_read": kv_bytes}), flush=True)
-    for mode in (0, 1, 2):
-        for part in (64, 128, 256, 512, 1024):
-            us = timed(probe(mode, part))
-            print(json.dumps({"layout": names[mode], "partition_tokens": part, "us": round(us, 2),
-                              "GB_s": round(kv_bytes / us / 1e3, 1),
-                              "frac_of_8TBs": round(kv_bytes / us / 8e6, 4)}), flush=True)
-    ctx = Context(0)
-    q = torch.from_numpy(wl.q).cuda()
-    out = torch.empty_like(q)
-
-    def op():
-        ctx.attn_decode_paged(q, kp, vp, DTYPE_F32, bt, cl, wl.max_context_len, wl.num_kv_heads,
-                              wl.block_size, wl.num_blocks, wl.scale, out)
-
-    us = timed(op)
-    alg = wl.algorithmic_bytes(4)
-    print(json.dumps({"layout": "fi_attn_decode_paged (partition + merge)", "us": round(us, 2),
-                      "GB_s": round(alg / us / 1e3, 1), "frac_of_8TBs": round(alg / us / 8e6, 4)}),
-          flush=True)
 
 
 def pmc_copy_reference():
@@ -647,6 +574,8 @@ def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"
     }
     if graph:
         out["graph_counters"] = rt.graph_counters()
+    # generated ids per request, for the graph-versus-eager comparison (not printed)
+    out["_tokens"] = [rt.generated(s) for s in rep["sequence_ids"]]
     rt.close()
     return out
 
@@ -816,9 +745,6 @@ def main():
     if args.gemm_shapes:
         gemm_shapes(args.seed)
         return
-    if args.paged_read_ceiling:
-        paged_read_ceiling(args.seed)
-        return
     if args.c4_layer_ops:
         c4_layer_ops(args.seed)
         return
@@ -919,6 +845,10 @@ def main():
             "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": alg_bytes,
             "avg_launch_us": round(kernel_ms * 1e3, 3),
+            # the fastest pure read of C2's f32 K/V bytes measured on MI355X (read-only kernels,
+            # per-kv-head chunks of <= 128 tokens, no arithmetic): the rate this access pattern allows
+            "ceiling_frac": C2_F32_READ_CEILING_FRAC if args.kv_dtype == "f32" else None,
+            "ceiling_source": "profiles/decode_c2_read_ceiling.md" if args.kv_dtype == "f32" else None,
         },
         "device": dict(info, host_cpu=cpu_model(), host_cpus=os.cpu_count()),
     }
@@ -936,10 +866,17 @@ def main():
         variants = [v for v in args.c4_variants.split(",") if v]
         main_graph = "graph" in variants or "eager" not in variants
         result["c4"] = c4_continuous(args.seed, args.c4_requests, graph=main_graph)
+        tokens = result["c4"].pop("_tokens")
         if main_graph and "eager" in variants:
-            # the same requests with every decode tick enqueued launch by launch
+            # the same requests with every decode tick enqueued launch by launch; greedy decode
+            # from replayed graphs must generate exactly the eager run's ids
             eager = c4_continuous(args.seed, args.c4_requests, graph=False)
             result["c4"]["eager"] = {k: eager[k] for k in keys}
+            differ = sum(1 for a, b in zip(tokens, eager["_tokens"]) if a != b)
+            result["c4"]["graph_tokens_equal_eager"] = differ == 0 and len(tokens) == len(eager["_tokens"])
+            result["c4"]["graph_eager_differing_requests"] = differ
+            if differ:
+                print(f"bench: C4 graph and eager runs differ on {differ} requests", file=sys.stderr, flush=True)
         if "sampled" in variants:
             # the same requests under the reference's chat_default sampler (sampler.rs:30-37):
             # logits head + device sampling in every tick

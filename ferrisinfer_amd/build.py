@@ -73,12 +73,6 @@ def build_runtime(verbose: bool = False) -> str:
 
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 
-# Read-only probes of the HBM rate the paged access pattern allows (bench.py's
-# --paged-read-ceiling); a separate library, not part of the kernel interface.
-PROBE_LIB = "libferrisinfer_probe.so"
-PROBE_PATH = os.path.join(PKG_DIR, PROBE_LIB)
-PROBE_SOURCES = ["probe/fp_read_ceiling.hip"]
-
 
 def _compile(src: str, verbose: bool) -> str:
     """One translation unit to an object (its device code embedded) under _build/."""
@@ -114,21 +108,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         raise RuntimeError(f"hipcc failed linking {LIB_NAME} (exit {res.returncode})")
     os.replace(tmp, LIB_PATH)
     build_runtime(verbose)
-    build_probe(verbose)
     return LIB_PATH
-
-
-def build_probe(verbose: bool = False) -> str:
-    tmp = PROBE_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *[os.path.join(CSRC, s) for s in PROBE_SOURCES]]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, cwd=PKG_DIR, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {PROBE_LIB} (exit {res.returncode})")
-    os.replace(tmp, PROBE_PATH)
-    return PROBE_PATH
 
 
 if __name__ == "__main__":

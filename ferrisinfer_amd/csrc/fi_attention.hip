@@ -543,6 +543,45 @@ __global__ __launch_bounds__(256) void kv_copy_blocks_kernel(KVT* __restrict__ k
   }
 }
 
+// One thread per 4 consecutive elements of an output row [t][h][d .. d + 3]: the pool's
+// (block, head) runs [bs][D] are read row by row into token-major [length][Hkv][D].
+template <typename KVT>
+__global__ __launch_bounds__(256) void kv_gather_kernel(const KVT* __restrict__ k_cache,
+                                                        const KVT* __restrict__ v_cache,
+                                                        const int* __restrict__ table, int64_t quads,
+                                                        int num_blocks, int block_size, int hkv, int d,
+                                                        float* __restrict__ k_out, float* __restrict__ v_out,
+                                                        uint32_t* __restrict__ faults) {
+  const int dq = d / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < quads; i += stride) {
+    const int dd = static_cast<int>(i % dq) * 4;
+    const int64_t row = i / dq;
+    const int h = static_cast<int>(row % hkv);
+    const int t = static_cast<int>(row / hkv);
+    const int b = table[t / block_size];
+    float4 kq = make_float4(0.f, 0.f, 0.f, 0.f), vq = kq;
+    if (b < 0 || b >= num_blocks) {
+      atomicOr(faults, FI_FAULT_BLOCK_RANGE);
+    } else {
+      const size_t src = (((size_t)b * hkv + h) * block_size + t % block_size) * d + dd;
+      if constexpr (sizeof(KVT) == 4) {
+        kq = *reinterpret_cast<const float4*>(k_cache + src);
+        vq = *reinterpret_cast<const float4*>(v_cache + src);
+      } else {
+        const uint2 kb = *reinterpret_cast<const uint2*>(k_cache + src);
+        const uint2 vb = *reinterpret_cast<const uint2*>(v_cache + src);
+        kq = make_float4(fi::bf16_bits_to_f32(kb.x & 0xffffu), fi::bf16_bits_to_f32(kb.x >> 16),
+                         fi::bf16_bits_to_f32(kb.y & 0xffffu), fi::bf16_bits_to_f32(kb.y >> 16));
+        vq = make_float4(fi::bf16_bits_to_f32(vb.x & 0xffffu), fi::bf16_bits_to_f32(vb.x >> 16),
+                         fi::bf16_bits_to_f32(vb.y & 0xffffu), fi::bf16_bits_to_f32(vb.y >> 16));
+      }
+    }
+    *reinterpret_cast<float4*>(k_out + i * 4) = kq;
+    *reinterpret_cast<float4*>(v_out + i * 4) = vq;
+  }
+}
+
 __global__ void fill_zero_kernel(uint8_t* __restrict__ p, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -713,6 +752,42 @@ int32_t fi_kv_copy_blocks(fi_context* ctx, void* d_k_cache, void* d_v_cache, int
                        ctx->d_faults);
   }
   FI_CHECK_LAUNCH("kv_copy_blocks_kernel");
+  return FI_OK;
+}
+
+int32_t fi_kv_gather(fi_context* ctx, const void* d_k_cache, const void* d_v_cache, int32_t kv_dtype,
+                     const int32_t* d_block_table, int32_t num_table_blocks, int32_t length,
+                     int32_t num_blocks, int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                     float* d_k_out, float* d_v_out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(length >= 0 && num_table_blocks >= 0, FI_ERR_INVALID_SHAPE, "fi_kv_gather: negative sizes");
+  FI_REQUIRE(kv_dtype == FI_DTYPE_F32 || kv_dtype == FI_DTYPE_BF16, FI_ERR_INVALID_TYPE,
+             "fi_kv_gather: KV dtype must be f32 or bf16");
+  FI_REQUIRE(num_blocks > 0 && block_size > 0 && num_kv_heads > 0 && head_dim > 0, FI_ERR_INVALID_CONFIG,
+             "fi_kv_gather: pool dimensions must be greater than zero");
+  FI_REQUIRE(head_dim % 4 == 0, FI_ERR_UNSUPPORTED, "fi_kv_gather: head_dim must be a multiple of 4");
+  // paged_kv.rs:303-308: a prefix longer than the sequence's pages
+  FI_REQUIRE(static_cast<int64_t>(length) <= static_cast<int64_t>(num_table_blocks) * block_size, FI_ERR_RUNTIME,
+             "fi_kv_gather: KV cache block table ran out of committed pages");
+  if (length == 0) return FI_OK;
+  FI_REQUIRE(d_k_cache && d_v_cache && d_block_table && d_k_out && d_v_out, FI_ERR_INVALID_CONFIG,
+             "fi_kv_gather: null pointer");
+  FI_REQUIRE(((reinterpret_cast<uintptr_t>(d_k_cache) | reinterpret_cast<uintptr_t>(d_v_cache) |
+               reinterpret_cast<uintptr_t>(d_k_out) | reinterpret_cast<uintptr_t>(d_v_out)) & 15) == 0,
+             FI_ERR_INVALID_LAYOUT, "fi_kv_gather: pools and outputs must be 16-byte aligned (vector accesses)");
+  const int64_t quads = static_cast<int64_t>(length) * num_kv_heads * (head_dim / 4);
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>((quads + 255) / 256, 4096));
+  if (kv_dtype == FI_DTYPE_F32) {
+    hipLaunchKernelGGL(kv_gather_kernel<float>, dim3(grid), dim3(256), 0, ctx->stream,
+                       static_cast<const float*>(d_k_cache), static_cast<const float*>(d_v_cache), d_block_table,
+                       quads, num_blocks, block_size, num_kv_heads, head_dim, d_k_out, d_v_out, ctx->d_faults);
+  } else {
+    hipLaunchKernelGGL(kv_gather_kernel<uint16_t>, dim3(grid), dim3(256), 0, ctx->stream,
+                       static_cast<const uint16_t*>(d_k_cache), static_cast<const uint16_t*>(d_v_cache),
+                       d_block_table, quads, num_blocks, block_size, num_kv_heads, head_dim, d_k_out, d_v_out,
+                       ctx->d_faults);
+  }
+  FI_CHECK_LAUNCH("kv_gather_kernel");
   return FI_OK;
 }
 

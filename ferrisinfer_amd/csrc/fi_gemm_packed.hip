@@ -406,6 +406,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_lds_kernel(PGemmArgs g) {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
+// Range: the split is exact for |x| < 3.3961e38.  At or above it (and for +-inf) hi rounds to
+// +-inf, the remainders become NaN and so does every product the operand enters, where the
+// reference's f32 product is finite or infinite.  No model input gets there: every projection
+// input leaves an RMSNorm, the attention's convex combination or SwiGLU, and the reference's own
+// RMSNorm already overflows its sum of squares for |x| > 1.8e19.  Guarding it would add three
+// VALU instructions per element to every weight split.
 __device__ __forceinline__ void split3(const f32x8& x, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
   hi = __builtin_convertvector(x, bf16x8);
   const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);

@@ -450,7 +450,9 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   reserve(T, B);
   const int32_t H = c.hidden_size, F = c.intermediate_size, W = H + 2 * c.num_key_value_heads * c.head_dim();
   const bool greedy = sampler.is_greedy();
-  const bool use_graph = graph_decode_ && b.kind == BatchKind::Decode;
+  // A graph records the copy-on-write launch and its pair count; the shape key does not carry
+  // them, so a decode tick with copies runs eagerly (today only prefill ticks carry copies).
+  const bool use_graph = graph_decode_ && b.kind == BatchKind::Decode && b.copy_src.empty();
 
   Plan p{};
   p.kind = b.kind;

@@ -57,6 +57,7 @@ _SIGNATURES = {
     "fi_buf_zero": [_P, _P, _SZ],
     "fi_kv_append": [_P, _P, _P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32],
     "fi_kv_copy_blocks": [_P, _P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
+    "fi_kv_gather": [_P, _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P],
     "fi_attn_decode_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                              _I32, _F32, _P],
     "fi_attn_decode_paged_noalloc": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32,
@@ -222,6 +223,13 @@ class Context:
                                          ptr(src_blocks), ptr(dst_blocks), ptr(token_counts),
                                          int(src_blocks.numel()), num_blocks, block_size,
                                          num_kv_heads, head_dim))
+
+    def kv_gather(self, k_cache, v_cache, kv_dtype, block_table, length, num_blocks, block_size,
+                  num_kv_heads, head_dim, k_out, v_out):
+        """read_prefix_f32 of one sequence: its first `length` rows as f32 [length, Hkv, D]."""
+        check(self.lib.fi_kv_gather(self.handle, ptr(k_cache), ptr(v_cache), kv_dtype, ptr(block_table),
+                                    int(block_table.numel()), int(length), num_blocks, block_size,
+                                    num_kv_heads, head_dim, ptr(k_out), ptr(v_out)))
 
     def attn_decode_paged(self, q, k_cache, v_cache, kv_dtype, block_tables, context_lens,
                           max_context_len, num_kv_heads, block_size, num_blocks, scale, out):

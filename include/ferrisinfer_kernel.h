@@ -146,6 +146,21 @@ int32_t fi_kv_copy_blocks(fi_context* ctx, void* d_k_cache, void* d_v_cache, int
                           const int32_t* d_token_counts, int32_t num_pairs, int32_t num_blocks,
                           int32_t block_size, int32_t num_kv_heads, int32_t head_dim);
 
+/* Gathers the first `length` token rows of one sequence's K and V from the paged pool of one
+ * layer into contiguous f32 [length, Hkv, D] tensors (bf16 pools widen exactly, bits << 16).
+ * Replaces KvCacheStorage::read_prefix_f32 (runtime/kv_cache.rs:63) over paged storage:
+ * PagedKvCacheStorage::read_prefix_f32 concatenating pages by block table
+ * (runtime/paged_kv.rs:769-791, block_table at :260-314).  block_table holds the sequence's
+ * num_table_blocks block ids in logical order; a length beyond num_table_blocks * block_size
+ * is Runtime (the reference's "ran out of committed pages"), a negative one InvalidShape.
+ * A block id outside the pool writes zero rows and is reported as Runtime by the next
+ * fi_ctx_check_faults().  head_dim must be a multiple of 4 and the pools and outputs 16-byte
+ * aligned. */
+int32_t fi_kv_gather(fi_context* ctx, const void* d_k_cache, const void* d_v_cache, int32_t kv_dtype,
+                     const int32_t* d_block_table, int32_t num_table_blocks, int32_t length,
+                     int32_t num_blocks, int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                     float* d_k_out, float* d_v_out);
+
 /* Reads and clears the context's device fault flags (out-of-range slots / token ids seen by
  * kernels since the last check); returns Runtime with a message when any was set.  Waits
  * for the stream. */
@@ -173,7 +188,8 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
 
 /* fi_attn_decode_paged without any allocation: the same kernels, same arguments and bit-identical
  * outputs, with the split-KV partials in a fixed device array of this library (96 MiB per GPU,
- * held from the library's first use of the decode kernels on that GPU until the process ends)
+ * part of the library's code object: every process that loads the library onto a GPU holds it
+ * there, whether or not it calls this entry point, until the process exits)
  * instead of the grow-only context workspace.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  A launch whose partials (num_seqs * Hq * ceil(max_context_len /

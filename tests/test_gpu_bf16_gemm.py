@@ -137,8 +137,19 @@ def test_bf16_swiglu(orc, gpu_ctx, m, k, f, bias):
     assert normwise_error(got, swiglu(a)) <= 2e-2
 
 
-# (200, 256, 20000): 79 column groups over 96-row blocks (the third one partial), as the C5 head
-@pytest.mark.parametrize("m,h,v", [(1, 64, 129), (4, 256, 4096), (257, 512, 3000), (8, 2048, 32000), (200, 256, 20000)])
+def logits_f64(hr, w, chunk=16384):
+    """hr [M, H] times w [V, H]^T in f64, over vocabulary chunks (bounded host memory)."""
+    out = np.empty((hr.shape[0], w.shape[0]), np.float64)
+    h64 = hr.astype(np.float64)
+    for v0 in range(0, w.shape[0], chunk):
+        out[:, v0:v0 + chunk] = h64 @ w[v0:v0 + chunk].astype(np.float64).T
+    return out
+
+
+# (200, 256, 20000): 79 column groups over 96-row blocks (the third one partial), as the C5 head;
+# (8, 4096, 128256): the C5 head itself (Llama-3-8B hidden and vocabulary)
+@pytest.mark.parametrize("m,h,v", [(1, 64, 129), (4, 256, 4096), (257, 512, 3000), (8, 2048, 32000), (200, 256, 20000),
+                                   (8, 4096, 128256)])
 def test_bf16_lm_head_argmax(orc, gpu_ctx, m, h, v):
     import torch
 
@@ -148,12 +159,13 @@ def test_bf16_lm_head_argmax(orc, gpu_ctx, m, h, v):
     wb = bf16_weights(rng, (v, h), 0.05)
     w = orc.bf16_to_f32(wb)
     bp = gpu_ctx.weight_pack_bf16(dev(wb.view(np.int16)), h, v, src_layout=1)
+    del wb
     tok = torch.empty(m, dtype=torch.int32, device="cuda")
     prob = torch.empty(m, device="cuda")
     gpu_ctx.lm_head_argmax_bf16(padded(hid), bp, v, tok, prob)
     torch.cuda.synchronize()
     hr = round_bf16(orc, hid)
-    logits = hr.astype(np.float64) @ w.T.astype(np.float64)
+    logits = logits_f64(hr, w)
     rows = range(m) if m <= 64 else list(range(32)) + [m - 1]
     for r in rows:
         top2 = np.sort(logits[r])[-2:]
@@ -246,20 +258,37 @@ def test_bf16_swiglu_bf16_in_out(orc, gpu_ctx, m, k, f):
     assert np.array_equal(out16.cpu().numpy().view(np.uint16), want)
 
 
-def test_bf16_head_bf16_activations(orc, gpu_ctx):
-    """The greedy head over bf16 activations: the f32 call's tokens and probabilities exactly."""
+@pytest.mark.parametrize("m,h,v", [(33, 200, 1000), (8, 4096, 128256)])
+def test_bf16_head_bf16_activations(orc, gpu_ctx, m, h, v):
+    """The greedy head over bf16 activations: the f32 call's tokens and probabilities exactly
+    (also at the C5 head, 4096 -> 128256); at the C5 head the tokens also match the oracle's
+    fused argmax over the bf16-rounded rows (matmul.rs:190-274) away from near ties."""
     import torch
 
-    rng = np.random.default_rng(21)
-    m, h, v = 33, 200, 1000
+    print(f"bf16 head bf16 activations m={m} h={h} v={v}", flush=True)
+    rng = np.random.default_rng(21 + v)
     hid = rng.standard_normal((m, h), dtype=np.float32)
-    bp = gpu_ctx.weight_pack_bf16(dev(bf16_weights(rng, (v, h)).view(np.int16)), h, v, src_layout=1)
+    wb = bf16_weights(rng, (v, h))
+    bp = gpu_ctx.weight_pack_bf16(dev(wb.view(np.int16)), h, v, src_layout=1)
     tok = [torch.empty(m, dtype=torch.int32, device="cuda") for _ in range(2)]
     prob = [torch.empty(m, device="cuda") for _ in range(2)]
     gpu_ctx.lm_head_argmax_bf16(padded(hid), bp, v, tok[0], prob[0])
     gpu_ctx.lm_head_argmax_bf16(padded16(orc.f32_to_bf16(hid)), bp, v, tok[1], prob[1])
     torch.cuda.synchronize()
     assert torch.equal(tok[0], tok[1]) and torch.equal(prob[0], prob[1])
+    if v < 100000:
+        return
+    w = orc.bf16_to_f32(wb)
+    del wb
+    hr = round_bf16(orc, hid)
+    logits = logits_f64(hr, w)
+    for r in range(m):
+        top2 = np.sort(logits[r])[-2:]
+        if top2[1] - top2[0] < 1e-4 * max(1.0, abs(top2[1])):
+            continue
+        ridx, rprob = orc.matmul_rhs_transposed_argmax(hr[r:r + 1], w)
+        assert int(tok[1][r]) == ridx, r
+        assert abs(float(prob[1][r]) - rprob) <= 1e-4 * max(rprob, 1e-30) + 1e-7
 
 
 @pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (4096 * 37 + 3, 0), (1000, 1), (1 << 20, 0)])

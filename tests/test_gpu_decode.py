@@ -280,3 +280,74 @@ def test_kv_copy_blocks(gpu_ctx):
     exp_k[2] = k0[4]
     exp_v[2] = v0[4]
     assert torch.equal(kc, exp_k) and torch.equal(vc, exp_v)
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("length,read", [(300, 300), (300, 113), (16, 16), (1, 1), (37, 0)])
+def test_kv_gather_matches_read_prefix(orc, gpu_ctx, kv_dtype, length, read):
+    """fi_kv_gather against the oracle's PagedKvCacheStorage::read_prefix_f32 (pages concatenated
+    by block table, runtime/paged_kv.rs:769-791): a sequence of `length` rows written to the
+    oracle's paged storage and, through the same block table mapped onto a permuted device
+    pool, appended with fi_kv_append; the first `read` rows gathered back are bit-identical
+    (bf16 pool: the oracle's rows rounded to nearest even and widened)."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+
+    print(f"kv gather length={length} read={read} dtype={kv_dtype}", flush=True)
+    rng = np.random.default_rng(length * 7 + read)
+    hkv, d, bs, nb = 2, 64, 16, 64
+    store = orc.PagedKvStorage(1, hkv, d, 1024, bs)
+    key = rng.standard_normal((length, hkv, d), dtype=np.float32)
+    val = rng.standard_normal((length, hkv, d), dtype=np.float32)
+    store.write_sequence(0, 0, key, val)
+    entries = store.block_table(0, length)
+    perm = rng.permutation(nb).astype(np.int32)
+    table = np.array([perm[block] for _, block, _, _ in entries], np.int32)
+    slots = np.array([int(table[p // bs]) * bs + p % bs for p in range(length)], np.int64)
+    dt = DTYPE_F32 if kv_dtype == "f32" else DTYPE_BF16
+    tdt = torch.float32 if kv_dtype == "f32" else torch.int16
+    kc = torch.zeros((nb, hkv, bs, d), dtype=tdt, device="cuda")
+    vc = torch.zeros_like(kc)
+    gpu_ctx.kv_append(_dev(key, torch), _dev(val, torch), _dev(slots, torch), kc, vc, dt, nb, bs, hkv, d)
+    k_out = torch.full((max(read, 1), hkv, d), float("nan"), device="cuda")
+    v_out = torch.full_like(k_out, float("nan"))
+    gpu_ctx.kv_gather(kc, vc, dt, _dev(table, torch), read, nb, bs, hkv, d, k_out, v_out)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    if read == 0:
+        assert torch.isnan(k_out).all() and torch.isnan(v_out).all()  # nothing written
+        return
+    ref_k, ref_v = store.read_prefix(0, read)
+    if kv_dtype == "bf16":
+        ref_k = orc.bf16_to_f32(orc.f32_to_bf16(ref_k))
+        ref_v = orc.bf16_to_f32(orc.f32_to_bf16(ref_v))
+    assert np.array_equal(k_out.cpu().numpy(), ref_k)
+    assert np.array_equal(v_out.cpu().numpy(), ref_v)
+
+
+def test_kv_gather_errors(gpu_ctx):
+    """A length beyond the table's pages is Runtime before any launch (paged_kv.rs:303-308); a
+    block id outside the pool gives zero rows and Runtime at the next fault check."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32, FerrisError
+
+    nb, bs, hkv, d = 8, 16, 2, 32
+    kc = torch.randn((nb, hkv, bs, d), device="cuda")
+    vc = torch.randn((nb, hkv, bs, d), device="cuda")
+    out_k = torch.zeros((40, hkv, d), device="cuda")
+    out_v = torch.zeros_like(out_k)
+    table = torch.tensor([3, 5], dtype=torch.int32, device="cuda")
+    with pytest.raises(FerrisError) as e:
+        gpu_ctx.kv_gather(kc, vc, DTYPE_F32, table, 33, nb, bs, hkv, d, out_k, out_v)
+    assert e.value.kind == "Runtime" and "committed pages" in str(e.value)
+    bad = torch.tensor([3, nb + 4, 1], dtype=torch.int32, device="cuda")
+    gpu_ctx.kv_gather(kc, vc, DTYPE_F32, bad, 40, nb, bs, hkv, d, out_k, out_v)
+    torch.cuda.synchronize()
+    with pytest.raises(FerrisError) as e:
+        gpu_ctx.check_faults()
+    assert e.value.kind == "Runtime"
+    assert torch.equal(out_k[:16], kc[3].transpose(0, 1))
+    assert not out_k[16:32].any() and not out_v[16:32].any()
+    assert torch.equal(out_v[32:40], vc[1, :, :8].transpose(0, 1))

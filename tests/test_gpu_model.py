@@ -341,6 +341,33 @@ def test_c4_qwen2_shape_reaches_decode_batch_64(orc):
     assert gpu.pool_free_count() == 512
 
 
+def test_c4_width_long_prompts_match_reference(orc):
+    """BASELINE config C4's prompt range at the C4 width (H 896, 14/2 heads, D 64, F 4864, full
+    vocab 151936, tied embeddings, q/k/v biases, theta 1e6; 4 of its 24 layers so the oracle
+    finishes in seconds): 3 requests with 700-, 1500- and 2048-token prompts (the lognormal
+    workload's clip) under the bench's scheduler settings (max batch 64, max_seq 4096, default
+    256-token chunks and 1024-token tick budget), so prefill runs as multi-chunk cached-prefix
+    ticks at the f32-pool prefill kernel's GQA-7 shape.  Ticks, reports, released blocks and
+    every tick's packing equal the oracle's; greedy tokens too, except at a near tie."""
+    from ferrisinfer_amd import seeded
+    from ferrisinfer_amd.seeded import tag_of
+    from ferrisinfer_amd.workloads import QWEN2_05B_C4, random_weights
+
+    print("C4 width, 700/1500/2048-token prompts", flush=True)
+    cfg = dict(QWEN2_05B_C4, layers=4)
+    weights = random_weights(cfg, seed=3, qkv_bias=True)
+    requests = [(seeded.integers(3, tag_of(f"c4r.prompt.{i}"), n, 0, cfg["vocab"] - 1).astype(np.uint32), 6)
+                for i, n in enumerate((700, 1500, 2048))]
+    model, ref, gpu = build_pair(orc, cfg, weights, dict(max_batch=64, max_seq=4096, max_gen=512),
+                                 num_blocks=1024)
+    del weights
+    ticks, ties = compare(model, ref, gpu, requests)
+    prefill_ticks = sum(1 for kind, _ in ticks if kind == 0)
+    assert prefill_ticks >= (700 + 1500 + 2048) // 1024  # chunked over several ticks
+    print(f"C4 long prompts: {len(ticks)} ticks ({prefill_ticks} prefill), near ties {ties}", flush=True)
+    assert gpu.pool_free_count() == 1024
+
+
 def bf16_rounded(orc, weights):
     """The weights a bf16 checkpoint holds: every matrix rounded to bf16 (nearest even) and
     widened back, which is what the reference's loader hands its f32 kernels

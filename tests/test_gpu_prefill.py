@@ -147,6 +147,86 @@ def test_prefill_bf16_mfma_rising_scores(orc, gpu_ctx):
     assert normwise_error(got, ref) <= 5e-3
 
 
+def rise_keys(wl, step):
+    """Scale each key row by 1 + position / step (position within its sequence; a shared
+    prefix is scaled where its source computes it), so scores grow along the sequence."""
+    for b in range(len(wl.context_lens)):
+        lo, hi = int(wl.cu_seqlens[b]), int(wl.cu_seqlens[b + 1])
+        pos = int(wl.shared_lens[b]) + np.arange(hi - lo, dtype=np.float32)
+        wl.k_new[lo:hi] *= (1.0 + pos / np.float32(step))[:, None, None]
+
+
+def lazy_point_moves(wl, chunk=32, headroom=8.0):
+    """Host replay of the f32-pool prefill kernel's exponent reference point: keys in chunks of
+    `chunk` from position 0, the point set by the first chunk and moved only when a later
+    chunk's maximum score (log2 units) passes it by more than `headroom`; every move after the
+    first chunk rescales the accumulators by alpha in (0, 1).  Returns the fraction of (query
+    row, head) pairs whose point moves at least once after the first chunk."""
+    c2 = wl.scale * np.log2(np.e)
+    group = wl.num_q_heads // wl.num_kv_heads
+    moved = total = 0
+    for b in range(len(wl.context_lens)):
+        k, _ = wl.full_kv(b)
+        lo, hi = int(wl.cu_seqlens[b]), int(wl.cu_seqlens[b + 1])
+        start = int(wl.context_lens[b]) - (hi - lo)
+        n = int(wl.context_lens[b])
+        nch = (n + chunk - 1) // chunk
+        for h in range(wl.num_q_heads):
+            s = (wl.q[lo:hi, h].astype(np.float64) @ k[:, h // group].astype(np.float64).T) * c2
+            s[np.arange(n)[None, :] > (start + np.arange(hi - lo))[:, None]] = -np.inf
+            pad = np.full((hi - lo, nch * chunk), -np.inf)
+            pad[:, :n] = s
+            cmax = pad.reshape(hi - lo, nch, chunk).max(axis=2)
+            m = cmax[:, 0].copy()
+            any_move = np.zeros(hi - lo, bool)
+            for c in range(1, nch):
+                mv = cmax[:, c] > m + headroom
+                any_move |= mv
+                m = np.where(mv, cmax[:, c], m)
+            moved += int(any_move.sum())
+            total += hi - lo
+    return moved / total
+
+
+RISING_CASES = [
+    # (num_seqs, min_len, max_len, groups, group_size, shared, hq, hkv, d, step)
+    (3, 300, 600, 0, 1, 0, 8, 2, 64, 16),           # GQA 4, D 64, no prefix
+    (4, 1500, 1600, 1, 4, 512, 14, 2, 64, 64),      # Qwen2 heads: ~1000-token prompts after a shared 512
+    (32, 200, 300, 2, 4, 96, 14, 2, 64, 16),        # GQA 7 at D 64 with two row groups a wave
+    (4, 300, 500, 1, 4, 128, 32, 8, 128, 16),       # C2/C3 heads at D 128
+]
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", RISING_CASES)
+def test_prefill_rising_scores(orc, gpu_ctx, case, kv_dtype):
+    """fi_attn_prefill_paged with keys whose norms grow along the sequence, so later chunks'
+    maxima pass the running reference point and the accumulators are rescaled (the
+    s > m branch of the reference's online softmax, kernel/cpu/attention.rs:1125-1149).  The f32
+    pool runs the three-piece kernel, whose point moves lazily (asserted to move on the host);
+    the bf16 pool runs the f32-math kernel on widened values.  Both within 1e-4 of the oracle's
+    cached-prefixed attention and of the f64 closed form on the same stored values."""
+    from ferrisinfer_amd.workloads import prefill_c3
+
+    b, lo, hi, g, gs, sh, hq, hkv, d, step = case
+    print(f"prefill rising scores case={case} dtype={kv_dtype}", flush=True)
+    wl = prefill_c3(seed=7, num_seqs=b, min_len=lo, max_len=hi, groups=g, group_size=gs,
+                    shared_prefix=sh, num_q_heads=hq, num_kv_heads=hkv, head_dim=d, block_size=16,
+                    num_blocks=1024)
+    rise_keys(wl, step)
+    assert lazy_point_moves(wl) >= 0.5
+    got = run_prefill(gpu_ctx, wl, kv_dtype)
+    assert np.isfinite(got).all()
+    assert normwise_error(got, oracle_prefill(orc, wl, kv_dtype)) <= 1e-4
+    rb = (lambda x: orc.bf16_to_f32(orc.f32_to_bf16(x))) if kv_dtype == "bf16" else (lambda x: x)
+    ref = np.empty(got.shape, np.float64)
+    for s in range(len(wl.context_lens)):
+        k, v = wl.full_kv(s)
+        r0, r1 = int(wl.cu_seqlens[s]), int(wl.cu_seqlens[s + 1])
+        ref[r0:r1] = brute_force_f64(wl.q[r0:r1], rb(k), rb(v), int(wl.context_lens[s]) - (r1 - r0))
+    assert normwise_error(got, ref) <= 1e-4
+
+
 def test_prefill_bf16_mfma_c3_full_size(orc, gpu_ctx):
     from ferrisinfer_amd.workloads import prefill_c3
 
