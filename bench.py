@@ -377,11 +377,25 @@ def kernel_legs(ctx, seed):
     del w, bp
     # device sampling (sample_last_token per row, one workgroup per row): the logits are
     # read once, so the bound is HBM at rows * vocab * 4 bytes per launch; N(0, 2.5) logits
-    # under the reference's chat_default sampler (top-k 20) and a greedy configuration
-    for tag, rows, vocab, cfg in (("c4_m64_topk20", 64, 151936, (0.7, 20, 0.9)),
-                                  ("c5_m257_topk20", 257, 128256, (0.7, 20, 0.9)),
-                                  ("c4_m64_greedy", 64, 151936, (0.0, 1, 1.0))):
-        logits = torch.randn(rows, vocab, device="cuda", generator=g) * 2.5
+    # under the reference's chat_default sampler (top-k 20) and a greedy configuration.  Then
+    # the paths off the fast one: top-k 1024 on N(0, 1) rows (equal values among the 1025
+    # largest in about a fifth of them), top-k 20 on bf16-rounded logits (equal values nearly
+    # everywhere), and top-k above 1024 (the reserved-area launch: a radix sort of each row and
+    # sequential walks over up to `vocab` weights, so not an HBM-bound figure; the reservation
+    # comes last, as a reserved context launches that kernel on every call)
+    for tag, rows, vocab, cfg, scale, bf16 in (
+            ("c4_m64_topk20", 64, 151936, (0.7, 20, 0.9), 2.5, False),
+            ("c5_m257_topk20", 257, 128256, (0.7, 20, 0.9), 2.5, False),
+            ("c4_m64_greedy", 64, 151936, (0.0, 1, 1.0), 2.5, False),
+            ("c4_m64_topk1024", 64, 151936, (1.0, 1024, 0.95), 1.0, False),
+            ("c4_m64_topk20_bf16_logits", 64, 151936, (0.7, 20, 0.9), 2.5, True),
+            ("c4_m64_topk2000", 64, 151936, (0.7, 2000, 0.9), 2.5, False),
+            ("c4_m64_topk_vocab", 64, 151936, (1.0, 151936, 1.0), 1.0, False)):
+        logits = torch.randn(rows, vocab, device="cuda", generator=g) * scale
+        if bf16:
+            logits = logits.to(torch.bfloat16).float()
+        if cfg[1] > 1024:
+            ctx.sample_reserve(rows, vocab)
         temp = torch.full((rows,), cfg[0], device="cuda")
         topk = torch.full((rows,), cfg[1], dtype=torch.int32, device="cuda")
         topp = torch.full((rows,), cfg[2], device="cuda")
@@ -391,7 +405,8 @@ def kernel_legs(ctx, seed):
         ms = timed(lambda: ctx.sample_tokens(logits, temp, topk, topp, st, tok, prob), 20)
         b = rows * vocab * 4
         out[f"sample_tokens_{tag}"] = {
-            "kernel": ("sample_row_kernel<4>" if rows >= 256 else "sample_scan_kernel<4> + sample_finish_kernel<4>"),
+            "kernel": ("sample_row_kernel<4>" if rows >= 256 else "sample_scan_kernel<4> + sample_finish_kernel<4>") +
+                      (" + sample_large_kernel<4>" if cfg[1] > 1024 else ""),
             "bound": "hbm", "rows": rows, "vocab": vocab,
             "temperature": cfg[0], "top_k": cfg[1], "top_p": cfg[2], "bytes_per_launch": b,
             "avg_launch_us": round(ms * 1e3, 2), "achieved_gbs": round(b / (ms * 1e-3) / 1e9, 1),

@@ -29,8 +29,10 @@ struct fi_context {
   size_t workspace_bytes = 0;
   int compute_units = 0;
   void* noalloc_scratch = nullptr;  // this device's address of the library's fixed decode scratch array
-  uint64_t workspace_generation = 0;  // bumped whenever the workspace is reallocated
+  uint64_t workspace_generation = 0;  // bumped whenever the workspace or the sampling area is reallocated
   bool capturing = false;             // the stream is being captured into a graph
+  void* sample_area = nullptr;        // fi_sample_reserve: per-row sort and replay arrays for top-k above 1024
+  size_t sample_bytes = 0;
 };
 
 // A captured and instantiated launch sequence of one context's stream.

@@ -111,6 +111,7 @@ int32_t fi_ctx_destroy(fi_context* ctx) {
   }
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->workspace) (void)hipFree(ctx->workspace);
+  if (ctx->sample_area) (void)hipFree(ctx->sample_area);
   if (ctx->d_faults) (void)hipFree(ctx->d_faults);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;

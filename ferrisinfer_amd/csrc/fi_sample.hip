@@ -11,14 +11,21 @@
 //     its running bound (the k+1-th largest of what it has buffered, raised to the other
 //     waves' bounds) and compacts the buffer by radix selection when it fills.  When the k+1
 //     largest values of the row are strictly decreasing and the row holds no NaN, the final
-//     list is exactly the k largest logits, in value order;
-//   * otherwise (equal values among the top k + 1, signed zeros, NaN) list positions decide
-//     which equal logit is kept and how equal candidates are ordered, and the replacement is
-//     replayed: in rounds of one 1024-logit step per wave, every wave keeps the logits of its step
-//     above the list minimum published at the round's start (the minimum never falls, so a
-//     logit not above it cannot enter later), in index order; wave 0, holding the list in
-//     registers, applies them one by one against the current minimum.  The list is then
-//     sorted stably by total_cmp descending.
+//     list is exactly the k largest logits, in value order.  With equal values among them the
+//     list still holds the same values in the same sorted order (equal values, equal weights),
+//     so the total, the top-p prefix and the drawn position are exact; only the token at the
+//     drawn position can differ, when its value is shared with another logit;
+//   * then, or with a NaN in the row, list positions decide which equal logit is kept and how
+//     equal candidates are ordered, and the replacement is replayed: in rounds of one
+//     1024-logit step per wave, every wave keeps the logits of its step above the list
+//     minimum published at the round's start (the minimum never falls, so a logit not above
+//     it cannot enter later), in index order; wave 0, holding the list in registers, applies
+//     them one by one against the current minimum.  The list is then sorted stably by
+//     total_cmp descending.
+// top_k above 1024 (up to the vocabulary) runs in sample_large_kernel over an area the host
+// reserves (fi_sample_reserve): a radix sort of the row's candidates and sequential walks over
+// the sorted weights, with the same replay, over a tree of list minima, for a shared drawn
+// value.
 // Weights exp(l / T - l0 / T) are computed in parallel; one lane then forms the total, the
 // top-p prefix, the retained total, the xorshift64* draw and the threshold walk, sequentially
 // in f32 in list order.  The exponential is the device expf; the reference's is the host
@@ -137,6 +144,20 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Inclusive prefix sum over the wave in DPP moves (no LDS round trips): row_shr 1, 2, 4, 8
+// scan each row of 16 lanes (lanes shifted in from outside the row add 0), row_bcast:15 adds
+// the last lane of rows 0 and 2 to rows 1 and 3, row_bcast:31 the last lane of row 1 to rows
+// 2 and 3.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  return x;
+}
+
 // Radix selection, one 8-bit digit: hist[256] holds the counts of the candidates matching the
 // digits chosen so far; returns the digit of the element of descending rank `want` among them
 // and makes `want` its rank within that digit (one wave).
@@ -148,17 +169,7 @@ __device__ __forceinline__ int pick_digit_desc(const int* hist, int lane, int& w
     c[q] = hist[255 - (4 * lane + q)];  // lanes ascending = digits descending
     tot += c[q];
   }
-  // inclusive prefix sum over the wave in DPP moves (no LDS round trips): row_shr 1, 2, 4, 8
-  // scan each row of 16 lanes (lanes shifted in from outside the row add 0), row_bcast:15
-  // adds the last lane of rows 0 and 2 to rows 1 and 3, row_bcast:31 the last lane of row 1
-  // to rows 2 and 3
-  int incl = tot;
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, false);
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, false);
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, false);
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, false);
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);
+  const int incl = wave_inclusive_sum(tot);
   const int excl = incl - tot;
   const bool here = excl <= want && want < incl;
   int digit = 0, below = 0, acc = excl;
@@ -305,6 +316,7 @@ struct SampleShared {
   int flags;  // bit 0: NaN seen, bit 1: buffer overflow, bit 2: not strictly decreasing
   int sel[2];
   int m;
+  int draw;       // the drawn list position, -1 when the row faulted
   float pub_min;  // replay: the list minimum at the start of the round
   float red_f[kWaves][2];
   int red_i[kWaves][3];
@@ -724,9 +736,10 @@ __device__ __forceinline__ int select_desc(SampleShared& sh, int rank, int tid, 
 }
 
 // Fast path after the buffering: the k+1-th largest key over the wave buffers, the candidates
-// at or above it sorted by (key descending, index ascending) into s_val / s_idx.  Returns true
-// when the top k+1 are strictly decreasing (the list is then exactly the top k in value order);
-// false sends the row to the replay.
+// at or above it sorted by (key descending, index ascending) into s_val / s_idx.  Sets flags
+// bit 2 unless the top k+1 are strictly decreasing (the list is then exactly the top k in value
+// order; otherwise tie_at decides whether the drawn token needs the replay).  Returns false,
+// sending the row to the replay, when more candidates share the boundary value than it sorts.
 __device__ __forceinline__ bool fast_top_k(SampleShared& sh, int k, int tid, int w, int lane) {
   int total = 0;
   for (int q = 0; q < kWaves; ++q) total += sh.count[q];
@@ -782,7 +795,20 @@ __device__ __forceinline__ bool fast_top_k(SampleShared& sh, int k, int tid, int
     if (!(sh.s_val[i] > sh.s_val[i + 1])) atomicOr(&sh.flags, 4);
   }
   __syncthreads();
-  return sh.flags == 0;
+  return true;
+}
+
+// With equal values among the k+1 largest (flags bit 2) the fast path's list holds the values
+// of the reference's list, in the same sorted order, but not necessarily its indices where
+// values are equal.  Equal values have equal weights, so the total, the top-p prefix and the
+// drawn position are the reference's; the token at that position is too unless its value is
+// shared with another logit of the row (IEEE equality, so +0 with -0).  Such a value's other
+// logits are all among the candidates (their keys reach the k+1-th largest), and sorted next
+// to it.  Zero is sent to the replay whenever flags bit 2 is set: a -0 below the candidates
+// can stand in the reference's list for a +0 here.
+__device__ __forceinline__ bool tie_at(const SampleShared& sh, int sel) {
+  const float v = sh.s_val[sel];
+  return v == 0.0f || (sel > 0 && sh.s_val[sel - 1] == v) || sh.s_val[sel + 1] == v;
 }
 
 // The reference's replacement over the whole row, replayed; then a stable sort by total_cmp
@@ -829,85 +855,107 @@ __device__ __forceinline__ void replay_sorted(const float* row, int vocab, int k
 }
 
 // Weights (parallel), then the total, top-p, draw and threshold walk (one lane, in the
-// reference's sequential f32 order) over the sorted list s_val / s_idx of k candidates.
+// reference's sequential f32 order) over the sorted list s_val / s_idx of k candidates.  Leaves
+// the drawn list position in sh.draw and writes the probability, or faults the row (sh.draw
+// -1).  Every thread returns after the closing barrier.
+// SamplerState::next_f32 (sampler.rs:62-75): advances rng[r] and returns the draw.
+__device__ __forceinline__ float next_draw(uint64_t* rng, int r) {
+  const uint64_t x = xorshift_step(rng[r]);
+  rng[r] = x;
+  const uint32_t upper = static_cast<uint32_t>((x * 0x2545F4914F6CDD1DULL) >> 40);
+  return static_cast<float>(upper) / 16777216.0f;
+}
+
+// The total, top-p prefix, draw and threshold walk of sampler.rs:190-233 over k weights in
+// list order (one lane; wts 16-byte aligned and zero from k to the next multiple of 8).  The
+// top-p loop's running sum repeats the total's additions in the same order from the same +0,
+// so the retained total, summed again from the start by the reference, is the running sum
+// where that loop stops.  Returns the drawn position and writes the probability, or faults the
+// row and returns -1.
+__device__ __forceinline__ int draw_one(const float* wts, int k, float P, uint64_t* rng, int32_t* token, float* prob,
+                                        uint32_t* faults, int r) {
+#pragma clang fp contract(off)
+  const float4* w4 = reinterpret_cast<const float4*>(wts);  // + 0.0f past k leaves a sum >= +0 unchanged
+  float total = 0.0f;
+  for (int i = 0; i < k; i += 8) {
+    const float4 a = w4[i / 4], b = w4[i / 4 + 1];
+    total = total + a.x;
+    total = total + a.y;
+    total = total + a.z;
+    total = total + a.w;
+    total = total + b.x;
+    total = total + b.y;
+    total = total + b.z;
+    total = total + b.w;
+  }
+  if (!(total <= 3.402823466e+38f) || total <= 0.0f) {  // not finite, or no mass
+    sampling_fault(faults, FI_FAULT_SAMPLE_NONFINITE, token, prob, r);
+    return -1;
+  }
+  float p = P;  // f32::clamp(0, 1): a NaN stays NaN
+  if (p < 0.0f) p = 0.0f;
+  if (p > 1.0f) p = 1.0f;
+  const float cutoff = p >= 1.0f ? total : total * p;
+  float kept = 0.0f;
+  int retained = 0;
+  for (int i = 0; i < k; i += 4) {
+    const float4 a = w4[i / 4];
+    const float t[4] = {a.x, a.y, a.z, a.w};
+    bool reached = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!reached && i + j < k) {
+        kept = kept + t[j];
+        ++retained;
+        reached = kept >= cutoff;
+      }
+    }
+    if (reached) break;
+  }
+  const float retained_total = kept;  // retained >= 1: the loop adds at least one weight
+  float threshold = next_draw(rng, r) * retained_total;
+  int sel = 0;
+  for (int i = 0; i < retained; i += 4) {
+    const float4 a = w4[i / 4];
+    const float t[4] = {a.x, a.y, a.z, a.w};
+    bool hit = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!hit && i + j < retained) {
+        threshold = threshold - t[j];
+        if (threshold <= 0.0f) {
+          sel = i + j;
+          hit = true;
+        }
+      }
+    }
+    if (hit) break;
+  }
+  prob[r] = wts[sel] / retained_total;
+  return sel;
+}
+
 __device__ __forceinline__ void weights_and_draw(SampleShared& sh, int k, float T, float P, uint64_t* rng,
                                                  int32_t* token, float* prob, uint32_t* faults, int r, int tid) {
   const float temp = fmaxf(T, 1.1920929e-7f);  // max(f32::EPSILON); a NaN temperature gives EPSILON
   const float scaled_max = sh.s_val[0] / temp;
   for (int i = tid; i < kMaxTopK; i += kThreads) sh.wts[i] = i < k ? expf((sh.s_val[i] / temp) - scaled_max) : 0.0f;
   __syncthreads();
-  if (tid == 0) {
-#pragma clang fp contract(off)
-    const float* wv = sh.wts;
-    const float4* w4 = reinterpret_cast<const float4*>(sh.wts);  // zero past k: + 0.0f leaves a sum >= +0 unchanged
-    float total = 0.0f;
-    for (int i = 0; i < k; i += 8) {
-      const float4 a = w4[i / 4], b = w4[i / 4 + 1];
-      total = total + a.x;
-      total = total + a.y;
-      total = total + a.z;
-      total = total + a.w;
-      total = total + b.x;
-      total = total + b.y;
-      total = total + b.z;
-      total = total + b.w;
-    }
-    if (!(total <= 3.402823466e+38f) || total <= 0.0f) {  // not finite, or no mass
-      sampling_fault(faults, FI_FAULT_SAMPLE_NONFINITE, token, prob, r);
-      return;
-    }
-    float p = P;  // f32::clamp(0, 1): a NaN stays NaN
-    if (p < 0.0f) p = 0.0f;
-    if (p > 1.0f) p = 1.0f;
-    const float cutoff = p >= 1.0f ? total : total * p;
-    float kept = 0.0f;
-    int retained = 0;
-    for (int i = 0; i < k; i += 4) {
-      const float4 a = w4[i / 4];
-      const float t[4] = {a.x, a.y, a.z, a.w};
-      bool reached = false;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (!reached && i + j < k) {
-          kept = kept + t[j];
-          ++retained;
-          reached = kept >= cutoff;
-        }
-      }
-      if (reached) break;
-    }
-    retained = max(retained, 1);
-    float retained_total = 0.0f;
-    for (int i = 0; i < retained; i += 4) {
-      const float4 a = w4[i / 4];
-      const float t[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) retained_total = retained_total + (i + j < retained ? t[j] : 0.0f);
-    }
-    const uint64_t x = xorshift_step(rng[r]);  // SamplerState::next_u64 / next_f32 (sampler.rs:62-75)
-    rng[r] = x;
-    const uint32_t upper = static_cast<uint32_t>((x * 0x2545F4914F6CDD1DULL) >> 40);
-    float threshold = (static_cast<float>(upper) / 16777216.0f) * retained_total;
-    int sel = 0;
-    for (int i = 0; i < retained; i += 4) {
-      const float4 a = w4[i / 4];
-      const float t[4] = {a.x, a.y, a.z, a.w};
-      bool hit = false;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (!hit && i + j < retained) {
-          threshold = threshold - t[j];
-          if (threshold <= 0.0f) {
-            sel = i + j;
-            hit = true;
-          }
-        }
-      }
-      if (hit) break;
-    }
-    token[r] = sh.s_idx[sel];
-    prob[r] = wv[sel] / retained_total;
-  }
+  if (tid == 0) sh.draw = draw_one(sh.wts, k, P, rng, token, prob, faults, r);
+  __syncthreads();
+}
+
+// The token at the drawn position (whole workgroup, after weights_and_draw): the fast path's
+// list answers unless tie_at finds the drawn value shared, in which case the reference's
+// replacement is replayed for the order of the equal values (their weights, and so the drawn
+// position, are unchanged).
+template <int VEC>
+__device__ __forceinline__ void write_token(SampleShared& sh, const float* row, int vocab, int k, bool fast,
+                                            int32_t* token, int r, int tid, int w, int lane) {
+  const int sel = sh.draw;
+  if (sel < 0) return;  // faulted
+  if (fast && (sh.flags & 4) && tie_at(sh, sel)) replay_sorted<VEC>(row, vocab, k, tid, w, lane, sh);
+  if (tid == 0) token[r] = sh.s_idx[sel];
 }
 
 // ---- launch 1: one workgroup per (row segment, row) ----
@@ -982,7 +1030,7 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
     const float* __restrict__ logits, int ld, int vocab, int segs, const float* __restrict__ temperature,
     const int32_t* __restrict__ top_k, const float* __restrict__ top_p, uint64_t* __restrict__ rng,
     const ScanMeta* __restrict__ meta, const int* __restrict__ cand_key, const int* __restrict__ cand_idx,
-    int32_t* __restrict__ token, float* __restrict__ prob, uint32_t* __restrict__ faults) {
+    int32_t* __restrict__ token, float* __restrict__ prob, uint32_t* __restrict__ faults, int large) {
   __shared__ SampleShared sh;
   const int r = blockIdx.x;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -1018,8 +1066,8 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
   }
 
   const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
-  if (k > kMaxTopK) {
-    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
+  if (k > kMaxTopK) {  // sample_large_kernel's row when the context reserved for it
+    if (!large && tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
     return;
   }
   // Wave q copies segment q's candidates (segs <= kWaves).  Its count and first 64 entries are
@@ -1063,6 +1111,7 @@ __global__ __launch_bounds__(kThreads) void sample_finish_kernel(
 
   if (!sorted) replay_sorted<VEC>(row, vocab, k, tid, w, lane, sh);
   weights_and_draw(sh, k, T, P, rng, token, prob, faults, r, tid);
+  write_token<VEC>(sh, row, vocab, k, sorted, token, r, tid, w, lane);
 }
 
 // ---- the single-launch form: one workgroup per row over the whole row ----
@@ -1075,7 +1124,8 @@ __global__ __launch_bounds__(kThreads) void sample_row_kernel(const float* __res
                                                               const int32_t* __restrict__ top_k,
                                                               const float* __restrict__ top_p,
                                                               uint64_t* __restrict__ rng, int32_t* __restrict__ token,
-                                                              float* __restrict__ prob, uint32_t* __restrict__ faults) {
+                                                              float* __restrict__ prob, uint32_t* __restrict__ faults,
+                                                              int large) {
   __shared__ SampleShared sh;
   const int r = blockIdx.x;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -1095,8 +1145,8 @@ __global__ __launch_bounds__(kThreads) void sample_row_kernel(const float* __res
     return;
   }
   const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
-  if (k > kMaxTopK) {
-    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
+  if (k > kMaxTopK) {  // sample_large_kernel's row when the context reserved for it
+    if (!large && tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_TOPK, token, prob, r);
     return;
   }
   if (tid < kWaves) sh.bound[tid] = kIntMin;
@@ -1112,6 +1162,778 @@ __global__ __launch_bounds__(kThreads) void sample_row_kernel(const float* __res
   }
   if (!sorted) replay_sorted<VEC>(row, vocab, k, tid, w, lane, sh);
   weights_and_draw(sh, k, T, P, rng, token, prob, faults, r, tid);
+  write_token<VEC>(sh, row, vocab, k, sorted, token, r, tid, w, lane);
+}
+
+// ---- rows whose top-k (clamped) exceeds 1024: one workgroup per row over a reserved area ----
+// Row r owns large_row_ints(vocab) ints of the area fi_sample_reserve allocates: two (key,
+// index) arrays of vocab entries and room for the replay's block minima.
+//   1. A NaN among the first k logits stays in the reference's list (nothing is strictly
+//      larger than NaN, so -NaN, the total_cmp minimum, is never replaced, and +NaN, the
+//      maximum, is never the minimum): its weight makes the total NaN, the Runtime fault.  A
+//      NaN past the first k never enters.
+//   2. The row is sorted by total_cmp descending, equal keys by index (stable LSD radix sort;
+//      NaN past the first k last).
+//   3. Its first k entries hold the values of the reference's list in the reference's sorted
+//      order (the list always holds the k largest values of the prefix; with k == vocab the
+//      list is the row in index order and the stable sort is exactly the reference's).  The
+//      total, top-p prefix and threshold walk run as in draw_one, one lane walking chunks of
+//      weights that the other waves stage in LDS one chunk ahead.
+//   4. k < vocab and the drawn value shared with another logit (IEEE equality): equal values
+//      have equal weights, so only the token at the drawn position can differ, and the
+//      reference's replacement is replayed for it.  The list's first minimum (smallest key,
+//      then smallest slot) is kept in a three-level tree of minima (64 slots a block, 64
+//      blocks a superblock), so an insertion costs three wave reductions instead of a pass
+//      over the list.
+constexpr int kWalkChunk = 4096;                              // weights staged per walk step
+constexpr int kLargeMaxVocab = 1 << 20;                       // vocabularies the large path takes
+constexpr int kMaxWalkChunks = kLargeMaxVocab / kWalkChunk;   // also bounds the superblocks
+constexpr int kListLds = 16384;                               // replay list keys held in LDS up to this k
+constexpr int kSortBatch = 16;                                // 64-key groups a wave loads at once in the sort
+constexpr int kStageIters = (kWalkChunk + 447) / 448;         // staging loads per thread (at least 7 waves)
+constexpr int kIntMax = 0x7fffffff;
+
+constexpr size_t large_row_ints(int vocab) {
+  return 4 * static_cast<size_t>(vocab) + 2 * static_cast<size_t>((vocab + 63) / 64);
+}
+
+// total_cmp as an unsigned order, with NaN (which never enters the list past its first k
+// slots) below every logit.  Its complement is the sort key: ascending is total_cmp descending.
+__device__ __forceinline__ uint32_t select_key(float v) {
+  return v != v ? 0u : static_cast<uint32_t>(total_key(v)) ^ 0x80000000u;
+}
+
+__device__ __forceinline__ float sort_key_value(uint32_t u) {
+  return key_value(static_cast<int32_t>(~u ^ 0x80000000u));
+}
+
+// f(x, i) for every logit of the row, in no particular order (whole workgroup; 16 loads in
+// flight a thread).
+template <typename F>
+__device__ __forceinline__ void row_pass(const float* row, int vocab, int tid, F&& f) {
+  for (int i0 = 0; i0 < vocab; i0 += 16 * kThreads) {
+    float x[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) x[u] = row[min(i0 + u * kThreads + tid, vocab - 1)];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = i0 + u * kThreads + tid;
+      if (i < vocab) f(x[u], i);
+    }
+  }
+}
+
+// f(x, g0) over [beg, end) in order, kSortBatch groups of 64 logits at a time (lane l's x[u] is
+// logit g0 + 64 u + l, clamped into the range; f masks by index), the next batch's loads issued
+// before f runs (one wave).
+template <typename F>
+__device__ __forceinline__ void range_pass(const float* row, int beg, int end, int lane, F&& f) {
+  if (beg >= end) return;
+  const int last = end - 1;
+  float cur[kSortBatch];
+#pragma unroll
+  for (int u = 0; u < kSortBatch; ++u) cur[u] = row[min(beg + u * 64 + lane, last)];
+  for (int g0 = beg; g0 < end; g0 += kSortBatch * 64) {
+    float nxt[kSortBatch];
+    const int g1 = g0 + kSortBatch * 64;
+    if (g1 < end) {
+#pragma unroll
+      for (int u = 0; u < kSortBatch; ++u) nxt[u] = row[min(g1 + u * 64 + lane, last)];
+    }
+    f(cur, g0);
+#pragma unroll
+    for (int u = 0; u < kSortBatch; ++u) cur[u] = nxt[u];
+  }
+}
+
+struct LargeShared {
+  union {
+    struct {
+      int hist[kWaves][256];  // each wave's digit counts
+      int off[kWaves][256];   // then each wave's running output offset per digit
+      int tot[256];
+      int base[256];
+      int single;  // one digit holds every key: the pass is skipped
+    } sort;
+    struct {
+      alignas(16) float buf[2][kWalkChunk];
+    } walk;
+    struct {
+      int list_key[kListLds];
+      int bmin_key[kListLds / 64];
+      int bmin_slot[kListLds / 64];
+      int ckey[kWaves][kStep];  // each wave's step: logits above the published minimum
+      int cidx[kWaves][kStep];
+      int count[kWaves];
+    } replay;
+  } u;
+  float chunk_end[kMaxWalkChunks];  // the running weight sum at each chunk's end
+  int smin_key[kMaxWalkChunks];     // superblock minima
+  int smin_slot[kMaxWalkChunks];
+  int cnt_a[kThreads];  // replay result: members of the drawn value per thread's slot range
+  int cnt_b[kThreads];
+  int stop[2];
+  int flag;
+  int cut_chunk;  // the chunk where the top-p prefix reaches the cutoff, -1 for a NaN cutoff
+  int sel;
+  int retained;
+  int target;
+  int target_rank;
+  int target_prim;
+  float total;
+  float rtotal;
+  float wsel;
+  float cutoff;
+  float run;  // the total's running sum between chunks
+  float thr;  // the threshold walk's running value between chunks
+  float pub_min;
+};
+
+// Stable LSD radix sort of key/val[0, n) by unsigned key ascending, 8 bits a pass, between the
+// two array pairs (whole workgroup).  Each wave scatters a contiguous range in order, 64 keys
+// at a time: a key goes to its digit's running offset for the wave plus its rank among the
+// lanes holding the same digit.  A pass whose digit is the same for every key is skipped.
+// Returns true when the result is in the second pair.
+__device__ __forceinline__ bool radix_sort_u32(uint32_t* k0, int* v0, uint32_t* k1, int* v1, int n, LargeShared& sh,
+                                               int tid, int w, int lane) {
+  const int per = (n + kWaves - 1) / kWaves;
+  const int beg = min(n, w * per), end = min(n, beg + per);
+  bool in1 = false;
+  for (int shift = 0; shift < 32; shift += 8) {
+    const uint32_t* sk = in1 ? k1 : k0;
+    const int* sv = in1 ? v1 : v0;
+    uint32_t* dk = in1 ? k0 : k1;
+    int* dv = in1 ? v0 : v1;
+    for (int d = lane; d < 256; d += 64) sh.u.sort.hist[w][d] = 0;
+    wave_sync();
+    // batches of kSortBatch groups, the next batch's loads issued before this one is counted
+    // (addresses clamped into the range, so the loads need no branch)
+    const int last = max(end - 1, beg);
+    uint32_t kk[kSortBatch];
+    if (beg < end) {
+#pragma unroll
+      for (int u = 0; u < kSortBatch; ++u) kk[u] = sk[min(beg + u * 64 + lane, last)];
+    }
+    for (int g0 = beg; g0 < end; g0 += kSortBatch * 64) {
+      uint32_t nk[kSortBatch];
+      const int g1 = g0 + kSortBatch * 64;
+      if (g1 < end) {
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) nk[u] = sk[min(g1 + u * 64 + lane, last)];
+      }
+#pragma unroll
+      for (int u = 0; u < kSortBatch; ++u) {
+        if (g0 + u * 64 + lane < end) atomicAdd(&sh.u.sort.hist[w][(kk[u] >> shift) & 255u], 1);
+      }
+#pragma unroll
+      for (int u = 0; u < kSortBatch; ++u) kk[u] = nk[u];
+    }
+    __syncthreads();
+    if (tid < 256) {
+      int t = 0;
+      for (int q = 0; q < kWaves; ++q) {
+        const int h = sh.u.sort.hist[q][tid];
+        sh.u.sort.off[q][tid] = t;
+        t += h;
+      }
+      sh.u.sort.tot[tid] = t;
+    }
+    __syncthreads();
+    if (w == 0) {  // exclusive scan of the digit totals, four digits a lane
+      int c[4], s = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        c[q] = sh.u.sort.tot[4 * lane + q];
+        s += c[q];
+      }
+      int excl = wave_inclusive_sum(s) - s;
+      bool all = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sh.u.sort.base[4 * lane + q] = excl;
+        excl += c[q];
+        all = all || c[q] == n;
+      }
+      const bool single = __ballot(all) != 0;
+      if (lane == 0) sh.u.sort.single = single ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sh.u.sort.single) {
+      if (tid < 256) {
+        for (int q = 0; q < kWaves; ++q) sh.u.sort.off[q][tid] += sh.u.sort.base[tid];
+      }
+      __syncthreads();
+      uint32_t sk_cur[kSortBatch];
+      int sv_cur[kSortBatch];
+      if (beg < end) {
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) {
+          const int i = min(beg + u * 64 + lane, last);
+          sk_cur[u] = sk[i];
+          sv_cur[u] = sv[i];
+        }
+      }
+      for (int g0 = beg; g0 < end; g0 += kSortBatch * 64) {
+        uint32_t sk_nxt[kSortBatch];
+        int sv_nxt[kSortBatch];
+        const int g1 = g0 + kSortBatch * 64;
+        if (g1 < end) {
+#pragma unroll
+          for (int u = 0; u < kSortBatch; ++u) {
+            const int i = min(g1 + u * 64 + lane, last);
+            sk_nxt[u] = sk[i];
+            sv_nxt[u] = sv[i];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) {
+          const uint32_t key = sk_cur[u];
+          const bool in = g0 + u * 64 + lane < end;
+          const uint32_t d = (key >> shift) & 255u;
+          // the lanes holding the same digit: the AND over its 8 bits of the ballot of lanes
+          // agreeing on that bit (32-bit halves, one select each)
+          const uint64_t valid = __ballot(in);
+          uint32_t plo = static_cast<uint32_t>(valid), phi = static_cast<uint32_t>(valid >> 32);
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const bool bit = (d >> b) & 1u;
+            const uint64_t bb = __ballot(bit);
+            const uint32_t blo = static_cast<uint32_t>(bb), bhi = static_cast<uint32_t>(bb >> 32);
+            plo &= bit ? blo : ~blo;
+            phi &= bit ? bhi : ~bhi;
+          }
+          const uint64_t peers = (static_cast<uint64_t>(phi) << 32) | plo;
+          const int rank = lanes_below(peers);
+          const int cnt = __popcll(peers);
+          int* offp = &sh.u.sort.off[w][d];
+          const int at = in ? *offp : 0;
+          if (in) {
+            dk[at + rank] = key;
+            dv[at + rank] = sv_cur[u];
+          }
+          wave_sync();  // every lane has read its offset before the last of each digit moves it
+          if (in && rank == cnt - 1) *offp = at + cnt;
+          wave_sync();
+        }
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) {
+          sk_cur[u] = sk_nxt[u];
+          sv_cur[u] = sv_nxt[u];
+        }
+      }
+      in1 = !in1;
+    }
+    __syncthreads();
+  }
+  return in1;
+}
+
+// (key, slot) minimum over the wave, smaller slot among equal keys (the first minimum in list
+// order); every lane returns it.
+__device__ __forceinline__ void wave_min_pair(int& key, int& slot) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int ok = __shfl_xor(key, off, 64);
+    const int os = __shfl_xor(slot, off, 64);
+    if (ok < key || (ok == key && os < slot)) {
+      key = ok;
+      slot = os;
+    }
+  }
+}
+
+// The replay list's first minimum from the superblock minima (one wave; every lane returns it).
+__device__ __forceinline__ void tree_root(const LargeShared& sh, int nsb, int lane, int& gkey, int& gslot) {
+  gkey = kIntMax;
+  gslot = kIntMax;
+  for (int j = lane; j < nsb; j += 64) {
+    const int kk = sh.smin_key[j], ss = sh.smin_slot[j];
+    if (kk < gkey || (kk == gkey && ss < gslot)) {
+      gkey = kk;
+      gslot = ss;
+    }
+  }
+  wave_min_pair(gkey, gslot);
+}
+
+__device__ __forceinline__ void wg_sync_memory() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Runs f(buf, c, n) on thread 0 for chunks c0, c0 + 1, ... of the weights of sorted positions
+// [0, lim) (buf holds chunk c's n weights, zero to the chunk's end) until f returns true; the
+// waves other than wave 0 stage the next chunk meanwhile (whole workgroup).
+template <typename Weight, typename F>
+__device__ __forceinline__ void walk_chunks(LargeShared& sh, int c0, int lim, int tid, Weight&& weight, F&& f) {
+  const int nch = (lim + kWalkChunk - 1) / kWalkChunk;
+  auto stage = [&](int c, int t0, int nt) {
+    float* b = sh.u.walk.buf[c & 1];
+    float v[kStageIters];
+#pragma unroll
+    for (int m = 0; m < kStageIters; ++m) {
+      const int j = t0 + m * nt, q = c * kWalkChunk + j;
+      v[m] = (j < kWalkChunk && q < lim) ? weight.value(q) : 0.0f;
+    }
+#pragma unroll
+    for (int m = 0; m < kStageIters; ++m) {
+      const int j = t0 + m * nt, q = c * kWalkChunk + j;
+      if (j < kWalkChunk) b[j] = q < lim ? weight.of(v[m]) : 0.0f;
+    }
+  };
+  if (c0 < nch) stage(c0, tid, kThreads);
+  __syncthreads();
+  for (int c = c0; c < nch; ++c) {
+    if (tid >= 64 && c + 1 < nch) stage(c + 1, tid - 64, kThreads - 64);
+    if (tid == 0) sh.stop[c & 1] = f(sh.u.walk.buf[c & 1], c, min(kWalkChunk, lim - c * kWalkChunk)) ? 1 : 0;
+    __syncthreads();
+    if (sh.stop[c & 1]) break;  // two flags: thread 0 sets the next while late waves read this one
+  }
+  __syncthreads();
+}
+
+// s + a.x + a.y + a.z + a.w and s - a.x - a.y - a.z - a.w, one rounding at a time in order.
+__device__ __forceinline__ float add4(float s, float4 a) {
+  s = s + a.x;
+  s = s + a.y;
+  s = s + a.z;
+  return s + a.w;
+}
+
+__device__ __forceinline__ float sub4(float s, float4 a) {
+  s = s - a.x;
+  s = s - a.y;
+  s = s - a.z;
+  return s - a.w;
+}
+
+// exp(l / T - l0 / T) of a sorted position, as the reference forms it (sampler.rs:184-188).
+struct SortedWeight {
+  const uint32_t* keys;
+  float temp;
+  float scaled_max;
+  __device__ float value(int q) const { return sort_key_value(keys[q]); }
+  __device__ float of(float v) const { return expf((v / temp) - scaled_max); }
+};
+
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void sample_large_kernel(const float* __restrict__ logits, int ld, int vocab,
+                                                                const float* __restrict__ temperature,
+                                                                const int32_t* __restrict__ top_k,
+                                                                const float* __restrict__ top_p,
+                                                                uint64_t* __restrict__ rng, int* __restrict__ area,
+                                                                int32_t* __restrict__ token, float* __restrict__ prob,
+                                                                uint32_t* __restrict__ faults) {
+#pragma clang fp contract(off)
+  __shared__ LargeShared sh;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float T = temperature[r];
+  const int K = top_k[r];
+  const float P = top_p[r];
+  if (greedy_row(T, K, P)) return;
+  const int k = min(max(K, 1), vocab);  // top_k.max(1).min(vocab_size)
+  if (k <= kMaxTopK) return;            // the scan / finish kernels' row
+  const float* row = logits + (size_t)r * ld;
+  int* base = area + r * large_row_ints(vocab);
+  uint32_t* key0 = reinterpret_cast<uint32_t*>(base);
+  int* idx0 = base + vocab;
+  uint32_t* key1 = reinterpret_cast<uint32_t*>(base + 2 * static_cast<size_t>(vocab));
+  int* idx1 = base + 3 * static_cast<size_t>(vocab);
+  int* aux = base + 4 * static_cast<size_t>(vocab);
+
+  // ---- 1. candidates in index order: every logit when k == vocab, else those at or above the
+  // k+1-th largest (a NaN past the first k counts as below every logit); a NaN among the
+  // first k faults the row ----
+  if (tid < 256) sh.u.sort.tot[tid] = 0;
+  if (tid == 0) sh.flag = 0;
+  __syncthreads();
+  bool nan_early = false;
+  row_pass(row, vocab, tid, [&](float x, int i) {
+    nan_early = nan_early || (x != x && i < k);
+    if (k < vocab) atomicAdd(&sh.u.sort.tot[select_key(x) >> 24], 1);
+  });
+  if (nan_early) sh.flag = 1;
+  __syncthreads();
+  if (sh.flag) {
+    if (tid == 0) sampling_fault(faults, FI_FAULT_SAMPLE_NONFINITE, token, prob, r);
+    return;
+  }
+  uint32_t bound = 0;  // select_key of the k+1-th largest
+  if (k < vocab) {
+    uint32_t prefix = 0, mask = 0;
+    int want = k;
+    for (int d = 24; d >= 0; d -= 8) {
+      if (d < 24) {  // the first digit's counts came with the NaN check
+        if (tid < 256) sh.u.sort.tot[tid] = 0;
+        __syncthreads();
+        row_pass(row, vocab, tid, [&](float x, int) {
+          const uint32_t u = select_key(x);
+          if ((u & mask) == prefix) atomicAdd(&sh.u.sort.tot[(u >> d) & 255u], 1);
+        });
+        __syncthreads();
+      }
+      if (w == 0) {
+        const int digit = pick_digit_desc(sh.u.sort.tot, lane, want);
+        if (lane == 0) {
+          sh.target = digit;
+          sh.target_rank = want;
+        }
+      }
+      __syncthreads();
+      prefix |= static_cast<uint32_t>(sh.target) << d;
+      mask |= 255u << d;
+      want = sh.target_rank;
+      __syncthreads();
+    }
+    bound = prefix;
+  }
+  // each wave compacts its contiguous range in index order at its offset: counts, then copies
+  const int span = ((vocab + kWaves - 1) / kWaves + 63) / 64 * 64;
+  const int beg = min(vocab, w * span), end = min(vocab, beg + span);
+  int mine = 0;
+  range_pass(row, beg, end, lane, [&](const float* x, int g0) {
+#pragma unroll
+    for (int u = 0; u < kSortBatch; ++u) {
+      mine += __popcll(__ballot(g0 + u * 64 + lane < end && select_key(x[u]) >= bound));
+    }
+  });
+  if (lane == 0) sh.cnt_a[w] = mine;
+  __syncthreads();
+  int at = 0, m = 0;
+  for (int q = 0; q < kWaves; ++q) {
+    at += q < w ? sh.cnt_a[q] : 0;
+    m += sh.cnt_a[q];
+  }
+  range_pass(row, beg, end, lane, [&](const float* x, int g0) {
+#pragma unroll
+    for (int u = 0; u < kSortBatch; ++u) {
+      const int i = g0 + u * 64 + lane;
+      const bool keep = i < end && select_key(x[u]) >= bound;
+      const uint64_t b = __ballot(keep);
+      if (keep) {
+        const int pos = at + lanes_below(b);
+        key0[pos] = ~select_key(x[u]);  // ascending = total_cmp descending; NaN last
+        idx0[pos] = i;
+      }
+      at += __popcll(b);
+    }
+  });
+  __syncthreads();
+
+  // ---- 2. sort ----
+  const bool in1 = radix_sort_u32(key0, idx0, key1, idx1, m, sh, tid, w, lane);
+  const uint32_t* sk = in1 ? key1 : key0;
+  const int* si = in1 ? idx1 : idx0;
+  int* free_key = reinterpret_cast<int*>(in1 ? key0 : key1);
+  int* free_idx = in1 ? idx0 : idx1;
+
+  // ---- 3. total, top-p, draw (sampler.rs:184-233) ----
+  const float temp = fmaxf(T, 1.1920929e-7f);  // max(f32::EPSILON); a NaN temperature gives EPSILON
+  const SortedWeight wt{sk, temp, sort_key_value(sk[0]) / temp};
+  // thread 0's running sums live in LDS between chunks (sh.run, sh.thr) and in a register
+  // within one
+  if (tid == 0) sh.run = 0.0f;
+  walk_chunks(sh, 0, k, tid, wt, [&](const float* b, int c, int n) {
+    // blocks of 64 weights: the block's 16 LDS reads issued together, so their latency is paid
+    // once per 64 dependent additions (the chunk is zero-padded: + 0.0f leaves a sum >= +0
+    // unchanged)
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    float s = sh.run;
+    for (int q = 0; q < n; q += 64) {
+      float4 x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = b4[q / 4 + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s = add4(s, x[u]);
+    }
+    sh.run = s;
+    sh.chunk_end[c] = s;
+    return false;
+  });
+  if (tid == 0) {
+    const float total = sh.run;
+    sh.total = total;
+    sh.flag = (!(total <= 3.402823466e+38f) || total <= 0.0f) ? 1 : 0;  // not finite, or no mass
+    if (sh.flag) {
+      sampling_fault(faults, FI_FAULT_SAMPLE_NONFINITE, token, prob, r);
+    } else {
+      float p = P;  // f32::clamp(0, 1): a NaN stays NaN
+      if (p < 0.0f) p = 0.0f;
+      if (p > 1.0f) p = 1.0f;
+      const float cutoff = p >= 1.0f ? total : total * p;
+      sh.cutoff = cutoff;
+      sh.retained = k;  // a NaN cutoff is never reached: every candidate is kept
+      sh.rtotal = total;
+      sh.cut_chunk = -1;
+      if (cutoff == cutoff) {
+        int c = 0;  // the first chunk whose running sum reaches the cutoff (total >= cutoff)
+        while (sh.chunk_end[c] < cutoff) ++c;
+        sh.cut_chunk = c;
+      }
+    }
+  }
+  __syncthreads();
+  if (sh.flag) return;
+  if (sh.cut_chunk >= 0) {
+    // the top-p loop's running sum is the total's (same additions, same order), so the walk
+    // restarts at the crossing chunk from the sum at its start
+    const int cc = sh.cut_chunk;
+    const float cutoff = sh.cutoff;
+    walk_chunks(sh, cc, k, tid, wt, [&](const float* b, int c, int n) {
+      // the running sum never falls, so a block of 32 whose last sum is below the cutoff holds
+      // no crossing; the first block that reaches it is walked again one weight at a time
+      float s = c > 0 ? sh.chunk_end[c - 1] : 0.0f;
+      for (int q = 0; q < n; q += 32) {
+        float e = s;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) e = e + b[q + j];
+        if (e >= cutoff) {
+          for (int j = 0; j < 32; ++j) {
+            s = s + b[q + j];
+            if (s >= cutoff) {
+              sh.retained = c * kWalkChunk + q + j + 1;
+              sh.rtotal = s;
+              break;
+            }
+          }
+          break;
+        }
+        s = e;
+      }
+      return true;
+    });
+  }
+  if (tid == 0) {
+    sh.thr = next_draw(rng, r) * sh.rtotal;
+    sh.sel = 0;
+    sh.wsel = wt.of(wt.value(0));
+  }
+  walk_chunks(sh, 0, sh.retained, tid, wt, [&](const float* b, int c, int n) {
+    // the threshold never rises, so a block of 64 whose last value is above zero holds no hit;
+    // the first block that reaches zero is walked again one weight at a time (weights past the
+    // retained ones are zero-padded and leave the threshold as it is)
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    float t = sh.thr;
+    int at = -1;  // the first block of 64 that brings the threshold to zero
+    for (int q = 0; q < n; q += 64) {
+      float4 x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = b4[q / 4 + u];
+      float e = t;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) e = sub4(e, x[u]);
+      if (e <= 0.0f) {
+        at = q;
+        break;
+      }
+      t = e;
+    }
+    if (at >= 0) {  // walked again one weight at a time from the block's start
+      for (int j = 0; j < 64; ++j) {
+        t = t - b[at + j];
+        if (t <= 0.0f) {
+          sh.sel = c * kWalkChunk + at + j;
+          sh.wsel = b[at + j];
+          break;
+        }
+      }
+    }
+    sh.thr = t;
+    return at >= 0;
+  });
+  const int sel = sh.sel;
+  const float vsel = sort_key_value(sk[sel]);
+  if (tid == 0) {
+    prob[r] = sh.wsel / sh.rtotal;
+    const bool tie = k < vocab && ((sel > 0 && sort_key_value(sk[sel - 1]) == vsel) ||
+                                   (sel + 1 < m && sort_key_value(sk[sel + 1]) == vsel));
+    sh.flag = tie ? 1 : 0;
+    if (tie) {
+      int lo = 0, hi = sel;  // the drawn value's first sorted position: everything before is larger
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sort_key_value(sk[mid]) > vsel) {
+          lo = mid + 1;
+        } else {
+          hi = mid;
+        }
+      }
+      sh.target_rank = sel - lo;
+    } else {
+      token[r] = si[sel];
+    }
+  }
+  __syncthreads();
+  if (!sh.flag) return;
+
+  // ---- 4. replay of the replacement (sampler.rs:157-171) for the drawn value's order ----
+  const bool in_lds = k <= kListLds;
+  const int nb = (k + 63) / 64, nsb = (nb + 63) / 64;
+  int* lkey = in_lds ? sh.u.replay.list_key : free_key;
+  int* lidx = free_idx;
+  int* bkey = in_lds ? sh.u.replay.bmin_key : aux;
+  int* bslot = in_lds ? sh.u.replay.bmin_slot : aux + (vocab + 63) / 64;
+  for (int p = tid; p < k; p += kThreads) {
+    lkey[p] = total_key(row[p]);
+    lidx[p] = p;
+  }
+  __syncthreads();
+  for (int b = w; b < nb; b += kWaves) {
+    const int slot = b * 64 + lane;
+    int kk = slot < k ? lkey[slot] : kIntMax, ss = slot;
+    wave_min_pair(kk, ss);
+    if (lane == 0) {
+      bkey[b] = kk;
+      bslot[b] = ss;
+    }
+  }
+  __syncthreads();
+  for (int q = w; q < nsb; q += kWaves) {
+    const int j = q * 64 + lane;
+    int kk = j < nb ? bkey[j] : kIntMax, ss = j < nb ? bslot[j] : kIntMax;
+    wave_min_pair(kk, ss);
+    if (lane == 0) {
+      sh.smin_key[q] = kk;
+      sh.smin_slot[q] = ss;
+    }
+  }
+  __syncthreads();
+  int gkey = kIntMax, gslot = kIntMax;  // wave 0: the list's first minimum
+  float min_val = 0.0f;
+  if (w == 0) {
+    tree_root(sh, nsb, lane, gkey, gslot);
+    min_val = key_value(gkey);
+    if (lane == 0) sh.pub_min = min_val;
+  }
+  __syncthreads();
+  const int nsteps = (vocab + kStep - 1) / kStep;
+  for (int r0 = k / kStep; r0 < nsteps; r0 += kWaves) {
+    // each wave keeps the logits of its step above the published minimum, in index order
+    const int s = r0 + w;
+    float v[kPerLane];
+    load_step<VEC>(row, vocab, min(s, nsteps - 1), lane, v);
+    const float bound = sh.pub_min;
+    int cnt = 0;
+#pragma unroll
+    for (int g = 0; g < kPerLane / VEC; ++g) {
+      uint64_t bl[VEC];
+      int before_lane = 0;
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) {
+        const int i = step_index<VEC>(s, lane, g * VEC + u);
+        bl[u] = __ballot(i >= k && i < vocab && v[g * VEC + u] > bound);
+        before_lane += lanes_below(bl[u]);
+      }
+      int within = 0;
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) {
+        if ((bl[u] >> lane) & 1) {
+          const int pos = cnt + before_lane + within;
+          sh.u.replay.ckey[w][pos] = __float_as_int(v[g * VEC + u]);
+          sh.u.replay.cidx[w][pos] = step_index<VEC>(s, lane, g * VEC + u);
+          ++within;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) cnt += __popcll(bl[u]);
+    }
+    if (lane == 0) sh.u.replay.count[w] = cnt;
+    __syncthreads();
+    if (w == 0) {
+      for (int q = 0; q < kWaves; ++q) {
+        const int c = sh.u.replay.count[q];
+        for (int base_i = 0; base_i < c; base_i += 64) {
+          const int i = base_i + lane;
+          const bool in = i < c;
+          const float x = in ? __int_as_float(sh.u.replay.ckey[q][i]) : 0.0f;
+          const int id = in ? sh.u.replay.cidx[q][i] : 0;
+          uint64_t ball = __ballot(in && x > min_val);
+          while (ball) {  // wave-uniform, in index order
+            const int j = __builtin_ctzll(ball);
+            ball &= ball - 1;
+            const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+            if (!(xj > min_val)) continue;
+            // the logit replaces the first minimum; its block, superblock and the root follow
+            const int slot = gslot, b = slot >> 6, sb = b >> 6;
+            if (lane == 0) {
+              lkey[slot] = total_key(xj);
+              lidx[slot] = __builtin_amdgcn_readlane(id, j);
+            }
+            wg_sync_memory();
+            int kk = b * 64 + lane < k ? lkey[b * 64 + lane] : kIntMax, ss = b * 64 + lane;
+            wave_min_pair(kk, ss);
+            if (lane == 0) {
+              bkey[b] = kk;
+              bslot[b] = ss;
+            }
+            wg_sync_memory();
+            const int jb = sb * 64 + lane;
+            kk = jb < nb ? bkey[jb] : kIntMax;
+            ss = jb < nb ? bslot[jb] : kIntMax;
+            wave_min_pair(kk, ss);
+            if (lane == 0) {
+              sh.smin_key[sb] = kk;
+              sh.smin_slot[sb] = ss;
+            }
+            wg_sync_memory();
+            tree_root(sh, nsb, lane, gkey, gslot);
+            min_val = key_value(gkey);
+          }
+        }
+      }
+      if (lane == 0) sh.pub_min = min_val;
+    }
+    __syncthreads();
+  }
+
+  // The drawn value's entries of the final list, in the stable sort's order (total_cmp
+  // descending, then slot): one key, or for zero +0 then -0.  The token is the one of rank
+  // target_rank.
+  const bool zero = vsel == 0.0f;
+  const int kp = zero ? 0 : total_key(vsel);  // total_key(+0.0f) == 0, total_key(-0.0f) == -1
+  const int per = (k + kThreads - 1) / kThreads;
+  const int p0 = min(k, tid * per), p1 = min(k, p0 + per);
+  int ca = 0, cb = 0;
+  for (int p = p0; p < p1; ++p) {
+    const int kk = lkey[p];
+    ca += kk == kp;
+    cb += zero && kk == -1;
+  }
+  sh.cnt_a[tid] = ca;
+  sh.cnt_b[tid] = cb;
+  __syncthreads();
+  if (tid == 0) {
+    int na = 0;
+    for (int t = 0; t < kThreads; ++t) na += sh.cnt_a[t];
+    int want = sh.target_rank;
+    const bool prim = want < na;
+    if (!prim) want -= na;
+    int t = 0;
+    for (; t < kThreads; ++t) {
+      const int c = prim ? sh.cnt_a[t] : sh.cnt_b[t];
+      if (want < c) break;
+      want -= c;
+    }
+    sh.target = t;
+    sh.target_rank = want;
+    sh.target_prim = prim ? 1 : 0;
+    if (t == kThreads) token[r] = si[sel];  // not reached: the list holds the drawn value
+  }
+  __syncthreads();
+  if (tid == sh.target) {
+    const int want_key = sh.target_prim ? kp : -1;
+    int want = sh.target_rank;
+    for (int p = p0; p < p1; ++p) {
+      if (lkey[p] == want_key) {
+        if (want == 0) {
+          token[r] = lidx[p];
+          break;
+        }
+        --want;
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -1138,38 +1960,74 @@ int32_t fi_sample_tokens(fi_context* ctx, const float* d_logits, int32_t ld, int
   const int segs = std::max(1, std::min({kMaxSegs, nsteps / 4, fill}));
   const int seg_steps = (nsteps + segs - 1) / segs;
   const bool vec4 = vocab % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(d_logits) % 16 == 0;
+  // rows with top-k above 1024 go to sample_large_kernel when the reserved area covers the call
+  const bool large = ctx->sample_area != nullptr && vocab <= kLargeMaxVocab &&
+                     static_cast<size_t>(rows) * large_row_ints(vocab) * sizeof(int) <= ctx->sample_bytes;
+  const int large_arg = large ? 1 : 0;
   if (segs == 1) {
     if (vec4) {
       hipLaunchKernelGGL(sample_row_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
-                         d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+                         d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults, large_arg);
     } else {
       hipLaunchKernelGGL(sample_row_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
-                         d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults);
+                         d_temperature, d_top_k, d_top_p, d_rng_state, d_token, d_prob, ctx->d_faults, large_arg);
     }
     FI_CHECK_LAUNCH("sample_row_kernel");
-    return FI_OK;
-  }
-  const size_t meta_bytes = ((size_t)rows * segs * sizeof(ScanMeta) + 255) / 256 * 256;
-  const size_t cand_bytes = (size_t)rows * segs * kRegion * sizeof(int);
-  FI_TRY(fi::ensure_workspace(ctx, meta_bytes + 2 * cand_bytes));
-  ScanMeta* meta = static_cast<ScanMeta*>(ctx->workspace);
-  int* cand_key = reinterpret_cast<int*>(static_cast<char*>(ctx->workspace) + meta_bytes);
-  int* cand_idx = reinterpret_cast<int*>(static_cast<char*>(ctx->workspace) + meta_bytes + cand_bytes);
-  const dim3 scan_grid(static_cast<unsigned>(segs), static_cast<unsigned>(rows));
-  if (vec4) {
-    hipLaunchKernelGGL(sample_scan_kernel<4>, scan_grid, dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
-                       seg_steps, d_temperature, d_top_k, d_top_p, meta, cand_key, cand_idx);
-    hipLaunchKernelGGL(sample_finish_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
-                       d_temperature, d_top_k, d_top_p, d_rng_state, meta, cand_key, cand_idx, d_token, d_prob,
-                       ctx->d_faults);
   } else {
-    hipLaunchKernelGGL(sample_scan_kernel<1>, scan_grid, dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
-                       seg_steps, d_temperature, d_top_k, d_top_p, meta, cand_key, cand_idx);
-    hipLaunchKernelGGL(sample_finish_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
-                       d_temperature, d_top_k, d_top_p, d_rng_state, meta, cand_key, cand_idx, d_token, d_prob,
-                       ctx->d_faults);
+    const size_t meta_bytes = ((size_t)rows * segs * sizeof(ScanMeta) + 255) / 256 * 256;
+    const size_t cand_bytes = (size_t)rows * segs * kRegion * sizeof(int);
+    FI_TRY(fi::ensure_workspace(ctx, meta_bytes + 2 * cand_bytes));
+    ScanMeta* meta = static_cast<ScanMeta*>(ctx->workspace);
+    int* cand_key = reinterpret_cast<int*>(static_cast<char*>(ctx->workspace) + meta_bytes);
+    int* cand_idx = reinterpret_cast<int*>(static_cast<char*>(ctx->workspace) + meta_bytes + cand_bytes);
+    const dim3 scan_grid(static_cast<unsigned>(segs), static_cast<unsigned>(rows));
+    if (vec4) {
+      hipLaunchKernelGGL(sample_scan_kernel<4>, scan_grid, dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
+                         seg_steps, d_temperature, d_top_k, d_top_p, meta, cand_key, cand_idx);
+      hipLaunchKernelGGL(sample_finish_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                         segs, d_temperature, d_top_k, d_top_p, d_rng_state, meta, cand_key, cand_idx, d_token, d_prob,
+                         ctx->d_faults, large_arg);
+    } else {
+      hipLaunchKernelGGL(sample_scan_kernel<1>, scan_grid, dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab, segs,
+                         seg_steps, d_temperature, d_top_k, d_top_p, meta, cand_key, cand_idx);
+      hipLaunchKernelGGL(sample_finish_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                         segs, d_temperature, d_top_k, d_top_p, d_rng_state, meta, cand_key, cand_idx, d_token, d_prob,
+                         ctx->d_faults, large_arg);
+    }
+    FI_CHECK_LAUNCH("sample_finish_kernel");
   }
-  FI_CHECK_LAUNCH("sample_finish_kernel");
+  if (large) {
+    int* area = static_cast<int*>(ctx->sample_area);
+    if (vec4) {
+      hipLaunchKernelGGL(sample_large_kernel<4>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                         d_temperature, d_top_k, d_top_p, d_rng_state, area, d_token, d_prob, ctx->d_faults);
+    } else {
+      hipLaunchKernelGGL(sample_large_kernel<1>, dim3(rows), dim3(kThreads), 0, ctx->stream, d_logits, ld, vocab,
+                         d_temperature, d_top_k, d_top_p, d_rng_state, area, d_token, d_prob, ctx->d_faults);
+    }
+    FI_CHECK_LAUNCH("sample_large_kernel");
+  }
+  return FI_OK;
+}
+
+int32_t fi_sample_reserve(fi_context* ctx, int32_t rows, int32_t vocab) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(rows >= 0 && rows <= 65535 && vocab >= 0, FI_ERR_INVALID_SHAPE,
+             "fi_sample_reserve: rows must be in [0, 65535] and vocab non-negative");
+  FI_REQUIRE(vocab <= kLargeMaxVocab, FI_ERR_UNSUPPORTED,
+             "fi_sample_reserve: top-k above 1024 is served for vocabularies of at most 1048576 logits");
+  const size_t bytes = static_cast<size_t>(rows) * large_row_ints(vocab) * sizeof(int);
+  if (bytes == 0 || bytes <= ctx->sample_bytes) return FI_OK;
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_sample_reserve: cannot allocate during graph capture");
+  if (ctx->sample_area != nullptr) {
+    FI_TRY_HIP(hipStreamSynchronize(ctx->stream));  // queued sampling may still read the old area
+    FI_TRY_HIP(hipFree(ctx->sample_area));
+    ctx->sample_area = nullptr;
+    ctx->sample_bytes = 0;
+  }
+  FI_TRY_HIP(hipMalloc(&ctx->sample_area, bytes));
+  ctx->sample_bytes = bytes;
+  ctx->workspace_generation += 1;  // graphs captured before hold the old launch sequence
   return FI_OK;
 }
 

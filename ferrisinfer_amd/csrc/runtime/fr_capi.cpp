@@ -76,8 +76,10 @@ int32_t fr_create(int32_t ordinal, const fr_model_config* mc, const fr_runtime_c
     r->session.sampler.top_p = rc->top_p;
     r->session.sampler.repetition_penalty = rc->repetition_penalty;
     r->session.sampler.seed = rc->seed;
-    if (!r->session.sampler.is_greedy() && std::min<int64_t>(std::max<int64_t>(rc->top_k, 1), mc->vocab_size) > 1024) {
-      fr::fail(fr::ErrorKind::Unsupported, "sampler top_k above 1024 is not supported by the device sampler");
+    if (!r->session.sampler.is_greedy() && std::min<int64_t>(std::max<int64_t>(rc->top_k, 1), mc->vocab_size) > 1024 &&
+        mc->vocab_size > (1 << 20)) {
+      fr::fail(fr::ErrorKind::Unsupported,
+               "sampler top_k above 1024 is served for vocabularies of at most 1048576 logits");
     }
     r->sched.max_batch_size = rc->max_batch_size;
     r->sched.max_prefill_chunk_tokens = rc->max_prefill_chunk_tokens;

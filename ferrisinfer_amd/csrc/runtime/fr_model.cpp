@@ -542,6 +542,11 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
     }
     grow(samp_, cfg.size());
     check(fi_buf_upload(ctx_, samp_.get(), cfg.size(), cfg.data(), cfg.size()));
+    // top_k above 1024 (after clamping to the vocabulary) samples from a reserved area; a
+    // reallocation bumps the workspace generation, which drops the captured graphs below
+    if (std::min<int64_t>(std::max<int64_t>(sampler.top_k, 1), c.vocab_size) > 1024) {
+      check(fi_sample_reserve(ctx_, B, c.vocab_size));
+    }
   }
 
   if (use_graph) {

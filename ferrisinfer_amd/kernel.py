@@ -97,6 +97,7 @@ _SIGNATURES = {
     "fi_splitk_residual_rms_norm_bf16": [_P, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32, _F32],
     "fi_convert_f32_to_bf16": [_P, _P, C.c_int64, _P],
     "fi_sample_tokens": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
+    "fi_sample_reserve": [_P, _I32, _I32],
 }
 _RESTYPES = {"fi_ctx_stream": _P, "fi_last_error": C.c_char_p}
 
@@ -484,6 +485,11 @@ class Context:
         check(self.lib.fi_sample_tokens(self.handle, ptr(logits), int(logits.stride(0)), int(rows),
                                         int(vocab), ptr(temperature), ptr(top_k), ptr(top_p),
                                         ptr(rng_state), ptr(token_out), ptr(prob_out)))
+
+    def sample_reserve(self, rows, vocab):
+        """Room for sample_tokens to serve top_k above 1024 (up to the vocabulary) in calls of
+        up to `rows` rows of `vocab` logits."""
+        check(self.lib.fi_sample_reserve(self.handle, int(rows), int(vocab)))
 
     def convert_to_f32(self, src, src_dtype, rows, cols, transpose, dst):
         """dst (f32) = the widening of src, a [rows, cols] row-major tensor of src_dtype

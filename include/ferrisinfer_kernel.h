@@ -456,14 +456,24 @@ int32_t fi_convert_f32_to_bf16(fi_context* ctx, const float* d_src, int64_t n, u
  * from [seq_len, vocab]); d_rng_state[r] is row r's SamplerState (sampler.rs:51-75; seed 0 maps
  * to 0x9e3779b97f4a7c15 when the state is created), advanced by one draw for a sampled row and
  * left as it is for a greedy row.  Writes the token id and its probability (weight / retained
- * total, or 1 / sum exp(l - max) when greedy).  top_k below 1 counts as 1 (usize::max(1)); a
- * top_k that stays above 1024 after clamping to the vocabulary, and a distribution whose total
- * weight is not finite and positive (sampler.rs:195-200, Runtime), write token -1 and are
- * reported as Runtime by the next fi_ctx_check_faults().  Probabilities may differ from the
- * host's in the last bits (device expf); tokens are the reference's. */
+ * total, or 1 / sum exp(l - max) when greedy).  top_k below 1 counts as 1 (usize::max(1)).  A
+ * top_k above 1024 after clamping to the vocabulary is served, up to the whole vocabulary, when
+ * fi_sample_reserve has set aside room for at least this call's rows and vocab; otherwise such
+ * a row, like a distribution whose total weight is not finite and positive
+ * (sampler.rs:195-200, Runtime), writes token -1 and is reported as Runtime by the next
+ * fi_ctx_check_faults().  Probabilities may differ from the host's in the last bits (device
+ * expf); tokens are the reference's. */
 int32_t fi_sample_tokens(fi_context* ctx, const float* d_logits, int32_t ld, int32_t rows, int32_t vocab,
                          const float* d_temperature, const int32_t* d_top_k, const float* d_top_p,
                          uint64_t* d_rng_state, int32_t* d_token, float* d_prob);
+
+/* Sets aside device memory (about 16 bytes per logit per row; grow-only, freed with the
+ * context) so that fi_sample_tokens serves rows whose clamped top_k exceeds 1024 in calls of
+ * up to `rows` rows of `vocab` logits (vocab at most 1048576, else Unsupported).  The same
+ * top_k field of SamplerConfig (runtime/sampler.rs:3-10, 152-172) is taken up to the
+ * vocabulary by the reference; device-side configurations need the room reserved on the host
+ * beforehand.  Not during graph capture; a reallocation bumps fi_ctx_workspace_generation. */
+int32_t fi_sample_reserve(fi_context* ctx, int32_t rows, int32_t vocab);
 
 /* ---------------------------------------------------------------- checkpoint import
  * d_dst = the f32 widening of d_src, a [rows, cols] row-major tensor of src_dtype (FI_DTYPE_F32,

@@ -114,10 +114,11 @@ def test_graph_decode_across_context_buckets(orc):
     compare(model, ref, make_runtime(cfg, weights, True, kw), requests)
 
 
-@pytest.mark.parametrize("sampler", [(0.8, 20, 0.9, 42)])
+@pytest.mark.parametrize("sampler", [(0.8, 20, 0.9, 42), (0.9, 3000, 0.95, 7)])
 def test_graph_decode_sampled_matches_eager(orc, sampler):
     """The device sampler inside the replayed tick: per-row states are uploaded before and read
-    back after every replay; tokens, probabilities and the tick log equal the eager run's."""
+    back after every replay; tokens, probabilities and the tick log equal the eager run's.  Top-k
+    3000 puts the reserved-area sampling launch in the graphs."""
     from ferrisinfer_amd.workloads import TINY_LLAMA_C1, c1_requests, random_weights
 
     print(f"graph decode sampled {sampler}", flush=True)

@@ -59,7 +59,8 @@ def is_greedy(t, k, p):
 
 def check_rows(orc, logits, configs, states, tok, prob, new_states, label):
     """Tokens and states exact.  Sampled rows: the probability within 1e-5 relative (both sides
-    sum at most 1024 weights in the same order).  Greedy rows: the reference sums all `vocab`
+    sum the same weights in the same order; a weight may differ in its last bit, device expf
+    against the host's).  Greedy rows: the reference sums all `vocab`
     exponentials one after another in f32, the device in a tree, so the device value is held to
     1e-5 of the exact (f64) 1 / sum exp(l - max) and the oracle's to the recursive-summation
     bound (vocab - 1) * 2^-24 of it."""
@@ -193,26 +194,118 @@ def test_sample_tokens_nan_logits(orc, gpu_ctx):
     gpu_ctx.check_faults()  # cleared by the previous check
 
 
-def test_sample_tokens_top_k_above_device_limit(orc, gpu_ctx):
-    """top_k above 1024 (after clamping to the vocabulary) is reported; one that clamps to a
-    vocabulary of at most 1024 is sampled."""
+def test_sample_tokens_top_k_above_1024_needs_reservation(orc):
+    """On a fresh context, top_k above 1024 (after clamping to the vocabulary) is reported until
+    fi_sample_reserve covers the call's rows and vocabulary, then sampled as the oracle does; a
+    top_k that clamps to a vocabulary of at most 1024 needs no reservation; a vocabulary above
+    2^20 cannot be reserved."""
+    from ferrisinfer_amd import Context, FerrisError
+
+    print("sample top_k reservation", flush=True)
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(6)
+        logits = rng.standard_normal((2, 2000)).astype(np.float32)
+        configs = [(0.8, 1500, 0.9), (0.8, 20, 0.9)]
+        states = [orc.sampler_state_new(7), orc.sampler_state_new(8)]
+        tok, _, new_states = run_device(ctx, padded_logits(logits, 0), configs, states)
+        assert tok[0] == -1 and new_states[0] == states[0]
+        assert tok[1] == orc.sample_last_token(logits[1], *configs[1], states[1])[0]
+        with pytest.raises(FerrisError, match="top_k"):
+            ctx.check_faults()
+        ctx.sample_reserve(1, 2000)  # one row: the two-row call is still not covered
+        tok, _, new_states = run_device(ctx, padded_logits(logits, 0), configs, states)
+        assert tok[0] == -1 and new_states[0] == states[0]
+        with pytest.raises(FerrisError, match="top_k"):
+            ctx.check_faults()
+        ctx.sample_reserve(2, 2000)
+        tok, prob, new_states = run_device(ctx, padded_logits(logits, 0), configs, states)
+        ctx.check_faults()
+        check_rows(orc, logits, configs, states, tok, prob, new_states, "reserved")
+        small = rng.standard_normal((1, 900)).astype(np.float32)
+        st = [orc.sampler_state_new(9)]
+        tok, prob, new_states = run_device(ctx, padded_logits(small, 0), [(0.8, 1500, 0.9)], st)
+        ctx.check_faults()
+        check_rows(orc, small, [(0.8, 1500, 0.9)], st, tok, prob, new_states, "clamped")
+        with pytest.raises(FerrisError, match="Unsupported"):
+            ctx.sample_reserve(1, (1 << 20) + 1)
+    finally:
+        ctx.close()
+
+
+# (vocab, top_k values): the C4 vocabulary with a k just above the fast path's limit, one
+# close to the vocabulary (the reference's replacement then runs over few logits) and the whole
+# vocabulary (no replacement: the stable sort alone); a 32000 vocabulary with a scalar-load
+# twin (32003) at mid-size k.
+LARGE_K = [(151936, (2000, 150000, 151936)), (32000, (1025, 16000, 32000)), (32003, (4000, 31999))]
+
+
+@pytest.mark.parametrize("vocab,ks", LARGE_K)
+def test_sample_tokens_large_top_k_match_oracle(orc, gpu_ctx, vocab, ks):
+    """top_k in (1024, vocab]: tokens and states exact against the oracle's replacement and
+    stable sort, over two consecutive calls carrying the states, at two temperatures and three
+    top-p values (NaN keeps every candidate)."""
+    print(f"sample large top_k vocab={vocab} ks={ks}", flush=True)
+    rng = np.random.default_rng(vocab)
+    configs = [(t, k, p) for k in ks for (t, p) in ((0.7, 0.9), (1.3, 1.0), (1.0, NAN))]
+    gpu_ctx.sample_reserve(len(configs), vocab)
+    states = [orc.sampler_state_new(50 + i) for i in range(len(configs))]
+    for call in range(2):
+        logits = (rng.standard_normal((len(configs), vocab)) * (1.0 + call)).astype(np.float32)
+        tok, prob, new_states = run_device(gpu_ctx, padded_logits(logits, 0), configs, states)
+        gpu_ctx.check_faults()
+        check_rows(orc, logits, configs, states, tok, prob, new_states, f"call {call}")
+        states = new_states
+
+
+@pytest.mark.parametrize("vocab", [4096, 32000])
+def test_sample_tokens_large_top_k_ties(orc, gpu_ctx, vocab):
+    """top_k in (1024, vocab] on a coarse grid (about 25 distinct values, so nearly every draw
+    lands on a value many logits share) with +0.0 / -0.0 and -inf mixed in: which of the equal
+    logits the reference's replacement keeps, and their order, decide the token, and the
+    device replays the replacement for them.  Then every logit equal (the earliest indices
+    are kept)."""
+    print(f"sample large top_k ties vocab={vocab}", flush=True)
+    rng = np.random.default_rng(vocab + 1)
+    configs = [(1.0, k, p) for k in (1500, 3000, vocab - 1, vocab) for p in (1.0, 0.6)]
+    gpu_ctx.sample_reserve(len(configs), vocab)
+    states = [orc.sampler_state_new(300 + i) for i in range(len(configs))]
+    for call in range(3):
+        logits = np.round(rng.standard_normal((len(configs), vocab)) * 2.0) / 2.0
+        logits = logits.astype(np.float32)
+        zero = rng.random(logits.shape) < 0.2
+        logits[zero] = np.where(rng.random(zero.sum()) < 0.5, 0.0, -0.0).astype(np.float32)
+        logits[rng.random(logits.shape) < 0.1] = -np.inf
+        if call == 2:
+            logits[:] = 1.5
+        tok, prob, new_states = run_device(gpu_ctx, padded_logits(logits, 0), configs, states)
+        gpu_ctx.check_faults()
+        check_rows(orc, logits, configs, states, tok, prob, new_states, f"large ties call {call}")
+        states = new_states
+
+
+def test_sample_tokens_large_top_k_nan(orc, gpu_ctx):
+    """top_k above 1024 with a NaN logit: past the first k it never enters the list (the row
+    samples as the oracle does); among the first k it makes the total NaN, reported as Runtime
+    with token -1 and the state unchanged."""
     from ferrisinfer_amd import FerrisError
 
-    print("sample top_k limit", flush=True)
-    rng = np.random.default_rng(6)
-    logits = rng.standard_normal((2, 2000)).astype(np.float32)
-    configs = [(0.8, 1500, 0.9), (0.8, 20, 0.9)]
-    states = [orc.sampler_state_new(7), orc.sampler_state_new(8)]
-    tok, _, new_states = run_device(gpu_ctx, padded_logits(logits, 0), configs, states)
-    assert tok[0] == -1 and new_states[0] == states[0]
-    assert tok[1] == orc.sample_last_token(logits[1], *configs[1], states[1])[0]
-    with pytest.raises(FerrisError, match="top_k"):
+    print("sample large top_k NaN", flush=True)
+    rng = np.random.default_rng(8)
+    logits = rng.standard_normal((2, 6000)).astype(np.float32)
+    logits[0, 4500] = np.nan
+    logits[1, 700] = -np.nan
+    configs = [(0.9, 2500, 0.95), (0.9, 2500, 0.95)]
+    gpu_ctx.sample_reserve(2, 6000)
+    states = [orc.sampler_state_new(11), orc.sampler_state_new(12)]
+    tok, prob, new_states = run_device(gpu_ctx, padded_logits(logits, 0), configs, states)
+    check_rows(orc, logits[:1], configs[:1], states[:1], tok[:1], prob[:1], new_states[:1], "nan late")
+    assert tok[1] == -1 and new_states[1] == states[1]
+    with pytest.raises(FerrisError, match="finite sampling distribution"):
         gpu_ctx.check_faults()
-    small = rng.standard_normal((1, 900)).astype(np.float32)
-    st = [orc.sampler_state_new(9)]
-    tok, prob, new_states = run_device(gpu_ctx, padded_logits(small, 0), [(0.8, 1500, 0.9)], st)
+    with pytest.raises(Exception, match="finite sampling distribution"):
+        orc.sample_last_token(logits[1], *configs[1], states[1])
     gpu_ctx.check_faults()
-    check_rows(orc, small, [(0.8, 1500, 0.9)], st, tok, prob, new_states, "clamped")
 
 
 def test_sample_tokens_rejects_bad_shapes(gpu_ctx):
