@@ -57,6 +57,8 @@ def parse_args():
     p.add_argument("--no-c5", action="store_true",
                    help="skip the C5 (Llama-3-8B-shaped, bf16 weights and KV) decode-step measurement")
     p.add_argument("--c5-steps", type=int, default=5)
+    p.add_argument("--c5-runtime-ticks", type=int, default=20,
+                   help="C5 decode ticks at batch 256 timed through the runtime (0 skips that leg)")
     p.add_argument("--no-kernels", action="store_true",
                    help="skip the C3 prefill/append and projection-GEMM kernel measurements")
     p.add_argument("--hf-load", action="store_true",
@@ -595,18 +597,167 @@ def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"
     return out
 
 
+C5_LAYER_SHAPES = ("attention.wq.weight", "attention.wk.weight", "attention.wv.weight", "attention.wo.weight",
+                   "feed_forward.w1.weight", "feed_forward.w2.weight", "feed_forward.w3.weight")
+
+
+def c5_shape_of(cfg, name):
+    h, f = cfg["hidden"], cfg["intermediate"]
+    kvw = cfg["kv_heads"] * (h // cfg["heads"])
+    return {"attention.wq.weight": (h, h), "attention.wk.weight": (h, kvw), "attention.wv.weight": (h, kvw),
+            "attention.wo.weight": (h, h), "feed_forward.w1.weight": (h, f), "feed_forward.w2.weight": (f, h),
+            "feed_forward.w3.weight": (h, f)}[name]
+
+
+def c5_seeded_layers(seed, cfg):
+    """Every layer's projection weights, N(0, 0.02) from ferrisinfer_amd.seeded (tag = CRC-32 of
+    "layers.<l>.<name>", the names and [in, out] layout of workloads.random_weights), drawn on
+    the device and held as bf16: {name: [layers, in, out] bf16}."""
+    import torch
+
+    from ferrisinfer_amd import seeded
+    from ferrisinfer_amd.seeded import tag_of
+
+    return {name: seeded.normals_torch(seed, [tag_of(f"layers.{li}.{name}") for li in range(cfg["layers"])],
+                                       c5_shape_of(cfg, name), scale=0.02, out_dtype=torch.bfloat16)
+            for name in C5_LAYER_SHAPES}
+
+
+def c5_seeded_matrix(seed, name, shape):
+    """One N(0, 0.02) seeded matrix (tag = CRC-32 of `name`) as bf16 on the device."""
+    import torch
+
+    from ferrisinfer_amd import seeded
+    from ferrisinfer_amd.seeded import tag_of
+
+    return seeded.normals_torch(seed, [tag_of(name)], shape, scale=0.02, out_dtype=torch.bfloat16)[0]
+
+
+def fill_tiled(flat, tile):
+    """flat[i] = tile[i % len(tile)] (device tensors)."""
+    n, t = flat.numel(), tile.numel()
+    full = n // t
+    if full:
+        flat[:full * t].view(full, t).copy_(tile.expand(full, t))
+    if n - full * t:
+        flat[full * t:].copy_(tile[:n - full * t])
+
+
+def c5_runtime_decode(seed, ticks, warmup=8, groups=16):
+    """C5 through the runtime ABI: the full 32-layer Llama-3-8B-shaped model with bf16 weights
+    and a bf16 KV pool (fr_create / fr_set_weight_device / fr_submit / fr_execute_next_tick,
+    decode ticks replayed from HIP graphs), 256 sequences with contexts U[512, 8192]
+    (ferrisinfer_amd.seeded).  Sequence i's prompt is a prefix of group (i mod 16)'s seeded
+    token stream: the group's longest prompt is prefilled first (2048-token chunks, the C5
+    tick budget), then the other 240 share its blocks through the scheduler's prefix sharing
+    and compute one token each.  Times `ticks` decode ticks at batch 256 after `warmup`."""
+    import numpy as np
+    import torch
+
+    from ferrisinfer_amd import seeded
+    from ferrisinfer_amd.bf16_decoder import LLAMA3_8B_C5
+    from ferrisinfer_amd.runtime import Runtime
+    from ferrisinfer_amd.seeded import tag_of
+
+    cfg = LLAMA3_8B_C5
+    h, v = cfg["hidden"], cfg["vocab"]
+    n = 256
+    lens = seeded.integers(seed, tag_of("c5.runtime.context_lens"), n, 512, 8192)
+    members = [[i for i in range(n) if i % groups == g] for g in range(groups)]
+    source = [max(m, key=lambda i: lens[i]) for m in members]
+    streams = [seeded.integers(seed, tag_of(f"c5.runtime.prompt.{g}"), int(lens[source[g]]), 0, v - 1)
+               .astype(np.uint32) for g in range(groups)]
+    prompts = [streams[i % groups][:int(lens[i])] for i in range(n)]
+    # no sequence may finish before the timed ticks: the sources decode between their prefill
+    # chunks (two prefill ticks, then a decode tick) and every sequence while the others are
+    # admitted
+    gen = 512
+    unique = sum(int(lens[s]) for s in source)
+    num_blocks = (unique + n * 160) // 16 + 2 * n
+    t0 = time.time()
+    rt = Runtime(h, cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"], v, cfg["max_pos"], cfg["eps"],
+                 cfg["theta"], tie=False, max_seq=cfg["max_pos"], max_gen=gen, max_batch=n, max_chunk=2048,
+                 max_batch_tokens=2048, num_blocks=num_blocks, block_size=16, kv_dtype="bf16",
+                 weight_dtype="bf16", graph_decode=True)
+    layers = c5_seeded_layers(seed, cfg)
+    for name, stack in layers.items():
+        for li in range(cfg["layers"]):
+            rt.set_weight_device(f"layers.{li}.{name}", stack[li])
+    del layers
+    ones = torch.ones(h, device="cuda")
+    for li in range(cfg["layers"]):
+        rt.set_weight_device(f"layers.{li}.attention_norm.weight", ones)
+        rt.set_weight_device(f"layers.{li}.ffn_norm.weight", ones)
+    rt.set_weight_device("norm.weight", ones)
+    for name in ("tok_embeddings.weight", "output.weight"):
+        rt.set_weight_device(name, c5_seeded_matrix(seed, name, (v, h)))
+    torch.cuda.empty_cache()
+    t_weights = time.time() - t0
+    print(f"bench: C5 runtime weights set in {t_weights:.1f} s; prefilling {groups} sources", file=sys.stderr,
+          flush=True)
+    t0 = time.time()
+    seqs = {}
+    for g in range(groups):
+        seqs[source[g]] = rt.submit(prompts[source[g]], max_new_tokens=gen)
+    while any(len(rt.generated(seqs[s])) == 0 for s in source):
+        rt.execute_next_tick()
+    for i in range(n):
+        if i not in seqs:
+            seqs[i] = rt.submit(prompts[i], max_new_tokens=gen)
+    while any(len(rt.generated(seqs[i])) == 0 for i in range(n)):
+        rt.execute_next_tick()
+    t_setup = time.time() - t0
+    print(f"bench: C5 runtime sequences admitted in {t_setup:.1f} s; timing decode ticks", file=sys.stderr,
+          flush=True)
+    times, batches, ctx_sums = [], [], []
+    while len(times) < warmup + ticks:
+        tick = rt.execute_next_tick()
+        if tick is None:
+            break
+        if tick[0] == 1:  # decode
+            times.append(rt.last_tick_seconds)
+            batches.append(len(tick[1]))
+            ctx_sums.append(rt.last_batch_context_sum())
+    timed = times[warmup:]
+    ms = 1e3 * sum(timed) / max(len(timed), 1)
+    counters = rt.graph_counters()
+    res = {
+        "workload": "C5 model through the runtime ABI: 32 layers, bf16 weights (N(0,0.02), seeded, widened on the "
+                    "device), bf16 activations into the projections, bf16 KV; 256 sequences, contexts "
+                    "U[512,8192] (seeded) as prefixes of 16 seeded prompts sharing pool blocks; decode ticks "
+                    "replayed from HIP graphs, wall time of fr_execute_next_tick",
+        "ms_per_tick": round(ms, 3),
+        "decode_tok_s": round(sum(batches[warmup:]) / max(sum(timed), 1e-9), 1),
+        "batch_min_max": [min(batches[warmup:]), max(batches[warmup:])] if len(batches) > warmup else None,
+        "ticks": len(timed),
+        "avg_context": round(float(np.sum(ctx_sums[warmup:])) / max(sum(batches[warmup:]), 1), 1),
+        # KV rows every tick reads (K and V, bf16, every layer), many of them from blocks the
+        # sequences share
+        "kv_read_gb_per_tick": round(float(np.mean(ctx_sums[warmup:])) * cfg["layers"] * cfg["kv_heads"] *
+                                     (h // cfg["heads"]) * 2 * 2 / 1e9, 1) if len(ctx_sums) > warmup else None,
+        "unique_kv_tokens": unique,
+        "graph_counters": counters,
+        "setup_s": {"weights": round(t_weights, 1), "prefill_and_admission": round(t_setup, 1)},
+    }
+    rt.close()
+    torch.cuda.empty_cache()
+    return res
+
+
 def c5_step(seed, steps):
     """C5: the Llama-3-8B-shaped decoder (32 layers, hidden 4096, Hq 32 / Hkv 8, D 128, FFN
-    14336, vocab 128256, untied head) with random N(0, 0.02) bf16 weights and a bf16 KV pool per
-    layer sized for the step's 257 sequences (about 147 GB over the 32 layers, N(0, 1) contents).
+    14336, vocab 128256, untied head) with N(0, 0.02) bf16 weights (ferrisinfer_amd.seeded) and
+    a bf16 KV pool per layer sized for the step's 257 sequences (about 147 GB over the 32 layers,
+    N(0, 1) contents from a seeded tile).
     One step = 256 decode tokens (contexts U[512, 8192]) + one 2048-token prefill chunk (2048
     tokens already cached) through every layer and the greedy head.  Also times layer 0's ops
     one by one for their roofline fractions."""
     import numpy as np
     import torch
 
-    from ferrisinfer_amd import Context
+    from ferrisinfer_amd import Context, seeded
     from ferrisinfer_amd.bf16_decoder import LLAMA3_8B_C5, Bf16Decoder, build_step_batch, c5_step_shape
+    from ferrisinfer_amd.seeded import tag_of
 
     cfg = LLAMA3_8B_C5
     h, f, v, hq, hkv = cfg["hidden"], cfg["intermediate"], cfg["vocab"], cfg["heads"], cfg["kv_heads"]
@@ -617,21 +768,25 @@ def c5_step(seed, steps):
     num_blocks = sum((n + bs - 1) // bs for n in lens)
     t = len(decode_ctx) + sum(n for _, n in prefill)
     ctx = Context(0)
-    g = torch.Generator(device="cuda").manual_seed(seed)
     dec = Bf16Decoder(ctx, cfg, num_blocks, bs, max_tokens=t, max_last_rows=len(lens))
-
-    def w(*shape):
-        return (torch.randn(*shape, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
-
+    layers = c5_seeded_layers(seed, cfg)
     ones = torch.ones(h, device="cuda")
-    for _ in range(cfg["layers"]):
-        dec.set_layer(w(h, h), w(h, hkv * d), w(h, hkv * d), w(h, h), w(h, f), w(f, h), w(h, f), ones, ones)
-    dec.set_head(ones, w(v, h))
-    for pool in dec.k_pools + dec.v_pools:
-        pool.view(torch.bfloat16).normal_(generator=g)
+    for li in range(cfg["layers"]):
+        lw = {k: layers[k][li] for k in layers}
+        dec.set_layer(lw["attention.wq.weight"], lw["attention.wk.weight"], lw["attention.wv.weight"],
+                      lw["attention.wo.weight"], lw["feed_forward.w1.weight"], lw["feed_forward.w2.weight"],
+                      lw["feed_forward.w3.weight"], ones, ones)
+    del layers
+    dec.set_head(ones, c5_seeded_matrix(seed, "output.weight", (v, h)))
+    for li, (kp, vp) in enumerate(zip(dec.k_pools, dec.v_pools)):  # N(0, 1) contents, a seeded 2^20-value tile
+        for name, pool in (("k", kp), ("v", vp)):
+            fill_tiled(pool.view(torch.bfloat16).view(-1),
+                       seeded.normals_torch(seed, [tag_of(f"c5.kv_pool.{li}.{name}")], (1 << 20,),
+                                            out_dtype=torch.bfloat16)[0])
     kv_bytes = sum(p.numel() * 2 for p in dec.k_pools + dec.v_pools)
     batch, _ = build_step_batch(decode_ctx, prefill, bs, num_blocks, seed)
-    x = torch.randn(t, h, device="cuda", generator=g) * 0.02  # synthetic embeddings of the step's tokens
+    # synthetic embeddings of the step's tokens
+    x = seeded.normals_torch(seed, [tag_of("c5.step_input")], (t, h), scale=0.02)[0]
     torch.cuda.synchronize()
 
     dec.step(x, batch)  # warm-up
@@ -701,7 +856,10 @@ def c5_step(seed, steps):
             row.update(flops=work, achieved_tflops=round(tf, 1), f32_mfma_frac=round(tf / FP32_PEAK_TFS, 4))
         out_ops[name] = row
     res = {
-        "workload": f"C5 Llama-3-8B shape, bf16 weights (random N(0,0.02)) and bf16 KV; step = {nd} decode "
+        "workload": "C5 Llama-3-8B shape composed from the kernel ABI, bf16 weights (N(0,0.02), seeded), bf16 "
+                    "activations (projection inputs rounded to bf16: bf16 x bf16 products with f32 accumulation, "
+                    "where the reference multiplies f32 activations by bf16-widened weights) and bf16 KV; "
+                    f"step = {nd} decode "
                     f"tokens (ctx U[512,8192], sum {sum(decode_ctx)}) + {sum(n for _, n in prefill)}-token "
                     "prefill chunk after a 2048-token cached prefix; 32 layers + greedy head; block 16",
         "kv_pool_gb": round(kv_bytes / 1e9, 1),
@@ -908,6 +1066,9 @@ def main():
     if not args.no_c5:
         print("bench: C5 bf16 decoder step", file=sys.stderr, flush=True)
         result["c5"] = c5_step(args.seed, args.c5_steps)
+        if args.c5_runtime_ticks > 0:
+            print("bench: C5 decode ticks through the runtime", file=sys.stderr, flush=True)
+            result["c5"]["runtime_decode_tick"] = c5_runtime_decode(args.seed, args.c5_runtime_ticks)
     if args.hf_load:
         print("bench: hf checkpoint import", file=sys.stderr, flush=True)
         result["hf_load"] = hf_load(args.seed)

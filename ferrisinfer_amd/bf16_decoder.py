@@ -194,16 +194,19 @@ def build_step_batch(decode_ctx, prefill, block_size: int, num_blocks: int, seed
 
     decode_ctx: context length (including the new token) of each decode sequence;
     prefill: list of (cached_prefix_len, new_tokens) chunks.
-    Block ids: the first sum(ceil(len / block_size)) entries of a seeded permutation of the pool,
-    assigned to the sequences in order (decode sequences first)."""
+    Block ids: the first sum(ceil(len / block_size)) entries of a permutation of the pool
+    (ferrisinfer_amd.seeded, tag "c5.block_ids"), assigned to the sequences in order (decode
+    sequences first)."""
     import numpy as np
     import torch
+
+    from . import seeded
 
     lens = [int(c) for c in decode_ctx] + [int(p + n) for p, n in prefill]
     need = [(n + block_size - 1) // block_size for n in lens]
     if sum(need) > num_blocks:
         raise FerrisError(6, f"step needs {sum(need)} blocks, pool has {num_blocks}")
-    perm = np.random.default_rng(seed).permutation(num_blocks).astype(np.int32)
+    perm = seeded.permutation(seed, seeded.tag_of("c5.block_ids"), num_blocks)
     tables, off = [], 0
     for k in need:
         tables.append(perm[off:off + k])
@@ -243,10 +246,10 @@ def build_step_batch(decode_ctx, prefill, block_size: int, num_blocks: int, seed
 
 def c5_step_shape(seed: int = 0, num_decode: int = 256, min_ctx: int = 512, max_ctx: int = 8192,
                   chunk: int = 2048, chunk_prefix: int = 2048):
-    """BASELINE C5's step: 256 decode sequences with context U[min_ctx, max_ctx] (seeded) and one
-    2048-token prefill chunk (the second chunk of a 4096-token prompt: 2048 tokens cached)."""
-    import numpy as np
+    """BASELINE C5's step: 256 decode sequences with context U[min_ctx, max_ctx]
+    (ferrisinfer_amd.seeded, tag "c5.context_lens") and one 2048-token prefill chunk (the
+    second chunk of a 4096-token prompt: 2048 tokens cached)."""
+    from . import seeded
 
-    rng = np.random.default_rng(seed)
-    decode_ctx = rng.integers(min_ctx, max_ctx + 1, size=num_decode).tolist()
+    decode_ctx = seeded.integers(seed, seeded.tag_of("c5.context_lens"), num_decode, min_ctx, max_ctx).tolist()
     return decode_ctx, [(chunk_prefix, chunk)]

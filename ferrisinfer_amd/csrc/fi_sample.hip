@@ -424,6 +424,16 @@ __device__ __forceinline__ void replay_top_k(const float* row, int vocab, int k,
   __syncthreads();
 }
 
+// A sampling weight's exponential, f32 in and out: the f64 exponential rounded once to f32,
+// which is the correctly rounded f32 result except when the exact value lies within an f64
+// error of an f32 rounding midpoint.  The reference calls the host libm's expf; glibc 2.35's
+// equals this on all but 0.0086 % of the floats in [-104, 0] (every 7th bit pattern checked),
+// where the device's own f32 exponential, accurate to about an ulp, differs far more often.
+// One differing weight can change the rounding of every later partial sum, so with hundreds
+// of thousands of weights in one sequential sum the closer exponential keeps the drawn token
+// the reference's.
+__device__ __forceinline__ float weight_exp(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+
 __device__ __forceinline__ uint64_t xorshift_step(uint64_t x) {
   x ^= x >> 12;
   x ^= x << 25;
@@ -939,7 +949,7 @@ __device__ __forceinline__ void weights_and_draw(SampleShared& sh, int k, float 
                                                  int32_t* token, float* prob, uint32_t* faults, int r, int tid) {
   const float temp = fmaxf(T, 1.1920929e-7f);  // max(f32::EPSILON); a NaN temperature gives EPSILON
   const float scaled_max = sh.s_val[0] / temp;
-  for (int i = tid; i < kMaxTopK; i += kThreads) sh.wts[i] = i < k ? expf((sh.s_val[i] / temp) - scaled_max) : 0.0f;
+  for (int i = tid; i < kMaxTopK; i += kThreads) sh.wts[i] = i < k ? weight_exp((sh.s_val[i] / temp) - scaled_max) : 0.0f;
   __syncthreads();
   if (tid == 0) sh.draw = draw_one(sh.wts, k, P, rng, token, prob, faults, r);
   __syncthreads();
@@ -1513,7 +1523,7 @@ struct SortedWeight {
   float temp;
   float scaled_max;
   __device__ float value(int q) const { return sort_key_value(keys[q]); }
-  __device__ float of(float v) const { return expf((v / temp) - scaled_max); }
+  __device__ float of(float v) const { return weight_exp((v / temp) - scaled_max); }
 };
 
 template <int VEC>

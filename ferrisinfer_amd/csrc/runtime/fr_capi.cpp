@@ -109,6 +109,14 @@ int32_t fr_set_weight(void* h, const char* name, const float* data, int64_t coun
   });
 }
 
+int32_t fr_set_weight_device(void* h, const char* name, const void* d_data, int32_t src_dtype, int64_t count) {
+  return guard([&] {
+    if (rt(h)->scheduler) fr::fail(fr::ErrorKind::Runtime, "weights are frozen once requests were submitted");
+    if (!d_data || count < 0) fr::fail(fr::ErrorKind::InvalidConfig, "fr_set_weight_device: null data or negative count");
+    rt(h)->model->set_weight_device(name, d_data, src_dtype, static_cast<size_t>(count));
+  });
+}
+
 int32_t fr_hf_read_config(const char* model_dir, fr_model_config* out) {
   return guard([&] {
     if (!model_dir || !out) fr::fail(fr::ErrorKind::InvalidConfig, "fr_hf_read_config: null argument");
@@ -274,6 +282,13 @@ int32_t fr_last_tick_profile(void* h, double* out) {
   return guard([&] {
     const auto p = rt(h)->scheduler_ready().last_tick_profile();
     for (size_t i = 0; i < p.size(); ++i) out[i] = p[i];
+  });
+}
+
+int32_t fr_last_logits(void* h, float* out, int64_t capacity, int64_t* rows) {
+  return guard([&] {
+    if (!rows || capacity < 0 || (capacity > 0 && !out)) fr::fail(fr::ErrorKind::InvalidConfig, "fr_last_logits: bad buffer");
+    rt(h)->scheduler_ready().executor().last_logits(out, static_cast<size_t>(capacity), rows);
   });
 }
 

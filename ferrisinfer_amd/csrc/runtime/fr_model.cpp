@@ -89,6 +89,12 @@ void DeviceModel::set_weight(const std::string& name, const float* host, size_t 
   check(fi_buf_upload(ctx_, dst->get(), count * sizeof(float), host, count * sizeof(float)));
 }
 
+void DeviceModel::set_weight_device(const std::string& name, const void* device, int32_t src_dtype, size_t count) {
+  DeviceBuffer* dst = weight_slot(name, count);
+  check(fi_convert_to_f32(ctx_, device, src_dtype, 1, static_cast<int64_t>(count), 0, static_cast<float*>(dst->get())));
+  check(fi_ctx_sync(ctx_));  // the caller may release the source once this returns
+}
+
 DeviceBuffer* DeviceModel::weight_slot(const std::string& name, size_t count) {
   if (finalized_) fail(ErrorKind::Runtime, "weights are packed; tensor " + name + " can no longer be set");
   const ModelConfig& c = config_;
@@ -435,6 +441,13 @@ void ForwardExecutor::enqueue(const Plan& p) {
   }
 }
 
+void ForwardExecutor::last_logits(float* host, size_t capacity, int64_t* rows) const {
+  const size_t n = static_cast<size_t>(logits_rows_) * model_->config().vocab_size;
+  if (n > capacity) fail(ErrorKind::InvalidShape, "last logits need " + std::to_string(n) + " floats");
+  if (n) check(fi_buf_download(ctx_, host, n * sizeof(float), logits_.get(), n * sizeof(float)));
+  *rows = logits_rows_;
+}
+
 std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const SamplerConfig& sampler,
                                               std::vector<uint64_t>* states) {
   const auto t_start = std::chrono::steady_clock::now();
@@ -442,6 +455,7 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   const ModelConfig& c = model_->config();
   const int32_t T = static_cast<int32_t>(b.token_ids.size());
   const int32_t B = static_cast<int32_t>(b.context_lens.size());
+  logits_rows_ = 0;
   if (T == 0 || B == 0) {
     copy_only(b);
     return {};
@@ -547,6 +561,7 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
     if (std::min<int64_t>(std::max<int64_t>(sampler.top_k, 1), c.vocab_size) > 1024) {
       check(fi_sample_reserve(ctx_, B, c.vocab_size));
     }
+    logits_rows_ = B;
   }
 
   if (use_graph) {

@@ -97,6 +97,9 @@ class DeviceModel {
   // weight_dtype: FI_DTYPE_F32 or FI_DTYPE_BF16, the storage of the packed projections and head.
   DeviceModel(fi_context* ctx, const ModelConfig& config, int32_t rope_positions, int32_t weight_dtype = FI_DTYPE_F32);
   void set_weight(const std::string& name, const float* host, size_t count);
+  // The same from device memory: `count` elements of src_dtype (FI_DTYPE_F32 / _BF16 / _F16)
+  // widened into the weight's f32 slot on the device.
+  void set_weight_device(const std::string& name, const void* device, int32_t src_dtype, size_t count);
   // The device buffer of weight `name` sized for `count` floats (contents undefined until
   // written); InvalidShape when count is not the tensor's size, MissingWeight for an unknown
   // name.  set_weight uploads into it; the checkpoint loader converts into it on the device.
@@ -356,6 +359,10 @@ class ForwardExecutor {
   double last_wait_seconds() const { return wait_s_; }
   // Decode ticks replayed from a graph, graphs captured, graphs dropped (since creation).
   std::array<uint64_t, 3> graph_counters() const { return {graph_replays_, graph_captures_, graph_drops_}; }
+  // The logits rows the last run sampled from ([rows, vocab] f32, batch order) into host
+  // memory of `capacity` floats; rows is 0 after a greedy run (its head is fused with the
+  // argmax and writes no logits).
+  void last_logits(float* host, size_t capacity, int64_t* rows) const;
 
  private:
   // Every scalar and device pointer of one tick's launch sequence.
@@ -389,6 +396,7 @@ class ForwardExecutor {
   std::map<std::array<int32_t, 4>, fi_graph*> graphs_;  // (B, stride, max_context_len, greedy)
   std::map<std::array<int32_t, 4>, int32_t> seen_;       // eager runs per shape since the last drop
   uint64_t graph_replays_ = 0, graph_captures_ = 0, graph_drops_ = 0;
+  int32_t logits_rows_ = 0;  // rows of logits_ the last run sampled from
 };
 
 // runtime/scheduler.rs:109-648 over the batched executor.

@@ -53,6 +53,7 @@ def load() -> C.CDLL:
             "fr_create": [_I32, C.POINTER(ModelConfig), C.POINTER(RuntimeConfig), C.POINTER(_P)],
             "fr_destroy": [_P],
             "fr_set_weight": [_P, C.c_char_p, _P, _I64],
+            "fr_set_weight_device": [_P, C.c_char_p, _P, _I32, _I64],
             "fr_submit": [_P, _P, _I64, _I64, _I64, C.POINTER(C.c_uint64)],
             "fr_execute_next_tick": [_P, C.POINTER(_I32)],
             "fr_has_pending": [_P],
@@ -63,6 +64,7 @@ def load() -> C.CDLL:
             "fr_pool_free_count": [_P, C.POINTER(_I64)],
             "fr_graph_counters": [_P, _P],
             "fr_last_batch_sizes": [_P, _P],
+            "fr_last_logits": [_P, _P, _I64, C.POINTER(_I64)],
             "fr_last_batch": [_P] + [_P] * 10,
             "fr_last_tick_profile": [_P, _P],
             "fr_hf_read_config": [C.c_char_p, C.POINTER(ModelConfig)],
@@ -182,6 +184,17 @@ class Runtime:
         a = np.ascontiguousarray(np.asarray(array, dtype=np.float32)).reshape(-1)
         _check(load().fr_set_weight(self.h, name.encode(), _addr(a), a.size))
 
+    def set_weight_device(self, name, tensor):
+        """set_weight from a contiguous torch tensor on this runtime's GPU (float32, bfloat16 or
+        float16), widened to f32 on the device."""
+        import torch
+
+        dtypes = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
+        if not tensor.is_cuda or not tensor.is_contiguous() or tensor.dtype not in dtypes:
+            raise FerrisError(6, "set_weight_device takes a contiguous f32 / bf16 / f16 device tensor")
+        _check(load().fr_set_weight_device(self.h, name.encode(), tensor.data_ptr(), dtypes[tensor.dtype],
+                                           tensor.numel()))
+
     @classmethod
     def from_hf(cls, model_dir, **kwargs):
         """A runtime for the Qwen2 checkpoint under model_dir: config.json gives the model
@@ -271,6 +284,15 @@ class Runtime:
     def last_batch_context_sum(self) -> int:
         """Sum of the context lengths of the last tick's packed batch (its KV tokens read)."""
         return int(self.last_batch()["context_lens"].sum())
+
+    def last_logits(self) -> np.ndarray:
+        """The logits rows the last tick sampled from ([B, vocab] f32, the batch's sequence
+        order); empty after a greedy tick."""
+        B = int(self.last_batch()["sequence_ids"].size)
+        out = np.zeros((B, self.vocab), np.float32)
+        rows = _I64()
+        _check(load().fr_last_logits(self.h, _addr(out), out.size, C.byref(rows)))
+        return out[: rows.value]
 
     def last_batch(self) -> dict:
         L = load()

@@ -29,6 +29,7 @@ per configuration.
 """
 from __future__ import annotations
 
+import os
 import zlib
 
 import numpy as np
@@ -97,9 +98,10 @@ def integers(seed: int, tag: int, n: int, lo: int, hi: int) -> np.ndarray:
     return (lo + np.floor(u * (hi - lo + 1))).astype(np.int64)
 
 
-def normals(seed: int, tag: int, shape, scale: float | None = None) -> np.ndarray:
+def normals(seed: int, tag: int, shape, scale: float | None = None, threads: int | None = None) -> np.ndarray:
     """N(0, 1) (times scale) f32 values of the given shape, laid out as the module docstring
-    says."""
+    says.  Large tensors split their streams over `threads` threads (default: the host's CPUs,
+    at most 16); every stream is independent, so the values do not depend on the split."""
     n = int(np.prod(shape)) if len(shape) else 1
     if n == 0:
         return np.zeros(shape, np.float32)
@@ -109,18 +111,83 @@ def normals(seed: int, tag: int, shape, scale: float | None = None) -> np.ndarra
     pairs = -(-draws // 2)
     out = np.empty((2 * pairs, s), np.float32)
     two_pi = 2.0 * np.pi
-    for p in range(pairs):
-        u1 = next_f32(st).astype(np.float64)
-        u2 = next_f32(st).astype(np.float64)
-        r = np.sqrt(-2.0 * np.log(1.0 - u1))
-        z0 = r * np.cos(two_pi * u2)
-        z1 = r * np.sin(two_pi * u2)
-        if scale is not None:
-            z0 *= scale
-            z1 *= scale
-        out[2 * p] = z0.astype(np.float32)
-        out[2 * p + 1] = z1.astype(np.float32)
+
+    def fill(c0, c1):
+        sub = st[c0:c1].copy()
+        for p in range(pairs):
+            u1 = next_f32(sub).astype(np.float64)
+            u2 = next_f32(sub).astype(np.float64)
+            r = np.sqrt(-2.0 * np.log(1.0 - u1))
+            z0 = r * np.cos(two_pi * u2)
+            z1 = r * np.sin(two_pi * u2)
+            if scale is not None:
+                z0 *= scale
+                z1 *= scale
+            out[2 * p, c0:c1] = z0.astype(np.float32)
+            out[2 * p + 1, c0:c1] = z1.astype(np.float32)
+
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    # narrower streams groups pay more interpreter time per value, so only tensors of 64M
+    # values and more are split
+    groups = max(1, min(threads, n >> 26, s // 4096))
+    if groups == 1:
+        fill(0, s)
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+
+        bounds = [s * g // groups for g in range(groups + 1)]
+        with ThreadPoolExecutor(groups) as ex:  # numpy's ufuncs release the GIL
+            list(ex.map(lambda g: fill(bounds[g], bounds[g + 1]), range(groups)))
     return out.reshape(-1)[:n].reshape(shape)
+
+
+def normals_torch(seed: int, tags, shape, scale: float | None = None, device="cuda", out_dtype=None):
+    """normals(seed, tag, shape, scale) for every tag of `tags`, stacked ([len(tags), *shape]),
+    computed with torch on `device`: the same streams, draws and Box-Muller arithmetic in
+    int64 / f64 tensor ops (logical shifts emulated by masking), all tags' streams advanced
+    together.  Values equal normals()'s wherever the device's f64 log, sqrt, cos and sin round
+    as the host's do (elsewhere an f32 may differ in its last bit).  out_dtype (default f32)
+    narrows each drawn row as it is produced, e.g. torch.bfloat16 for bf16 weights."""
+    import torch
+
+    out_dtype = torch.float32 if out_dtype is None else out_dtype
+    n = int(np.prod(shape)) if len(shape) else 1
+    tags = list(tags)
+    out = torch.empty((len(tags), n), dtype=out_dtype, device=device)
+    if n == 0 or not tags:
+        return out.reshape(len(tags), *shape)
+    s = min(STREAMS, n)
+    st = torch.from_numpy(np.stack([stream_states(seed, t, s) for t in tags]).view(np.int64)).to(device)
+    draws = -(-n // s)
+    pairs = -(-draws // 2)
+    m12 = (1 << 52) - 1  # (x >> 12) as a logical shift
+    m27 = (1 << 37) - 1
+    m40 = (1 << 24) - 1
+    mult = torch.tensor(MULT, dtype=torch.int64, device=device)  # below 2^63; products wrap mod 2^64
+    two_pi = 2.0 * np.pi
+
+    def draw():
+        nonlocal st
+        st = st ^ ((st >> 12) & m12)
+        st = st ^ (st << 25)
+        st = st ^ ((st >> 27) & m27)
+        upper = ((st * mult) >> 40) & m40
+        return upper.to(torch.float32) / float(1 << 24)
+
+    view = out.view(len(tags), -1)
+    for p in range(pairs):
+        u1 = draw().to(torch.float64)
+        u2 = draw().to(torch.float64)
+        r = torch.sqrt(-2.0 * torch.log(1.0 - u1))
+        z = torch.stack((r * torch.cos(two_pi * u2), r * torch.sin(two_pi * u2)), dim=1)  # [tags, 2, s]
+        if scale is not None:
+            z = z * scale
+        z = z.to(torch.float32).reshape(len(tags), 2 * s)
+        lo = 2 * p * s
+        hi = min(n, lo + 2 * s)
+        view[:, lo:hi] = z[:, :hi - lo].to(out_dtype)
+    return out.reshape(len(tags), *shape)
 
 
 def permutation(seed: int, tag: int, n: int) -> np.ndarray:

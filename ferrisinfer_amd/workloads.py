@@ -205,30 +205,45 @@ def random_weights(cfg: dict, seed: int = 0, qkv_bias: bool = False, std: float 
     """Weights named as model/decoder.rs:30-52 in the reference's [in, out] layout.  Matrices,
     embeddings and (optional, Qwen2-style) q/k/v biases ~ N(0, std), each tensor seeded by its
     name (tag = CRC-32 of the name); RMSNorm weights = 1."""
+    from concurrent.futures import ThreadPoolExecutor
+
     h, f, v = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
     kvw = cfg["kv_heads"] * (h // cfg["heads"])
-
-    def n(name, *shape):
-        return seeded.normals(seed, tag_of(name), shape, scale=std)
-
-    w = {"tok_embeddings.weight": n("tok_embeddings.weight", v, h)}
+    shapes = {"tok_embeddings.weight": (v, h)}
+    for layer in range(cfg["layers"]):
+        p = f"layers.{layer}."
+        for name, shape in (("attention.wq.weight", (h, h)), ("attention.wk.weight", (h, kvw)),
+                            ("attention.wv.weight", (h, kvw))):
+            shapes[p + name] = shape
+        if qkv_bias:
+            for name, width in (("attention.wq.bias", h), ("attention.wk.bias", kvw), ("attention.wv.bias", kvw)):
+                shapes[p + name] = (width,)
+        shapes[p + "attention.wo.weight"] = (h, h)
+        for name, shape in (("feed_forward.w1.weight", (h, f)), ("feed_forward.w2.weight", (f, h)),
+                            ("feed_forward.w3.weight", (h, f))):
+            shapes[p + name] = shape
+    if not cfg.get("tie", False):
+        shapes["output.weight"] = (v, h)
+    # tensors are independent streams: generated on a thread pool (numpy's ufuncs release the
+    # GIL), the values do not depend on it
+    with ThreadPoolExecutor(min(8, os.cpu_count() or 1)) as ex:
+        drawn = dict(zip(shapes, ex.map(lambda k: seeded.normals(seed, tag_of(k), shapes[k], scale=std), shapes)))
+    w = {"tok_embeddings.weight": drawn["tok_embeddings.weight"]}
     for layer in range(cfg["layers"]):
         p = f"layers.{layer}."
         w[p + "attention_norm.weight"] = np.ones(h, np.float32)
-        for name, shape in (("attention.wq.weight", (h, h)), ("attention.wk.weight", (h, kvw)),
-                            ("attention.wv.weight", (h, kvw))):
-            w[p + name] = n(p + name, *shape)
+        for name in ("attention.wq.weight", "attention.wk.weight", "attention.wv.weight"):
+            w[p + name] = drawn[p + name]
         if qkv_bias:
-            for name, width in (("attention.wq.bias", h), ("attention.wk.bias", kvw), ("attention.wv.bias", kvw)):
-                w[p + name] = n(p + name, width)
-        w[p + "attention.wo.weight"] = n(p + "attention.wo.weight", h, h)
+            for name in ("attention.wq.bias", "attention.wk.bias", "attention.wv.bias"):
+                w[p + name] = drawn[p + name]
+        w[p + "attention.wo.weight"] = drawn[p + "attention.wo.weight"]
         w[p + "ffn_norm.weight"] = np.ones(h, np.float32)
-        for name, shape in (("feed_forward.w1.weight", (h, f)), ("feed_forward.w2.weight", (f, h)),
-                            ("feed_forward.w3.weight", (h, f))):
-            w[p + name] = n(p + name, *shape)
+        for name in ("feed_forward.w1.weight", "feed_forward.w2.weight", "feed_forward.w3.weight"):
+            w[p + name] = drawn[p + name]
     w["norm.weight"] = np.ones(h, np.float32)
     if not cfg.get("tie", False):
-        w["output.weight"] = n("output.weight", v, h)
+        w["output.weight"] = drawn["output.weight"]
     return w
 
 

@@ -72,6 +72,11 @@ int32_t fr_create(int32_t ordinal, const fr_model_config* model, const fr_runtim
                   void** out);
 int32_t fr_destroy(void* runtime);
 int32_t fr_set_weight(void* runtime, const char* name, const float* data, int64_t count);
+/* fr_set_weight from device memory on the runtime's GPU: `count` elements of src_dtype
+ * (FI_DTYPE_F32, _BF16 or _F16), widened to f32 as the checkpoint loader widens them
+ * (fi_convert_to_f32; io/safetensors.rs:437-471, 538-568).  For weights generated or staged in
+ * HBM, which then never cross PCIe. */
+int32_t fr_set_weight_device(void* runtime, const char* name, const void* d_data, int32_t src_dtype, int64_t count);
 
 /* ReferenceScheduler::submit (scheduler.rs:204-250); stop < 0 means no stop token. */
 /* ---------------------------------------------------------------- checkpoint import
@@ -125,6 +130,12 @@ int32_t fr_graph_counters(void* runtime, uint64_t* out3);
  * max_context_len]; then its arrays (token ids, positions, slot mapping, cu_seqlens, context
  * lengths, block tables [B, max_blocks], copy-on-write src/dst/count, sequence ids). */
 int32_t fr_last_batch_sizes(void* runtime, int64_t* sizes);
+/* The logits rows the last tick sampled from, one per batch sequence in the batch's order
+ * ([rows, vocab] f32 into `capacity` floats): each sequence's last-row logits, the
+ * decode-workspace / prefill logits the reference's session passes to sample_last_token
+ * (session.rs:357-373, 399-406).  rows = 0 after a greedy tick, whose head is fused with the
+ * argmax and writes no logits. */
+int32_t fr_last_logits(void* runtime, float* out, int64_t capacity, int64_t* rows);
 int32_t fr_last_batch(void* runtime, int32_t* token_ids, int32_t* positions, int64_t* slots,
                       int32_t* cu_seqlens, int32_t* context_lens, int32_t* block_tables,
                       int32_t* copy_src, int32_t* copy_dst, int32_t* copy_count,

@@ -93,6 +93,26 @@ def test_layout_rule_streams_and_draws():
     np.testing.assert_array_equal(z[seeded.STREAMS:2 * seeded.STREAMS], (r * np.sin(2 * np.pi * u2)).astype(np.float32))
 
 
+def test_torch_streams_equal_the_numpy_ones():
+    """normals_torch (int64 / f64 tensor ops, several tags advanced together) against normals()
+    on the host: bit-identical f32 values for short, stream-wide and multi-draw tensors, with and
+    without a scale; the bf16 output is the f32 value rounded to nearest even; a split of the
+    streams over threads changes nothing."""
+    import torch
+
+    for shape, scale in (((7,), 0.02), ((1000,), None), ((300, 500), 0.02), ((2 * seeded.STREAMS + 5,), 0.5)):
+        want = np.stack([seeded.normals(3, t, shape, scale=scale) for t in (11, 12, 13)])
+        got = seeded.normals_torch(3, [11, 12, 13], shape, scale=scale, device="cpu").numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=str(shape))
+    b16 = seeded.normals_torch(3, [11], (4096,), scale=0.02, device="cpu", out_dtype=torch.bfloat16)[0]
+    f32 = torch.from_numpy(seeded.normals(3, 11, (4096,), scale=0.02))
+    assert torch.equal(b16, f32.to(torch.bfloat16))
+    big = (1 << 26) + 3  # long enough to be split over threads
+    a = seeded.normals(9, 4, (big,), threads=1)
+    b = seeded.normals(9, 4, (big,), threads=4)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_c1_c2_c3_inputs_match_the_fixtures(golden):
     from ferrisinfer_amd import workloads as W
 
