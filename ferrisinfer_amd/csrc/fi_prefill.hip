@@ -458,10 +458,14 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
   constexpr int RV = D / 8;              // 16-byte vectors per K/V row
   constexpr int PER_T = KB * RV / kThreads;
   static_assert(KB * RV % kThreads == 0 && kThreads % KB == 0, "chunk must split over the workgroup");
-  constexpr int KP = D + 8;              // padded LDS rows (conflict-free fragment reads)
+  constexpr int KP = D + 8;              // padded LDS rows of V (transposing reads)
+  // K rows of D = 128 at 288 bytes: the score fragments' 16-byte reads (16 rows, 4 column
+  // groups) run at ~190 B/clk per CU against ~113 B/clk at 272 bytes (measured on gfx950;
+  // the transposing V reads run at ~110 B/clk at either pitch)
+  constexpr int KPK = D == 128 ? D + 16 : D + 8;
   // double-buffered: chunk c + 1 is staged into the other buffer while chunk c is consumed,
   // so one barrier per chunk orders both the reuse and the new contents
-  __shared__ __align__(16) uint16_t Ks[2][KB][KP];
+  __shared__ __align__(16) uint16_t Ks[2][KB][KPK];
   __shared__ __align__(16) uint16_t Vs[2][KB][KP];  // row-major like K; read through transpose loads
 
   const uint16_t* __restrict__ k_cache = static_cast<const uint16_t*>(a.k_cache);
@@ -584,6 +588,14 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- S^T = K Q^T: 64 keys x 16 rows per group ----
+    // every K fragment of the chunk is read before the first MFMA (the fence keeps the
+    // compiler from sinking the reads back next to their uses)
+    bf16x8 kfr[JT][DS];
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int t = 0; t < DS; ++t) kfr[jt][t] = *reinterpret_cast<const bf16x8*>(&Ks[buf][16 * jt + li][32 * t + 8 * lk]);
+    __builtin_amdgcn_sched_barrier(0);
     v4f s_acc[RG][JT];
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt) {
@@ -591,10 +603,9 @@ __global__ __launch_bounds__(kThreads, FI_PREFILL_BF16_WAVES) void prefill_bf16_
       for (int g = 0; g < RG; ++g) s_acc[g][jt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < DS; ++t) {
-        const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Ks[buf][16 * jt + li][32 * t + 8 * lk]);
 #pragma unroll
         for (int g = 0; g < RG; ++g)
-          s_acc[g][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qf[g][t], s_acc[g][jt], 0, 0, 0);
+          s_acc[g][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[jt][t], qf[g][t], s_acc[g][jt], 0, 0, 0);
       }
     }
     // causal / context mask only where the chunk reaches past the tile's first query position
@@ -993,21 +1004,19 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
     // (+ 16 for the upper half), d 16 dt + 4 (li % 4) .. + 3, and receives V at d = 16 dt + li
     // for keys 4 lk + e (+ 16)
     const int vrow = 4 * lk + (li >> 2), vcol = 4 * (li & 3);
-    bf16x8 vf[2][3];  // V^T fragments one d tile ahead, as the K fragments above
-    auto read_v = [&](int dt, int slot) {
+    // one d tile's V^T fragments at a time: the staging registers of the next chunk are live
+    // here, and a second slot (reads one tile ahead) measured slower for the spills it adds
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      bf16x8 vf[3];
 #pragma unroll
       for (int p = 0; p < 3; ++p) {
         const v4s lo = lds_read_tr16(&Vs[p][vrow][16 * dt + vcol]);
         const v4s hi = lds_read_tr16(&Vs[p][vrow + 16][16 * dt + vcol]);
-        vf[slot][p] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        vf[p] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
-    };
-    read_v(0, 0);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      if (dt + 1 < DT) read_v(dt + 1, (dt + 1) & 1);
-#pragma unroll
-      for (int g = 0; g < RG; ++g) o[g][dt] = mma6(vf[dt & 1], pp[g], o[g][dt]);
+      for (int g = 0; g < RG; ++g) o[g][dt] = mma6(vf, pp[g], o[g][dt]);
       __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();  // every wave is done with this chunk's K/V
