@@ -1,4 +1,4 @@
-// Paged decode attention (split-KV with a log-sum-exp merge kernel), KV append and
+// Paged decode attention (split-KV with a log-sum-exp merge), KV append and
 // block copy for gfx950.  The arithmetic replaces the reference's per-sequence gather +
 // online-softmax loops (crates/ferrisinfer-kernel/src/cpu/attention.rs:332-686,
 // runtime/paged_kv.rs:769-791).
@@ -84,6 +84,9 @@ struct DecodeArgs {
   const int* context_lens;
   float* part_acc;  // [num_seqs * Hq * parts_per_seq, D]
   float* part_ml;   // [num_seqs * Hq * parts_per_seq, 2]
+  // Merge in the partition kernel: one arrival counter per (sequence, kv head), zero between
+  // launches (the last arriver resets it).  Null: decode_merge_kernel merges.
+  unsigned* counters;
   float* out;
   uint32_t* faults;
   int num_seqs;
@@ -105,6 +108,84 @@ __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMI
 // before it stay ahead of the arithmetic after it (the ring's depth is what stays in flight).
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// A partial of another workgroup: a plain load after a kernel boundary, a device-coherent
+// load (past the XCDs' private L2s) inside the partition kernel.
+template <bool COHERENT>
+__device__ __forceinline__ float load_partial(float* p) {
+  if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
+// Combines the partitions of one (sequence, kv_head) group: M = max m_p,
+// L = sum l_p e^(m_p-M), out = sum acc_p e^(m_p-M) / L per query head.  The first
+// partitions' partials are fetched before the weights are known so the loads overlap.  The
+// same arithmetic, in the same order, runs in decode_merge_kernel and in the partition
+// kernel's last-arriving workgroup, so both give identical outputs.
+template <int D, int MAXG, bool COHERENT>
+__device__ __forceinline__ void merge_unit(const DecodeArgs& a, size_t head0, int nparts, float (*s_w)[kMaxParts],
+                                           float* s_inv) {
+  constexpr int kPrefetch = 8;
+  constexpr int kPerThread = (MAXG * D + kThreads - 1) / kThreads;
+  const int group = a.group;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int P = a.parts_per_seq;
+
+  float pre[kPerThread][kPrefetch];
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int i = tid + k * kThreads;
+    const int g = i / D, d = i % D;
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p)
+      pre[k][p] = (g < group && p < nparts) ? load_partial<COHERENT>(&a.part_acc[((head0 + g) * P + p) * D + d]) : 0.0f;
+  }
+  for (int g = w; g < group; g += 4) {
+    // each lane's (max, sum) pairs are read once and kept for the weights
+    constexpr int kPartsPerLane = kMaxParts / 64;
+    float* ml = a.part_ml + (head0 + g) * P * 2;
+    float2 mlv[kPartsPerLane];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPartsPerLane; ++j) {
+      const int p = lane + 64 * j;
+      if constexpr (COHERENT)
+        mlv[j] = p < nparts ? make_float2(load_partial<true>(&ml[2 * p]), load_partial<true>(&ml[2 * p + 1]))
+                            : make_float2(-INFINITY, 0.0f);
+      else
+        mlv[j] = p < nparts ? reinterpret_cast<const float2*>(ml)[p] : make_float2(-INFINITY, 0.0f);
+      m = fmaxf(m, mlv[j].x);
+    }
+    m = fi::wave_max(m);
+    float l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPartsPerLane; ++j) {
+      const int p = lane + 64 * j;
+      if (p < nparts) {
+        const float wgt = __expf(mlv[j].x - m);
+        s_w[g][p] = wgt;
+        l += mlv[j].y * wgt;
+      }
+    }
+    l = fi::wave_sum(l);
+    if (lane == 0) s_inv[g] = 1.0f / l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int i = tid + k * kThreads;
+    const int g = i / D, d = i % D;
+    if (g >= group) continue;
+    float acc = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) acc += pre[k][p] * (p < nparts ? s_w[g][p] : 0.0f);
+    for (int p = kPrefetch; p < nparts; ++p)
+      acc += load_partial<COHERENT>(&a.part_acc[((head0 + g) * P + p) * D + d]) * s_w[g][p];
+    a.out[(head0 + g) * D + d] = acc * s_inv[g];
+  }
+}
+
 // One workgroup = one (sequence, kv_head, partition of 4*WT tokens); partitions are
 // numbered fastest across (sequence, kv_head) so the first-dispatched workgroups hold the
 // full leading partitions and the ragged tails come last.  The GQA group of query heads
@@ -123,7 +204,9 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 //   combine: the waves' (max, sum, acc) are merged through LDS in wave order.
 // Rows past the end are clamped to the last valid row (same addresses, no extra traffic)
 // and carry probability 0.  A sequence with one partition writes its normalised output;
-// otherwise each workgroup stores (max, sum, unnormalised acc) for decode_merge_kernel.
+// otherwise each workgroup stores (max, sum, unnormalised acc), and the last workgroup of the
+// (sequence, kv_head) group to finish merges them (counters given), or decode_merge_kernel
+// does in a launch of its own.
 template <int D, typename KVT, int G, int WT>
 __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a) {
   constexpr int kWaveTokens = WT;
@@ -357,6 +440,13 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
     }
     if (nparts == 1) {
       a.out[(head0 + g) * D + d] = sum * (1.0f / l);
+    } else if (a.counters) {  // read by another workgroup of this launch: device-coherent stores
+      const size_t slot = (head0 + g) * a.parts_per_seq + part;
+      __hip_atomic_store(&a.part_acc[slot * D + d], sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(&a.part_ml[slot * 2], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&a.part_ml[slot * 2 + 1], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     } else {
       const size_t slot = (head0 + g) * a.parts_per_seq + part;
       a.part_acc[slot * D + d] = sum;
@@ -366,18 +456,35 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
       }
     }
   }
+  if (nparts <= 1 || a.counters == nullptr) return;  // workgroup-uniform
+
+  // ---- the last of the group's partitions to finish merges them ----
+  // Each thread waits until its coherent stores have completed, so when the counter shows
+  // every partition arrived, every partial is readable at the coherence point.  No cache-wide
+  // fence is used (a device-scope fence writes back the whole L2 of the XCD).  The last
+  // arriver resets the counter for the next launch or graph replay.
+  __shared__ float s_w[G][kMaxParts];
+  __shared__ float s_inv[G];
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned arrived =
+        __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    s_last = arrived == static_cast<unsigned>(nparts);
+    if (s_last) __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  merge_unit<D, G, true>(a, head0, nparts, s_w, s_inv);
 }
 
-// Combines the partitions of one (sequence, kv_head) group: M = max m_p,
-// L = sum l_p e^(m_p-M), out = sum acc_p e^(m_p-M) / L per query head.  Sequences with a
-// single partition were finished by the partition kernel.  A separate launch orders the
-// partials' stores before these loads.  The first partitions' partials are fetched before
-// the weights are known so the loads overlap.
+// The separate merge launch (used where the partition kernel does not merge): one workgroup
+// per (sequence, kv_head) group; sequences with a single partition were finished by the
+// partition kernel, and the launch boundary orders the partials' stores before these loads.
 template <int D, int MAXG, int WT>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   constexpr int kPartTokens = kWaves * WT;
-  constexpr int kPrefetch = 8;
-  constexpr int kPerThread = (MAXG * D + kThreads - 1) / kThreads;
   __shared__ float s_w[MAXG][kMaxParts];
   __shared__ float s_inv[MAXG];
   const int pair = blockIdx.x;
@@ -386,60 +493,8 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   const int ctx = min(a.context_lens[seq], a.parts_per_seq * kPartTokens);  // clamped as in the partitions
   const int nparts = (ctx + kPartTokens - 1) / kPartTokens;
   if (nparts <= 1) return;
-  const int group = a.group;
-  const int tid = threadIdx.x;
-  const int w = tid >> 6;
-  const int lane = tid & 63;
-  const size_t head0 = (size_t)seq * a.hq + (size_t)kvh * group;
-  const int P = a.parts_per_seq;
-
-  float pre[kPerThread][kPrefetch];
-#pragma unroll
-  for (int k = 0; k < kPerThread; ++k) {
-    const int i = tid + k * kThreads;
-    const int g = i / D, d = i % D;
-#pragma unroll
-    for (int p = 0; p < kPrefetch; ++p)
-      pre[k][p] = (g < group && p < nparts) ? a.part_acc[((head0 + g) * P + p) * D + d] : 0.0f;
-  }
-  for (int g = w; g < group; g += 4) {
-    // each lane's (max, sum) pairs are read once, as float2, and kept for the weights
-    constexpr int kPartsPerLane = kMaxParts / 64;
-    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + (head0 + g) * P;
-    float2 mlv[kPartsPerLane];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kPartsPerLane; ++j) {
-      const int p = lane + 64 * j;
-      mlv[j] = p < nparts ? ml[p] : make_float2(-INFINITY, 0.0f);
-      m = fmaxf(m, mlv[j].x);
-    }
-    m = fi::wave_max(m);
-    float l = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kPartsPerLane; ++j) {
-      const int p = lane + 64 * j;
-      if (p < nparts) {
-        const float wgt = __expf(mlv[j].x - m);
-        s_w[g][p] = wgt;
-        l += mlv[j].y * wgt;
-      }
-    }
-    l = fi::wave_sum(l);
-    if (lane == 0) s_inv[g] = 1.0f / l;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kPerThread; ++k) {
-    const int i = tid + k * kThreads;
-    const int g = i / D, d = i % D;
-    if (g >= group) continue;
-    float acc = 0.0f;
-#pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) acc += pre[k][p] * (p < nparts ? s_w[g][p] : 0.0f);
-    for (int p = kPrefetch; p < nparts; ++p) acc += a.part_acc[((head0 + g) * P + p) * D + d] * s_w[g][p];
-    a.out[(head0 + g) * D + d] = acc * s_inv[g];
-  }
+  const size_t head0 = (size_t)seq * a.hq + (size_t)kvh * a.group;
+  merge_unit<D, MAXG, false>(a, head0, nparts, s_w, s_inv);
 }
 
 // One workgroup per token: copies the token's [Hkv, D] K and V rows into their pool slot.
@@ -608,7 +663,7 @@ int32_t launch_decode_group(fi_context* ctx, const DecodeArgs& args, unsigned gr
                        0, ctx->stream, args);
   }
   FI_CHECK_LAUNCH("decode_partition_kernel");
-  if (args.parts_per_seq > 1) {
+  if (args.parts_per_seq > 1 && args.counters == nullptr) {
     const dim3 grid2(static_cast<unsigned>(args.num_seqs) * args.hkv);
     if (wt == FI_DECODE_WIDE_WAVE_TOKENS) {
       hipLaunchKernelGGL((decode_merge_kernel<D, G, FI_DECODE_WIDE_WAVE_TOKENS>), grid2, dim3(kThreads), 0, ctx->stream,
@@ -859,6 +914,15 @@ int32_t decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache, c
     }
   }
   const unsigned grid = static_cast<unsigned>(num_seqs) * num_kv_heads * parts;
+  // Small launches (at most six workgroups a CU, e.g. a decode tick of a small model) merge
+  // in the last-arriving partition workgroup: the separate merge launch's fixed cost is a large
+  // share there (C4 tick at batch 64: 2.375 against 2.403-2.410 ms).  Large launches keep the
+  // separate merge, where the merging workgroups' tail costs more than the launch (C2, 2048
+  // workgroups: 113.2 against 111.4 us).
+  const int64_t cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  if (parts > 1 && !noalloc && ctx->d_merge_counters != nullptr &&
+      static_cast<int64_t>(num_seqs) * num_kv_heads <= FI_MERGE_COUNTERS && static_cast<int64_t>(grid) <= 6 * cus)
+    args.counters = ctx->d_merge_counters;
   switch (head_dim) {
     case 32:
       return launch_decode_dtype<32>(ctx, kv_dtype, args, grid, wt);

@@ -20,6 +20,10 @@ enum : uint32_t {
   FI_FAULT_POSITION_RANGE = 1u << 7,    // RoPE: a position outside the cos/sin table
 };
 
+// Arrival counters a context holds for decode attention's in-kernel merge: launches with more
+// (sequence, kv head) groups than this merge in a separate launch.
+#define FI_MERGE_COUNTERS 65536
+
 struct fi_context {
   int device = 0;
   hipStream_t own_stream = nullptr;
@@ -33,6 +37,9 @@ struct fi_context {
   bool capturing = false;             // the stream is being captured into a graph
   void* sample_area = nullptr;        // fi_sample_reserve: per-row sort and replay arrays for top-k above 1024
   size_t sample_bytes = 0;
+  // decode attention: arrival counters of the split-KV merge, one per (sequence, kv head),
+  // FI_MERGE_COUNTERS of them, zeroed at create; each launch leaves them zero
+  unsigned* d_merge_counters = nullptr;
 };
 
 // A captured and instantiated launch sequence of one context's stream.

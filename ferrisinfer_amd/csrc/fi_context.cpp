@@ -90,8 +90,18 @@ int32_t fi_ctx_create(int32_t ordinal, fi_context** out) {
     delete ctx;
     return fi::hip_error(err, "hipMalloc(fault flags)");
   }
+  err = hipMalloc(&ctx->d_merge_counters, FI_MERGE_COUNTERS * sizeof(unsigned));
+  if (err == hipSuccess) err = hipMemset(ctx->d_merge_counters, 0, FI_MERGE_COUNTERS * sizeof(unsigned));
+  if (err != hipSuccess) {
+    if (ctx->d_merge_counters) (void)hipFree(ctx->d_merge_counters);
+    (void)hipFree(ctx->d_faults);
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return fi::hip_error(err, "hipMalloc(merge counters)");
+  }
   int32_t st = fi::decode_noalloc_attach(ctx);
   if (st != FI_OK) {
+    (void)hipFree(ctx->d_merge_counters);
     (void)hipFree(ctx->d_faults);
     (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -113,6 +123,7 @@ int32_t fi_ctx_destroy(fi_context* ctx) {
   if (ctx->workspace) (void)hipFree(ctx->workspace);
   if (ctx->sample_area) (void)hipFree(ctx->sample_area);
   if (ctx->d_faults) (void)hipFree(ctx->d_faults);
+  if (ctx->d_merge_counters) (void)hipFree(ctx->d_merge_counters);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
   return FI_OK;

@@ -159,6 +159,49 @@ def test_decode_split_merge_repeatable(gpu_ctx, shape):
 
 
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [
+    (64, 1, 2300, 14, 2, 64),    # a C4 decode tick at batch 64: up to 9 partitions of 256 tokens
+    (6, 600, 4096, 32, 8, 128),  # few long sequences at the C5 head shape: up to 8 of 512
+])
+def test_decode_in_kernel_merge_matches_merge_launch(orc, gpu_ctx, kv_dtype, shape):
+    """Small launches (at most six workgroups a CU) merge the split-KV partials in the
+    partition kernel's last-arriving workgroup, with device-coherent stores and loads and a
+    per-(sequence, kv head) arrival counter.  The no-allocation entry point always merges in
+    a separate launch: both must give bit-identical outputs, three launches in a row (the
+    counters are reset by each launch's last arrivers), and match the oracle."""
+    import torch
+
+    import oracle
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    n, lo, hi, hq, hkv, d = shape
+    wl = paged_decode_c2(seed=31, num_seqs=n, min_len=lo, max_len=hi, num_q_heads=hq,
+                         num_kv_heads=hkv, head_dim=d, num_blocks=12288)
+    parts = -(-int(wl.max_context_len) // (256 if hkv * d < 512 else 512))
+    assert parts > 1 and n * hkv * parts <= 6 * 256, "the shape must take the in-kernel merge"
+    if kv_dtype == "bf16":
+        kp = torch.from_numpy(oracle.f32_to_bf16(wl.k_pool).view(np.int16)).cuda()
+        vp = torch.from_numpy(oracle.f32_to_bf16(wl.v_pool).view(np.int16)).cuda()
+        dt = DTYPE_BF16
+    else:
+        kp, vp, dt = _dev(wl.k_pool, torch), _dev(wl.v_pool, torch), DTYPE_F32
+    q, bt, cl = _dev(wl.q, torch), _dev(wl.block_tables, torch), _dev(wl.context_lens, torch)
+    args = (wl.max_context_len, wl.num_kv_heads, wl.block_size, wl.num_blocks, wl.scale)
+    sep = torch.full_like(q, float("nan"))
+    gpu_ctx.attn_decode_paged_noalloc(q, kp, vp, dt, bt, cl, *args, sep)
+    outs = [torch.full_like(q, float("nan")) for _ in range(3)]
+    for o in outs:
+        gpu_ctx.attn_decode_paged(q, kp, vp, dt, bt, cl, *args, o)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    for o in outs:
+        assert torch.equal(o, sep)
+    ref = oracle_decode(orc, wl, kv_dtype)
+    assert normwise_error(outs[0].cpu().numpy(), ref) < (F32_TOL if kv_dtype == "f32" else BF16_TOL)
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("d,misaligned", [(64, False), (6, False), (64, True)])
 def test_kv_append_scatter_exact(orc, gpu_ctx, kv_dtype, d, misaligned):
     """fi_kv_append writes each token row to block_id*bs+offset, bit-exact (bf16: RNE): the
