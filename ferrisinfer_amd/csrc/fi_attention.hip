@@ -87,6 +87,21 @@ struct DecodeArgs {
   // Merge in the partition kernel: one arrival counter per (sequence, kv head), zero between
   // launches (the last arriver resets it).  Null: decode_merge_kernel merges.
   unsigned* counters;
+  // Fused q|k|v consumer (decode ticks, one new token per sequence), when qkv_parts is set:
+  // every workgroup forms its group's query rows from the q|k|v projection's split-K partials
+  // (+ bias, RoPE) instead of reading q, and the last partition's workgroup of each
+  // (sequence, kv head) first writes the new token's K/V row into the pool at slots[seq].
+  const float* qkv_parts;  // [qkv_splits][num_seqs][Hq D + 2 Hkv D]
+  int qkv_splits;
+  const float* bias_q;
+  const float* bias_k;
+  const float* bias_v;
+  const int* positions;  // [num_seqs] RoPE positions
+  const float* cos_t;    // [max_positions][rotary_dims / 2]
+  const float* sin_t;
+  int rotary_dims;
+  int max_positions;
+  const int64_t* slots;  // [num_seqs] pool slots of the new tokens
   float* out;
   uint32_t* faults;
   int num_seqs;
@@ -186,6 +201,75 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, size_t head0, in
   }
 }
 
+// The fused q|k|v consumer's share of one workgroup: the group's query rows into s_q and,
+// with `append`, the new token's K and V rows of kv head kvh into the pool.  The arithmetic
+// is qkv_rope_append4_kernel's (fi::qkv_value4, fi::rope4, fi::put_kv4), so the rows equal
+// that kernel's bit for bit.
+template <int D, typename KVT, int G>
+__device__ __forceinline__ void qkv_prologue(const DecodeArgs& a, int seq, int kvh, bool append, float (*s_q)[D],
+                                             int tid) {
+  const int half = a.rotary_dims / 2;
+  const int pass = D - 2 * half;
+  const int qph = (half + pass) / 4;  // four-column items per head row
+  const int group = a.group;
+  const int qw = a.hq * D, kw = a.hkv * D;
+  const int width = qw + 2 * kw;
+  const size_t plane = (size_t)a.num_seqs * width;
+  const float* p0 = a.qkv_parts + (size_t)seq * width;
+  const int64_t pool_slots = (int64_t)a.num_blocks * a.block_size;
+  const int64_t slot = a.slots[seq];
+  const bool write_kv = append && slot >= 0 && slot < pool_slots;
+  if (append && tid == 0 && slot >= pool_slots) atomicOr(a.faults, FI_FAULT_SLOT_RANGE);
+  const int64_t blk = write_kv ? slot / a.block_size : 0;
+  const int off = write_kv ? static_cast<int>(slot % a.block_size) : 0;
+  const size_t row = (((size_t)blk * a.hkv + kvh) * a.block_size + off) * D;
+  KVT* k_pool = static_cast<KVT*>(const_cast<void*>(a.k_cache));
+  KVT* v_pool = static_cast<KVT*>(const_cast<void*>(a.v_cache));
+  const int rot_items = (group + (write_kv ? 1 : 0)) * qph;
+  const int items = rot_items + (write_kv ? D / 4 : 0);
+  for (int idx = tid; idx < items; idx += kThreads) {
+    if (idx < rot_items) {
+      const int g = idx / qph, r = 4 * (idx - g * qph);
+      const bool is_q = g < group;
+      const int col0 = is_q ? (kvh * group + g) * D : qw + kvh * D;
+      const int bcol0 = is_q ? (kvh * group + g) * D : kvh * D;
+      const float* bias = is_q ? a.bias_q : a.bias_k;
+      if (r < half) {
+        int pos = a.positions[seq];
+        if (pos < 0 || pos >= a.max_positions) {
+          atomicOr(a.faults, FI_FAULT_POSITION_RANGE);
+          pos = 0;
+        }
+        const float4 lo = fi::qkv_value4(p0, plane, a.qkv_splits, bias, bcol0 + r, col0 + r);
+        const float4 hi = fi::qkv_value4(p0, plane, a.qkv_splits, bias, bcol0 + r + half, col0 + r + half);
+        const float4 c = *reinterpret_cast<const float4*>(a.cos_t + (size_t)pos * half + r);
+        const float4 sn = *reinterpret_cast<const float4*>(a.sin_t + (size_t)pos * half + r);
+        float4 y0, y1;
+        fi::rope4(lo, hi, c, sn, y0, y1);
+        if (is_q) {
+          *reinterpret_cast<float4*>(&s_q[g][r]) = y0;
+          *reinterpret_cast<float4*>(&s_q[g][r + half]) = y1;
+        } else {
+          fi::put_kv4(k_pool, row + r, y0);
+          fi::put_kv4(k_pool, row + r + half, y1);
+        }
+      } else {
+        const int i = 2 * half + (r - half);
+        const float4 y = fi::qkv_value4(p0, plane, a.qkv_splits, bias, bcol0 + i, col0 + i);
+        if (is_q) {
+          *reinterpret_cast<float4*>(&s_q[g][i]) = y;
+        } else {
+          fi::put_kv4(k_pool, row + i, y);
+        }
+      }
+    } else {
+      const int i = 4 * (idx - rot_items);
+      const float4 x = fi::qkv_value4(p0, plane, a.qkv_splits, a.bias_v, kvh * D + i, qw + kw + kvh * D + i);
+      fi::put_kv4(v_pool, row + i, x);
+    }
+  }
+}
+
 // One workgroup = one (sequence, kv_head, partition of 4*WT tokens); partitions are
 // numbered fastest across (sequence, kv_head) so the first-dispatched workgroups hold the
 // full leading partitions and the ragged tails come last.  The GQA group of query heads
@@ -234,6 +318,7 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   static_assert(kWaveTokens % KR == 0 && kWaveTokens % VR == 0, "wave chunk must tile the rows");
 
   __shared__ uint32_t s_row[kPartTokens];
+  __shared__ float s_q[G][D];  // fused q|k|v: the group's query rows
   __shared__ float s_p[kWaves][kWaveTokens][G];
   __shared__ float s_ml[kWaves][G][2];
   __shared__ float s_acc[kWaves][G][D];
@@ -253,9 +338,11 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
     ctx = a.parts_per_seq * kPartTokens;
   }
   const size_t head0 = (size_t)seq * a.hq + (size_t)kvh * group;  // first query head of the group
-  if (ctx <= 0) {  // no keys: defined output of zeros
+  const bool fused = a.qkv_parts != nullptr;  // uniform
+  if (ctx <= 0) {  // no keys: defined output of zeros (the new token's K/V still appended)
     if (part == 0) {
       for (int i = tid; i < group * D; i += kThreads) a.out[head0 * D + i] = 0.0f;
+      if (fused) qkv_prologue<D, KVT, G>(a, seq, kvh, true, s_q, tid);
     }
     return;
   }
@@ -271,29 +358,39 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   // K-pass lane roles: row r of each step, vector column c
   const int r = lane / KL;
   const int c = lane % KL;
+  // this lane's slice of the group's query rows: from q (issued before the block lookups, so
+  // the loads overlap them), or from the fused consumer's rows in LDS after the barrier below
   float qreg[G][KE];
+  auto load_q = [&](const float* src, size_t stride) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int j = 0; j < KV; ++j) {
-      float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
-      if (g < group) {
-        const float* qp = a.q + (head0 + g) * D + (j * KL + c) * EPV;
-        lo = *reinterpret_cast<const float4*>(qp);
-        if constexpr (EPV == 8) hi = *reinterpret_cast<const float4*>(qp + 4);
+      for (int j = 0; j < KV; ++j) {
+        float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+        if (g < group) {
+          const float* qp = src + g * stride + (j * KL + c) * EPV;
+          lo = *reinterpret_cast<const float4*>(qp);
+          if constexpr (EPV == 8) hi = *reinterpret_cast<const float4*>(qp + 4);
+        }
+        float* dst = &qreg[g][j * EPV];
+        dst[0] = lo.x;
+        dst[1] = lo.y;
+        dst[2] = lo.z;
+        dst[3] = lo.w;
+        if constexpr (EPV == 8) {
+          dst[4] = hi.x;
+          dst[5] = hi.y;
+          dst[6] = hi.z;
+          dst[7] = hi.w;
+        }
       }
-      float* dst = &qreg[g][j * EPV];
-      dst[0] = lo.x;
-      dst[1] = lo.y;
-      dst[2] = lo.z;
-      dst[3] = lo.w;
-      if constexpr (EPV == 8) {
-        dst[4] = hi.x;
-        dst[5] = hi.y;
-        dst[6] = hi.z;
-        dst[7] = hi.w;
-      }
-    }
+  };
+  if (fused) {
+    // the last partition holds the new token: its K/V row is written before the keys are read
+    qkv_prologue<D, KVT, G>(a, seq, kvh, part == nparts - 1, s_q, tid);
+  } else {
+    load_q(a.q + head0 * D, D);
+  }
   {
     const int bs = a.block_size;
     for (int t = tid; t < n_part; t += kThreads) {
@@ -307,7 +404,10 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
       s_row[t] = (static_cast<uint32_t>(id) * a.hkv + kvh) * bs + (pos - lb * bs);
     }
   }
+  // orders the fused consumer's query rows (LDS) and the new token's K/V row (global memory,
+  // written by this workgroup) before their reads
   __syncthreads();
+  if (fused) load_q(&s_q[0][0], D);
 
   if (n > 0) {  // wave-uniform
     const uint32_t* rows = s_row + wt0;
@@ -853,11 +953,26 @@ namespace {
 // Shared by both decode entry points: validation, launch shape and launches.  With
 // `noalloc` the partials go to the library's fixed scratch array instead of the context
 // workspace (nothing is allocated).
+// The fused q|k|v consumer's inputs (fi_attn_decode_paged_qkv).
+struct QkvIn {
+  const float* parts;
+  int32_t splits;
+  const float* bias_q;
+  const float* bias_k;
+  const float* bias_v;
+  const int32_t* positions;
+  const float* cos_t;
+  const float* sin_t;
+  int32_t rotary_dims;
+  int32_t max_positions;
+  const int64_t* slots;
+};
+
 int32_t decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache, const void* d_v_cache,
                      int32_t kv_dtype, const int32_t* d_block_tables, int32_t max_blocks_per_seq,
                      const int32_t* d_context_lens, int32_t num_seqs, int32_t max_context_len,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                     int32_t num_blocks, float scale, float* d_out, bool noalloc) {
+                     int32_t num_blocks, float scale, float* d_out, bool noalloc, const QkvIn* qkv = nullptr) {
   FI_TRY(fi::enter(ctx));
   FI_REQUIRE(num_seqs >= 0 && max_context_len >= 0, FI_ERR_INVALID_SHAPE,
              "fi_attn_decode_paged: negative sizes");
@@ -875,9 +990,28 @@ int32_t decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache, c
   const int part_tokens = kWaves * wt;
   FI_REQUIRE(max_context_len <= part_tokens * kMaxParts, FI_ERR_UNSUPPORTED,
              "fi_attn_decode_paged: context longer than " + std::to_string(part_tokens * kMaxParts) + " tokens");
+  if (qkv) {
+    FI_REQUIRE(qkv->splits >= 1, FI_ERR_INVALID_SHAPE, "fi_attn_decode_paged_qkv: splits must be at least 1");
+    FI_REQUIRE(qkv->rotary_dims >= 0 && qkv->rotary_dims <= head_dim && qkv->rotary_dims % 2 == 0,
+               FI_ERR_INVALID_CONFIG, "rope.rotary_dims must be even and at most the head dimension");
+    const int32_t half = qkv->rotary_dims / 2, pass = head_dim - 2 * half;
+    FI_REQUIRE(half % 4 == 0 && pass % 4 == 0, FI_ERR_UNSUPPORTED,
+               "fi_attn_decode_paged_qkv: rotary_dims / 2 and the pass-through width must be multiples of 4");
+  }
   if (num_seqs == 0) return FI_OK;
-  FI_REQUIRE(d_q && d_k_cache && d_v_cache && d_block_tables && d_context_lens && d_out,
+  FI_REQUIRE((d_q || qkv) && d_k_cache && d_v_cache && d_block_tables && d_context_lens && d_out,
              FI_ERR_INVALID_CONFIG, "fi_attn_decode_paged: null pointer");
+  if (qkv) {
+    auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    FI_REQUIRE(qkv->parts && qkv->positions && qkv->slots, FI_ERR_INVALID_CONFIG,
+               "fi_attn_decode_paged_qkv: null pointer");
+    FI_REQUIRE(qkv->rotary_dims == 0 || (qkv->cos_t && qkv->sin_t && qkv->max_positions > 0), FI_ERR_INVALID_CONFIG,
+               "fi_attn_decode_paged_qkv: rope tables required");
+    FI_REQUIRE(aligned16(qkv->parts) && (!qkv->bias_q || aligned16(qkv->bias_q)) &&
+                   (!qkv->bias_k || aligned16(qkv->bias_k)) && (!qkv->bias_v || aligned16(qkv->bias_v)) &&
+                   (qkv->rotary_dims == 0 || (aligned16(qkv->cos_t) && aligned16(qkv->sin_t))),
+               FI_ERR_INVALID_CONFIG, "fi_attn_decode_paged_qkv: partials, biases and rope tables must be 16-byte aligned");
+  }
   const int32_t parts = max_context_len == 0 ? 1 : (max_context_len + part_tokens - 1) / part_tokens;
   DecodeArgs args{};
   args.q = d_q;
@@ -896,6 +1030,20 @@ int32_t decode_paged(fi_context* ctx, const float* d_q, const void* d_k_cache, c
   args.block_size = block_size;
   args.num_blocks = num_blocks;
   args.scale = scale;
+  if (qkv) {
+    args.q = nullptr;
+    args.qkv_parts = qkv->parts;
+    args.qkv_splits = qkv->splits;
+    args.bias_q = qkv->bias_q;
+    args.bias_k = qkv->bias_k;
+    args.bias_v = qkv->bias_v;
+    args.positions = qkv->positions;
+    args.cos_t = qkv->cos_t;
+    args.sin_t = qkv->sin_t;
+    args.rotary_dims = qkv->rotary_dims;
+    args.max_positions = qkv->max_positions;
+    args.slots = qkv->slots;
+  }
   if (parts > 1) {
     if (noalloc) {
       const size_t slots = static_cast<size_t>(num_seqs) * num_q_heads * parts;
@@ -946,6 +1094,21 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
   return decode_paged(ctx, d_q, d_k_cache, d_v_cache, kv_dtype, d_block_tables, max_blocks_per_seq,
                       d_context_lens, num_seqs, max_context_len, num_q_heads, num_kv_heads, head_dim,
                       block_size, num_blocks, scale, d_out, false);
+}
+
+int32_t fi_attn_decode_paged_qkv(fi_context* ctx, const float* d_qkv_parts, int32_t splits, const float* d_bias_q,
+                                 const float* d_bias_k, const float* d_bias_v, const int32_t* d_positions,
+                                 const float* d_cos, const float* d_sin, int32_t rotary_dims, int32_t max_positions,
+                                 const int64_t* d_slot_mapping, void* d_k_cache, void* d_v_cache, int32_t kv_dtype,
+                                 const int32_t* d_block_tables, int32_t max_blocks_per_seq,
+                                 const int32_t* d_context_lens, int32_t num_seqs, int32_t max_context_len,
+                                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t num_blocks, float scale, float* d_out) {
+  const QkvIn qkv{d_qkv_parts, splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin,
+                  rotary_dims, max_positions, d_slot_mapping};
+  return decode_paged(ctx, nullptr, d_k_cache, d_v_cache, kv_dtype, d_block_tables, max_blocks_per_seq,
+                      d_context_lens, num_seqs, max_context_len, num_q_heads, num_kv_heads, head_dim,
+                      block_size, num_blocks, scale, d_out, false, &qkv);
 }
 
 int32_t fi_attn_decode_paged_noalloc(fi_context* ctx, const float* d_q, const void* d_k_cache,

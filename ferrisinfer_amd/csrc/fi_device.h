@@ -66,4 +66,66 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return w >> 16;
 }
 
+// ---- the q|k|v consumer's arithmetic (split-K sum + bias, RoPE, pool store), shared by
+// qkv_rope_append4_kernel and decode attention's fused q|k|v prologue so both give identical
+// values ----
+
+__device__ __forceinline__ float add(float a, float b) { return a + b; }
+__device__ __forceinline__ float4 add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+// sum over z < splits of p[z * plane], added in split order; the split loads are issued in
+// batches of eight before their adds (one memory latency per batch)
+template <typename T>
+__device__ __forceinline__ T sum_splits(const T* __restrict__ p, size_t plane, int splits) {
+  T x = p[0];
+  for (int z0 = 1; z0 < splits; z0 += 8) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int z = z0 + u;
+      v[u] = p[(size_t)(z < splits ? z : 0) * plane];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (z0 + u < splits) x = add(x, v[u]);
+    }
+  }
+  return x;
+}
+
+// Four consecutive columns of the q|k|v projection: the split-K partials [splits][tokens][width]
+// of one token (p0 = its row in split 0) summed in split order, plus the bias, if any.
+__device__ __forceinline__ float4 qkv_value4(const float* __restrict__ p0, size_t plane, int splits,
+                                             const float* __restrict__ bias, int bias_col, int col) {
+  float4 x = sum_splits(reinterpret_cast<const float4*>(p0 + col), plane / 4, splits);
+  if (bias) x = add(x, *reinterpret_cast<const float4*>(bias + bias_col));
+  return x;
+}
+
+// RoPE of four consecutive rotary pairs (lo, hi) = (x[i], x[i + half]) with their cos / sin:
+// y0 = lo cos - hi sin, y1 = hi cos + lo sin, each product rounded before the add
+// (kernel/cpu/attention.rs:165-220).
+__device__ __forceinline__ void rope4(const float4& lo, const float4& hi, const float4& c, const float4& sn,
+                                      float4& y0, float4& y1) {
+#pragma clang fp contract(off)
+  y0 = make_float4(lo.x * c.x - hi.x * sn.x, lo.y * c.y - hi.y * sn.y, lo.z * c.z - hi.z * sn.z,
+                   lo.w * c.w - hi.w * sn.w);
+  y1 = make_float4(hi.x * c.x + lo.x * sn.x, hi.y * c.y + lo.y * sn.y, hi.z * c.z + lo.z * sn.z,
+                   hi.w * c.w + lo.w * sn.w);
+}
+
+// Four consecutive pool elements from one 16-byte (f32) or 8-byte (bf16, nearest even) store;
+// idx is a multiple of 4 (the pool's rows are D elements, D a multiple of 4).
+template <typename KVT>
+__device__ __forceinline__ void put_kv4(KVT* cache, size_t idx, const float4& x) {
+  if constexpr (sizeof(KVT) == 4) {
+    *reinterpret_cast<float4*>(cache + idx) = x;
+  } else {
+    uint2 w;
+    w.x = f32_to_bf16_bits(x.x) | (f32_to_bf16_bits(x.y) << 16);
+    w.y = f32_to_bf16_bits(x.z) | (f32_to_bf16_bits(x.w) << 16);
+    *reinterpret_cast<uint2*>(cache + idx) = w;
+  }
+}
+
 }  // namespace fi

@@ -806,26 +806,11 @@ template <>
 __device__ __forceinline__ float zero_like<float>() { return 0.0f; }
 template <>
 __device__ __forceinline__ float4 zero_like<float4>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
-__device__ __forceinline__ float add(float a, float b) { return a + b; }
-__device__ __forceinline__ float4 add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
-
-template <typename T>
-__device__ __forceinline__ T sum_splits(const T* __restrict__ p, size_t plane, int splits) {
-  T x = p[0];
-  for (int z0 = 1; z0 < splits; z0 += 8) {
-    T v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int z = z0 + u;
-      v[u] = p[(size_t)(z < splits ? z : 0) * plane];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (z0 + u < splits) x = add(x, v[u]);
-    }
-  }
-  return x;
-}
+using fi::add;
+using fi::put_kv4;
+using fi::qkv_value4;
+using fi::rope4;
+using fi::sum_splits;
 
 // One workgroup per row: h = sum_z parts[z][row] (+ bias) + residual -> sum_out; out =
 // rms_norm(h) * w (reduction.rs:3-73: ms = sum(x^2)/H, inv = 1/sqrt(ms + eps), (x*inv)*w).
@@ -938,19 +923,6 @@ __device__ __forceinline__ void put_kv(KVT* cache, size_t idx, float x) {
   }
 }
 
-// Four consecutive pool elements from one 16-byte (f32) or 8-byte (bf16) store; idx is a
-// multiple of 4 (the pool's rows are D elements, D a multiple of 4).
-template <typename KVT>
-__device__ __forceinline__ void put_kv4(KVT* cache, size_t idx, const float4& x) {
-  if constexpr (sizeof(KVT) == 4) {
-    *reinterpret_cast<float4*>(cache + idx) = x;
-  } else {
-    uint2 w;
-    w.x = fi::f32_to_bf16_bits(x.x) | (fi::f32_to_bf16_bits(x.y) << 16);
-    w.y = fi::f32_to_bf16_bits(x.z) | (fi::f32_to_bf16_bits(x.w) << 16);
-    *reinterpret_cast<uint2*>(cache + idx) = w;
-  }
-}
 
 // The split-K sum of one column of the fused q|k|v partials (splits added in order) plus its
 // bias, if any.
@@ -1032,13 +1004,6 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
 
 // The split-K sum of one float4 of the fused q|k|v partials (splits added in order) plus its
 // bias, if any: column col of the [T, Hq*D + 2*Hkv*D] row at p0.
-__device__ __forceinline__ float4 qkv_value4(const float* __restrict__ p0, size_t plane, int splits,
-                                             const float* __restrict__ bias, int bias_col, int col) {
-  // the split loads are issued in batches before their adds (one memory latency per batch)
-  float4 x = sum_splits(reinterpret_cast<const float4*>(p0 + col), plane / 4, splits);
-  if (bias) x = add(x, *reinterpret_cast<const float4*>(bias + bias_col));
-  return x;
-}
 
 // Four consecutive columns per thread: the same per-element arithmetic as
 // qkv_rope_append_kernel (splits summed in order, bias added, RoPE with each product rounded
@@ -1091,10 +1056,8 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append4_kernel(
       const float4 hi = qkv_value4(p0, plane, splits, bias, bcol0 + r + half, col0 + r + half);
       const float4 c = *reinterpret_cast<const float4*>(cos_t + (size_t)pos * half + r);
       const float4 sn = *reinterpret_cast<const float4*>(sin_t + (size_t)pos * half + r);
-      const float4 y0 = make_float4(lo.x * c.x - hi.x * sn.x, lo.y * c.y - hi.y * sn.y, lo.z * c.z - hi.z * sn.z,
-                                    lo.w * c.w - hi.w * sn.w);
-      const float4 y1 = make_float4(hi.x * c.x + lo.x * sn.x, hi.y * c.y + lo.y * sn.y, hi.z * c.z + lo.z * sn.z,
-                                    hi.w * c.w + lo.w * sn.w);
+      float4 y0, y1;
+      rope4(lo, hi, c, sn, y0, y1);
       if (is_q) {
         *reinterpret_cast<float4*>(qdst + r) = y0;
         *reinterpret_cast<float4*>(qdst + r + half) = y1;

@@ -363,6 +363,9 @@ void ForwardExecutor::enqueue(const Plan& p) {
   const int32_t hkv = c.num_key_value_heads, D = c.head_dim(), W = H + 2 * hkv * D;
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // attention.rs:659
   const bool bf16 = model_->weight_dtype() == FI_DTYPE_BF16;
+  // the fused decode path needs four-column RoPE items (rotary_dims / 2 and the pass-through
+  // width multiples of 4)
+  const bool fused_qkv_decode = (c.rotary_dims / 2) % 4 == 0 && (D - c.rotary_dims) % 4 == 0;
   float* hidden = hidden_.f32();
   float* normed = normed_.f32();
   float* q = q_.f32();
@@ -377,22 +380,38 @@ void ForwardExecutor::enqueue(const Plan& p) {
     const DeviceModel::Layer& w = model_->layer(l);
     const DeviceModel::Packed& pk = model_->packed(l);
     projection(normed, H, pk.qkv, H, W, DeviceModel::kQkvPack, T, p.s_qkv, part);
-    check(fi_qkv_rope_append(ctx_, part, p.s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), p.pos,
-                             model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(), p.slot,
-                             pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(), pool_->block_size(), T,
-                             hq, hkv, D, q));
-    if (p.n_copy > 0) {
-      check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.cs, p.cd, p.cc, p.n_copy,
-                              pool_->num_blocks(), pool_->block_size(), hkv, D));
-    }
-    if (p.kind == BatchKind::Decode) {
-      check(fi_attn_decode_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.ctx, B,
-                                 p.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
-                                 attn));
+    if (p.kind == BatchKind::Decode && fused_qkv_decode) {
+      // one launch: every attention workgroup forms its query rows from the partials and the
+      // last partition of each sequence appends the new token's K/V before reading the keys.
+      // The copy-on-write copies only committed rows, never the new token's slot, so it may
+      // run first.
+      if (p.n_copy > 0) {
+        check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.cs, p.cd, p.cc, p.n_copy,
+                                pool_->num_blocks(), pool_->block_size(), hkv, D));
+      }
+      check(fi_attn_decode_paged_qkv(ctx_, part, p.s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), p.pos,
+                                     model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(),
+                                     p.slot, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.ctx, B,
+                                     p.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
+                                     attn));
     } else {
-      check(fi_attn_prefill_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.cu,
-                                  p.ctx, B, p.max_query_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(),
-                                  scale, attn));
+      check(fi_qkv_rope_append(ctx_, part, p.s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), p.pos,
+                               model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(),
+                               p.slot, pool_->k(l), pool_->v(l), pool_->kv_dtype(), pool_->num_blocks(),
+                               pool_->block_size(), T, hq, hkv, D, q));
+      if (p.n_copy > 0) {
+        check(fi_kv_copy_blocks(ctx_, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.cs, p.cd, p.cc, p.n_copy,
+                                pool_->num_blocks(), pool_->block_size(), hkv, D));
+      }
+      if (p.kind == BatchKind::Decode) {
+        check(fi_attn_decode_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.ctx,
+                                   B, p.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
+                                   attn));
+      } else {
+        check(fi_attn_prefill_paged(ctx_, q, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.cu,
+                                    p.ctx, B, p.max_query_len, hq, hkv, D, pool_->block_size(),
+                                    pool_->num_blocks(), scale, attn));
+      }
     }
     projection(attn, H, pk.wo, H, H, DeviceModel::kWoPack, T, p.s_o, part);
     check(fi_splitk_residual_rms_norm(ctx_, part, p.s_o, w.wo_bias.f32(), hidden, h1, w.ffn_norm.f32(), normed, T, H,

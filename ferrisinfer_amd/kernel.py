@@ -60,6 +60,8 @@ _SIGNATURES = {
     "fi_kv_gather": [_P, _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P],
     "fi_attn_decode_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                              _I32, _F32, _P],
+    "fi_attn_decode_paged_qkv": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I32, _P, _I32,
+                                 _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
     "fi_attn_decode_paged_noalloc": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32,
                                      _I32, _I32, _F32, _P],
     "fi_attn_prefill_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32,
@@ -240,6 +242,21 @@ class Context:
                                             ptr(context_lens), num_seqs, int(max_context_len),
                                             num_q_heads, num_kv_heads, head_dim, block_size,
                                             num_blocks, float(scale), ptr(out)))
+
+    def attn_decode_paged_qkv(self, parts, splits, biases, positions, cos_t, sin_t, rotary_dims,
+                              max_positions, slot_mapping, k_cache, v_cache, kv_dtype, block_tables,
+                              context_lens, max_context_len, num_q_heads, num_kv_heads, head_dim,
+                              block_size, num_blocks, scale, out):
+        """qkv_rope_append + attn_decode_paged in one launch (one new token per sequence)."""
+        bq, bk, bv = biases if biases is not None else (None, None, None)
+        check(self.lib.fi_attn_decode_paged_qkv(self.handle, ptr(parts), int(splits), ptr(bq), ptr(bk),
+                                                ptr(bv), ptr(positions), ptr(cos_t), ptr(sin_t),
+                                                int(rotary_dims), int(max_positions), ptr(slot_mapping),
+                                                ptr(k_cache), ptr(v_cache), int(kv_dtype), ptr(block_tables),
+                                                int(block_tables.shape[1]), ptr(context_lens),
+                                                int(context_lens.numel()), int(max_context_len),
+                                                int(num_q_heads), int(num_kv_heads), int(head_dim),
+                                                int(block_size), int(num_blocks), float(scale), ptr(out)))
 
     def attn_decode_paged_noalloc(self, q, k_cache, v_cache, kv_dtype, block_tables, context_lens,
                                   max_context_len, num_kv_heads, block_size, num_blocks, scale, out):

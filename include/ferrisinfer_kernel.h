@@ -186,6 +186,29 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                              int32_t num_blocks, float scale, float* d_out);
 
+/* A decode step's attention with the q|k|v consumer folded in: fi_qkv_rope_append followed by
+ * fi_attn_decode_paged in one launch, for batches of one new token per sequence (sequence b's
+ * token is row b of the projection).  Replaces the bias adds, rope_f32, the
+ * KvCacheStorage::write_*_f32 append and the paged decode attention of the block
+ * (runtime/reference.rs:163-300, 497-508; kernel/cpu/attention.rs:165-220, 332-686;
+ * runtime/kv_cache.rs:48-62).  The arguments are those two calls' (the pools are written:
+ * sequence b's new K/V row lands at slot_mapping[b], which must lie inside context_lens[b]
+ * through the block table).  Every workgroup of the attention forms its query rows from
+ * qkv_parts [splits, num_seqs, (Hq + 2 Hkv) * D] (+ biases, each may be NULL, + RoPE at
+ * positions[b]); the workgroup holding a sequence's last partition appends the K/V row of its
+ * kv head before reading the keys.  Outputs and the pool contents equal those of the two
+ * calls bit for bit.  rotary_dims / 2 and head_dim - rotary_dims must be multiples of 4
+ * (Unsupported otherwise); the partials, biases and RoPE tables 16-byte aligned.  A slot or a
+ * position out of range is reported as by fi_qkv_rope_append. */
+int32_t fi_attn_decode_paged_qkv(fi_context* ctx, const float* d_qkv_parts, int32_t splits, const float* d_bias_q,
+                                 const float* d_bias_k, const float* d_bias_v, const int32_t* d_positions,
+                                 const float* d_cos, const float* d_sin, int32_t rotary_dims, int32_t max_positions,
+                                 const int64_t* d_slot_mapping, void* d_k_cache, void* d_v_cache, int32_t kv_dtype,
+                                 const int32_t* d_block_tables, int32_t max_blocks_per_seq,
+                                 const int32_t* d_context_lens, int32_t num_seqs, int32_t max_context_len,
+                                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t num_blocks, float scale, float* d_out);
+
 /* fi_attn_decode_paged without any allocation: the same kernels, same arguments and bit-identical
  * outputs, with the split-KV partials in a fixed device array of this library (96 MiB per GPU,
  * part of the library's code object: every process that loads the library onto a GPU holds it

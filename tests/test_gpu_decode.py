@@ -394,3 +394,71 @@ def test_kv_gather_errors(gpu_ctx):
     assert torch.equal(out_k[:16], kc[3].transpose(0, 1))
     assert not out_k[16:32].any() and not out_v[16:32].any()
     assert torch.equal(out_v[32:40], vc[1, :, :8].transpose(0, 1))
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", [
+    # (num_seqs, min_len, max_len, hq, hkv, d, rotary_dims, splits, biases)
+    (64, 1, 2300, 14, 2, 64, 64, 7, True),     # a C4 decode tick (Qwen2-0.5B heads, q/k/v biases)
+    (6, 300, 3000, 32, 8, 128, 128, 3, False),  # C5 heads, no biases
+    (9, 1, 700, 8, 2, 64, 32, 2, True),         # partial rotary (pass-through half), GQA 4
+    (5, 1, 300, 8, 8, 32, 32, 1, True),         # MHA, D 32, one split
+])
+def test_decode_fused_qkv_matches_consumer_then_decode(gpu_ctx, kv_dtype, case):
+    """fi_attn_decode_paged_qkv == fi_qkv_rope_append followed by fi_attn_decode_paged, bit for
+    bit: the attention output and both pools (the new token's K/V rows appended at their
+    slots).  The fused launch runs three times in a row: the appends write the same rows and
+    the outputs repeat."""
+    import torch
+
+    import oracle
+    from ferrisinfer_amd import DTYPE_BF16, DTYPE_F32
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
+    n, lo, hi, hq, hkv, d, rot, splits, with_bias = case
+    print(f"fused qkv decode case={case} dtype={kv_dtype}", flush=True)
+    wl = paged_decode_c2(seed=41, num_seqs=n, min_len=lo, max_len=hi, num_q_heads=hq,
+                         num_kv_heads=hkv, head_dim=d, num_blocks=12288)
+    rng = np.random.default_rng(n * d + splits)
+    width = (hq + 2 * hkv) * d
+    parts = _dev(rng.standard_normal((splits, n, width), dtype=np.float32), torch)
+    qw, kw = hq * d, hkv * d
+    biases = None
+    if with_bias:
+        b = rng.standard_normal(width, dtype=np.float32)
+        biases = (_dev(b[:qw], torch), _dev(b[qw:qw + kw], torch), _dev(b[qw + kw:], torch))
+    ctxl = wl.context_lens.astype(np.int64)
+    pos = (ctxl - 1).astype(np.int32)  # the new token is each sequence's last position
+    bs = wl.block_size
+    slots = np.array([int(wl.block_tables[b, p // bs]) * bs + p % bs for b, p in enumerate(pos)], np.int64)
+    max_pos = int(pos.max()) + 1
+    cos_t = torch.empty((max_pos, max(rot // 2, 1)), device="cuda")
+    sin_t = torch.empty_like(cos_t)
+    gpu_ctx.rope_table(max_pos, d, rot, 1e6, cos_t, sin_t)
+    if kv_dtype == "bf16":
+        k0 = torch.from_numpy(oracle.f32_to_bf16(wl.k_pool).view(np.int16)).cuda()
+        v0 = torch.from_numpy(oracle.f32_to_bf16(wl.v_pool).view(np.int16)).cuda()
+        dt = DTYPE_BF16
+    else:
+        k0, v0, dt = _dev(wl.k_pool, torch), _dev(wl.v_pool, torch), DTYPE_F32
+    bt, cl = _dev(wl.block_tables, torch), _dev(wl.context_lens, torch)
+    dpos, dslots = _dev(pos, torch), _dev(slots, torch)
+    # the two separate launches
+    k1, v1 = k0.clone(), v0.clone()
+    q1 = torch.empty((n, hq, d), device="cuda")
+    gpu_ctx.qkv_rope_append(parts, splits, biases, dpos, cos_t, sin_t, rot, max_pos, dslots, k1, v1, dt,
+                            wl.num_blocks, bs, hq, hkv, d, q1)
+    out1 = torch.full((n, hq, d), float("nan"), device="cuda")
+    gpu_ctx.attn_decode_paged(q1, k1, v1, dt, bt, cl, wl.max_context_len, hkv, bs, wl.num_blocks, wl.scale, out1)
+    # the fused launch
+    k2, v2 = k0.clone(), v0.clone()
+    outs = [torch.full((n, hq, d), float("nan"), device="cuda") for _ in range(3)]
+    for o in outs:
+        gpu_ctx.attn_decode_paged_qkv(parts, splits, biases, dpos, cos_t, sin_t, rot, max_pos, dslots, k2, v2,
+                                      dt, bt, cl, wl.max_context_len, hq, hkv, d, bs, wl.num_blocks, wl.scale, o)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    assert not torch.equal(k1, k0)  # the appends happened
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    for o in outs:
+        assert torch.equal(o, out1)
