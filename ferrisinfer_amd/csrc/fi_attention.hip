@@ -1103,7 +1103,26 @@ int32_t fi_attn_decode_paged_qkv(fi_context* ctx, const float* d_qkv_parts, int3
                                  const int32_t* d_block_tables, int32_t max_blocks_per_seq,
                                  const int32_t* d_context_lens, int32_t num_seqs, int32_t max_context_len,
                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                 int32_t num_blocks, float scale, float* d_out) {
+                                 int32_t num_blocks, float scale, float* d_q_out, float* d_out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(num_kv_heads > 0 && head_dim > 0 && block_size > 0 && max_context_len >= 0 && num_seqs >= 0,
+             FI_ERR_INVALID_SHAPE, "fi_attn_decode_paged_qkv: bad shape");
+  // Large launches (more than six workgroups a CU) run the consumer and the attention as two
+  // launches: every workgroup of the fused kernel forms its query rows again (one more
+  // dependent load round each), which costs more there than the consumer launch (C5's
+  // 256-sequence decode, 32768 workgroups: 27.4 against 24.7 ms a tick).
+  const int part_tokens = kWaves * wave_tokens_for(num_kv_heads, head_dim);
+  const int64_t parts = max_context_len == 0 ? 1 : (max_context_len + part_tokens - 1) / part_tokens;
+  const int64_t cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+  if (static_cast<int64_t>(num_seqs) * num_kv_heads * parts > 6 * cus) {
+    FI_REQUIRE(d_q_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_attn_decode_paged_qkv: null q_out");
+    FI_TRY(fi_qkv_rope_append(ctx, d_qkv_parts, splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin,
+                              rotary_dims, max_positions, d_slot_mapping, d_k_cache, d_v_cache, kv_dtype, num_blocks,
+                              block_size, num_seqs, num_q_heads, num_kv_heads, head_dim, d_q_out));
+    return decode_paged(ctx, d_q_out, d_k_cache, d_v_cache, kv_dtype, d_block_tables, max_blocks_per_seq,
+                        d_context_lens, num_seqs, max_context_len, num_q_heads, num_kv_heads, head_dim,
+                        block_size, num_blocks, scale, d_out, false);
+  }
   const QkvIn qkv{d_qkv_parts, splits, d_bias_q, d_bias_k, d_bias_v, d_positions, d_cos, d_sin,
                   rotary_dims, max_positions, d_slot_mapping};
   return decode_paged(ctx, nullptr, d_k_cache, d_v_cache, kv_dtype, d_block_tables, max_blocks_per_seq,

@@ -393,7 +393,7 @@ void ForwardExecutor::enqueue(const Plan& p) {
                                      model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(),
                                      p.slot, pool_->k(l), pool_->v(l), pool_->kv_dtype(), p.bt, p.max_blocks, p.ctx, B,
                                      p.max_context_len, hq, hkv, D, pool_->block_size(), pool_->num_blocks(), scale,
-                                     attn));
+                                     q, attn));
     } else {
       check(fi_qkv_rope_append(ctx_, part, p.s_qkv, w.wq_bias.f32(), w.wk_bias.f32(), w.wv_bias.f32(), p.pos,
                                model_->rope_cos(), model_->rope_sin(), c.rotary_dims, model_->rope_positions(),

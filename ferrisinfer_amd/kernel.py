@@ -61,7 +61,7 @@ _SIGNATURES = {
     "fi_attn_decode_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                              _I32, _F32, _P],
     "fi_attn_decode_paged_qkv": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I32, _P, _I32,
-                                 _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+                                 _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P],
     "fi_attn_decode_paged_noalloc": [_P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32,
                                      _I32, _I32, _F32, _P],
     "fi_attn_prefill_paged": [_P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32,
@@ -246,8 +246,9 @@ class Context:
     def attn_decode_paged_qkv(self, parts, splits, biases, positions, cos_t, sin_t, rotary_dims,
                               max_positions, slot_mapping, k_cache, v_cache, kv_dtype, block_tables,
                               context_lens, max_context_len, num_q_heads, num_kv_heads, head_dim,
-                              block_size, num_blocks, scale, out):
-        """qkv_rope_append + attn_decode_paged in one launch (one new token per sequence)."""
+                              block_size, num_blocks, scale, out, q_out=None):
+        """qkv_rope_append + attn_decode_paged in one launch (one new token per sequence);
+        large launches run the two kernels with q_out [num_seqs, Hq, D] between them."""
         bq, bk, bv = biases if biases is not None else (None, None, None)
         check(self.lib.fi_attn_decode_paged_qkv(self.handle, ptr(parts), int(splits), ptr(bq), ptr(bk),
                                                 ptr(bv), ptr(positions), ptr(cos_t), ptr(sin_t),
@@ -256,7 +257,8 @@ class Context:
                                                 int(block_tables.shape[1]), ptr(context_lens),
                                                 int(context_lens.numel()), int(max_context_len),
                                                 int(num_q_heads), int(num_kv_heads), int(head_dim),
-                                                int(block_size), int(num_blocks), float(scale), ptr(out)))
+                                                int(block_size), int(num_blocks), float(scale), ptr(q_out),
+                                                ptr(out)))
 
     def attn_decode_paged_noalloc(self, q, k_cache, v_cache, kv_dtype, block_tables, context_lens,
                                   max_context_len, num_kv_heads, block_size, num_blocks, scale, out):

@@ -196,8 +196,10 @@ int32_t fi_attn_decode_paged(fi_context* ctx, const float* d_q, const void* d_k_
  * through the block table).  Every workgroup of the attention forms its query rows from
  * qkv_parts [splits, num_seqs, (Hq + 2 Hkv) * D] (+ biases, each may be NULL, + RoPE at
  * positions[b]); the workgroup holding a sequence's last partition appends the K/V row of its
- * kv head before reading the keys.  Outputs and the pool contents equal those of the two
- * calls bit for bit.  rotary_dims / 2 and head_dim - rotary_dims must be multiples of 4
+ * kv head before reading the keys.  Launches of more than six workgroups a CU (large batches
+ * of long contexts) run the two calls instead, with q_out [num_seqs, Hq, D] as the query
+ * buffer between them; q_out is left unwritten otherwise.  Outputs and the pool contents
+ * equal those of the two calls bit for bit either way.  rotary_dims / 2 and head_dim - rotary_dims must be multiples of 4
  * (Unsupported otherwise); the partials, biases and RoPE tables 16-byte aligned.  A slot or a
  * position out of range is reported as by fi_qkv_rope_append. */
 int32_t fi_attn_decode_paged_qkv(fi_context* ctx, const float* d_qkv_parts, int32_t splits, const float* d_bias_q,
@@ -207,7 +209,7 @@ int32_t fi_attn_decode_paged_qkv(fi_context* ctx, const float* d_qkv_parts, int3
                                  const int32_t* d_block_tables, int32_t max_blocks_per_seq,
                                  const int32_t* d_context_lens, int32_t num_seqs, int32_t max_context_len,
                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                 int32_t num_blocks, float scale, float* d_out);
+                                 int32_t num_blocks, float scale, float* d_q_out, float* d_out);
 
 /* fi_attn_decode_paged without any allocation: the same kernels, same arguments and bit-identical
  * outputs, with the split-KV partials in a fixed device array of this library (96 MiB per GPU,

@@ -403,12 +403,14 @@ def test_kv_gather_errors(gpu_ctx):
     (6, 300, 3000, 32, 8, 128, 128, 3, False),  # C5 heads, no biases
     (9, 1, 700, 8, 2, 64, 32, 2, True),         # partial rotary (pass-through half), GQA 4
     (5, 1, 300, 8, 8, 32, 32, 1, True),         # MHA, D 32, one split
+    (24, 1000, 3000, 8, 8, 32, 32, 2, True),    # 2304 workgroups: the two-kernel path
 ])
 def test_decode_fused_qkv_matches_consumer_then_decode(gpu_ctx, kv_dtype, case):
     """fi_attn_decode_paged_qkv == fi_qkv_rope_append followed by fi_attn_decode_paged, bit for
     bit: the attention output and both pools (the new token's K/V rows appended at their
     slots).  The fused launch runs three times in a row: the appends write the same rows and
-    the outputs repeat."""
+    the outputs repeat.  Launches of more than six workgroups a CU run the two kernels inside
+    the entry point, with q_out between them (the last case)."""
     import torch
 
     import oracle
@@ -418,7 +420,9 @@ def test_decode_fused_qkv_matches_consumer_then_decode(gpu_ctx, kv_dtype, case):
     n, lo, hi, hq, hkv, d, rot, splits, with_bias = case
     print(f"fused qkv decode case={case} dtype={kv_dtype}", flush=True)
     wl = paged_decode_c2(seed=41, num_seqs=n, min_len=lo, max_len=hi, num_q_heads=hq,
-                         num_kv_heads=hkv, head_dim=d, num_blocks=12288)
+                         num_kv_heads=hkv, head_dim=d, num_blocks=12288 if d >= 64 else 4608)
+    parts_n = -(-int(wl.max_context_len) // (256 if hkv * d < 512 else 512))
+    two_kernel = n * hkv * parts_n > 6 * 256
     rng = np.random.default_rng(n * d + splits)
     width = (hq + 2 * hkv) * d
     parts = _dev(rng.standard_normal((splits, n, width), dtype=np.float32), torch)
@@ -452,13 +456,19 @@ def test_decode_fused_qkv_matches_consumer_then_decode(gpu_ctx, kv_dtype, case):
     gpu_ctx.attn_decode_paged(q1, k1, v1, dt, bt, cl, wl.max_context_len, hkv, bs, wl.num_blocks, wl.scale, out1)
     # the fused launch
     k2, v2 = k0.clone(), v0.clone()
+    q2 = torch.full((n, hq, d), float("nan"), device="cuda")
     outs = [torch.full((n, hq, d), float("nan"), device="cuda") for _ in range(3)]
     for o in outs:
         gpu_ctx.attn_decode_paged_qkv(parts, splits, biases, dpos, cos_t, sin_t, rot, max_pos, dslots, k2, v2,
-                                      dt, bt, cl, wl.max_context_len, hq, hkv, d, bs, wl.num_blocks, wl.scale, o)
+                                      dt, bt, cl, wl.max_context_len, hq, hkv, d, bs, wl.num_blocks, wl.scale, o,
+                                      q_out=q2)
     torch.cuda.synchronize()
     gpu_ctx.check_faults()
     assert not torch.equal(k1, k0)  # the appends happened
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
     for o in outs:
         assert torch.equal(o, out1)
+    if two_kernel:
+        assert torch.equal(q2, q1)
+    else:
+        assert torch.isnan(q2).all()  # the fused kernel leaves q_out unwritten
