@@ -79,14 +79,21 @@ def parse_args():
 
 def c4_layer_ops(seed):
     """One C4 decode-tick layer's kernels at batch 64 on random inputs, 10 launches each."""
+    import numpy as np
     import torch
 
     from ferrisinfer_amd import DTYPE_F32, Context
 
+    from ferrisinfer_amd.workloads import paged_decode_c2
+
     ctx = Context(0)
     g = torch.Generator(device="cuda").manual_seed(seed)
     m, h, f, v, hq, hkv, d = 64, 896, 4864, 151936, 14, 2, 64
-    nb, bs = 4096, 16
+    nb, bs = 12288, 16
+    # the tick's attention: 64 sequences with C4-like contexts; each new token is the last
+    # position of its sequence, at the slot its block table gives
+    wl = paged_decode_c2(seed=seed, num_seqs=m, min_len=64, max_len=2300, num_q_heads=hq,
+                         num_kv_heads=hkv, head_dim=d, block_size=bs, num_blocks=nb)
 
     def rn(*shape):
         return torch.randn(*shape, device="cuda", generator=g)
@@ -108,10 +115,14 @@ def c4_layer_ops(seed):
     act = torch.empty(m, f, device="cuda")
     tok = torch.empty(m, dtype=torch.int32, device="cuda")
     prob = torch.empty(m, device="cuda")
-    kp = torch.zeros(nb, hkv, bs, d, device="cuda")
-    vp = torch.zeros_like(kp)
-    pos = torch.arange(1000, 1000 + m, dtype=torch.int32, device="cuda")
-    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(seed + 1))[:m].to(torch.int64).cuda()
+    kp = torch.from_numpy(wl.k_pool).cuda()
+    vp = torch.from_numpy(wl.v_pool).cuda()
+    last = wl.context_lens.astype(np.int64) - 1
+    pos = torch.from_numpy(last.astype(np.int32)).cuda()
+    slots = torch.from_numpy(np.array([int(wl.block_tables[b, p // bs]) * bs + p % bs
+                                       for b, p in enumerate(last)], np.int64)).cuda()
+    bt, cl = torch.from_numpy(wl.block_tables).cuda(), torch.from_numpy(wl.context_lens).cuda()
+    attn = torch.empty(m, hq, d, device="cuda")
     cos = torch.empty(4096, d // 2, device="cuda")
     sin = torch.empty_like(cos)
     ctx.rope_table(4096, d, d, 1e6, cos, sin)
@@ -126,6 +137,10 @@ def c4_layer_ops(seed):
         ctx.qkv_rope_append(p_qkv, s_qkv, None, pos, cos, sin, d, 4096, slots, kp, vp, DTYPE_F32, nb, bs,
                             hq, hkv, d, q)
         ctx.kv_append(kn, vn, slots, kp, vp, DTYPE_F32, nb, bs, hkv, d)
+        # the decode tick's attention: the q|k|v consumer folded in (decode_partition_kernel
+        # merging in its last-arriving workgroups), as the runtime runs it
+        ctx.attn_decode_paged_qkv(p_qkv, s_qkv, None, pos, cos, sin, d, 4096, slots, kp, vp, DTYPE_F32, bt, cl,
+                                  wl.max_context_len, hq, hkv, d, bs, nb, wl.scale, attn, q_out=q)
         ctx.gemm_packed(x, w_o, h, h, pw, s_o, p_o)
         ctx.splitk_residual_rms_norm(p_o, s_o, None, res, ssum, nw, nout, 1e-6)
         ctx.gemm_packed_swiglu(x, pair, h, f, act)

@@ -207,7 +207,7 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, size_t head0, in
 // that kernel's bit for bit.
 template <int D, typename KVT, int G>
 __device__ __forceinline__ void qkv_prologue(const DecodeArgs& a, int seq, int kvh, bool append, float (*s_q)[D],
-                                             int tid) {
+                                             int tid, int ctx_raw) {
   const int half = a.rotary_dims / 2;
   const int pass = D - 2 * half;
   const int qph = (half + pass) / 4;  // four-column items per head row
@@ -235,6 +235,12 @@ __device__ __forceinline__ void qkv_prologue(const DecodeArgs& a, int seq, int k
       const int bcol0 = is_q ? (kvh * group + g) * D : kvh * D;
       const float* bias = is_q ? a.bias_q : a.bias_k;
       if (r < half) {
+        // a decode token's position is its sequence's last key, context_lens - 1: the table
+        // rows at that position are loaded with the partials (no dependent round trip on the
+        // position), and again at the given position where it differs
+        const int guess = min(max(ctx_raw - 1, 0), a.max_positions - 1);
+        float4 c = *reinterpret_cast<const float4*>(a.cos_t + (size_t)guess * half + r);
+        float4 sn = *reinterpret_cast<const float4*>(a.sin_t + (size_t)guess * half + r);
         int pos = a.positions[seq];
         if (pos < 0 || pos >= a.max_positions) {
           atomicOr(a.faults, FI_FAULT_POSITION_RANGE);
@@ -242,8 +248,10 @@ __device__ __forceinline__ void qkv_prologue(const DecodeArgs& a, int seq, int k
         }
         const float4 lo = fi::qkv_value4(p0, plane, a.qkv_splits, bias, bcol0 + r, col0 + r);
         const float4 hi = fi::qkv_value4(p0, plane, a.qkv_splits, bias, bcol0 + r + half, col0 + r + half);
-        const float4 c = *reinterpret_cast<const float4*>(a.cos_t + (size_t)pos * half + r);
-        const float4 sn = *reinterpret_cast<const float4*>(a.sin_t + (size_t)pos * half + r);
+        if (pos != guess) {
+          c = *reinterpret_cast<const float4*>(a.cos_t + (size_t)pos * half + r);
+          sn = *reinterpret_cast<const float4*>(a.sin_t + (size_t)pos * half + r);
+        }
         float4 y0, y1;
         fi::rope4(lo, hi, c, sn, y0, y1);
         if (is_q) {
@@ -333,6 +341,7 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   const int kvh = unit - seq * a.hkv;
   const int tid = threadIdx.x;
   int ctx = a.context_lens[seq];
+  const int ctx_raw = ctx;
   if (ctx > a.parts_per_seq * kPartTokens) {  // beyond the grid: clamp and report
     if (part == 0 && tid == 0) atomicOr(a.faults, FI_FAULT_CONTEXT_RANGE);
     ctx = a.parts_per_seq * kPartTokens;
@@ -342,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   if (ctx <= 0) {  // no keys: defined output of zeros (the new token's K/V still appended)
     if (part == 0) {
       for (int i = tid; i < group * D; i += kThreads) a.out[head0 * D + i] = 0.0f;
-      if (fused) qkv_prologue<D, KVT, G>(a, seq, kvh, true, s_q, tid);
+      if (fused) qkv_prologue<D, KVT, G>(a, seq, kvh, true, s_q, tid, ctx_raw);
     }
     return;
   }
@@ -385,18 +394,30 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
         }
       }
   };
+  // the partition's block-table entries are loaded first, so that their round trip overlaps
+  // the query rows' (or the fused consumer's partials')
+  constexpr int kRowsPerThread = (kPartTokens + kThreads - 1) / kThreads;
+  const int bs = a.block_size;
+  int ids[kRowsPerThread];
+#pragma unroll
+  for (int i = 0; i < kRowsPerThread; ++i) {
+    const int pos = t0 + min(tid + i * kThreads, n_part - 1);  // clamped: a valid entry
+    const int lb = pos / bs;
+    ids[i] = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
+  }
   if (fused) {
     // the last partition holds the new token: its K/V row is written before the keys are read
-    qkv_prologue<D, KVT, G>(a, seq, kvh, part == nparts - 1, s_q, tid);
+    qkv_prologue<D, KVT, G>(a, seq, kvh, part == nparts - 1, s_q, tid, ctx_raw);
   } else {
     load_q(a.q + head0 * D, D);
   }
-  {
-    const int bs = a.block_size;
-    for (int t = tid; t < n_part; t += kThreads) {
+#pragma unroll
+  for (int i = 0; i < kRowsPerThread; ++i) {
+    const int t = tid + i * kThreads;
+    if (t < n_part) {
       const int pos = t0 + t;
       const int lb = pos / bs;
-      int id = lb < a.max_blocks ? a.block_tables[(size_t)seq * a.max_blocks + lb] : -1;
+      int id = ids[i];
       if (id < 0 || id >= a.num_blocks) {
         atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
         id = 0;

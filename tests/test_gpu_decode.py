@@ -432,9 +432,12 @@ def test_decode_fused_qkv_matches_consumer_then_decode(gpu_ctx, kv_dtype, case):
         b = rng.standard_normal(width, dtype=np.float32)
         biases = (_dev(b[:qw], torch), _dev(b[qw:qw + kw], torch), _dev(b[qw + kw:], torch))
     ctxl = wl.context_lens.astype(np.int64)
-    pos = (ctxl - 1).astype(np.int32)  # the new token is each sequence's last position
+    last = ctxl - 1  # the new token is each sequence's last key
     bs = wl.block_size
-    slots = np.array([int(wl.block_tables[b, p // bs]) * bs + p % bs for b, p in enumerate(pos)], np.int64)
+    slots = np.array([int(wl.block_tables[b, p // bs]) * bs + p % bs for b, p in enumerate(last)], np.int64)
+    # RoPE positions: the last key's, except every third sequence (the kernel loads the table
+    # rows at the last key's position first and again where the given position differs)
+    pos = (last + np.where(np.arange(n) % 3 == 2, 5, 0)).astype(np.int32)
     max_pos = int(pos.max()) + 1
     cos_t = torch.empty((max_pos, max(rot // 2, 1)), device="cuda")
     sin_t = torch.empty_like(cos_t)
