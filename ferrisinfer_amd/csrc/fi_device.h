@@ -66,6 +66,23 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return w >> 16;
 }
 
+// ---- three-piece bf16 split of f32 operands (the f32-accuracy products on bf16 MFMA) ----
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 values a, b as x = hi + mid + lo exactly: hi = RNE_bf16(x), mid = RNE_bf16(x - hi),
+// lo = x - hi - mid (exact in bf16).  Each piece pair is rounded once (v_cvt_pk_bf16_f32, a in
+// the low half) and widened back by shift and mask, so no value is converted twice.
+__device__ __forceinline__ void split3_pk(float a, float b, uint32_t& h, uint32_t& m, uint32_t& l) {
+  h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+  const float ra = a - __builtin_bit_cast(float, h << 16);
+  const float rb = b - __builtin_bit_cast(float, h & 0xffff0000u);
+  m = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{ra, rb}, bf16x2_t));
+  const float sa = ra - __builtin_bit_cast(float, m << 16);
+  const float sb = rb - __builtin_bit_cast(float, m & 0xffff0000u);
+  l = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{sa, sb}, bf16x2_t));
+}
+
 // ---- the q|k|v consumer's arithmetic (split-K sum + bias, RoPE, pool store), shared by
 // qkv_rope_append4_kernel and decode attention's fused q|k|v prologue so both give identical
 // values ----

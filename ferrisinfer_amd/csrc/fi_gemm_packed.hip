@@ -413,11 +413,14 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 // RMSNorm already overflows its sum of squares for |x| > 1.8e19.  Guarding it would add three
 // VALU instructions per element to every weight split.
 __device__ __forceinline__ void split3(const f32x8& x, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
-  hi = __builtin_convertvector(x, bf16x8);
-  const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
-  mid = __builtin_convertvector(r1, bf16x8);
-  const f32x8 r2 = r1 - __builtin_convertvector(mid, f32x8);
-  lo = __builtin_convertvector(r2, bf16x8);
+  uint4 h, m, l;
+  fi::split3_pk(x[0], x[1], h.x, m.x, l.x);
+  fi::split3_pk(x[2], x[3], h.y, m.y, l.y);
+  fi::split3_pk(x[4], x[5], h.z, m.z, l.z);
+  fi::split3_pk(x[6], x[7], h.w, m.w, l.w);
+  hi = __builtin_bit_cast(bf16x8, h);
+  mid = __builtin_bit_cast(bf16x8, m);
+  lo = __builtin_bit_cast(bf16x8, l);
 }
 
 __device__ __forceinline__ v4f mfma_s3(const bf16x8& ah, const bf16x8& am, const bf16x8& al, const bf16x8& bh,

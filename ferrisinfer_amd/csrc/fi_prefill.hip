@@ -751,28 +751,21 @@ int32_t launch_prefill_bf16(fi_context* ctx, const PrefillArgs& args_in) {
 // rounding together), accumulated in f32 on v_mfma_f32_16x16x32_bf16: the f32 result at 2.7x
 // the f32 MFMA rate.  One LDS buffer (52 KB at D = 128, two workgroups per CU); the next chunk
 // is in registers while the current one is multiplied, two barriers per chunk.
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ void split3(const f32x8& x, bf16x8 (&p)[3]) {
-  p[0] = __builtin_convertvector(x, bf16x8);
-  const f32x8 r1 = x - __builtin_convertvector(p[0], f32x8);
-  p[1] = __builtin_convertvector(r1, bf16x8);
-  const f32x8 r2 = r1 - __builtin_convertvector(p[1], f32x8);
-  p[2] = __builtin_convertvector(r2, bf16x8);
+  uint4 h, m, l;
+  fi::split3_pk(x[0], x[1], h.x, m.x, l.x);
+  fi::split3_pk(x[2], x[3], h.y, m.y, l.y);
+  fi::split3_pk(x[4], x[5], h.z, m.z, l.z);
+  fi::split3_pk(x[6], x[7], h.w, m.w, l.w);
+  p[0] = __builtin_bit_cast(bf16x8, h);
+  p[1] = __builtin_bit_cast(bf16x8, m);
+  p[2] = __builtin_bit_cast(bf16x8, l);
 }
 
 // four f32 values -> their three bf16 pieces, each as 8 bytes
 __device__ __forceinline__ void split3_quad(const float4& v, uint2 (&p)[3]) {
-  const f32x4 x = {v.x, v.y, v.z, v.w};
-  const bf16x4 hi = __builtin_convertvector(x, bf16x4);
-  const f32x4 r1 = x - __builtin_convertvector(hi, f32x4);
-  const bf16x4 mid = __builtin_convertvector(r1, bf16x4);
-  const f32x4 r2 = r1 - __builtin_convertvector(mid, f32x4);
-  const bf16x4 lo = __builtin_convertvector(r2, bf16x4);
-  p[0] = __builtin_bit_cast(uint2, hi);
-  p[1] = __builtin_bit_cast(uint2, mid);
-  p[2] = __builtin_bit_cast(uint2, lo);
+  fi::split3_pk(v.x, v.y, p[0].x, p[1].x, p[2].x);
+  fi::split3_pk(v.z, v.w, p[0].y, p[1].y, p[2].y);
 }
 
 // acc += A B over three-piece operands: the six cross products above 2^-24, smallest first
