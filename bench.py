@@ -51,9 +51,10 @@ def parse_args():
     p.add_argument("--no-c4", action="store_true",
                    help="skip the C4 (Qwen2-0.5B-shaped) continuous-batching measurement")
     p.add_argument("--c4-requests", type=int, default=128)
-    p.add_argument("--c4-variants", default="graph,eager,sampled,bf16",
-                   help="C4 runs to make (comma list of graph, eager, sampled, bf16); the first "
-                        "listed of graph / eager fills the top-level c4 figures")
+    p.add_argument("--c4-variants", default="graph,ahead,eager,sampled,bf16",
+                   help="C4 runs to make (comma list of graph, ahead, eager, sampled, bf16); graph "
+                        "(else eager) fills the top-level c4 figures; ahead runs the top-level "
+                        "configuration with FR_TICK_RUN_AHEAD")
     p.add_argument("--no-c5", action="store_true",
                    help="skip the C5 (Llama-3-8B-shaped, bf16 weights and KV) decode-step measurement")
     p.add_argument("--c5-steps", type=int, default=5)
@@ -550,14 +551,17 @@ def c4_weights(seed):
     return _C4_WEIGHTS[seed]
 
 
-def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"):
+def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32", run_ahead=False):
     """C4: the Qwen2-0.5B-shaped model (f32, tied, q/k/v biases, random N(0, 0.02) weights)
     served by the GPU runtime under continuous batching (max batch 64, block 16, the
     reference scheduler's other defaults), Poisson arrivals at 8 req/s on 50 ms virtual
     ticks.  Decode tok/s = generated tokens / summed decode-tick wall time, the reference's
     continuous-batching definition (cli/main.rs:1502-1512, 1619-1622).  sampler: None for
     greedy sessions, or (temperature, top_k, top_p, seed) for sampled ones; graph: decode ticks
-    replayed from HIP graphs; weight_dtype: storage of the packed projections and head."""
+    replayed from HIP graphs; weight_dtype: storage of the packed projections and head;
+    run_ahead: each tick followed by no arrival enqueues the next decode tick before it returns
+    (FR_TICK_RUN_AHEAD), and such a tick's seconds run from the previous tick's return, the
+    driver's own time in between included."""
     import numpy as np
 
     from ferrisinfer_amd.runtime import Runtime
@@ -576,7 +580,7 @@ def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"
                              arrival_tick=0)])
     reqs = c4_requests(seed=seed, n=n_requests)
     t0 = time.perf_counter()
-    rep = run_continuous(rt, reqs)
+    rep = run_continuous(rt, reqs, run_ahead=run_ahead)
     wall = time.perf_counter() - t0
     full = [t for t in rep["ticks"] if t["kind"] == 1 and t["batch"] == 64]
     full_s = sum(t["seconds"] for t in full)
@@ -589,7 +593,9 @@ def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"
                     "U[64,256], " + ("greedy" if sampler is None else
                                      "sampled (temperature, top_k, top_p, seed) = " + str(sampler))
                     + f", max batch 64, block 16, {weight_dtype} weights, f32 KV, decode ticks "
-                    + ("replayed from HIP graphs" if graph else "enqueued eagerly"),
+                    + ("replayed from HIP graphs" if graph else "enqueued eagerly")
+                    + (", the next decode tick enqueued before each tick returns when no request "
+                       "arrives in between" if run_ahead else ""),
         "decode_tok_s": round(rep["decode_tok_s"], 1),
         "decode_tok_s_at_batch_64": round(64 * len(full) / full_s, 1) if full_s > 0 else None,
         "ms_per_decode_tick_at_batch_64": round(full_s / len(full) * 1e3, 3) if full else None,
@@ -606,6 +612,8 @@ def c4_continuous(seed, n_requests, sampler=None, graph=True, weight_dtype="f32"
     }
     if graph:
         out["graph_counters"] = rt.graph_counters()
+    if run_ahead:
+        out["run_ahead_counters"] = rt.run_ahead_counters()
     # generated ids per request, for the graph-versus-eager comparison (not printed)
     out["_tokens"] = [rt.generated(s) for s in rep["sequence_ids"]]
     rt.close()
@@ -1065,6 +1073,13 @@ def main():
             result["c4"]["graph_eager_differing_requests"] = differ
             if differ:
                 print(f"bench: C4 graph and eager runs differ on {differ} requests", file=sys.stderr, flush=True)
+        if "ahead" in variants:
+            # the same requests with each decode tick enqueued while the previous one runs
+            # (stream overlap of host planning with the device); the ids must equal the serial run's
+            ahead = c4_continuous(args.seed, args.c4_requests, graph=main_graph, run_ahead=True)
+            result["c4"]["run_ahead"] = {k: ahead[k] for k in keys + ("run_ahead_counters",)}
+            differ = sum(1 for a, b in zip(tokens, ahead["_tokens"]) if a != b)
+            result["c4"]["run_ahead"]["tokens_equal_serial"] = differ == 0 and len(tokens) == len(ahead["_tokens"])
         if "sampled" in variants:
             # the same requests under the reference's chat_default sampler (sampler.rs:30-37):
             # logits head + device sampling in every tick

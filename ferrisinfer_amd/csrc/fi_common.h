@@ -49,6 +49,11 @@ struct fi_graph {
   int device = 0;
 };
 
+struct fi_event {
+  hipEvent_t event = nullptr;
+  int device = 0;
+};
+
 namespace fi {
 
 // Records `message` as the thread's last error and returns `code`.

@@ -207,6 +207,100 @@ int32_t fi_buf_download(fi_context* ctx, void* dst, size_t dst_bytes, const void
   return FI_OK;
 }
 
+// ---------------------------------------------------------------- stream overlap
+// Pinned host memory, copies that return once enqueued, and events: what a host runtime needs
+// to enqueue the next step while the device still runs the current one.
+
+int32_t fi_host_alloc(fi_context* ctx, size_t bytes, void** h_out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_host_alloc: the stream is being captured into a graph");
+  FI_REQUIRE(h_out != nullptr, FI_ERR_INVALID_CONFIG, "fi_host_alloc: null output pointer");
+  FI_REQUIRE(bytes > 0, FI_ERR_INVALID_SHAPE, "host buffers must be larger than zero bytes");
+  FI_TRY_HIP(hipHostMalloc(h_out, bytes, hipHostMallocDefault));
+  return FI_OK;
+}
+
+int32_t fi_host_free(fi_context* ctx, void* h_ptr) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_host_free: the stream is being captured into a graph");
+  if (h_ptr == nullptr) return FI_OK;
+  // queued copies may still read or write it
+  FI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+  FI_TRY_HIP(hipHostFree(h_ptr));
+  return FI_OK;
+}
+
+int32_t fi_buf_upload_async(fi_context* ctx, void* d_dst, size_t dst_bytes, const void* h_src,
+                            size_t src_bytes) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_buf_upload_async: the stream is being captured into a graph");
+  FI_REQUIRE(dst_bytes == src_bytes, FI_ERR_INVALID_SHAPE,
+             "upload requires matching lengths; buffer has " + std::to_string(dst_bytes) +
+                 " bytes but host slice has " + std::to_string(src_bytes) + " bytes");
+  if (src_bytes == 0) return FI_OK;
+  FI_REQUIRE(d_dst && h_src, FI_ERR_INVALID_CONFIG, "fi_buf_upload_async: null pointer");
+  FI_TRY_HIP(hipMemcpyAsync(d_dst, h_src, src_bytes, hipMemcpyHostToDevice, ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_buf_download_async(fi_context* ctx, void* h_dst, size_t dst_bytes, const void* d_src,
+                              size_t src_bytes) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_buf_download_async: the stream is being captured into a graph");
+  FI_REQUIRE(dst_bytes == src_bytes, FI_ERR_INVALID_SHAPE,
+             "download requires matching lengths; host slice has " + std::to_string(dst_bytes) +
+                 " bytes but buffer has " + std::to_string(src_bytes) + " bytes");
+  if (src_bytes == 0) return FI_OK;
+  FI_REQUIRE(h_dst && d_src, FI_ERR_INVALID_CONFIG, "fi_buf_download_async: null pointer");
+  FI_TRY_HIP(hipMemcpyAsync(h_dst, d_src, src_bytes, hipMemcpyDeviceToHost, ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_ctx_faults_async(fi_context* ctx, uint32_t* h_words) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_ctx_faults_async: the stream is being captured into a graph");
+  FI_REQUIRE(h_words != nullptr, FI_ERR_INVALID_CONFIG, "fi_ctx_faults_async: null pointer");
+  FI_TRY_HIP(hipMemcpyAsync(h_words, ctx->d_faults, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_event_create(fi_context* ctx, fi_event** out) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(out != nullptr, FI_ERR_INVALID_CONFIG, "fi_event_create: null output pointer");
+  hipEvent_t e = nullptr;
+  FI_TRY_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  auto* ev = new fi_event();
+  ev->event = e;
+  ev->device = ctx->device;
+  *out = ev;
+  return FI_OK;
+}
+
+int32_t fi_event_record(fi_context* ctx, fi_event* ev) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(ev != nullptr && ev->device == ctx->device, FI_ERR_INVALID_CONFIG,
+             "fi_event_record: event of another device or null");
+  FI_REQUIRE(!ctx->capturing, FI_ERR_RUNTIME, "fi_event_record: the stream is being captured into a graph");
+  FI_TRY_HIP(hipEventRecord(ev->event, ctx->stream));
+  return FI_OK;
+}
+
+int32_t fi_event_wait(fi_event* ev) {
+  FI_REQUIRE(ev != nullptr, FI_ERR_INVALID_CONFIG, "fi_event_wait: null event");
+  FI_TRY_HIP(hipSetDevice(ev->device));
+  FI_TRY_HIP(hipEventSynchronize(ev->event));
+  return FI_OK;
+}
+
+int32_t fi_event_destroy(fi_event* ev) {
+  if (ev == nullptr) return FI_OK;
+  FI_TRY_HIP(hipSetDevice(ev->device));
+  hipError_t err = hipEventDestroy(ev->event);
+  delete ev;
+  if (err != hipSuccess) return fi::hip_error(err, "hipEventDestroy");
+  return FI_OK;
+}
+
 int32_t fi_ctx_workspace_generation(fi_context* ctx, uint64_t* generation) {
   FI_REQUIRE(ctx != nullptr && generation != nullptr, FI_ERR_INVALID_CONFIG,
              "fi_ctx_workspace_generation: null argument");

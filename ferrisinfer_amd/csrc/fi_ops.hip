@@ -22,6 +22,24 @@ __device__ float block_sum(float v, float* s_scratch) {
   return total;
 }
 
+// ids[i] = prev[rows[i]] where rows[i] >= 0: the previous step's sampled tokens fed as this
+// step's inputs (runtime/session.rs:246-262 feeds the last sample).  A row outside prev leaves
+// the entry unchanged and raises the TOKEN_RANGE fault bit.
+__global__ __launch_bounds__(kRowThreads) void token_feed_kernel(const int32_t* __restrict__ prev, int prev_count,
+                                                                 const int32_t* __restrict__ rows, int n,
+                                                                 int32_t* __restrict__ ids,
+                                                                 uint32_t* __restrict__ faults) {
+  const int i = blockIdx.x * kRowThreads + threadIdx.x;
+  if (i >= n) return;
+  const int r = rows[i];
+  if (r < 0) return;
+  if (r >= prev_count) {
+    atomicOr(faults, FI_FAULT_TOKEN_RANGE);
+    return;
+  }
+  ids[i] = prev[r];
+}
+
 // out[r, :] = table[ids[r], :]  (kernel/cpu/attention.rs:3-99).  An id outside the vocabulary
 // writes a zero row and raises the TOKEN_RANGE fault bit.
 __global__ __launch_bounds__(kRowThreads) void embedding_kernel(const float* __restrict__ table, int vocab,
@@ -146,6 +164,18 @@ int32_t fi_embedding(fi_context* ctx, const float* d_table, int32_t vocab, int32
   hipLaunchKernelGGL(embedding_kernel, dim3(num_tokens), dim3(kRowThreads), 0, ctx->stream, d_table, vocab,
                      hidden, d_ids, d_out, ctx->d_faults);
   FI_CHECK_LAUNCH("embedding_kernel");
+  return FI_OK;
+}
+
+int32_t fi_token_feed(fi_context* ctx, const int32_t* d_prev_tokens, int32_t prev_count, const int32_t* d_rows,
+                      int32_t n, int32_t* d_ids) {
+  FI_TRY(fi::enter(ctx));
+  FI_REQUIRE(n >= 0 && prev_count >= 0, FI_ERR_INVALID_SHAPE, "fi_token_feed: negative count");
+  if (n == 0) return FI_OK;
+  FI_REQUIRE(d_prev_tokens && d_rows && d_ids, FI_ERR_INVALID_CONFIG, "fi_token_feed: null pointer");
+  hipLaunchKernelGGL(token_feed_kernel, dim3((n + kRowThreads - 1) / kRowThreads), dim3(kRowThreads), 0,
+                     ctx->stream, d_prev_tokens, prev_count, d_rows, n, d_ids, ctx->d_faults);
+  FI_CHECK_LAUNCH("token_feed_kernel");
   return FI_OK;
 }
 

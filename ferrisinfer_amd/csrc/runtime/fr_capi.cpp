@@ -206,6 +206,21 @@ int32_t fr_execute_next_tick(void* h, int32_t* executed) {
   });
 }
 
+int32_t fr_execute_next_tick_ex(void* h, int32_t flags, int32_t* executed) {
+  return guard([&] {
+    if ((flags & ~FR_TICK_RUN_AHEAD) != 0) fr::fail(fr::ErrorKind::InvalidConfig, "unknown tick flags");
+    rt(h)->last = rt(h)->scheduler_ready().execute_next_tick((flags & FR_TICK_RUN_AHEAD) != 0);
+    *executed = rt(h)->last ? 1 : 0;
+  });
+}
+
+int32_t fr_run_ahead_counters(void* h, uint64_t* out) {
+  return guard([&] {
+    const auto c = rt(h)->scheduler_ready().run_ahead_counters();
+    for (size_t i = 0; i < c.size(); ++i) out[i] = c[i];
+  });
+}
+
 int32_t fr_has_pending(void* h) { return rt(h)->scheduler && rt(h)->scheduler->has_pending() ? 1 : 0; }
 
 int32_t fr_last_report(void* h, int32_t* kind, int64_t* rows, float* probs, int64_t capacity, int64_t* n_out) {

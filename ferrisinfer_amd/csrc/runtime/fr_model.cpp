@@ -273,7 +273,33 @@ void BlockPool::decref(int32_t block) {
 ForwardExecutor::ForwardExecutor(const DeviceModel* model, BlockPool* pool, bool graph_decode)
     : model_(model), pool_(pool), ctx_(model->ctx()), graph_decode_(graph_decode) {}
 
-ForwardExecutor::~ForwardExecutor() { drop_graphs(); }
+ForwardExecutor::~ForwardExecutor() {
+  // ticks still in flight read the buffers freed below
+  if (!inflight_.empty()) (void)fi_ctx_sync(ctx_);
+  drop_graphs();
+  for (int i = 0; i < 2; ++i) {
+    (void)fi_host_free(ctx_, h_meta_[i]);
+    (void)fi_host_free(ctx_, h_out_[i]);
+    (void)fi_event_destroy(events_[i]);
+  }
+}
+
+void ForwardExecutor::host_reserve(int slot, size_t meta_bytes, size_t out_bytes) {
+  auto fit = [&](void*& p, size_t& cap, size_t bytes) {
+    if (bytes <= cap) return;
+    const size_t want = (std::max(bytes, 2 * cap) + 4095) & ~static_cast<size_t>(4095);
+    if (p != nullptr) {
+      check(fi_host_free(ctx_, p));  // waits for the copies that may still use it
+      p = nullptr;
+      cap = 0;
+    }
+    check(fi_host_alloc(ctx_, want, &p));
+    cap = want;
+  };
+  fit(h_meta_[slot], h_meta_bytes_[slot], meta_bytes);
+  fit(h_out_[slot], h_out_bytes_[slot], out_bytes);
+  if (events_[slot] == nullptr) check(fi_event_create(ctx_, &events_[slot]));
+}
 
 void ForwardExecutor::drop_graphs() {
   if (!graphs_.empty()) graph_drops_ += graphs_.size();
@@ -469,15 +495,33 @@ void ForwardExecutor::last_logits(float* host, size_t capacity, int64_t* rows) c
 
 std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const SamplerConfig& sampler,
                                               std::vector<uint64_t>* states) {
+  launch(b, sampler, states);
+  return collect(states);
+}
+
+bool ForwardExecutor::can_feed(const PackedBatch& b) const {
+  // out_ holds the previous launch's samples; reserve() reallocates it only past cap_seqs_ rows
+  return inflight_.size() == 1 && inflight_.front().B > 0 && b.kind == BatchKind::Decode &&
+         b.copy_src.empty() && !b.context_lens.empty() && b.context_lens.size() <= cap_seqs_;
+}
+
+void ForwardExecutor::launch(const PackedBatch& b, const SamplerConfig& sampler, const std::vector<uint64_t>* states,
+                             const std::vector<int32_t>* feed) {
   const auto t_start = std::chrono::steady_clock::now();
-  enqueue_s_ = wait_s_ = 0.0;
+  enqueue_s_ = 0.0;
+  if (inflight_.size() >= 2) fail(ErrorKind::Runtime, "two ticks are already in flight");
   const ModelConfig& c = model_->config();
   const int32_t T = static_cast<int32_t>(b.token_ids.size());
   const int32_t B = static_cast<int32_t>(b.context_lens.size());
+  if (feed != nullptr &&
+      (!sampler.is_greedy() || feed->size() != static_cast<size_t>(B) || T != B || !can_feed(b))) {
+    fail(ErrorKind::Runtime, "a tick fed from the previous tick's samples must be a greedy decode tick behind it");
+  }
   logits_rows_ = 0;
   if (T == 0 || B == 0) {
-    copy_only(b);
-    return {};
+    copy_only(b);  // waits for the stream
+    inflight_.push_back(Pending{-1, 0, true});
+    return;
   }
   if (!model_->finalized()) fail(ErrorKind::Runtime, "model weights are not packed (DeviceModel::finalize)");
   reserve(T, B);
@@ -545,8 +589,18 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   const size_t o_cs = section(b.copy_src.data(), b.copy_src.size() * 4);
   const size_t o_cd = section(b.copy_dst.data(), b.copy_dst.size() * 4);
   const size_t o_cc = section(b.copy_count.data(), b.copy_count.size() * 4);
+  // last, so the sections above keep the offsets the graphs recorded; present in every launch
+  // (all -1 when nothing is fed), so the buffer's size does not depend on feeding
+  std::vector<int32_t> no_feed;
+  if (feed == nullptr) no_feed.assign(static_cast<size_t>(B), -1);
+  const size_t o_feed = section(feed ? feed->data() : no_feed.data(), static_cast<size_t>(B) * 4);
+  // through the launch's pinned slot: the copy is ordered on the stream behind a tick still in
+  // flight, which reads the previous contents
+  const int32_t slot = next_slot_;
+  host_reserve(slot, host.size(), static_cast<size_t>(B) * 8 + 16);
+  std::memcpy(h_meta_[slot], host.data(), host.size());
   grow(meta_, host.size());
-  check(fi_buf_upload(ctx_, meta_.get(), host.size(), host.data(), host.size()));
+  check(fi_buf_upload_async(ctx_, meta_.get(), host.size(), h_meta_[slot], host.size()));
   auto at = [&](size_t off) { return static_cast<uint8_t*>(meta_.get()) + off; };
   p.ids = reinterpret_cast<const int32_t*>(at(o_ids));
   p.pos = reinterpret_cast<const int32_t*>(at(o_pos));
@@ -558,6 +612,10 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
   p.cs = reinterpret_cast<const int32_t*>(at(o_cs));
   p.cd = reinterpret_cast<const int32_t*>(at(o_cd));
   p.cc = reinterpret_cast<const int32_t*>(at(o_cc));
+  if (feed != nullptr) {
+    check(fi_token_feed(ctx_, static_cast<const int32_t*>(out_.get()), out_rows_,
+                        reinterpret_cast<const int32_t*>(at(o_feed)), B, reinterpret_cast<int32_t*>(at(o_ids))));
+  }
 
   if (!greedy) {
     // one upload: states [B] u64, temperature [B] f32, top_k [B] i32, top_p [B] f32
@@ -617,20 +675,59 @@ std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const Sample
     enqueue(p);
   }
 
-  const auto t_enqueued = std::chrono::steady_clock::now();
-  std::vector<int32_t> tok(static_cast<size_t>(B) * 2);  // B ids, then B probabilities
-  check(fi_buf_download(ctx_, tok.data(), B * 8, out_.get(), B * 8));
-  if (!greedy) check(fi_buf_download(ctx_, states->data(), B * 8, samp_.get(), B * 8));
-  check(fi_ctx_check_faults(ctx_));
-  enqueue_s_ = std::chrono::duration<double>(t_enqueued - t_start).count();
-  wait_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_enqueued).count();
-  std::vector<TokenSample> out(B);
-  for (int32_t i = 0; i < B; ++i) {
-    float prob;
-    std::memcpy(&prob, &tok[B + i], 4);
-    out[i] = TokenSample{static_cast<uint32_t>(tok[i]), prob};
+  // the samples (B ids, then B probabilities) and the fault words into the pinned slot
+  out_rows_ = B;
+  uint8_t* h = static_cast<uint8_t*>(h_out_[slot]);
+  check(fi_buf_download_async(ctx_, h, static_cast<size_t>(B) * 8, out_.get(), static_cast<size_t>(B) * 8));
+  check(fi_ctx_faults_async(ctx_, reinterpret_cast<uint32_t*>(h + static_cast<size_t>(B) * 8)));
+  check(fi_event_record(ctx_, events_[slot]));
+  inflight_.push_back(Pending{slot, B, greedy});
+  next_slot_ ^= 1;
+  enqueue_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
+}
+
+std::vector<TokenSample> ForwardExecutor::collect(std::vector<uint64_t>* states) {
+  const auto t_start = std::chrono::steady_clock::now();
+  wait_s_ = 0.0;
+  if (inflight_.empty()) fail(ErrorKind::Runtime, "no tick in flight");
+  const Pending p = inflight_.front();
+  inflight_.pop_front();
+  if (p.B == 0) return {};
+  check(fi_event_wait(events_[p.slot]));
+  const uint8_t* h = static_cast<const uint8_t*>(h_out_[p.slot]);
+  uint32_t words[4];
+  std::memcpy(words, h + static_cast<size_t>(p.B) * 8, sizeof(words));
+  // a fault bit: the check waits for the stream, reports and clears it
+  if ((words[0] | words[1] | words[2] | words[3]) != 0) check(fi_ctx_check_faults(ctx_));
+  if (!p.greedy) {
+    // sampled ticks are never launched ahead, so nothing else is in flight behind this one
+    if (states == nullptr || states->size() != static_cast<size_t>(p.B)) {
+      fail(ErrorKind::InvalidShape, "sampled batch requires one sampler state per sequence");
+    }
+    check(fi_buf_download(ctx_, states->data(), static_cast<size_t>(p.B) * 8, samp_.get(),
+                          static_cast<size_t>(p.B) * 8));
   }
+  std::vector<TokenSample> out(p.B);
+  for (int32_t i = 0; i < p.B; ++i) {
+    int32_t id;
+    float prob;
+    std::memcpy(&id, h + static_cast<size_t>(i) * 4, 4);
+    std::memcpy(&prob, h + static_cast<size_t>(p.B + i) * 4, 4);
+    out[i] = TokenSample{static_cast<uint32_t>(id), prob};
+  }
+  wait_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
   return out;
+}
+
+void ForwardExecutor::discard() {
+  if (inflight_.empty()) return;
+  const Pending p = inflight_.front();
+  inflight_.pop_front();
+  if (p.B == 0) return;
+  check(fi_event_wait(events_[p.slot]));
+  uint32_t words[4];
+  std::memcpy(words, static_cast<const uint8_t*>(h_out_[p.slot]) + static_cast<size_t>(p.B) * 8, sizeof(words));
+  if ((words[0] | words[1] | words[2] | words[3]) != 0) check(fi_ctx_check_faults(ctx_));
 }
 
 }  // namespace fr

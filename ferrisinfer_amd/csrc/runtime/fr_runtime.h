@@ -12,6 +12,7 @@
 
 #include <array>
 #include <cstdint>
+#include <deque>
 #include <map>
 #include <optional>
 #include <string>
@@ -145,6 +146,10 @@ class BlockPool {
   BlockPool(fi_context* ctx, int32_t layers, int32_t num_blocks, int32_t block_size, int32_t kv_heads,
             int32_t head_dim, int32_t kv_dtype);
   int32_t allocate();
+  // The block the k-th next allocate() would return with no frees in between, or -1.
+  int32_t peek(size_t k) const {
+    return k < free_.size() ? free_[free_.size() - 1 - k] : -1;
+  }
   void incref(int32_t block);
   void decref(int32_t block);
   int32_t refcount(int32_t block) const { return refs_.at(block); }
@@ -352,9 +357,25 @@ class ForwardExecutor {
   ForwardExecutor& operator=(const ForwardExecutor&) = delete;
   // Returns one sample per batch sequence from its last row: the fused argmax head for a
   // greedy sampler, else the row's logits through the device sampler with states[i]
-  // (advanced in place by one draw per sequence).
+  // (advanced in place by one draw per sequence).  run = launch + collect.
   std::vector<TokenSample> run(const PackedBatch& batch, const SamplerConfig& sampler, std::vector<uint64_t>* states);
-  // Host seconds of the last run: enqueueing every launch, then waiting for the samples.
+  // Enqueues one tick (uploads, forward, the copy of its samples and fault words into pinned
+  // host memory) and returns without waiting.  feed_rows (a greedy decode tick enqueued behind
+  // the previous launch): row i's input token is the previous launch's sample feed_rows[i] when
+  // that is >= 0, read on the device; other rows keep the batch's token id.
+  void launch(const PackedBatch& batch, const SamplerConfig& sampler, const std::vector<uint64_t>* states,
+              const std::vector<int32_t>* feed_rows = nullptr);
+  // Waits for the oldest launched tick and returns its samples (states: the sampled path's
+  // advanced states, downloaded).
+  std::vector<TokenSample> collect(std::vector<uint64_t>* states);
+  // Waits for the oldest launched tick and drops its samples.
+  void discard();
+  size_t in_flight() const { return inflight_.size(); }
+  // Whether launch(batch, ..., feed_rows) can run behind the single tick in flight: a greedy
+  // decode tick that keeps the previous tick's samples in place (no reallocation of them).
+  bool can_feed(const PackedBatch& batch) const;
+  // Host seconds of the last launch (enqueueing every launch) and the last collect (waiting for
+  // the samples).
   double last_enqueue_seconds() const { return enqueue_s_; }
   double last_wait_seconds() const { return wait_s_; }
   // Decode ticks replayed from a graph, graphs captured, graphs dropped (since creation).
@@ -382,6 +403,13 @@ class ForwardExecutor {
                   int32_t m, int32_t splits, float* out) const;
   void enqueue(const Plan& p);
   void drop_graphs();
+  void host_reserve(int slot, size_t meta_bytes, size_t out_bytes);
+  // One launched tick: its pinned slot and batch size (B = 0: a copy-only tick, no samples).
+  struct Pending {
+    int32_t slot;
+    int32_t B;
+    bool greedy;
+  };
   const DeviceModel* model_;
   BlockPool* pool_;
   fi_context* ctx_;
@@ -397,6 +425,15 @@ class ForwardExecutor {
   std::map<std::array<int32_t, 4>, int32_t> seen_;       // eager runs per shape since the last drop
   uint64_t graph_replays_ = 0, graph_captures_ = 0, graph_drops_ = 0;
   int32_t logits_rows_ = 0;  // rows of logits_ the last run sampled from
+  // Consecutive launches alternate between two pinned slots (metadata staging; samples, then the
+  // four fault words) and two events; at most two ticks are in flight.
+  std::deque<Pending> inflight_;
+  void* h_meta_[2] = {nullptr, nullptr};
+  void* h_out_[2] = {nullptr, nullptr};
+  size_t h_meta_bytes_[2] = {0, 0}, h_out_bytes_[2] = {0, 0};
+  fi_event* events_[2] = {nullptr, nullptr};
+  int32_t next_slot_ = 0;
+  int32_t out_rows_ = 0;  // samples the last launch leaves in out_
 };
 
 // runtime/scheduler.rs:109-648 over the batched executor.
@@ -406,7 +443,17 @@ class Scheduler {
             bool graph_decode = false);
   uint64_t submit(const std::vector<uint32_t>& prompt, size_t max_new_tokens, std::optional<uint32_t> stop_token);
   std::optional<std::pair<BatchKind, std::vector<uint64_t>>> plan_next_tick() const;
-  std::optional<TickReport> execute_next_tick();
+  // run_ahead: once this tick is enqueued, also enqueue the next tick when it will be a greedy
+  // decode tick (stream overlap, docs/performance-roadmap.md:321-326).  Its batch follows from
+  // the state this tick leaves except the token ids, which are this tick's samples, fed on the
+  // device.  The next call keeps it when its own planning packs the same batch and drops it
+  // otherwise (after a submit, for instance): the ticks and their results are those of calls
+  // without run_ahead.
+  std::optional<TickReport> execute_next_tick(bool run_ahead = false);
+  // [ticks enqueued ahead, kept, dropped, 1 if the last tick was one enqueued ahead]
+  std::array<uint64_t, 4> run_ahead_counters() const {
+    return {ahead_launched_, ahead_kept_, ahead_dropped_, last_tick_ahead_ ? 1u : 0u};
+  }
   bool has_pending() const;
   const Sequence* sequence(uint64_t id) const;
   const PackedBatch& last_batch() const { return last_batch_; }
@@ -429,6 +476,9 @@ class Scheduler {
   void append_to_batch(Sequence& s, const std::vector<uint32_t>& tokens, PackedBatch* batch);
   std::vector<ManagedBlockId> release(uint64_t id);
   void finalize_batch(PackedBatch* batch) const;
+  bool launch_ahead(const PackedBatch& current);
+  bool ahead_matches(const PackedBatch& batch) const;
+  void drop_ahead();
 
   DeviceModel* model_;
   BlockPool* pool_;
@@ -443,6 +493,19 @@ class Scheduler {
   std::vector<Sequence> sequences_;
   PackedBatch last_batch_;
   std::array<double, 4> tick_profile_{};
+  // The tick enqueued ahead: its batch (token ids of fed rows unset), the row of the previous
+  // tick each of its rows is fed from (-1: the batch's own id), and that tick's samples.
+  struct Ahead {
+    bool active = false;
+    uint64_t state = 0;
+    PackedBatch batch;
+    std::vector<int32_t> feed_rows;
+    std::vector<TokenSample> fed;
+  };
+  Ahead ahead_;
+  uint64_t state_ = 0;  // bumped by every submit: an ahead tick planned before one is dropped
+  uint64_t ahead_launched_ = 0, ahead_kept_ = 0, ahead_dropped_ = 0;
+  bool last_tick_ahead_ = false;
 };
 
 }  // namespace fr

@@ -14,6 +14,7 @@
 // the tick return to the pool only after the forward.
 #include <algorithm>
 #include <chrono>
+#include <map>
 
 #include "fr_runtime.h"
 
@@ -210,6 +211,7 @@ uint64_t Scheduler::submit(const std::vector<uint32_t>& prompt, size_t max_new_t
   s.sampler_state = sampler_state_new(session_.sampler.seed);  // Session::new (session.rs:110, 138)
   const uint64_t id = s.sequence_id;
   sequences_.push_back(std::move(s));
+  state_ += 1;  // the next tick's plan may change
   block_manager_.update_shared_prefix(id, std::nullopt);
   refresh_prefix_metadata(id);
   return id;
@@ -383,17 +385,117 @@ void Scheduler::finalize_batch(PackedBatch* batch) const {
   }
 }
 
+bool Scheduler::launch_ahead(const PackedBatch& current) {
+  // The next tick as its own call would pack it (execute_next_tick's decode branch with
+  // append_to_batch and finalize_batch), from the state this tick leaves: positions, phases and
+  // finished sequences are settled before its forward, and blocks are taken from the top of the
+  // pool's free list in row order.  Only the token ids wait for this tick's samples.
+  if (!session_.sampler.is_greedy() || executor_.in_flight() != 1) return false;
+  const auto plan = plan_next_tick();
+  if (!plan || plan->first != BatchKind::Decode) return false;
+  const size_t bs = static_cast<size_t>(pool_->block_size());
+  std::map<uint64_t, int32_t> row_of;
+  for (size_t i = 0; i < current.sequence_ids.size(); ++i) row_of[current.sequence_ids[i]] = static_cast<int32_t>(i);
+  PackedBatch nb;
+  nb.kind = BatchKind::Decode;
+  nb.cu_seqlens.push_back(0);
+  std::vector<int32_t> feed;
+  std::vector<std::vector<int32_t>> tables;
+  size_t taken = 0;
+  for (uint64_t id : plan->second) {
+    const Sequence& s = sequences_[index_of(id)];
+    if (s.position >= session_.max_sequence_length) continue;  // finishes with no row
+    if (s.history.empty()) return false;                       // that call fails on its own
+    const auto it = row_of.find(id);
+    const int32_t row = it == row_of.end() ? -1 : it->second;
+    if (row < 0 && !s.last_sample) return false;
+    std::vector<int32_t> blocks = s.blocks;
+    const size_t pos = s.position, end = pos + 1;
+    while (blocks.size() * bs < end) {
+      const int32_t blk = pool_->peek(taken++);
+      if (blk < 0) return false;  // the pool runs out: that call reports it
+      blocks.push_back(blk);
+    }
+    nb.token_ids.push_back(row < 0 ? static_cast<int32_t>(s.last_sample->token_id) : 0);
+    nb.positions.push_back(static_cast<int32_t>(pos));
+    nb.slot_mapping.push_back(static_cast<int64_t>(blocks[pos / bs]) * static_cast<int64_t>(bs) +
+                              static_cast<int64_t>(pos % bs));
+    nb.sequence_ids.push_back(id);
+    nb.context_lens.push_back(static_cast<int32_t>(end));
+    nb.cu_seqlens.push_back(static_cast<int32_t>(nb.token_ids.size()));
+    nb.last_rows.push_back(static_cast<int32_t>(nb.token_ids.size()) - 1);
+    nb.max_query_len = std::max<int32_t>(nb.max_query_len, 1);
+    nb.max_context_len = std::max<int32_t>(nb.max_context_len, static_cast<int32_t>(end));
+    tables.push_back(std::move(blocks));
+    feed.push_back(row);
+  }
+  if (nb.sequence_ids.empty() || !executor_.can_feed(nb)) return false;
+  int32_t max_blocks = 1;
+  for (int32_t len : nb.context_lens) max_blocks = std::max<int32_t>(max_blocks, static_cast<int32_t>((len + bs - 1) / bs));
+  nb.max_blocks = max_blocks;
+  nb.block_tables.assign(nb.sequence_ids.size() * max_blocks, 0);
+  for (size_t i = 0; i < tables.size(); ++i) {
+    const size_t n = (static_cast<size_t>(nb.context_lens[i]) + bs - 1) / bs;
+    for (size_t j = 0; j < n; ++j) nb.block_tables[i * max_blocks + j] = tables[i][j];
+  }
+  executor_.launch(nb, session_.sampler, nullptr, &feed);
+  ahead_.active = true;
+  ahead_.state = state_;
+  ahead_.batch = std::move(nb);
+  ahead_.feed_rows = std::move(feed);
+  ahead_.fed.clear();
+  ahead_launched_ += 1;
+  return true;
+}
+
+bool Scheduler::ahead_matches(const PackedBatch& b) const {
+  const PackedBatch& a = ahead_.batch;
+  if (a.kind != b.kind || a.sequence_ids != b.sequence_ids || a.positions != b.positions ||
+      a.slot_mapping != b.slot_mapping || a.cu_seqlens != b.cu_seqlens || a.context_lens != b.context_lens ||
+      a.block_tables != b.block_tables || a.max_blocks != b.max_blocks || a.last_rows != b.last_rows ||
+      a.max_query_len != b.max_query_len || a.max_context_len != b.max_context_len || !b.copy_src.empty() ||
+      a.token_ids.size() != b.token_ids.size() || ahead_.feed_rows.size() != b.token_ids.size()) {
+    return false;
+  }
+  // the device fed row i with the previous tick's sample feed_rows[i]
+  for (size_t i = 0; i < b.token_ids.size(); ++i) {
+    const int32_t r = ahead_.feed_rows[i];
+    const int32_t fed = r >= 0 ? (static_cast<size_t>(r) < ahead_.fed.size()
+                                      ? static_cast<int32_t>(ahead_.fed[r].token_id) : -1)
+                               : a.token_ids[i];
+    if (fed != b.token_ids[i]) return false;
+  }
+  return true;
+}
+
+void Scheduler::drop_ahead() {
+  ahead_.active = false;
+  ahead_dropped_ += 1;
+  executor_.discard();  // waits for it; its K/V rows sit in slots the kept ticks write again
+}
+
 std::vector<ManagedBlockId> Scheduler::release(uint64_t id) {
   // scheduler.rs:590-599: the session goes; its pool blocks are returned after the forward
   sequences_[index_of(id)].resident = false;
   return block_manager_.remove_sequence(id);
 }
 
-std::optional<TickReport> Scheduler::execute_next_tick() {
+std::optional<TickReport> Scheduler::execute_next_tick(bool run_ahead) {
   // scheduler.rs:393-538
   const auto t0 = std::chrono::steady_clock::now();
+  last_tick_ahead_ = false;
+  // a call that failed may have left launched ticks behind
+  if (!ahead_.active) {
+    while (executor_.in_flight() > 0) executor_.discard();
+  }
+  // a tick enqueued ahead was planned from the state the last tick left; a submit since may
+  // change this tick's plan
+  if (ahead_.active && ahead_.state != state_) drop_ahead();
   auto plan = plan_next_tick();
-  if (!plan) return std::nullopt;
+  if (!plan) {
+    if (ahead_.active) drop_ahead();
+    return std::nullopt;
+  }
   TickReport report;
   report.kind = plan->first;
   report.sequence_ids = plan->second;
@@ -495,28 +597,46 @@ std::optional<TickReport> Scheduler::execute_next_tick() {
   finalize_batch(&batch);
   const double sched_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   double enqueue_s = 0.0, wait_s = 0.0;
-  if (!batch.sequence_ids.empty() || !batch.copy_src.empty()) {
-    std::vector<uint64_t> states(batch.sequence_ids.size());
-    for (size_t i = 0; i < states.size(); ++i) states[i] = sequences_[index_of(batch.sequence_ids[i])].sampler_state;
-    std::vector<TokenSample> samples = executor_.run(batch, session_.sampler, &states);
-    enqueue_s = executor_.last_enqueue_seconds();
+  bool in_flight = false;  // this tick is the one enqueued ahead by the last call
+  if (ahead_.active) {
+    if (ahead_matches(batch)) {
+      in_flight = true;
+      ahead_.active = false;
+      ahead_kept_ += 1;
+      last_tick_ahead_ = true;
+    } else {
+      drop_ahead();
+    }
+  }
+  const bool work = !batch.sequence_ids.empty() || !batch.copy_src.empty();
+  std::vector<uint64_t> states(batch.sequence_ids.size());
+  for (size_t i = 0; i < states.size(); ++i) states[i] = sequences_[index_of(batch.sequence_ids[i])].sampler_state;
+  const auto t_enqueue = std::chrono::steady_clock::now();
+  if (work && !in_flight) executor_.launch(batch, session_.sampler, &states);
+  // The blocks of finished sequences go back to the pool now (the reference returns them after
+  // the forward): every later use of them is enqueued behind this tick.
+  for (uint64_t id : to_release) {
+    Sequence& s = sequences_[index_of(id)];
+    for (int32_t blk : s.blocks) pool_->decref(blk);
+    s.blocks.clear();
+  }
+  if (run_ahead && work && copy_sample.empty()) launch_ahead(batch);
+  enqueue_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_enqueue).count();
+  if (work) {
+    std::vector<TokenSample> samples = executor_.collect(&states);
     wait_s = executor_.last_wait_seconds();
     for (size_t i = 0; i < batch.sequence_ids.size(); ++i) {
       Sequence& s = sequences_[index_of(batch.sequence_ids[i])];
       s.last_sample = samples[i];
       s.sampler_state = states[i];
     }
+    if (ahead_.active) ahead_.fed = std::move(samples);
   }
   for (auto& [target, source] : copy_sample) {
     Sequence& t = sequences_[index_of(target)];
     const Sequence& src = sequences_[index_of(source)];
     t.last_sample = src.last_sample;
     t.sampler_state = src.sampler_state;
-  }
-  for (uint64_t id : to_release) {
-    Sequence& s = sequences_[index_of(id)];
-    for (int32_t blk : s.blocks) pool_->decref(blk);
-    s.blocks.clear();
   }
   last_batch_ = std::move(batch);
   tick_profile_ = {sched_s, enqueue_s, wait_s,

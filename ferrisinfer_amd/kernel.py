@@ -55,6 +55,16 @@ _SIGNATURES = {
     "fi_buf_upload": [_P, _P, _SZ, _P, _SZ],
     "fi_buf_download": [_P, _P, _SZ, _P, _SZ],
     "fi_buf_zero": [_P, _P, _SZ],
+    "fi_host_alloc": [_P, _SZ, C.POINTER(_P)],
+    "fi_host_free": [_P, _P],
+    "fi_buf_upload_async": [_P, _P, _SZ, _P, _SZ],
+    "fi_buf_download_async": [_P, _P, _SZ, _P, _SZ],
+    "fi_ctx_faults_async": [_P, _P],
+    "fi_event_create": [_P, C.POINTER(_P)],
+    "fi_event_record": [_P, _P],
+    "fi_event_wait": [_P],
+    "fi_event_destroy": [_P],
+    "fi_token_feed": [_P, _P, _I32, _P, _I32, _P],
     "fi_kv_append": [_P, _P, _P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32],
     "fi_kv_copy_blocks": [_P, _P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
     "fi_kv_gather": [_P, _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P],

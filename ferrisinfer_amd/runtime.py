@@ -56,6 +56,8 @@ def load() -> C.CDLL:
             "fr_set_weight_device": [_P, C.c_char_p, _P, _I32, _I64],
             "fr_submit": [_P, _P, _I64, _I64, _I64, C.POINTER(C.c_uint64)],
             "fr_execute_next_tick": [_P, C.POINTER(_I32)],
+            "fr_execute_next_tick_ex": [_P, _I32, C.POINTER(_I32)],
+            "fr_run_ahead_counters": [_P, _P],
             "fr_has_pending": [_P],
             "fr_last_report": [_P, C.POINTER(_I32), _P, _P, _I64, C.POINTER(_I64)],
             "fr_last_released": [_P, _I64, _P, _I64, C.POINTER(_I64)],
@@ -161,6 +163,8 @@ class Runtime:
         h = _P()
         _check(L.fr_create(ordinal, C.byref(mc), C.byref(rc), C.byref(h)))
         self.h = h
+        self._ahead_used = False  # a call asked to run ahead: later ticks may have started early
+        self._last_return = None  # perf_counter when the last execute call returned
         self.vocab = vocab
 
     def close(self):
@@ -173,6 +177,12 @@ class Runtime:
             self.close()
         except Exception:
             pass
+
+    def run_ahead_counters(self) -> dict:
+        """Ticks enqueued ahead, kept, dropped; whether the last tick was one enqueued ahead."""
+        out = np.zeros(4, np.uint64)
+        _check(load().fr_run_ahead_counters(self.h, _addr(out)))
+        return dict(launched=int(out[0]), kept=int(out[1]), dropped=int(out[2]), last_ahead=bool(out[3]))
 
     def graph_counters(self) -> dict:
         """Decode ticks replayed from graphs, graphs captured, graphs dropped."""
@@ -223,16 +233,30 @@ class Runtime:
                                 -1 if stop_token is None else stop_token, C.byref(out)))
         return int(out.value)
 
-    def execute_next_tick(self):
+    def execute_next_tick(self, run_ahead=False):
         """Returns None or (kind, [update dicts]) in the oracle Scheduler's format.  The wall
         time of the native tick (host scheduling, the batched forward, the sample download) is
-        kept in ``last_tick_seconds``."""
+        kept in ``last_tick_seconds``.
+
+        run_ahead (FR_TICK_RUN_AHEAD): also enqueue the next tick when it will be a greedy decode
+        tick, so the device runs it while this call returns; the results are those of calls
+        without it.  A tick that ran ahead started on the device during the previous call, so
+        its ``last_tick_seconds`` is the time since the previous call returned (the caller's
+        time in between included), not the call's own duration."""
         L = load()
         ex = C.c_int32()
         t0 = time.perf_counter()
-        status = L.fr_execute_next_tick(self.h, C.byref(ex))
-        self.last_tick_seconds = time.perf_counter() - t0
+        if run_ahead or self._ahead_used:
+            self._ahead_used = True
+            status = L.fr_execute_next_tick_ex(self.h, 1 if run_ahead else 0, C.byref(ex))
+        else:
+            status = L.fr_execute_next_tick(self.h, C.byref(ex))
+        t1 = time.perf_counter()
+        self.last_tick_seconds = t1 - t0
         _check(status)
+        if self._ahead_used and self._last_return is not None and self.run_ahead_counters()["last_ahead"]:
+            self.last_tick_seconds = t1 - self._last_return
+        self._last_return = t1
         if not ex.value:
             return None
         cap = 4096

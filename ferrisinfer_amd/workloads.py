@@ -282,13 +282,16 @@ def c4_requests(seed: int = 0, n: int = 128, vocab: int = 151936) -> list:
             for i, (L, o, t) in enumerate(zip(lens, outs, ticks))]
 
 
-def run_continuous(sched, requests: list, max_ticks: int | None = None) -> dict:
+def run_continuous(sched, requests: list, max_ticks: int | None = None, run_ahead: bool = False) -> dict:
     """Drives a scheduler (the GPU Runtime or the oracle's ReferenceScheduler) the way the
     reference's continuous-batching profile does (cli/main.rs:1716-1834): requests arriving
     at the current tick are submitted before it runs, an idle scheduler jumps to the next
     arrival, and each tick's wall time is the scheduler's own ``execute_next_tick``.  Returns
     the tick log and per-request generated tokens; ``decode_tok_s`` is generated tokens over
-    the summed decode-tick time (cli/main.rs:1502-1512, 1619-1622)."""
+    the summed decode-tick time (cli/main.rs:1502-1512, 1619-1622).
+
+    run_ahead (GPU Runtime only): a tick followed by no arrival is executed with run_ahead, so
+    the next decode tick is already on the device when the driver comes back."""
     ticks, seq_of = [], []
     nxt, tick_index = 0, 0
     while nxt < len(requests) or sched.has_pending():
@@ -301,7 +304,11 @@ def run_continuous(sched, requests: list, max_ticks: int | None = None) -> dict:
             r = requests[nxt]
             seq_of.append(sched.submit(r["prompt"], max_new_tokens=r["max_new_tokens"]))
             nxt += 1
-        rep = sched.execute_next_tick()
+        if run_ahead:
+            quiet = nxt >= len(requests) or requests[nxt]["arrival_tick"] > tick_index + 1
+            rep = sched.execute_next_tick(run_ahead=quiet)
+        else:
+            rep = sched.execute_next_tick()
         if rep is None:
             if nxt < len(requests):
                 tick_index = requests[nxt]["arrival_tick"]

@@ -124,6 +124,42 @@ int32_t fi_buf_download(fi_context* ctx, void* dst, size_t dst_bytes, const void
  * Unsupported (nvidia.rs:319-323). */
 int32_t fi_buf_zero(fi_context* ctx, void* d_ptr, size_t bytes);
 
+/* ---------------------------------------------------------------- stream overlap
+ * No counterpart in the reference's kernel layer, whose copies all wait (cuMemcpyHtoD/DtoH,
+ * kernel/gpu/nvidia.rs:340-470).  These serve the roadmap's stream overlap
+ * (docs/performance-roadmap.md:321-326): a host runtime enqueues the next decode step while the
+ * device still runs the current one, and waits only for the samples it needs.
+ *   - fi_host_alloc / fi_host_free: pinned host memory (fi_host_free waits for the stream).
+ *   - fi_buf_upload_async / fi_buf_download_async: the copies of fi_buf_upload / download,
+ *     enqueued on the context's stream without waiting (same exact-length rule).  The host
+ *     memory should be pinned so the copy overlaps the host; it must stay valid and unchanged
+ *     until the copy has run, which an event recorded after it reports.
+ *   - fi_ctx_faults_async: enqueues a copy of the context's four device fault words into
+ *     h_words[4]; a non-zero word means fi_ctx_check_faults will report (and clear) a fault.
+ *   - fi_event_record marks the context's stream; fi_event_wait returns once everything
+ *     enqueued before the mark has run. */
+int32_t fi_host_alloc(fi_context* ctx, size_t bytes, void** h_out);
+int32_t fi_host_free(fi_context* ctx, void* h_ptr);
+int32_t fi_buf_upload_async(fi_context* ctx, void* d_dst, size_t dst_bytes, const void* h_src,
+                            size_t src_bytes);
+int32_t fi_buf_download_async(fi_context* ctx, void* h_dst, size_t dst_bytes, const void* d_src,
+                              size_t src_bytes);
+int32_t fi_ctx_faults_async(fi_context* ctx, uint32_t* h_words);
+typedef struct fi_event fi_event;
+int32_t fi_event_create(fi_context* ctx, fi_event** out);
+int32_t fi_event_record(fi_context* ctx, fi_event* ev);
+int32_t fi_event_wait(fi_event* ev);
+int32_t fi_event_destroy(fi_event* ev);
+
+/* Feeds one step's sampled token ids into the next step's input ids on the device:
+ * ids[i] = prev_tokens[rows[i]] where rows[i] >= 0; other entries keep their value.  A row at or
+ * beyond prev_count leaves its entry unchanged and is reported as Runtime by the next
+ * fi_ctx_check_faults.  The device side of the reference's step_reference feeding the previous
+ * sample (runtime/session.rs:246-262), for a host that enqueues the step before it has read the
+ * sample back. */
+int32_t fi_token_feed(fi_context* ctx, const int32_t* d_prev_tokens, int32_t prev_count,
+                      const int32_t* d_rows, int32_t n, int32_t* d_ids);
+
 /* ---------------------------------------------------------------- KV pool ops */
 
 /* Scatters this step's K/V rows into the paged pool by slot_mapping, converting f32 to the
