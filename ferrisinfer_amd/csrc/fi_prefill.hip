@@ -805,7 +805,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
   if (q0 >= qlen) return;
   const int ctx = a.context_lens[seq];
   const int start = ctx - qlen;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // the wave index is wave-uniform: held in a scalar register through the chunk loop
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 15, lk = lane >> 4;
 
   // Q stays f32 (B operand row li of group g, d = 32 t + 8 lk .. +7) and is split on use
@@ -863,18 +864,28 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
     id_next = in_table ? id : -1;
     off_next = exact ? key_off : kpc - lb * a.block_size;
   };
+  // K rows of the next chunk are fetched after the score products, V rows after P V: the V
+  // registers are then not live through P V, which with the K registers and f32 Q would
+  // exceed the 256 VGPRs of two waves a SIMD
+  size_t row_next = 0;
   auto fetch = [&](int c) {
     c = min(c, nchunks - 1);
     part_next = (c + 1) * KB > kend;  // workgroup-uniform: the chunk has padding keys
     valid_next = c * KB + skey < kend;
     const bool bad = id_next < 0 || id_next >= a.num_blocks;
     bad_block |= bad;
-    const size_t row = ((size_t)(bad ? 0 : id_next) * a.hkv + kvh) * a.block_size + off_next;
+    row_next = ((size_t)(bad ? 0 : id_next) * a.hkv + kvh) * a.block_size + off_next;
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int dq = sq0 + KR * r;
-      kr[r] = *reinterpret_cast<const float4*>(k_cache + row * D + 4 * dq);
-      vr[r] = *reinterpret_cast<const float4*>(v_cache + row * D + 4 * dq);
+      kr[r] = *reinterpret_cast<const float4*>(k_cache + row_next * D + 4 * dq);
+    }
+  };
+  auto fetch_v = [&]() {
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) {
+      const int dq = sq0 + KR * r;
+      vr[r] = *reinterpret_cast<const float4*>(v_cache + row_next * D + 4 * dq);
     }
   };
   // padding keys of a partial chunk are stored as zero (their clamped loads hold a valid row)
@@ -894,11 +905,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
         *reinterpret_cast<uint2*>(&Ks[p][skey][4 * dq]) = pk[p];
         *reinterpret_cast<uint2*>(&Vs[p][skey][4 * dq]) = pv[p];
       }
+      __builtin_amdgcn_sched_barrier(0);  // one quad's pieces live at a time
     }
   };
 
   lookup(0);
   fetch(0);
+  fetch_v();
   lookup(1);
   stage();
   __syncthreads();
@@ -934,8 +947,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // the next chunk's rows are fetched here, after the score products (whose K fragments and
-    // Q pieces are the register peak), and land during the softmax and P V
+    // the next chunk's K rows are fetched here, after the score products (whose K fragments
+    // and Q pieces are the register peak), and land during the softmax and P V
     __builtin_amdgcn_sched_barrier(0);
     fetch(c + 1);  // the last chunk re-reads itself: the loads stay unconditional
     lookup(c + 2);
@@ -1012,6 +1025,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
       for (int g = 0; g < RG; ++g) o[g][dt] = mma6(vf, pp[g], o[g][dt]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    fetch_v();  // its V rows: the loads are in flight while the waves meet at the barrier
     __syncthreads();  // every wave is done with this chunk's K/V
     if (c + 1 < nchunks) {  // workgroup-uniform
       stage();
@@ -1022,17 +1036,23 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
   if (bad_block) atomicOr(a.faults, FI_FAULT_BLOCK_RANGE);
 
   // ---- normalise and store: lane holds row li of each group, d = 16 dt + 4 lk + v ----
+  // the lane's row and column are formed again here (lane id from mbcnt, the sequence's rows
+  // reloaded) rather than kept live through the chunk loop, where registers are at the limit
+  const int lane_e = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int li_e = lane_e & 15, lk_e = lane_e >> 4;
+  const int qs_e = a.cu_seqlens[seq], qlen_e = a.cu_seqlens[seq + 1] - qs_e;
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     float l_row = l_part[g] + fi::lane_xor16(l_part[g], lane);
     l_row += fi::lane_xor32(l_row, lane);
-    const int h = row_r[g] / QT, t = row_r[g] % QT;
-    if (h < a.group && q0 + t < qlen) {
+    const int rr = 16 * (w + 4 * g) + li_e;
+    const int h = rr / QT, t = rr % QT;
+    if (h < a.group && q0 + t < qlen_e) {
       const float inv = 1.0f / l_row;
-      float* op = a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D;
+      float* op = a.out + ((size_t)(qs_e + q0 + t) * a.hq + kvh * a.group + h) * D;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        *reinterpret_cast<float4*>(op + 16 * dt + 4 * lk) =
+        *reinterpret_cast<float4*>(op + 16 * dt + 4 * lk_e) =
             make_float4(o[g][dt][0] * inv, o[g][dt][1] * inv, o[g][dt][2] * inv, o[g][dt][3] * inv);
       }
     }
