@@ -118,19 +118,21 @@ def test_run_ahead_matches_serial_with_arrivals_and_stops(graph):
         assert rt.pool_free_count() == 4096
 
 
-def test_run_ahead_more_decoding_sequences_than_the_batch():
+@pytest.mark.parametrize("weight_dtype,kv_dtype", [("f32", "f32"), ("f32", "bf16"), ("bf16", "f32")])
+def test_run_ahead_more_decoding_sequences_than_the_batch(weight_dtype, kv_dtype):
     """12 sequences decoding at once with max_batch 4: a tick's rows come partly from the
     previous tick (fed on the device) and partly from sequences that sat out (ids from the
-    host)."""
+    host).  Also over a bf16 KV pool and bf16-stored weights."""
     from ferrisinfer_amd.workloads import TINY_LLAMA_C1, random_weights
 
-    print("run ahead: batch-limited decode", flush=True)
+    print(f"run ahead: batch-limited decode, weights {weight_dtype}, KV {kv_dtype}", flush=True)
     cfg = dict(TINY_LLAMA_C1, layers=2)
     weights = random_weights(cfg, seed=6)
     kw = dict(max_batch=4)
     reqs = arrivals(cfg, 22, 12, (5, 40), (20, 40), 1)
-    base = drive(make_runtime(cfg, weights, True, kw), reqs, None)
-    rt = make_runtime(cfg, weights, True, kw)
+    mk = lambda: make_runtime(cfg, weights, True, kw, weight_dtype=weight_dtype, kv_dtype=kv_dtype)
+    base = drive(mk(), reqs, None)
+    rt = mk()
     assert_same(base, drive(rt, reqs, "quiet"))
     c = rt.run_ahead_counters()
     print(f"counters {c}", flush=True)
