@@ -453,8 +453,13 @@ void ForwardExecutor::enqueue(const Plan& p) {
     check(fi_splitk_residual_rms_norm(ctx_, part, p.s_w2, w.w2_bias.f32(), h1, hidden, next_norm, normed, T, H,
                                       c.rms_norm_eps));
   }
-  // the final norm ran over every row; each sequence's last row feeds the head
-  check(fi_embedding(ctx_, normed, T, H, p.last, B, last_norm_.f32()));
+  // the final norm ran over every row; each sequence's last row feeds the head.  A decode tick
+  // has one row per sequence, in sequence order, so the head reads the normed rows in place.
+  const float* head_in = normed;
+  if (!(p.kind == BatchKind::Decode && T == B)) {
+    check(fi_embedding(ctx_, normed, T, H, p.last, B, last_norm_.f32()));
+    head_in = last_norm_.f32();
+  }
   const void* lm = model_->lm_head_packed();
   int32_t* tok = static_cast<int32_t*>(out_.get());
   float* prob = out_.f32() + B;
@@ -462,10 +467,10 @@ void ForwardExecutor::enqueue(const Plan& p) {
     // fused greedy head (matmul_rhs_transposed_argmax_f32, matmul.rs:190-274), as the
     // reference session's greedy path (session.rs:349-356, 393-398)
     if (bf16) {
-      check(fi_lm_head_argmax_bf16(ctx_, last_norm_.f32(), FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), B, H,
+      check(fi_lm_head_argmax_bf16(ctx_, head_in, FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), B, H,
                                    c.vocab_size, tok, prob));
     } else {
-      check(fi_lm_head_argmax_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), B, H, c.vocab_size,
+      check(fi_lm_head_argmax_packed(ctx_, head_in, H, static_cast<const float*>(lm), B, H, c.vocab_size,
                                      tok, prob));
     }
   } else {
@@ -473,10 +478,10 @@ void ForwardExecutor::enqueue(const Plan& p) {
     // (session.rs:357-373, 399-406) with each sequence's sampler state; the states and the
     // per-row configuration were uploaded to samp_ before this sequence
     if (bf16) {
-      check(fi_gemm_bf16(ctx_, last_norm_.f32(), FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), H, c.vocab_size,
+      check(fi_gemm_bf16(ctx_, head_in, FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), H, c.vocab_size,
                          B, 1, logits_.f32()));
     } else {
-      check(fi_gemm_packed(ctx_, last_norm_.f32(), H, static_cast<const float*>(lm), H, c.vocab_size,
+      check(fi_gemm_packed(ctx_, head_in, H, static_cast<const float*>(lm), H, c.vocab_size,
                            DeviceModel::kLmPack, B, 1, logits_.f32()));
     }
     uint8_t* d = static_cast<uint8_t*>(samp_.get());
