@@ -1,4 +1,5 @@
 // C entry points of libferrisinfer_runtime.so (include/ferrisinfer_runtime.h).
+#include <array>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -45,6 +46,11 @@ int32_t guard(F&& f) {
   }
 }
 Runtime* rt(void* h) { return static_cast<Runtime*>(h); }
+// the last tick's batch, or an empty one before the first tick (observers create nothing)
+const fr::PackedBatch& last_batch_of(void* h) {
+  static const fr::PackedBatch empty;
+  return rt(h)->scheduler ? rt(h)->scheduler->last_batch() : empty;
+}
 }  // namespace
 
 extern "C" {
@@ -216,7 +222,8 @@ int32_t fr_execute_next_tick_ex(void* h, int32_t flags, int32_t* executed) {
 
 int32_t fr_run_ahead_counters(void* h, uint64_t* out) {
   return guard([&] {
-    const auto c = rt(h)->scheduler_ready().run_ahead_counters();
+    std::array<uint64_t, 4> c{};
+    if (rt(h)->scheduler) c = rt(h)->scheduler->run_ahead_counters();
     for (size_t i = 0; i < c.size(); ++i) out[i] = c[i];
   });
 }
@@ -264,7 +271,7 @@ int32_t fr_last_released(void* h, int64_t update, int64_t* out, int64_t capacity
 
 int32_t fr_generated(void* h, uint64_t seq, uint32_t* out, int64_t capacity, int64_t* n_out) {
   return guard([&] {
-    const fr::Sequence* s = rt(h)->scheduler_ready().sequence(seq);
+    const fr::Sequence* s = rt(h)->scheduler ? rt(h)->scheduler->sequence(seq) : nullptr;
     if (!s) fr::fail(fr::ErrorKind::Runtime, "unknown sequence");
     if (static_cast<int64_t>(s->generated.size()) > capacity) fr::fail(fr::ErrorKind::InvalidShape, "capacity too small");
     std::memcpy(out, s->generated.data(), s->generated.size() * sizeof(uint32_t));
@@ -274,7 +281,7 @@ int32_t fr_generated(void* h, uint64_t seq, uint32_t* out, int64_t capacity, int
 
 int32_t fr_sequence_blocks(void* h, uint64_t seq, int32_t* out, int64_t capacity, int64_t* n_out) {
   return guard([&] {
-    const fr::Sequence* s = rt(h)->scheduler_ready().sequence(seq);
+    const fr::Sequence* s = rt(h)->scheduler ? rt(h)->scheduler->sequence(seq) : nullptr;
     if (!s) fr::fail(fr::ErrorKind::Runtime, "unknown sequence");
     if (static_cast<int64_t>(s->blocks.size()) > capacity) fr::fail(fr::ErrorKind::InvalidShape, "capacity too small");
     std::memcpy(out, s->blocks.data(), s->blocks.size() * sizeof(int32_t));
@@ -288,14 +295,18 @@ int32_t fr_pool_free_count(void* h, int64_t* out) {
 
 int32_t fr_graph_counters(void* h, uint64_t* out) {
   return guard([&] {
-    const auto c = rt(h)->scheduler_ready().executor().graph_counters();
+    // observers report an empty state before the first submit (creating the scheduler here
+    // would freeze the weights)
+    std::array<uint64_t, 3> c{};
+    if (rt(h)->scheduler) c = rt(h)->scheduler->executor().graph_counters();
     for (size_t i = 0; i < c.size(); ++i) out[i] = c[i];
   });
 }
 
 int32_t fr_last_tick_profile(void* h, double* out) {
   return guard([&] {
-    const auto p = rt(h)->scheduler_ready().last_tick_profile();
+    std::array<double, 4> p{};
+    if (rt(h)->scheduler) p = rt(h)->scheduler->last_tick_profile();
     for (size_t i = 0; i < p.size(); ++i) out[i] = p[i];
   });
 }
@@ -303,13 +314,14 @@ int32_t fr_last_tick_profile(void* h, double* out) {
 int32_t fr_last_logits(void* h, float* out, int64_t capacity, int64_t* rows) {
   return guard([&] {
     if (!rows || capacity < 0 || (capacity > 0 && !out)) fr::fail(fr::ErrorKind::InvalidConfig, "fr_last_logits: bad buffer");
-    rt(h)->scheduler_ready().executor().last_logits(out, static_cast<size_t>(capacity), rows);
+    *rows = 0;
+    if (rt(h)->scheduler) rt(h)->scheduler->executor().last_logits(out, static_cast<size_t>(capacity), rows);
   });
 }
 
 int32_t fr_last_batch_sizes(void* h, int64_t* sizes) {
   return guard([&] {
-    const fr::PackedBatch& b = rt(h)->scheduler_ready().last_batch();
+    const fr::PackedBatch& b = last_batch_of(h);
     sizes[0] = static_cast<int64_t>(b.token_ids.size());
     sizes[1] = static_cast<int64_t>(b.sequence_ids.size());
     sizes[2] = b.max_blocks;
@@ -324,7 +336,7 @@ int32_t fr_last_batch(void* h, int32_t* token_ids, int32_t* positions, int64_t* 
                       int32_t* context_lens, int32_t* block_tables, int32_t* copy_src, int32_t* copy_dst,
                       int32_t* copy_count, uint64_t* sequence_ids) {
   return guard([&] {
-    const fr::PackedBatch& b = rt(h)->scheduler_ready().last_batch();
+    const fr::PackedBatch& b = last_batch_of(h);
     auto cp = [](void* dst, const void* src, size_t bytes) {
       if (bytes) std::memcpy(dst, src, bytes);
     };

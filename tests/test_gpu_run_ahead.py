@@ -218,3 +218,24 @@ def test_run_ahead_c4_shape_batch_64():
     c = rt.run_ahead_counters()
     print(f"counters {c}", flush=True)
     assert c["kept"] >= 10 and c["dropped"] == 0
+
+
+def test_observers_before_submit_leave_weights_open():
+    """The counters, the tick profile, the last batch and the last logits report an empty state
+    before the first submit and create no scheduler: the weights can still be set."""
+    from ferrisinfer_amd.workloads import TINY_LLAMA_C1, random_weights
+
+    cfg = dict(TINY_LLAMA_C1, layers=1)
+    from ferrisinfer_amd.runtime import Runtime
+
+    rt = Runtime(cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
+                 cfg["vocab"], cfg["max_pos"], cfg["eps"], cfg["theta"], tie=cfg["tie"], graph_decode=True)
+    assert rt.run_ahead_counters() == dict(launched=0, kept=0, dropped=0, last_ahead=False)
+    assert rt.graph_counters() == dict(replays=0, captures=0, drops=0)
+    assert rt.last_tick_profile()["total"] == 0.0
+    assert rt.last_logits().shape[0] == 0
+    rt.set_weights(random_weights(cfg, seed=1))  # not frozen by the observers above
+    seq = rt.submit(np.arange(5, dtype=np.uint32), max_new_tokens=3)
+    while rt.execute_next_tick(run_ahead=True) is not None:
+        pass
+    assert len(rt.generated(seq)) == 3
