@@ -317,8 +317,23 @@ __global__ __launch_bounds__(kMergeThreads) void argmax_merge_kernel(const float
   const float* p = amax + (size_t)row * n_tiles * 3;
   float mx = -INFINITY, sum = 0.0f;
   int best = -1;
-  for (int t = threadIdx.x; t < n_tiles; t += kMergeThreads) {
-    argmax_combine(mx, best, sum, p[t * 3], reinterpret_cast<const int*>(p)[t * 3 + 1], p[t * 3 + 2]);
+  // a thread's tiles t, t + 256, ... are loaded kUnroll at a time before they are combined (in
+  // the same order, so the same sums): one memory round trip per kUnroll tiles instead of one
+  // per tile.  Loads past n_tiles read tile 0 and are dropped.
+  constexpr int kUnroll = 8;
+  for (int t0 = threadIdx.x; t0 < n_tiles; t0 += kMergeThreads * kUnroll) {
+    float omx[kUnroll], osum[kUnroll];
+    int obest[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int t = t0 + u * kMergeThreads;
+      const int tc = t < n_tiles ? t : 0;
+      omx[u] = p[tc * 3];
+      obest[u] = t < n_tiles ? reinterpret_cast<const int*>(p)[tc * 3 + 1] : -1;
+      osum[u] = p[tc * 3 + 2];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) argmax_combine(mx, best, sum, omx[u], obest[u], osum[u]);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
