@@ -1085,6 +1085,15 @@ def main():
             # logits head + device sampling in every tick
             sampled = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42), graph=main_graph)
             result["c4"]["sampled_chat_default"] = {k: sampled[k] for k in keys}
+            if "ahead" in variants:
+                # the same sampled pass run ahead: each tick's sampler states continue on the
+                # device; the ids must equal the serial sampled run's
+                sa = c4_continuous(args.seed, args.c4_requests, sampler=(0.7, 20, 0.9, 42), graph=main_graph,
+                                   run_ahead=True)
+                result["c4"]["sampled_chat_default_run_ahead"] = {k: sa[k] for k in keys + ("run_ahead_counters",)}
+                differ = sum(1 for a, b in zip(sampled["_tokens"], sa["_tokens"]) if a != b)
+                result["c4"]["sampled_chat_default_run_ahead"]["tokens_equal_serial"] = (
+                    differ == 0 and len(sampled["_tokens"]) == len(sa["_tokens"]))
         if "bf16" in variants:
             # bf16-stored projections and head (the storage of the real Qwen2.5-0.5B checkpoints)
             b16 = c4_continuous(args.seed, args.c4_requests, graph=main_graph, weight_dtype="bf16")

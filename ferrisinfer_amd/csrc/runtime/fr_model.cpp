@@ -477,25 +477,28 @@ void ForwardExecutor::enqueue(const Plan& p) {
     // last-row logits (matmul_rhs_transposed, one K split) and sample_last_token per row
     // (session.rs:357-373, 399-406) with each sequence's sampler state; the states and the
     // per-row configuration were uploaded to samp_ before this sequence
+    float* logits = logits_[p.ss].f32();
     if (bf16) {
       check(fi_gemm_bf16(ctx_, head_in, FI_DTYPE_F32, H, static_cast<const uint16_t*>(lm), H, c.vocab_size,
-                         B, 1, logits_.f32()));
+                         B, 1, logits));
     } else {
       check(fi_gemm_packed(ctx_, head_in, H, static_cast<const float*>(lm), H, c.vocab_size,
-                           DeviceModel::kLmPack, B, 1, logits_.f32()));
+                           DeviceModel::kLmPack, B, 1, logits));
     }
-    uint8_t* d = static_cast<uint8_t*>(samp_.get());
-    check(fi_sample_tokens(ctx_, logits_.f32(), c.vocab_size, B, c.vocab_size, reinterpret_cast<const float*>(d + B * 8),
+    uint8_t* d = static_cast<uint8_t*>(samp_[p.ss].get());
+    check(fi_sample_tokens(ctx_, logits, c.vocab_size, B, c.vocab_size, reinterpret_cast<const float*>(d + B * 8),
                            reinterpret_cast<const int32_t*>(d + B * 12), reinterpret_cast<const float*>(d + B * 16),
                            reinterpret_cast<uint64_t*>(d), tok, prob));
   }
 }
 
 void ForwardExecutor::last_logits(float* host, size_t capacity, int64_t* rows) const {
-  const size_t n = static_cast<size_t>(logits_rows_) * model_->config().vocab_size;
+  const int32_t lrows = samp_last_ >= 0 ? logits_rows_[samp_last_] : 0;
+  const size_t n = static_cast<size_t>(lrows) * model_->config().vocab_size;
   if (n > capacity) fail(ErrorKind::InvalidShape, "last logits need " + std::to_string(n) + " floats");
-  if (n) check(fi_buf_download(ctx_, host, n * sizeof(float), logits_.get(), n * sizeof(float)));
-  *rows = logits_rows_;
+  // the slot of the last returned tick: a tick enqueued behind it writes the other one
+  if (n) check(fi_buf_download(ctx_, host, n * sizeof(float), logits_[samp_last_].get(), n * sizeof(float)));
+  *rows = lrows;
 }
 
 std::vector<TokenSample> ForwardExecutor::run(const PackedBatch& b, const SamplerConfig& sampler,
@@ -518,14 +521,12 @@ void ForwardExecutor::launch(const PackedBatch& b, const SamplerConfig& sampler,
   const ModelConfig& c = model_->config();
   const int32_t T = static_cast<int32_t>(b.token_ids.size());
   const int32_t B = static_cast<int32_t>(b.context_lens.size());
-  if (feed != nullptr &&
-      (!sampler.is_greedy() || feed->size() != static_cast<size_t>(B) || T != B || !can_feed(b))) {
-    fail(ErrorKind::Runtime, "a tick fed from the previous tick's samples must be a greedy decode tick behind it");
+  if (feed != nullptr && (feed->size() != static_cast<size_t>(B) || T != B || !can_feed(b))) {
+    fail(ErrorKind::Runtime, "a tick fed from the previous tick's samples must be a decode tick behind it");
   }
-  logits_rows_ = 0;
   if (T == 0 || B == 0) {
     copy_only(b);  // waits for the stream
-    inflight_.push_back(Pending{-1, 0, true});
+    inflight_.push_back(Pending{-1, 0, true, 0});
     return;
   }
   if (!model_->finalized()) fail(ErrorKind::Runtime, "model weights are not packed (DeviceModel::finalize)");
@@ -599,11 +600,42 @@ void ForwardExecutor::launch(const PackedBatch& b, const SamplerConfig& sampler,
   std::vector<int32_t> no_feed;
   if (feed == nullptr) no_feed.assign(static_cast<size_t>(B), -1);
   const size_t o_feed = section(feed ? feed->data() : no_feed.data(), static_cast<size_t>(B) * 4);
-  // through the launch's pinned slot: the copy is ordered on the stream behind a tick still in
-  // flight, which reads the previous contents
+  // the same rows for the 8-byte sampler states, as pairs of 4-byte words
+  std::vector<int32_t> feed2(static_cast<size_t>(B) * 2, -1);
+  if (feed != nullptr) {
+    for (int32_t i = 0; i < B; ++i) {
+      const int32_t r = (*feed)[static_cast<size_t>(i)];
+      if (r >= 0) {
+        feed2[2 * static_cast<size_t>(i)] = 2 * r;
+        feed2[2 * static_cast<size_t>(i) + 1] = 2 * r + 1;
+      }
+    }
+  }
+  const size_t o_feed2 = section(feed2.data(), feed2.size() * 4);
+  // a sampled tick's sampler buffer: states [B] u64, temperature [B] f32, top_k [B] i32,
+  // top_p [B] f32, in the tick's sampling slot
+  const int32_t ss = greedy ? 0 : samp_next_;
+  std::vector<uint8_t> cfg;
+  if (!greedy) {
+    if (states == nullptr || states->size() != static_cast<size_t>(B)) {
+      fail(ErrorKind::InvalidShape, "sampled batch requires one sampler state per sequence");
+    }
+    cfg.resize(static_cast<size_t>(B) * 20);
+    std::memcpy(cfg.data(), states->data(), static_cast<size_t>(B) * 8);
+    const int32_t k32 = static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(sampler.top_k, 0), INT32_MAX));
+    for (int32_t i = 0; i < B; ++i) {
+      std::memcpy(cfg.data() + B * 8 + i * 4, &sampler.temperature, 4);
+      std::memcpy(cfg.data() + B * 12 + i * 4, &k32, 4);
+      std::memcpy(cfg.data() + B * 16 + i * 4, &sampler.top_p, 4);
+    }
+  }
+  // through the launch's pinned slot: the copies are ordered on the stream behind a tick still
+  // in flight, which reads the previous contents
   const int32_t slot = next_slot_;
-  host_reserve(slot, host.size(), static_cast<size_t>(B) * 8 + 16);
+  const size_t cfg_off = (host.size() + 7) & ~static_cast<size_t>(7);
+  host_reserve(slot, cfg_off + cfg.size(), static_cast<size_t>(B) * 16 + 16);
   std::memcpy(h_meta_[slot], host.data(), host.size());
+  if (!cfg.empty()) std::memcpy(static_cast<uint8_t*>(h_meta_[slot]) + cfg_off, cfg.data(), cfg.size());
   grow(meta_, host.size());
   check(fi_buf_upload_async(ctx_, meta_.get(), host.size(), h_meta_[slot], host.size()));
   auto at = [&](size_t off) { return static_cast<uint8_t*>(meta_.get()) + off; };
@@ -623,27 +655,24 @@ void ForwardExecutor::launch(const PackedBatch& b, const SamplerConfig& sampler,
   }
 
   if (!greedy) {
-    // one upload: states [B] u64, temperature [B] f32, top_k [B] i32, top_p [B] f32
-    if (states == nullptr || states->size() != static_cast<size_t>(B)) {
-      fail(ErrorKind::InvalidShape, "sampled batch requires one sampler state per sequence");
+    p.ss = ss;
+    grow(logits_[ss], static_cast<size_t>(B) * c.vocab_size * 4);
+    grow(samp_[ss], cfg.size());
+    check(fi_buf_upload_async(ctx_, samp_[ss].get(), cfg.size(), static_cast<uint8_t*>(h_meta_[slot]) + cfg_off,
+                              cfg.size()));
+    if (feed != nullptr) {
+      // fed rows continue from the states the previous tick advanced, in the other slot
+      check(fi_token_feed(ctx_, static_cast<const int32_t*>(samp_[ss ^ 1].get()), 2 * out_rows_,
+                          reinterpret_cast<const int32_t*>(at(o_feed2)), 2 * B,
+                          static_cast<int32_t*>(samp_[ss].get())));
     }
-    grow(logits_, static_cast<size_t>(B) * c.vocab_size * 4);
-    std::vector<uint8_t> cfg(static_cast<size_t>(B) * 20);
-    std::memcpy(cfg.data(), states->data(), static_cast<size_t>(B) * 8);
-    const int32_t k32 = static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(sampler.top_k, 0), INT32_MAX));
-    for (int32_t i = 0; i < B; ++i) {
-      std::memcpy(cfg.data() + B * 8 + i * 4, &sampler.temperature, 4);
-      std::memcpy(cfg.data() + B * 12 + i * 4, &k32, 4);
-      std::memcpy(cfg.data() + B * 16 + i * 4, &sampler.top_p, 4);
-    }
-    grow(samp_, cfg.size());
-    check(fi_buf_upload(ctx_, samp_.get(), cfg.size(), cfg.data(), cfg.size()));
     // top_k above 1024 (after clamping to the vocabulary) samples from a reserved area; a
     // reallocation bumps the workspace generation, which drops the captured graphs below
     if (std::min<int64_t>(std::max<int64_t>(sampler.top_k, 1), c.vocab_size) > 1024) {
       check(fi_sample_reserve(ctx_, B, c.vocab_size));
     }
-    logits_rows_ = B;
+    logits_rows_[ss] = B;
+    samp_next_ = ss ^ 1;
   }
 
   if (use_graph) {
@@ -654,7 +683,7 @@ void ForwardExecutor::launch(const PackedBatch& b, const SamplerConfig& sampler,
       graphs_workspace_ = ws;
       graphs_buffers_ = buffers_moved_;
     }
-    const std::array<int32_t, 4> key{B, p.max_blocks, p.max_context_len, greedy ? 1 : 0};
+    const std::array<int32_t, 4> key{B, p.max_blocks, p.max_context_len, greedy ? 1 : 2 + ss};
     auto it = graphs_.find(key);
     if (it != graphs_.end()) {
       check(fi_graph_launch(ctx_, it->second));
@@ -680,13 +709,18 @@ void ForwardExecutor::launch(const PackedBatch& b, const SamplerConfig& sampler,
     enqueue(p);
   }
 
-  // the samples (B ids, then B probabilities) and the fault words into the pinned slot
+  // the samples (B ids, then B probabilities), the fault words and a sampled tick's advanced
+  // states into the pinned slot
   out_rows_ = B;
   uint8_t* h = static_cast<uint8_t*>(h_out_[slot]);
   check(fi_buf_download_async(ctx_, h, static_cast<size_t>(B) * 8, out_.get(), static_cast<size_t>(B) * 8));
   check(fi_ctx_faults_async(ctx_, reinterpret_cast<uint32_t*>(h + static_cast<size_t>(B) * 8)));
+  if (!greedy) {
+    check(fi_buf_download_async(ctx_, h + static_cast<size_t>(B) * 8 + 16, static_cast<size_t>(B) * 8,
+                                samp_[ss].get(), static_cast<size_t>(B) * 8));
+  }
   check(fi_event_record(ctx_, events_[slot]));
-  inflight_.push_back(Pending{slot, B, greedy});
+  inflight_.push_back(Pending{slot, B, greedy, ss});
   next_slot_ ^= 1;
   enqueue_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
 }
@@ -705,13 +739,12 @@ std::vector<TokenSample> ForwardExecutor::collect(std::vector<uint64_t>* states)
   // a fault bit: the check waits for the stream, reports and clears it
   if ((words[0] | words[1] | words[2] | words[3]) != 0) check(fi_ctx_check_faults(ctx_));
   if (!p.greedy) {
-    // sampled ticks are never launched ahead, so nothing else is in flight behind this one
     if (states == nullptr || states->size() != static_cast<size_t>(p.B)) {
       fail(ErrorKind::InvalidShape, "sampled batch requires one sampler state per sequence");
     }
-    check(fi_buf_download(ctx_, states->data(), static_cast<size_t>(p.B) * 8, samp_.get(),
-                          static_cast<size_t>(p.B) * 8));
+    std::memcpy(states->data(), h + static_cast<size_t>(p.B) * 8 + 16, static_cast<size_t>(p.B) * 8);
   }
+  samp_last_ = p.greedy ? -1 : p.ss;
   std::vector<TokenSample> out(p.B);
   for (int32_t i = 0; i < p.B; ++i) {
     int32_t id;

@@ -360,9 +360,10 @@ class ForwardExecutor {
   // (advanced in place by one draw per sequence).  run = launch + collect.
   std::vector<TokenSample> run(const PackedBatch& batch, const SamplerConfig& sampler, std::vector<uint64_t>* states);
   // Enqueues one tick (uploads, forward, the copy of its samples and fault words into pinned
-  // host memory) and returns without waiting.  feed_rows (a greedy decode tick enqueued behind
-  // the previous launch): row i's input token is the previous launch's sample feed_rows[i] when
-  // that is >= 0, read on the device; other rows keep the batch's token id.
+  // host memory) and returns without waiting.  feed_rows (a decode tick enqueued behind the
+  // previous launch): row i's input token, and for a sampled tick its sampler state, are the
+  // previous launch's sample and advanced state of row feed_rows[i] when that is >= 0, read on
+  // the device; other rows keep the batch's token id and states[i].
   void launch(const PackedBatch& batch, const SamplerConfig& sampler, const std::vector<uint64_t>* states,
               const std::vector<int32_t>* feed_rows = nullptr);
   // Waits for the oldest launched tick and returns its samples (states: the sampled path's
@@ -371,8 +372,8 @@ class ForwardExecutor {
   // Waits for the oldest launched tick and drops its samples.
   void discard();
   size_t in_flight() const { return inflight_.size(); }
-  // Whether launch(batch, ..., feed_rows) can run behind the single tick in flight: a greedy
-  // decode tick that keeps the previous tick's samples in place (no reallocation of them).
+  // Whether launch(batch, ..., feed_rows) can run behind the single tick in flight: a decode
+  // tick that keeps the previous tick's samples in place (no reallocation of them).
   bool can_feed(const PackedBatch& batch) const;
   // Host seconds of the last launch (enqueueing every launch) and the last collect (waiting for
   // the samples).
@@ -394,6 +395,7 @@ class ForwardExecutor {
     const int32_t *ids, *pos, *cu, *ctx, *bt, *last, *cs, *cd, *cc;
     const int64_t* slot;
     bool greedy;
+    int32_t ss;  // sampling slot: the logits and sampler buffers of a sampled tick
   };
   void reserve(size_t tokens, size_t seqs);
   void grow(DeviceBuffer& b, size_t bytes);  // reserve, noting a moved buffer
@@ -409,11 +411,16 @@ class ForwardExecutor {
     int32_t slot;
     int32_t B;
     bool greedy;
+    int32_t ss;
   };
   const DeviceModel* model_;
   BlockPool* pool_;
   fi_context* ctx_;
-  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_, logits_, samp_;
+  DeviceBuffer meta_, hidden_, normed_, q_, attn_, h1_, act_, parts_, last_norm_;
+  // Sampled ticks alternate between two sampling slots, each a logits buffer [B, vocab] and a
+  // sampler buffer (states [B] u64, temperature [B], top_k [B], top_p [B]): a tick enqueued
+  // behind a sampled tick reads that tick's advanced states from the other slot.
+  DeviceBuffer logits_[2], samp_[2];
   // one tick's samples: B token ids, then B probabilities (one download)
   DeviceBuffer out_;
   size_t cap_tokens_ = 0, cap_seqs_ = 0, cap_parts_ = 0;
@@ -421,12 +428,16 @@ class ForwardExecutor {
   bool graph_decode_;
   uint64_t buffers_moved_ = 0;             // bumped whenever an executor buffer is reallocated
   uint64_t graphs_buffers_ = 0, graphs_workspace_ = 0;  // generations the cached graphs recorded
-  std::map<std::array<int32_t, 4>, fi_graph*> graphs_;  // (B, stride, max_context_len, greedy)
+  // (B, stride, max_context_len, 1 greedy / 2 + sampling slot)
+  std::map<std::array<int32_t, 4>, fi_graph*> graphs_;
   std::map<std::array<int32_t, 4>, int32_t> seen_;       // eager runs per shape since the last drop
   uint64_t graph_replays_ = 0, graph_captures_ = 0, graph_drops_ = 0;
-  int32_t logits_rows_ = 0;  // rows of logits_ the last run sampled from
-  // Consecutive launches alternate between two pinned slots (metadata staging; samples, then the
-  // four fault words) and two events; at most two ticks are in flight.
+  int32_t logits_rows_[2] = {0, 0};  // rows each sampling slot's logits hold
+  int32_t samp_next_ = 0;            // the slot of the next sampled launch
+  int32_t samp_last_ = -1;           // the slot of the last collected tick (-1: greedy or none)
+  // Consecutive launches alternate between two pinned slots (metadata staging, then a sampled
+  // tick's sampler configuration; samples, the four fault words, then the advanced sampler
+  // states) and two events; at most two ticks are in flight.
   std::deque<Pending> inflight_;
   void* h_meta_[2] = {nullptr, nullptr};
   void* h_out_[2] = {nullptr, nullptr};
@@ -443,10 +454,10 @@ class Scheduler {
             bool graph_decode = false);
   uint64_t submit(const std::vector<uint32_t>& prompt, size_t max_new_tokens, std::optional<uint32_t> stop_token);
   std::optional<std::pair<BatchKind, std::vector<uint64_t>>> plan_next_tick() const;
-  // run_ahead: once this tick is enqueued, also enqueue the next tick when it will be a greedy
-  // decode tick (stream overlap, docs/performance-roadmap.md:321-326).  Its batch follows from
-  // the state this tick leaves except the token ids, which are this tick's samples, fed on the
-  // device.  The next call keeps it when its own planning packs the same batch and drops it
+  // run_ahead: once this tick is enqueued, also enqueue the next tick when it will be a decode
+  // tick (stream overlap, docs/performance-roadmap.md:321-326).  Its batch follows from the
+  // state this tick leaves except the token ids (and a sampled session's sampler states), which
+  // are this tick's samples, fed on the device.  The next call keeps it when its own planning packs the same batch and drops it
   // otherwise (after a submit, for instance): the ticks and their results are those of calls
   // without run_ahead.
   std::optional<TickReport> execute_next_tick(bool run_ahead = false);

@@ -389,8 +389,9 @@ bool Scheduler::launch_ahead(const PackedBatch& current) {
   // The next tick as its own call would pack it (execute_next_tick's decode branch with
   // append_to_batch and finalize_batch), from the state this tick leaves: positions, phases and
   // finished sequences are settled before its forward, and blocks are taken from the top of the
-  // pool's free list in row order.  Only the token ids wait for this tick's samples.
-  if (!session_.sampler.is_greedy() || executor_.in_flight() != 1) return false;
+  // pool's free list in row order.  Only the token ids, and a sampled session's sampler states,
+  // wait for this tick's samples.
+  if (executor_.in_flight() != 1) return false;
   const auto plan = plan_next_tick();
   if (!plan || plan->first != BatchKind::Decode) return false;
   const size_t bs = static_cast<size_t>(pool_->block_size());
@@ -438,7 +439,12 @@ bool Scheduler::launch_ahead(const PackedBatch& current) {
     const size_t n = (static_cast<size_t>(nb.context_lens[i]) + bs - 1) / bs;
     for (size_t j = 0; j < n; ++j) nb.block_tables[i * max_blocks + j] = tables[i][j];
   }
-  executor_.launch(nb, session_.sampler, nullptr, &feed);
+  // states of rows fed from this tick are gathered on the device; the others are the host's
+  std::vector<uint64_t> states(nb.sequence_ids.size(), 0);
+  for (size_t i = 0; i < states.size(); ++i) {
+    if (feed[i] < 0) states[i] = sequences_[index_of(nb.sequence_ids[i])].sampler_state;
+  }
+  executor_.launch(nb, session_.sampler, &states, &feed);
   ahead_.active = true;
   ahead_.state = state_;
   ahead_.batch = std::move(nb);

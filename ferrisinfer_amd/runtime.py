@@ -238,8 +238,8 @@ class Runtime:
         time of the native tick (host scheduling, the batched forward, the sample download) is
         kept in ``last_tick_seconds``.
 
-        run_ahead (FR_TICK_RUN_AHEAD): also enqueue the next tick when it will be a greedy decode
-        tick, so the device runs it while this call returns; the results are those of calls
+        run_ahead (FR_TICK_RUN_AHEAD): also enqueue the next tick when it will be a decode tick,
+        so the device runs it while this call returns; the results are those of calls
         without it.  A tick that ran ahead started on the device during the previous call, so
         its ``last_tick_seconds`` is the time since the previous call returned (the caller's
         time in between included), not the call's own duration."""

@@ -112,18 +112,20 @@ int32_t fr_submit(void* runtime, const uint32_t* prompt, int64_t n, int64_t max_
 /* ReferenceScheduler::execute_next_tick (scheduler.rs:393-415); *executed = 0 when idle. */
 int32_t fr_execute_next_tick(void* runtime, int32_t* executed);
 /* fr_execute_next_tick with flags.  FR_TICK_RUN_AHEAD: once this tick is enqueued, also enqueue
- * the next tick when it will be a greedy decode tick, so the device runs it while the host
- * returns this tick's report and plans the next call (the roadmap's stream overlap,
+ * the next tick when it will be a decode tick, so the device runs it while the host returns
+ * this tick's report and plans the next call (the roadmap's stream overlap,
  * docs/performance-roadmap.md:321-326; the reference runs its ticks one after the other).  The
- * next tick's batch follows from the state this tick leaves, except its token ids, which are
- * this tick's samples and are fed on the device.  The next call (with or without the flag) keeps
+ * next tick's batch follows from the state this tick leaves, except its token ids and, for a
+ * sampled session, its sampler states, which are this tick's samples and advanced states and
+ * are fed on the device.  The next call (with or without the flag) keeps
  * the enqueued tick when its own planning packs the same batch, and otherwise waits for it and
  * drops it: a submit in between drops it.  Reports, tokens, probabilities, block ids and
  * released blocks are those of calls without the flag.  A caller that expects no submit before
  * its next call sets the flag; a wrong expectation costs the dropped tick's device time. */
 #define FR_TICK_RUN_AHEAD 1
 int32_t fr_execute_next_tick_ex(void* runtime, int32_t flags, int32_t* executed);
-/* [ticks enqueued ahead, kept, dropped, 1 if the last executed tick was one enqueued ahead]. */
+/* [ticks enqueued ahead, kept, dropped, 1 if the last executed tick was one enqueued ahead].
+ * Before the first submit it reports zeros (observers create no scheduler). */
 int32_t fr_run_ahead_counters(void* runtime, uint64_t* out4);
 int32_t fr_has_pending(void* runtime);
 /* Report of the last tick: rows of 9 int64 (sequence_id, batch_kind, reused, appended,
