@@ -53,6 +53,11 @@ struct PrefillArgs {
   int num_seqs;
   int max_query_len;
   const int* order;          // (sequence, query tile) pairs, largest first
+  // prefill_x3_kernel with key splits: each (tile, kv head) runs as kv_splits workgroups over
+  // consecutive ranges of its key chunks, writing partials (unnormalised O, reference point and
+  // row sum per row) that prefill_split_merge_kernel combines in split order
+  int kv_splits;
+  float* part;
 };
 
 // One workgroup sorts the (sequence, query tile) pairs by the number of kb-key chunks they
@@ -371,20 +376,26 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
 #define FI_PREFILL_FOLD 1
 #endif
 
-int32_t plan_tiles(fi_context* ctx, PrefillArgs& args, int qt, int kb, const char* name, dim3* grid) {
+int32_t plan_tiles(fi_context* ctx, PrefillArgs& args, int qt, int kb, const char* name, dim3* grid, int splits = 1,
+                   size_t part_floats = 0) {
   const int ntiles = (args.max_query_len + qt - 1) / qt;
   const long pairs = (long)ntiles * args.num_seqs;
-  FI_REQUIRE(pairs * args.hkv <= 0x7fffffffL, FI_ERR_INVALID_SHAPE, std::string(name) + ": grid too large");
-  FI_TRY(fi::ensure_workspace(ctx, (size_t)pairs * sizeof(int)));
+  FI_REQUIRE(pairs * args.hkv * splits <= 0x7fffffffL, FI_ERR_INVALID_SHAPE, std::string(name) + ": grid too large");
+  // the tile order, then (split launches) each workgroup's partials
+  const size_t order_bytes = ((size_t)pairs * sizeof(int) + 255) & ~static_cast<size_t>(255);
+  const size_t part_bytes = splits > 1 ? (size_t)pairs * args.hkv * splits * part_floats * sizeof(float) : 0;
+  FI_TRY(fi::ensure_workspace(ctx, order_bytes + part_bytes));
   int* order = static_cast<int*>(ctx->workspace);
+  args.kv_splits = splits;
+  args.part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->workspace) + order_bytes) : nullptr;
   // one round of workgroups (two per CU): pair long and short tiles on each CU
   const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
-  const int fold = FI_PREFILL_FOLD && pairs * args.hkv <= 2 * cus;
+  const int fold = FI_PREFILL_FOLD && splits == 1 && pairs * args.hkv <= 2 * cus;
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, ctx->stream, args.cu_seqlens, args.context_lens,
                      args.num_seqs, ntiles, qt, kb, fold, order, ctx->d_faults);
   FI_CHECK_LAUNCH("prefill_plan_kernel");
   args.order = order;
-  *grid = dim3(static_cast<unsigned>(pairs * args.hkv));
+  *grid = dim3(static_cast<unsigned>(pairs * args.hkv * splits));
   return FI_OK;
 }
 
@@ -778,7 +789,7 @@ __device__ __forceinline__ v4f mma6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
 }
 
-template <int D, int G, int RG>
+template <int D, int G, int RG, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) {
   constexpr int QT = kRows * RG / G;    // query tokens per workgroup (RG 16-row groups a wave)
   constexpr int KB = 32;                 // keys per chunk: one 32-key step of P V
@@ -796,7 +807,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
   const float* __restrict__ k_cache = static_cast<const float*>(a.k_cache);
   const float* __restrict__ v_cache = static_cast<const float*>(a.v_cache);
   const int ntiles = (a.max_query_len + QT - 1) / QT;
-  const int rank = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
+  const int wg = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
+  const int rank = SPLIT ? wg / a.kv_splits : wg;
+  const int split = SPLIT ? wg - rank * a.kv_splits : 0;
   const int tile = a.order[rank];
   const int qt = tile % ntiles, seq = tile / ntiles;
   const int qs = a.cu_seqlens[seq];
@@ -842,6 +855,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
 
   const int kend = start + min(qlen, q0 + QT);
   const int nchunks = max((kend + KB - 1) / KB, 1);
+  // the chunks this workgroup multiplies: all, or its split's consecutive share
+  const int c_lo = SPLIT ? split * nchunks / a.kv_splits : 0;
+  const int c_hi = SPLIT ? (split + 1) * nchunks / a.kv_splits : nchunks;
 
   // staging: thread owns key tid % KB of the chunk and quad columns tid / KB + KR r; one block
   // lookup per chunk, looked up a chunk ahead; loads unconditional (clamped key)
@@ -909,13 +925,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
     }
   };
 
-  lookup(0);
-  fetch(0);
+  lookup(c_lo);
+  fetch(c_lo);
   fetch_v();
-  lookup(1);
+  lookup(c_lo + 1);
   stage();
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
+  for (int c = c_lo; c < c_hi; ++c) {
     const int k0 = c * KB;
 
     // ---- S^T = K Q^T: 32 keys x 16 rows per group ----
@@ -979,14 +995,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
       mx = fmaxf(mx, fi::lane_xor32(mx, lane));
       const float m_chunk = mx * c2;
       const float m_new = m_chunk > m_row[g] + kLazy ? m_chunk : m_row[g];
-      const float alpha = __builtin_amdgcn_exp2f(m_row[g] - m_new);
+      // a split's first chunks may hold no key a row sees (it starts past the row's
+      // position): its reference point stays -inf and its probabilities 0 until one does
+      const bool none = SPLIT && m_new == -INFINITY;
+      const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_row[g] - m_new);
       m_row[g] = m_new;
       float ls = 0.0f;
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float pexp = __builtin_amdgcn_exp2f(fmaf(s_acc[g][jt][v], c2, -m_new));
+          const float pexp = none ? 0.0f : __builtin_amdgcn_exp2f(fmaf(s_acc[g][jt][v], c2, -m_new));
           s_acc[g][jt][v] = pexp;
           ls += pexp;
         }
@@ -1027,7 +1046,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
     }
     fetch_v();  // its V rows: the loads are in flight while the waves meet at the barrier
     __syncthreads();  // every wave is done with this chunk's K/V
-    if (c + 1 < nchunks) {  // workgroup-uniform
+    if (c + 1 < c_hi) {  // workgroup-uniform
       stage();
       __syncthreads();
     }
@@ -1040,6 +1059,26 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
   // reloaded) rather than kept live through the chunk loop, where registers are at the limit
   const int lane_e = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   const int li_e = lane_e & 15, lk_e = lane_e >> 4;
+  if constexpr (SPLIT) {
+    // this split's partials: O [rows][D] unnormalised, then (reference point, row sum) [rows],
+    // for every row of the tile (the merge skips the padding ones)
+    constexpr int ROWS = kRows * RG;
+    const size_t unit = ((size_t)tile * a.kv_splits + split) * a.hkv + kvh;
+    float* po = a.part + unit * ROWS * D;
+    float* pml = a.part + (size_t)gridDim.x * ROWS * D + unit * ROWS * 2;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      float l_row = l_part[g] + fi::lane_xor16(l_part[g], lane);
+      l_row += fi::lane_xor32(l_row, lane);
+      const int rr = 16 * (w + 4 * g) + li_e;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<float4*>(po + (size_t)rr * D + 16 * dt + 4 * lk_e) =
+            make_float4(o[g][dt][0], o[g][dt][1], o[g][dt][2], o[g][dt][3]);
+      if (lk_e == 0) *reinterpret_cast<float2*>(pml + (size_t)rr * 2) = make_float2(m_row[g], l_row);
+    }
+    return;
+  }
   const int qs_e = a.cu_seqlens[seq], qlen_e = a.cu_seqlens[seq + 1] - qs_e;
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
@@ -1059,25 +1098,99 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
   }
 }
 
+// One workgroup per (tile, kv head) of a split launch: each row's output is the splits'
+// partials combined in split order, each rescaled from its own reference point to the largest
+// (a split with no key the row sees carries -inf and adds nothing; the split holding key 0
+// always sees one), then normalised by the combined row sum.
+template <int D, int RG>
+__global__ __launch_bounds__(kThreads) void prefill_split_merge_kernel(PrefillArgs a, int qt_tokens, int ntiles) {
+  constexpr int ROWS = kRows * RG, DQ = D / 4;
+  const int tile = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
+  const int seq = tile / ntiles, q0 = (tile % ntiles) * qt_tokens;
+  const int qs = a.cu_seqlens[seq], qlen = a.cu_seqlens[seq + 1] - qs;
+  if (q0 >= qlen) return;
+  const int S = a.kv_splits;
+  const float* pml = a.part + (size_t)gridDim.x * S * ROWS * D;
+  for (int idx = threadIdx.x; idx < ROWS * DQ; idx += kThreads) {
+    const int r = idx / DQ, dq = idx - (idx / DQ) * DQ;
+    const int h = r / qt_tokens, t = r - (r / qt_tokens) * qt_tokens;
+    if (h >= a.group || q0 + t >= qlen) continue;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < S; ++sp) {
+      const size_t unit = ((size_t)tile * S + sp) * a.hkv + kvh;
+      mx = fmaxf(mx, pml[(unit * ROWS + r) * 2]);
+    }
+    float l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int sp = 0; sp < S; ++sp) {
+      const size_t unit = ((size_t)tile * S + sp) * a.hkv + kvh;
+      const float2 ml = *reinterpret_cast<const float2*>(pml + (unit * ROWS + r) * 2);
+      if (ml.x == -INFINITY) continue;
+      const float wgt = __builtin_amdgcn_exp2f(ml.x - mx);
+      const float4 ov = *reinterpret_cast<const float4*>(a.part + (unit * ROWS + r) * D + 4 * dq);
+      l = l + wgt * ml.y;
+      acc = make_float4(acc.x + wgt * ov.x, acc.y + wgt * ov.y, acc.z + wgt * ov.z, acc.w + wgt * ov.w);
+    }
+    const float inv = 1.0f / l;
+    *reinterpret_cast<float4*>(a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D + 4 * dq) =
+        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+  }
+}
+
+#ifndef FI_PREFILL_MAX_SPLITS
+#define FI_PREFILL_MAX_SPLITS 4  // key splits of a small f32-pool prefill launch, at most
+#endif
+
+template <int D, int G, int RG, bool SPLIT>
+void launch_x3(fi_context* ctx, const PrefillArgs& args, dim3 grid) {
+  hipLaunchKernelGGL((prefill_x3_kernel<D, G, RG, SPLIT>), grid, dim3(kThreads), 0, ctx->stream, args);
+}
+
+template <int D, int RG, bool SPLIT>
+void launch_x3_g(fi_context* ctx, const PrefillArgs& args, dim3 grid, int g) {
+  switch (g) {
+    case 1:
+      launch_x3<D, 1, RG, SPLIT>(ctx, args, grid);
+      break;
+    case 2:
+      launch_x3<D, 2, RG, SPLIT>(ctx, args, grid);
+      break;
+    case 4:
+      launch_x3<D, 4, RG, SPLIT>(ctx, args, grid);
+      break;
+    default:
+      launch_x3<D, 8, RG, SPLIT>(ctx, args, grid);
+      break;
+  }
+}
+
 template <int D, int RG>
 int32_t launch_prefill_x3_rg(fi_context* ctx, PrefillArgs& args, int g) {
   const int qt = kRows * RG / g;
-  dim3 grid;
-  FI_TRY(plan_tiles(ctx, args, qt, 32, "fi_attn_prefill_paged", &grid));
-  switch (g) {
-    case 1:
-      hipLaunchKernelGGL((prefill_x3_kernel<D, 1, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
-      break;
-    case 2:
-      hipLaunchKernelGGL((prefill_x3_kernel<D, 2, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
-      break;
-    case 4:
-      hipLaunchKernelGGL((prefill_x3_kernel<D, 4, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
-      break;
-    default:
-      hipLaunchKernelGGL((prefill_x3_kernel<D, 8, RG>), grid, dim3(kThreads), 0, ctx->stream, args);
-      break;
+  // Key splits for launches that leave most workgroup slots empty (one row group; a launch with
+  // two per CU runs two row groups a wave instead): up to four workgroups a CU, each with at
+  // least two 32-key chunks (a tile's keys are at least max_query_len).
+  int splits = 1;
+  if (RG == 1) {
+    const long cus = ctx->compute_units > 0 ? ctx->compute_units : 256;
+    const long wgs = (long)((args.max_query_len + qt - 1) / qt) * args.num_seqs * args.hkv;
+    splits = static_cast<int>(std::min<long>(FI_PREFILL_MAX_SPLITS, (4 * cus) / std::max<long>(wgs, 1)));
+    splits = std::max(1, std::min(splits, args.max_query_len / 64));
   }
+  dim3 grid;
+  FI_TRY(plan_tiles(ctx, args, qt, 32, "fi_attn_prefill_paged", &grid, splits, kRows * RG * (D + 2)));
+  if constexpr (RG == 1) {
+    if (splits > 1) {
+      launch_x3_g<D, RG, true>(ctx, args, grid, g);
+      FI_CHECK_LAUNCH("prefill_x3_kernel");
+      const int ntiles = (args.max_query_len + qt - 1) / qt;
+      hipLaunchKernelGGL((prefill_split_merge_kernel<D, RG>), dim3(grid.x / splits), dim3(kThreads), 0, ctx->stream,
+                         args, qt, ntiles);
+      FI_CHECK_LAUNCH("prefill_split_merge_kernel");
+      return FI_OK;
+    }
+  }
+  launch_x3_g<D, RG, false>(ctx, args, grid, g);
   FI_CHECK_LAUNCH("prefill_x3_kernel");
   return FI_OK;
 }

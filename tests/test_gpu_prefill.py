@@ -353,6 +353,61 @@ def test_prefill_c5_chunk_after_cached_prefix(orc, gpu_ctx):
             assert normwise_error(got16, got) <= 5e-3
 
 
+@pytest.mark.parametrize("prefixes,qlen", [((256, 768, 1280, 1792), 256), ((1536,), 256), ((0, 40, 1000), 130)])
+def test_prefill_key_splits_small_launch(orc, gpu_ctx, prefixes, qlen):
+    """A C4-shaped prefill tick (Qwen2 heads 14/2, D 64) on an f32 pool: so few (tile, kv head)
+    workgroups that the launch splits each tile's key chunks over up to four workgroups and
+    merges their partials.  Rows whose keys all lie in later splits, splits with no chunk and
+    a chunk with no prefix are included.  Every row against the f64 closed form and the first
+    and last rows of each chunk against the oracle's cached-prefixed attention, at 1e-4."""
+    import torch
+
+    from ferrisinfer_amd import DTYPE_F32
+
+    print(f"prefill key splits prefixes={prefixes} qlen={qlen}", flush=True)
+    rng = np.random.default_rng(61)
+    hq, hkv, d, bs = 14, 2, 64, 16
+    n = len(prefixes)
+    ctx_lens = np.array([p + qlen for p in prefixes], np.int32)
+    qlens = np.full(n, qlen, np.int32)
+    nblk = (ctx_lens + bs - 1) // bs
+    num_blocks = int(nblk.sum()) + 8
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    tables = np.zeros((n, nblk.max()), np.int32)
+    o = 0
+    for b in range(n):
+        tables[b, :nblk[b]] = perm[o:o + nblk[b]]
+        o += nblk[b]
+    ks = [rng.standard_normal((L, hkv, d), dtype=np.float32) for L in ctx_lens]
+    vs = [rng.standard_normal((L, hkv, d), dtype=np.float32) for L in ctx_lens]
+    pool_k = np.zeros((num_blocks, hkv, bs, d), np.float32)
+    pool_v = np.zeros_like(pool_k)
+    for b in range(n):
+        for p in range(int(ctx_lens[b])):
+            pool_k[tables[b, p // bs], :, p % bs] = ks[b][p]
+            pool_v[tables[b, p // bs], :, p % bs] = vs[b][p]
+    q = rng.standard_normal((int(qlens.sum()), hq, d), dtype=np.float32)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    scale = float(1.0 / np.sqrt(np.float32(d)))
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    out = torch.empty((q.shape[0], hq, d), device="cuda")
+    gpu_ctx.attn_prefill_paged(dev(q), dev(pool_k), dev(pool_v), DTYPE_F32, dev(tables), dev(cu), dev(ctx_lens),
+                               qlen, hkv, bs, num_blocks, scale, out)
+    torch.cuda.synchronize()
+    gpu_ctx.check_faults()
+    got = out.cpu().numpy()
+    ref = np.concatenate([brute_force_f64(q[cu[b]:cu[b + 1]], ks[b], vs[b], int(prefixes[b])) for b in range(n)])
+    assert normwise_error(got, ref) <= 1e-4, normwise_error(got, ref)
+    for b in range(n):
+        start = int(prefixes[b])
+        for r0 in (0, qlen - 8):
+            rows = slice(int(cu[b]) + r0, int(cu[b]) + r0 + 8)
+            ref_o = orc.cached_prefixed_causal_attention(q[rows], ks[b][:start + r0], vs[b][:start + r0], start + r0,
+                                                         ks[b][start + r0:start + r0 + 8],
+                                                         vs[b][start + r0:start + r0 + 8])
+            assert normwise_error(got[rows], ref_o) <= 1e-4
+
+
 def test_prefill_query_beyond_max_query_len_reported(gpu_ctx):
     """A cu_seqlens entry longer than max_query_len: the tiles max_query_len sized are computed,
     the sequence's rows past them are not, and the host gets Runtime with its own message; the
