@@ -1098,6 +1098,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
   }
 }
 
+#ifndef FI_PREFILL_MAX_SPLITS
+#define FI_PREFILL_MAX_SPLITS 4  // key splits of a small f32-pool prefill launch, at most
+#endif
+
 // One workgroup per (tile, kv head) of a split launch: each row's output is the splits'
 // partials combined in split order, each rescaled from its own reference point to the largest
 // (a split with no key the row sees carries -inf and adds nothing; the split holding key 0
@@ -1105,41 +1109,59 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_x3_kernel(PrefillArgs a) 
 template <int D, int RG>
 __global__ __launch_bounds__(kThreads) void prefill_split_merge_kernel(PrefillArgs a, int qt_tokens, int ntiles) {
   constexpr int ROWS = kRows * RG, DQ = D / 4;
+  constexpr int ITER = ROWS * DQ / kThreads;  // (row, column quad) items a thread
+  constexpr int BATCH = ITER < 4 ? ITER : 4;  // items whose loads are issued together
+  constexpr int MAXS = FI_PREFILL_MAX_SPLITS;
+  static_assert(ROWS * DQ % kThreads == 0 && ITER % BATCH == 0, "items must split over the workgroup");
   const int tile = blockIdx.x / a.hkv, kvh = blockIdx.x % a.hkv;
   const int seq = tile / ntiles, q0 = (tile % ntiles) * qt_tokens;
   const int qs = a.cu_seqlens[seq], qlen = a.cu_seqlens[seq + 1] - qs;
   if (q0 >= qlen) return;
   const int S = a.kv_splits;
   const float* pml = a.part + (size_t)gridDim.x * S * ROWS * D;
-  for (int idx = threadIdx.x; idx < ROWS * DQ; idx += kThreads) {
-    const int r = idx / DQ, dq = idx - (idx / DQ) * DQ;
-    const int h = r / qt_tokens, t = r - (r / qt_tokens) * qt_tokens;
-    if (h >= a.group || q0 + t >= qlen) continue;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < S; ++sp) {
-      const size_t unit = ((size_t)tile * S + sp) * a.hkv + kvh;
-      mx = fmaxf(mx, pml[(unit * ROWS + r) * 2]);
+  const size_t unit0 = (size_t)tile * S * a.hkv + kvh;  // split sp: unit0 + sp * hkv
+  for (int it0 = 0; it0 < ITER; it0 += BATCH) {
+    // every split's (point, sum) and O quad of BATCH items are loaded before any is combined
+    // (splits past S read split 0 and are dropped)
+    float2 ml[BATCH][MAXS];
+    float4 ov[BATCH][MAXS];
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int idx = threadIdx.x + (it0 + b) * kThreads;
+      const int r = idx / DQ, dq = idx - (idx / DQ) * DQ;
+#pragma unroll
+      for (int sp = 0; sp < MAXS; ++sp) {
+        const size_t unit = unit0 + (size_t)(sp < S ? sp : 0) * a.hkv;
+        ml[b][sp] = *reinterpret_cast<const float2*>(pml + (unit * ROWS + r) * 2);
+        ov[b][sp] = *reinterpret_cast<const float4*>(a.part + (unit * ROWS + r) * D + 4 * dq);
+      }
     }
-    float l = 0.0f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int sp = 0; sp < S; ++sp) {
-      const size_t unit = ((size_t)tile * S + sp) * a.hkv + kvh;
-      const float2 ml = *reinterpret_cast<const float2*>(pml + (unit * ROWS + r) * 2);
-      if (ml.x == -INFINITY) continue;
-      const float wgt = __builtin_amdgcn_exp2f(ml.x - mx);
-      const float4 ov = *reinterpret_cast<const float4*>(a.part + (unit * ROWS + r) * D + 4 * dq);
-      l = l + wgt * ml.y;
-      acc = make_float4(acc.x + wgt * ov.x, acc.y + wgt * ov.y, acc.z + wgt * ov.z, acc.w + wgt * ov.w);
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int idx = threadIdx.x + (it0 + b) * kThreads;
+      const int r = idx / DQ, dq = idx - (idx / DQ) * DQ;
+      const int h = r / qt_tokens, t = r - (r / qt_tokens) * qt_tokens;
+      if (h >= a.group || q0 + t >= qlen) continue;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sp = 0; sp < MAXS; ++sp)
+        if (sp < S) mx = fmaxf(mx, ml[b][sp].x);
+      float l = 0.0f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int sp = 0; sp < MAXS; ++sp) {
+        if (sp >= S || ml[b][sp].x == -INFINITY) continue;
+        const float wgt = __builtin_amdgcn_exp2f(ml[b][sp].x - mx);
+        const float4 o = ov[b][sp];
+        l = l + wgt * ml[b][sp].y;
+        acc = make_float4(acc.x + wgt * o.x, acc.y + wgt * o.y, acc.z + wgt * o.z, acc.w + wgt * o.w);
+      }
+      const float inv = 1.0f / l;
+      *reinterpret_cast<float4*>(a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D + 4 * dq) =
+          make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
     }
-    const float inv = 1.0f / l;
-    *reinterpret_cast<float4*>(a.out + ((size_t)(qs + q0 + t) * a.hq + kvh * a.group + h) * D + 4 * dq) =
-        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
   }
 }
-
-#ifndef FI_PREFILL_MAX_SPLITS
-#define FI_PREFILL_MAX_SPLITS 4  // key splits of a small f32-pool prefill launch, at most
-#endif
 
 template <int D, int G, int RG, bool SPLIT>
 void launch_x3(fi_context* ctx, const PrefillArgs& args, dim3 grid) {
