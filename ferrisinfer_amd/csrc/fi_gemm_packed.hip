@@ -708,6 +708,42 @@ __global__ void splitk_swiglu_kernel(const float* __restrict__ parts, int splits
   }
 }
 
+// The same for even n: two adjacent output columns a thread, their (up, gate) pairs read as
+// one 16-byte vector per split.  Each value's arithmetic and order are the kernel's above.
+__global__ void splitk_swiglu2_kernel(const float* __restrict__ parts, int splits, const float* __restrict__ b_up,
+                                      const float* __restrict__ b_gate, int m, int n, void* __restrict__ out,
+                                      int out_bf16) {
+  const size_t total2 = (size_t)m * n / 2;  // column pairs = float4 elements per split plane
+  const float4* p4 = reinterpret_cast<const float4*>(parts);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total2; i += (size_t)gridDim.x * blockDim.x) {
+    float4 x = p4[i];
+    for (int z0 = 1; z0 < splits; z0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p4[(size_t)(z0 + u < splits ? z0 + u : 0) * total2 + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (z0 + u < splits) {
+          x.x = x.x + v[u].x;
+          x.y = x.y + v[u].y;
+          x.z = x.z + v[u].z;
+          x.w = x.w + v[u].w;
+        }
+    }
+    const int c = static_cast<int>((2 * i) % n);  // even: columns c and c + 1 share the row
+    const float up0 = b_up ? x.x + b_up[c] : x.x;
+    const float up1 = b_up ? x.z + b_up[c + 1] : x.z;
+    float g0 = b_gate ? x.y + b_gate[c] : x.y;
+    float g1 = b_gate ? x.w + b_gate[c + 1] : x.w;
+    g0 = g0 * (1.0f / (1.0f + __expf(-g0)));
+    g1 = g1 * (1.0f / (1.0f + __expf(-g1)));
+    if (out_bf16)
+      static_cast<uint32_t*>(out)[i] = fi::f32_to_bf16_bits(up0 * g0) | (fi::f32_to_bf16_bits(up1 * g1) << 16);
+    else
+      reinterpret_cast<float2*>(out)[i] = make_float2(up0 * g0, up1 * g1);
+  }
+}
+
 // Up to three source matrices; in column mode they are concatenated along N.
 struct PackSources {
   const float* src[3];
@@ -1250,6 +1286,15 @@ namespace fi {
 int32_t splitk_swiglu(fi_context* ctx, const float* parts, int32_t splits, const float* bias_up,
                       const float* bias_gate, int32_t m, int32_t n, void* out, bool out_bf16) {
   const size_t total = (size_t)m * n;
+  const bool pairs = n % 2 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) & (out_bf16 ? 3 : 7)) == 0;
+  if (pairs) {
+    const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total / 2 + 255) / 256, 4096));
+    hipLaunchKernelGGL(splitk_swiglu2_kernel, dim3(blocks), dim3(256), 0, ctx->stream, parts, splits, bias_up,
+                       bias_gate, m, n, out, out_bf16 ? 1 : 0);
+    FI_CHECK_LAUNCH("splitk_swiglu2_kernel");
+    return FI_OK;
+  }
   const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 4096));
   hipLaunchKernelGGL(splitk_swiglu_kernel, dim3(blocks), dim3(256), 0, ctx->stream, parts, splits, bias_up, bias_gate,
                      m, n, out, out_bf16 ? 1 : 0);
