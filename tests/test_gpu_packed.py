@@ -107,8 +107,11 @@ def test_packed_gemm_transposed_source_and_exact_integers(gpu_ctx):
             assert np.array_equal(sum_splits(out.cpu().numpy()), a @ w), (m, k, n, pw, layout)
 
 
-@pytest.mark.parametrize("m,k,f,bias", [(64, 896, 4864, True), (7, 256, 688, False), (100, 64, 40, True)])
+@pytest.mark.parametrize("m,k,f,bias", [(64, 896, 4864, True), (7, 256, 688, False), (100, 64, 40, True),
+                                         (9, 512, 1001, True)])
 def test_packed_swiglu(orc, gpu_ctx, m, k, f, bias):
+    """Even widths take the two-columns-a-thread split consumer, the odd one (split K, 4 splits)
+    the one-column consumer."""
     import torch
 
     rng = np.random.default_rng(m + f)
